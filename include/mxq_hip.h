@@ -1,0 +1,110 @@
+/* mxq_hip.h -- C ABI of libmxq_hip.so, the gfx950 implementation of mxq's block quantization, LUT and
+ * systolic-emulation hot path.
+ *
+ * Conventions
+ *   - Every pointer argument named as an array is device memory (HIP), allocated by the caller; the library
+ *     allocates nothing except where an entry point says so.
+ *   - Shapes are int64.  A tensor quantized along one axis is viewed as (outer, n, inner), row-major, with the
+ *     block axis n in the middle: element (o, k, i) is at (o * n + k) * inner + i.  Its scales are
+ *     (outer, ceil(n / block_size), inner).
+ *   - `stream` is a hipStream_t (NULL: the default stream).  Kernels are enqueued asynchronously; an entry
+ *     point returns before they run, except where it says it synchronises.
+ *   - Every entry point returns 0 (MXQ_OK) or an error code; mxq_last_error() then describes the failure
+ *     (thread-local, valid until the next call on that thread).
+ *   - Rounding codes: 0 ties_away ("nearest"), 1 rne ("even"), 2 truncate ("floor"), the order of
+ *     mxq.rounding.MODES.  Grid codes: 0 qtorch, 1 ieee, 2 ocp, the order of mxq.element_quant.float_em.GRIDS.
+ *
+ * Reference citations are relative to the chloe-wong/microscaling-quant repository.
+ */
+#ifndef MXQ_HIP_H
+#define MXQ_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mxq_stream_t;
+
+enum { MXQ_OK = 0, MXQ_EINVAL = 1, MXQ_EHIP = 2 };
+
+/* Input element types of the block quantizer. */
+enum { MXQ_DT_F32 = 0, MXQ_DT_BF16 = 1, MXQ_DT_F16 = 2 };
+
+/* Step 1 (scale factor) rules: mxq/scale_factor.py:40-81. */
+enum { MXQ_SCALE_NONE = 0, MXQ_SCALE_MXQUANT = 1, MXQ_SCALE_OCP = 2, MXQ_SCALE_OCP_NO_CLIP = 3 };
+/* Step 2 (element) rules: float_em grids (mxq/element_quant/float_em.py:64-134) and microxcaling's
+ * _quantize_elemwise (mxq/element_quant/microsoft.py:18-23). */
+enum { MXQ_ELEM_NONE = 0, MXQ_ELEM_QTORCH = 1, MXQ_ELEM_IEEE = 2, MXQ_ELEM_OCP = 3, MXQ_ELEM_MICROSOFT = 4 };
+
+typedef struct mxq_block_spec {
+  int32_t scale_rule;   /* MXQ_SCALE_* */
+  float scale_floor;    /* MXQUANT: the float32 value of the floor (1e-38 or 2^-23) */
+  int32_t scale_emax;   /* OCP, OCP_NO_CLIP: the format's emax (emax - 1 for placement "below_top") */
+  int32_t scale_bits;   /* OCP, OCP_NO_CLIP: E8M0 width (8) */
+  int32_t elem;         /* MXQ_ELEM_* */
+  int32_t e, m;         /* float_em widths; MICROSOFT: ebits and mbits (sign and implicit bit included) */
+  int32_t rounding;     /* rounding code */
+  float max_norm;       /* OCP grid and MICROSOFT saturation */
+  int32_t via_e, via_m; /* OCP grid only: round on the ieee float(via_e, via_m) grid first; via_e = 0: none */
+} mxq_block_spec;
+
+/* Library identity and the last error of the calling thread. */
+const char* mxq_last_error(void);
+int mxq_version(void);
+
+/* Fused block quantization: per block, amax -> scale X (step 1) -> z = block / X -> P = element rule (step 2).
+ * V: (outer, n, inner) of type v_dtype; P: float32, same shape; X: float32 (outer, ceil(n/bs), inner).
+ * The last block along n is zero-padded for the amax.
+ * Replaces mxq/block/_driver.py:45-66 `compose` with the pairs of mxq/block/mxquant.py:26-32,
+ * mxq/block/mxgemmini.py:37-59 and mxq/block/ocp.py:35-49. */
+int mxq_block_quantize(const void* V, int32_t v_dtype, float* P, float* X, int64_t outer, int64_t n,
+                       int64_t inner, int64_t block_size, const mxq_block_spec* spec, mxq_stream_t stream);
+
+/* out = P * expand(X) along n.  Replaces mxq/block/_driver.py:69-72 `dequantize`. */
+int mxq_block_dequantize(const float* P, const float* X, float* out, int64_t outer, int64_t n, int64_t inner,
+                         int64_t block_size, mxq_stream_t stream);
+
+/* ---- elementwise primitives over flat arrays of n elements (the caller broadcasts) ---------------------- */
+
+/* rounding.round_bits on int64 arrays of uint32 patterns; keep per element (int64 array) or, when keep is
+ * NULL, keep_scalar.  Replaces mxq/rounding/__init__.py:51-55. */
+int mxq_round_bits(const int64_t* bits, const int64_t* keep, int32_t keep_scalar, int64_t* out, int64_t n,
+                   int32_t mode, mxq_stream_t stream);
+
+/* rounding.round_int on float32 (dtype 0) or float64 (dtype 3).  Replaces mxq/rounding/__init__.py:58-61. */
+int mxq_round_int(const void* k, int32_t dtype, void* out, int64_t n, int32_t mode, mxq_stream_t stream);
+
+/* rounding.bf16.  Replaces mxq/rounding/__init__.py:64-85. */
+int mxq_bf16(const float* x, float* out, int64_t n, mxq_stream_t stream);
+
+/* float_em.quantize on a float32 (dtype 0) or float64 (dtype 3) input, float32 out; max_norm for grid ocp.
+ * Replaces mxq/element_quant/float_em.py:50-61. */
+int mxq_float_em(const void* z, int32_t dtype, float* out, int64_t n, int32_t e, int32_t m, int32_t mode,
+                 int32_t grid, float max_norm, mxq_stream_t stream);
+
+/* microxcaling _quantize_elemwise (float formats, allow_denorm) on float32.  Replaces
+ * mxq/element_quant/microsoft.py:18-23 (mxq/microxcaling/elemwise.py:63-169). */
+int mxq_microsoft(const float* z, float* out, int64_t n, int32_t ebits, int32_t mbits, float max_norm,
+                  int32_t mode, int32_t saturate, mxq_stream_t stream);
+
+/* A scale-factor rule of `spec` (MXQUANT, OCP or OCP_NO_CLIP with the MICROSOFT element fields) applied to
+ * block maxima.  Replaces mxq/scale_factor.py:40-81. */
+int mxq_scale_factor(const float* amax, float* out, int64_t n, const mxq_block_spec* spec, mxq_stream_t stream);
+
+/* arith.exact_add (float32 operands).  Replaces mxq/arith.py:68-103. */
+int mxq_exact_add(const float* a, const float* b, float* out, int64_t n, int32_t e, int32_t m, int32_t mode,
+                  int32_t grid, float max_norm, mxq_stream_t stream);
+
+/* arith.truncate_significand, flush_product (threshold = float32 2^floor_exp), saturate.
+ * Replace mxq/arith.py:106-117, :120-124, :127-137. */
+int mxq_truncate_significand(const float* x, float* out, int64_t n, int32_t m, mxq_stream_t stream);
+int mxq_flush_product(const float* x, float* out, int64_t n, float threshold, mxq_stream_t stream);
+int mxq_saturate(const float* x, float* out, int64_t n, float limit, float value, mxq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXQ_HIP_H */

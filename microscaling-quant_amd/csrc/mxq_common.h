@@ -1,0 +1,28 @@
+// Host-side plumbing shared by the library's translation units: error state and launch checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/mxq_hip.h"
+
+namespace mxq {
+
+void set_error(const std::string& msg);
+
+// Record `msg` and return MXQ_EINVAL.
+int invalid(const std::string& msg);
+
+// After a launch: MXQ_OK, or MXQ_EHIP with hipGetLastError's text.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(mxq_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// One-dimensional grid of `threads` threads in blocks of `block`; grid.x caps at 2^31 - 1 blocks.
+inline dim3 grid_for(int64_t threads, int block) { return dim3((unsigned)ceil_div(threads, block)); }
+
+}  // namespace mxq

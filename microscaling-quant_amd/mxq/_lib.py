@@ -1,0 +1,128 @@
+"""Loader and call plumbing for libmxq_hip.so, the gfx950 kernels behind every mxq operation.
+
+The library is a plain C ABI (include/mxq_hip.h) loaded with ctypes.  torch is imported first, so the
+library's libamdhip64.so.7 dependency resolves to the HIP runtime torch already loaded: one runtime, one set
+of streams and device pointers.  Tensors are passed as device pointers; outputs are allocated by torch on the
+input's device; kernels run on torch's current stream of that device.
+
+There is no CPU implementation behind this package.  CPU tensors are copied to the current GPU, computed
+there, and copied back (the reference returns outputs on the input's device).  Without a GPU, or without the
+built library, every computing call raises RuntimeError.
+"""
+import ctypes
+import os
+import threading
+from typing import Optional, Sequence
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("MXQ_HIP_LIB", os.path.join(_HERE, "libmxq_hip.so"))
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+c_i32, c_i64, c_f32, c_f64, c_ptr = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
+
+
+class BlockSpec(ctypes.Structure):
+    """mxq_block_spec (include/mxq_hip.h)."""
+    _fields_ = [("scale_rule", c_i32), ("scale_floor", c_f32), ("scale_emax", c_i32), ("scale_bits", c_i32),
+                ("elem", c_i32), ("e", c_i32), ("m", c_i32), ("rounding", c_i32), ("max_norm", c_f32),
+                ("via_e", c_i32), ("via_m", c_i32)]
+
+
+# exported symbol -> (restype, argtypes); every symbol include/mxq_hip.h declares
+SIGNATURES = {
+    "mxq_last_error": (ctypes.c_char_p, []),
+    "mxq_version": (c_i32, []),
+    "mxq_block_quantize": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64,
+                                   ctypes.POINTER(BlockSpec), c_ptr]),
+    "mxq_block_dequantize": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr]),
+    "mxq_round_bits": (c_i32, [c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i32, c_ptr]),
+    "mxq_round_int": (c_i32, [c_ptr, c_i32, c_ptr, c_i64, c_i32, c_ptr]),
+    "mxq_bf16": (c_i32, [c_ptr, c_ptr, c_i64, c_ptr]),
+    "mxq_float_em": (c_i32, [c_ptr, c_i32, c_ptr, c_i64, c_i32, c_i32, c_i32, c_i32, c_f32, c_ptr]),
+    "mxq_microsoft": (c_i32, [c_ptr, c_ptr, c_i64, c_i32, c_i32, c_f32, c_i32, c_i32, c_ptr]),
+    "mxq_scale_factor": (c_i32, [c_ptr, c_ptr, c_i64, ctypes.POINTER(BlockSpec), c_ptr]),
+    "mxq_exact_add": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i32, c_i32, c_i32, c_i32, c_f32, c_ptr]),
+    "mxq_truncate_significand": (c_i32, [c_ptr, c_ptr, c_i64, c_i32, c_ptr]),
+    "mxq_flush_product": (c_i32, [c_ptr, c_ptr, c_i64, c_f32, c_ptr]),
+    "mxq_saturate": (c_i32, [c_ptr, c_ptr, c_i64, c_f32, c_f32, c_ptr]),
+}
+
+# mxq_block_spec codes
+SCALE_NONE, SCALE_MXQUANT, SCALE_OCP, SCALE_OCP_NO_CLIP = 0, 1, 2, 3
+ELEM_NONE, ELEM_QTORCH, ELEM_IEEE, ELEM_OCP, ELEM_MICROSOFT = 0, 1, 2, 3, 4
+MODE_CODE = {"ties_away": 0, "rne": 1, "truncate": 2}
+MS_MODE_CODE = {"nearest": 0, "even": 1, "floor": 2}
+GRID_CODE = {"qtorch": 0, "ieee": 1, "ocp": 2}
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Open the library (once) and declare every entry point's C signature."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(path):
+                raise RuntimeError(f"mxq: the HIP library {path} is not built; run __graft_entry__.build() "
+                                   "or microscaling-quant_amd/csrc/build.py")
+            lib = ctypes.CDLL(path)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype, fn.argtypes = res, args
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().mxq_last_error()
+        raise RuntimeError(f"mxq: {what} failed ({rc}): {msg.decode() if msg else 'unknown error'}")
+
+
+def compute_device(*tensors: torch.Tensor) -> torch.device:
+    """The GPU the kernels run on: the tensors' CUDA device, or the current one for CPU tensors."""
+    for t in tensors:
+        if isinstance(t, torch.Tensor) and t.device.type == "cuda":
+            return t.device
+    if not torch.cuda.is_available():
+        raise RuntimeError("mxq: no GPU is visible; this implementation runs its kernels on gfx950 only "
+                           "(CPU tensors are computed on the current GPU and copied back)")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def to_device(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    return t if t.device == dev else t.to(dev)
+
+
+def stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def ptr(t: Optional[torch.Tensor]) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def back(t: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    """Return a result on the device of the caller's tensor `like`."""
+    return t if t.device == like.device else t.to(like.device)
+
+
+def numel(shape: Sequence[int]) -> int:
+    n = 1
+    for s in shape:
+        n *= int(s)
+    return n
+
+
+def run(name: str, *args) -> None:
+    """Call entry point `name` with args; raise RuntimeError on a nonzero status."""
+    check(getattr(load(), name)(*args), name)
+
+
+def ew_prepare(x: torch.Tensor, dtype: torch.dtype):
+    """(compute device, contiguous copy of x converted to dtype on that device)."""
+    dev = compute_device(x)
+    xd = to_device(x.detach(), dev).to(dtype).contiguous()
+    return dev, xd

@@ -1,0 +1,118 @@
+"""Block quantization driver (mxq/block/_driver.py:1-72): `compose` and `dequantize`.
+
+Layout contract (MXQuant's mx_block32_quantize):
+    quantize(V, axis) -> (P, X)   P: V's shape, the codes (float32)
+                                  X: V's shape with axis of length ceil(len / block_size), the scales (float32)
+    V_hat = P * expand(X), each scale repeated block_size times along axis (the last block zero-padded).
+
+The named quantizers (block.mxquant, block.mxgemmini, block.ocp) hand `quantize_fused` a step-1/step-2 spec and
+run as one gfx950 kernel: V is viewed as (outer, n, inner) with the block axis n in the middle, so no
+transpose, padding or reassembly copy is made.  `compose` with arbitrary Python callables keeps the
+reference's generic composition: the layout steps are torch views and copies on the tensor's device, the
+callables run as given.
+"""
+from typing import Callable, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from .. import _lib
+
+BLOCK = 32
+
+_NATIVE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def _axis(V: torch.Tensor, axis: int) -> int:
+    if not -V.ndim <= axis < V.ndim:
+        raise IndexError(f"axis {axis} out of range for {V.ndim}-D tensor")
+    return axis % V.ndim
+
+
+def _check_block(block_size: int) -> None:
+    if block_size == 0:
+        raise ZeroDivisionError("integer division or modulo by zero")
+    if block_size < 0:
+        raise ValueError(f"block_size must be positive, got {block_size}")
+
+
+def _view3(shape, axis: int):
+    outer = _lib.numel(shape[:axis])
+    inner = _lib.numel(shape[axis + 1:])
+    return outer, int(shape[axis]), inner
+
+
+def quantize_fused(V: torch.Tensor, axis: int, block_size: int, spec: _lib.BlockSpec) -> Tuple[torch.Tensor, torch.Tensor]:
+    """One kernel: amax, scale, divide, element rule, for every block of V along `axis` (already validated)."""
+    axis = _axis(V, axis)
+    _check_block(block_size)
+    dev = _lib.compute_device(V)
+    Vd = _lib.to_device(V.detach(), dev)
+    if Vd.dtype not in _NATIVE:
+        Vd = Vd.to(torch.float32)                       # the reference's V.to(float32) (RNE from float64)
+    Vd = Vd.contiguous()
+    outer, n, inner = _view3(Vd.shape, axis)
+    nb = -(-n // block_size)
+    xshape = list(Vd.shape)
+    xshape[axis] = nb
+    P = torch.empty(Vd.shape, dtype=torch.float32, device=dev)
+    X = torch.empty(xshape, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.run("mxq_block_quantize", _lib.ptr(Vd), _NATIVE[Vd.dtype], _lib.ptr(P), _lib.ptr(X), outer, n, inner,
+                 block_size, spec, _lib.stream(dev))
+    return _lib.back(P, V), _lib.back(X, V)
+
+
+def compose(V: torch.Tensor, *, scale: Optional[Callable[[torch.Tensor], torch.Tensor]],
+            elem: Optional[Callable[[torch.Tensor], torch.Tensor]],
+            axis: int = 0, block_size: int = BLOCK) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Block quantization from its two steps; returns (P codes, X scales), float32.
+
+    scale(amax) -> X   step 1: amax is each block's max |value|, shape (..., nblocks, 1); X the same shape
+    elem(z) -> P       step 2: z = block / X, shape (..., nblocks, block_size); P the same shape
+    Either may be None: no scale step means X = 1, no element step means P = V / X; both None is FP32
+    pass-through (one kernel)."""
+    if scale is None and elem is None:
+        return quantize_fused(V, axis, block_size, _lib.BlockSpec())
+    V = V.to(torch.float32)
+    axis = _axis(V, axis)
+    _check_block(block_size)
+    Vt = V.movedim(axis, -1)
+    n = Vt.shape[-1]
+    pad = (-n) % block_size
+    if pad:
+        Vt = F.pad(Vt, (0, pad))
+    data = Vt.reshape(*Vt.shape[:-1], -1, block_size)
+    if scale is None:
+        X = torch.ones(data.shape[:-1] + (1,), dtype=torch.float32, device=V.device)
+        z = data
+    else:
+        X = scale(data.abs().amax(dim=-1, keepdim=True))
+        z = data / X
+    P = z.clone() if elem is None else elem(z)
+    P = P.reshape(*P.shape[:-2], -1)[..., :n].movedim(-1, axis).contiguous()
+    X = X.squeeze(-1).movedim(-1, axis).contiguous()
+    return P, X
+
+
+def dequantize(P: torch.Tensor, X: torch.Tensor, axis: int = 0, block_size: int = BLOCK) -> torch.Tensor:
+    """V_hat = P * expand(X): each scale repeated block_size times along `axis`, cut to P's length."""
+    axis = axis % P.ndim
+    _check_block(block_size)
+    n = P.shape[axis]
+    nb = -(-n // block_size)
+    want = list(P.shape)
+    want[axis] = nb
+    if P.dtype == torch.float32 and X.dtype == torch.float32 and list(X.shape) == want and P.device == X.device:
+        dev = _lib.compute_device(P)
+        Pd = _lib.to_device(P.detach(), dev).contiguous()
+        Xd = _lib.to_device(X.detach(), dev).contiguous()
+        out = torch.empty_like(Pd)
+        outer, n, inner = _view3(Pd.shape, axis)
+        with torch.cuda.device(dev):
+            _lib.run("mxq_block_dequantize", _lib.ptr(Pd), _lib.ptr(Xd), _lib.ptr(out), outer, n, inner, block_size,
+                     _lib.stream(dev))
+        return _lib.back(out, P)
+    # any other dtype or a broadcasting X: the reference's expression, on the tensors' device
+    Xe = torch.repeat_interleave(X, block_size, dim=axis).narrow(axis, 0, P.shape[axis])
+    return P * Xe

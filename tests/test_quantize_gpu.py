@@ -1,0 +1,182 @@
+"""Block quantization and the elementwise primitives on the GPU, bit for bit against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_bits_equal, random_f32, special_f32
+from oracle import block as ob
+from oracle import numerics as nx
+
+pytestmark = pytest.mark.gpu
+
+FMTS = list(nx.FORMATS)
+
+
+def _edge_matrix(rng, rows, cols, scale=1.0):
+    V = (rng.standard_normal((rows, cols)) * scale).astype(np.float32)
+    sp = special_f32()
+    idx = rng.choice(V.size, size=min(sp.size, V.size // 4), replace=False)
+    V.flat[idx] = sp[: idx.size]
+    if rows >= 40 and cols >= 3:
+        V[0:32, 1] = 0.0                                   # an all-zero block
+        V[0:32, 2] = np.float32(2.0 ** -130)               # a subnormal block
+    return V
+
+
+def _run(fn, V, *args, **kw):
+    import mxq
+    P, X = fn(torch.from_numpy(V).cuda(), *args, **kw)
+    return P.cpu().numpy(), X.cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt", FMTS + ["FP32"])
+def test_mxquant(cuda, fmt):
+    from mxq import block
+    rng = np.random.default_rng(1)
+    for shape, axis, bs in [((4096, 512), 0, 32), ((4100, 64), 0, 32), ((64, 4100), 1, 32), ((96, 8, 5), 1, 32),
+                            ((100, 33), 0, 7), ((128, 128), -1, 16)]:
+        V = _edge_matrix(rng, shape[0], int(np.prod(shape[1:]))).reshape(shape)
+        P, X = _run(block.mxquant.quantize, V, fmt, axis=axis, block_size=bs)
+        wP, wX = ob.mxquant_quantize(V, fmt, axis, bs)
+        assert_bits_equal(P, wP, f"P {fmt} {shape} {axis} {bs}")
+        assert_bits_equal(X, wX, f"X {fmt} {shape} {axis} {bs}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("mode", ["ties_away", "rne", "truncate"])
+def test_mxgemmini(cuda, fmt, mode):
+    from mxq import block
+    rng = np.random.default_rng(2)
+    for shape, axis, bs, floor, via in [((4096, 512), 0, 32, 1e-38, None), ((4100, 96), 0, 32, 2.0 ** -23, None),
+                                        ((64, 4096), 1, 32, 1e-38, (3, 1)), ((50, 30), 0, 3, 2.0 ** -23, (5, 4))]:
+        V = _edge_matrix(rng, shape[0], shape[1], scale=float(np.exp2(rng.integers(-20, 20))))
+        P, X = _run(block.mxgemmini.quantize, V, fmt, axis=axis, block_size=bs, rounding_mode=mode,
+                    scale_floor=floor, via=via)
+        wP, wX = ob.mxgemmini_quantize(V, fmt, axis, bs, mode, floor, via)
+        assert_bits_equal(P, wP, f"P {fmt} {mode} {shape}")
+        assert_bits_equal(X, wX, f"X {fmt} {mode} {shape}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("placement", ["top", "below_top", "no_clip"])
+def test_ocp(cuda, fmt, placement):
+    from mxq import block
+    rng = np.random.default_rng(3)
+    for mode in ("even", "nearest", "floor"):
+        for shape, axis in [((4096, 512), 0), ((4100, 40), 0), ((40, 4100), 1)]:
+            V = _edge_matrix(rng, shape[0], shape[1], scale=float(np.exp2(rng.integers(-30, 30))))
+            P, X = _run(block.ocp.quantize, V, fmt, axis=axis, rounding_mode=mode, placement=placement)
+            wP, wX = ob.ocp_quantize(V, fmt, axis, 32, mode, 8, placement)
+            assert_bits_equal(P, wP, f"P {fmt} {mode} {placement} {shape}")
+            assert_bits_equal(X, wX, f"X {fmt} {mode} {placement} {shape}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float64])
+def test_low_precision_inputs(cuda, dtype):
+    from mxq import block
+    rng = np.random.default_rng(4)
+    V = torch.from_numpy(_edge_matrix(rng, 512, 256) * 3).to(dtype)
+    V32 = V.to(torch.float32).numpy()
+    for fmt in FMTS:
+        P, X = block.mxgemmini.quantize(V.cuda(), fmt, axis=0, rounding_mode="rne")
+        wP, wX = ob.mxgemmini_quantize(V32, fmt, 0, 32, "rne")
+        assert_bits_equal(P.cpu().numpy(), wP, f"P {dtype} {fmt}")
+        assert_bits_equal(X.cpu().numpy(), wX, f"X {dtype} {fmt}")
+
+
+def test_contiguous_block_layout(cuda):
+    """axis = last with 32 | n runs the eight-lanes-per-block kernel; odd n runs the strided one."""
+    from mxq import block
+    rng = np.random.default_rng(5)
+    for shape in [(300, 256), (7, 3, 64), (33, 100)]:
+        V = _edge_matrix(rng, shape[0], int(np.prod(shape[1:]))).reshape(shape)
+        for fn, ref in [(block.mxgemmini.quantize, ob.mxgemmini_quantize), (block.ocp.quantize, ob.ocp_quantize),
+                        (block.mxquant.quantize, ob.mxquant_quantize)]:
+            P, X = _run(fn, V, "MXFP8_E4M3", axis=-1)
+            wP, wX = ref(V, "MXFP8_E4M3", -1)
+            assert_bits_equal(P, wP, f"P {shape} {fn.__module__}")
+            assert_bits_equal(X, wX, f"X {shape} {fn.__module__}")
+
+
+def test_cpu_tensors_round_trip_through_gpu(cuda):
+    from mxq import block
+    V = torch.randn(64, 8)
+    P, X = block.mxgemmini.quantize(V, "MXFP4", axis=0)
+    assert P.device.type == "cpu" and X.device.type == "cpu"
+    wP, wX = ob.mxgemmini_quantize(V.numpy(), "MXFP4", 0)
+    assert_bits_equal(P.numpy(), wP, "P")
+    assert_bits_equal(X.numpy(), wX, "X")
+
+
+def test_dequantize(cuda):
+    from mxq import block
+    rng = np.random.default_rng(6)
+    V = _edge_matrix(rng, 4100, 64)
+    P, X = block.ocp.quantize(torch.from_numpy(V).cuda(), "MXFP6_E3M2", axis=0)
+    got = block.dequantize(P, X, axis=0).cpu().numpy()
+    assert_bits_equal(got, ob.dequantize(P.cpu().numpy(), X.cpu().numpy(), 0), "dequantize axis 0")
+    P2, X2 = block.mxgemmini.quantize(torch.from_numpy(V).cuda(), "MXFP8_E5M2", axis=1, block_size=5)
+    got2 = block.mxgemmini.dequantize(P2, X2, axis=1, block_size=5).cpu().numpy()
+    assert_bits_equal(got2, ob.dequantize(P2.cpu().numpy(), X2.cpu().numpy(), 1, 5), "dequantize axis 1")
+
+
+# ------------------------------------------------------------------------------------------ elementwise
+@pytest.fixture(scope="module")
+def corpus():
+    rng = np.random.default_rng(11)
+    return np.concatenate([special_f32(), random_f32(rng, 200000, -40, 40), random_f32(rng, 50000, -149, 128)])
+
+
+def test_elementwise_rounding(cuda, corpus):
+    from mxq import rounding
+    x = torch.from_numpy(corpus).cuda()
+    assert_bits_equal(rounding.bf16(x).cpu().numpy(), nx.bf16(corpus), "bf16")
+    b = torch.from_numpy(nx.bits_of(corpus)).cuda()
+    for keep in (0, 3, 7, 22):
+        for mode in ("ties_away", "rne", "truncate"):
+            got = rounding.round_bits(b, keep, mode).cpu().numpy()
+            assert_bits_equal(got, nx.round_bits(nx.bits_of(corpus), keep, mode), f"round_bits {keep} {mode}")
+    k = (corpus * np.float32(3.5)).astype(np.float32)
+    for mode in ("ties_away", "rne", "truncate"):
+        assert_bits_equal(rounding.round_int(torch.from_numpy(k).cuda(), mode).cpu().numpy(),
+                          nx.round_int(k, mode), f"round_int {mode}")
+
+
+def test_elementwise_float_em(cuda, corpus):
+    from mxq.element_quant import float_em, microsoft
+    x = torch.from_numpy(corpus).cuda()
+    for grid, pairs in [("qtorch", [(4, 3), (8, 7), (6, 9)]), ("ieee", [(4, 4), (8, 7), (8, 22), (5, 10)]),
+                        ("ocp", [(4, 3), (2, 1), (3, 2)])]:
+        for e, m in pairs:
+            for mode in ("ties_away", "rne", "truncate"):
+                got = float_em.quantize(x, e, m, mode, grid).cpu().numpy()
+                assert_bits_equal(got, nx.float_em(corpus, e, m, mode, grid), f"{grid} e{e}m{m} {mode}")
+    x64 = torch.from_numpy(corpus.astype(np.float64) * 1.000001).cuda()
+    got = float_em.quantize(x64, 8, 7, "rne", "ieee").cpu().numpy()
+    assert_bits_equal(got, nx.float_em(corpus.astype(np.float64) * 1.000001, 8, 7, "rne", "ieee"), "f64 ieee")
+    for fmt in FMTS:
+        for mode in ("even", "nearest", "floor"):
+            got = microsoft.quantize(x, fmt, mode).cpu().numpy()
+            assert_bits_equal(got, nx.microsoft_fmt(corpus, fmt, mode), f"microsoft {fmt} {mode}")
+
+
+def test_elementwise_scale_and_arith(cuda, corpus):
+    from mxq import arith, scale_factor
+    a = np.abs(corpus)
+    at = torch.from_numpy(a).cuda()
+    assert_bits_equal(scale_factor.mxquant(at).cpu().numpy(), nx.scale_mxquant(a), "mxquant")
+    assert_bits_equal(scale_factor.mxquant(at, 2.0 ** -23).cpu().numpy(), nx.scale_mxquant(a, 2.0 ** -23), "mxquant hw")
+    assert_bits_equal(scale_factor.ocp(at, 8).cpu().numpy(), nx.scale_ocp(a, 8), "ocp")
+    assert_bits_equal(scale_factor.ocp_below_top(at, 4).cpu().numpy(), nx.scale_ocp_below_top(a, 4), "ocp_below_top")
+    for fmt in FMTS:
+        assert_bits_equal(scale_factor.ocp_no_clip(at, fmt).cpu().numpy(), nx.scale_ocp_no_clip(a, fmt), f"no_clip {fmt}")
+    rng = np.random.default_rng(12)
+    b = rng.permutation(corpus)
+    bt = torch.from_numpy(b).cuda()
+    x = torch.from_numpy(corpus).cuda()
+    for e, m in [(4, 4), (4, 6), (7, 10), (8, 7), (8, 23)]:
+        got = arith.exact_add(x, bt, e, m).cpu().numpy()
+        assert_bits_equal(got, nx.exact_add(corpus, b, e, m), f"exact_add e{e}m{m}")
+    assert_bits_equal(arith.truncate_significand(x, 3).cpu().numpy(), nx.truncate_significand(corpus, 3), "trunc")
+    assert_bits_equal(arith.flush_product(x, -16).cpu().numpy(), nx.flush_product(corpus, -16), "flush")
+    assert_bits_equal(arith.saturate(x, 448.0, 448.0).cpu().numpy(), nx.saturate(corpus, 448.0, 448.0), "sat")
