@@ -50,6 +50,18 @@ typedef struct mxq_block_spec {
   int32_t via_e, via_m; /* OCP grid only: round on the ieee float(via_e, via_m) grid first; via_e = 0: none */
 } mxq_block_spec;
 
+/* The rounding points of a reducer (mxq/matmul/_arithmetic.py:41-134). */
+enum { MXQ_ARITH_MXGEMMINI = 0, MXQ_ARITH_MXQUANT = 1 };
+
+typedef struct mxq_arith_spec {
+  int32_t kind;          /* MXQ_ARITH_* */
+  int32_t prod_e, prod_m;/* product format */
+  int32_t has_floor;     /* MXGEMMINI: flush products below flush_thr to +0 */
+  float flush_thr;       /* float32 value of 2^prod_floor */
+  float sat_limit;       /* MXGEMMINI saturation: |p| > sat_limit becomes sign(p) * sat_value (float32 values) */
+  float sat_value;
+} mxq_arith_spec;
+
 /* Library identity and the last error of the calling thread. */
 const char* mxq_last_error(void);
 int mxq_version(void);
@@ -65,6 +77,18 @@ int mxq_block_quantize(const void* V, int32_t v_dtype, float* P, float* X, int64
 /* out = P * expand(X) along n.  Replaces mxq/block/_driver.py:69-72 `dequantize`. */
 int mxq_block_dequantize(const float* P, const float* X, float* out, int64_t outer, int64_t n, int64_t inner,
                          int64_t block_size, mxq_stream_t stream);
+
+/* The systolic PE column: C = A^T B (M x N float32) from codes A (K x M), B (K x N) and block scales X_A
+ * (ceil(K/block_size) x M), X_B (ceil(K/block_size) x N), all float32 row-major.  Per block of K the scale map
+ * X_A[g] (x) X_B[g]; per reduction of `size` k a fresh sum accumulated lane by lane (lane i has the format
+ * (lane_e[i], lane_m[i]), host arrays of `size` entries), rescaled and added into C; K tails as the reference.
+ * size must divide block_size and 32.  `workspace` is device memory of at least 8 bytes (operand statistics
+ * that select the kernel on the device; the call makes no host synchronisation).  force_general = 1 skips the
+ * fast kernel.  Replaces mxq/matmul/_systolic.py:23-62 with mxq/matmul/_arithmetic.py:64-134. */
+int mxq_systolic(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C, int64_t K,
+                 int64_t M, int64_t N, const int32_t* lane_e, const int32_t* lane_m, int32_t size,
+                 int32_t block_size, const mxq_arith_spec* arith, uint32_t* workspace, int32_t force_general,
+                 mxq_stream_t stream);
 
 /* ---- elementwise primitives over flat arrays of n elements (the caller broadcasts) ---------------------- */
 

@@ -52,6 +52,10 @@ MXQ_HD double copysign_d(double mag, double sgn) {
   return u2d((d2u(mag) & 0x7FFFFFFFFFFFFFFFull) | (d2u(sgn) & 0x8000000000000000ull));
 }
 MXQ_HD float f_inf() { return u2f(0x7F800000u); }
+// NaN payloads are not part of the datapath's spec: a NaN produced by arithmetic is replaced by the canonical
+// quiet NaN 0x7FC00000 before any rounding that reads a NaN's bits (the qtorch grid carries a large payload
+// into the exponent and sign; x86 and CUDA propagate different payloads, so the reference itself differs there).
+MXQ_HD float canon_nan(float x) { return ((__builtin_bit_cast(uint32_t, x) & 0x7FFFFFFFu) > 0x7F800000u) ? __builtin_bit_cast(float, 0x7FC00000u) : x; }
 MXQ_HD float f_nan() { return u2f(0x7FC00000u); }
 MXQ_HD double d_inf() { return u2d(0x7FF0000000000000ull); }
 // 2^k as float32 for k in [-149, 127] (exact, subnormal included); 0 below, Inf above.
@@ -443,7 +447,7 @@ MXQ_HD float mxg_product(float a, float b, int prod_m, bool do_flush, float flus
 // MXQUANT (mxq/matmul/_arithmetic.py:64-73): qtorch ties_away on the product and on the fp32 lane sum.
 MXQ_HD float mxq_q(float x, int e, int m) {
   if (e == 8 && m == 23) return x;
-  return qtorch_round(x, e, m, MXQ_TIES_AWAY);
+  return qtorch_round(canon_nan(x), e, m, MXQ_TIES_AWAY);
 }
 
 // ------------------------------------------------------------------------------ block quantization steps
@@ -496,7 +500,8 @@ MXQ_HD float ocp_grid_fast(float z, int e, int m, int mode, float max_norm) {
 template <int ELEM>
 MXQ_HD float elem_q(float z, const mxq_block_spec& s) {
   if constexpr (ELEM == MXQ_ELEM_QTORCH) {
-    return (s.e == 8 && s.m == 23) ? z : qtorch_round(z, s.e, s.m, s.rounding);
+    // a NaN made by the division is taken as the canonical quiet NaN before the bit rounding
+    return (s.e == 8 && s.m == 23) ? z : qtorch_round(canon_nan(z), s.e, s.m, s.rounding);
   } else if constexpr (ELEM == MXQ_ELEM_IEEE) {
     return float_em_quantize32(z, s.e, s.m, s.rounding, MXQ_GRID_IEEE, 0.0f);
   } else if constexpr (ELEM == MXQ_ELEM_OCP) {

@@ -32,6 +32,12 @@ class BlockSpec(ctypes.Structure):
                 ("via_e", c_i32), ("via_m", c_i32)]
 
 
+class ArithSpec(ctypes.Structure):
+    """mxq_arith_spec (include/mxq_hip.h)."""
+    _fields_ = [("kind", c_i32), ("prod_e", c_i32), ("prod_m", c_i32), ("has_floor", c_i32), ("flush_thr", c_f32),
+                ("sat_limit", c_f32), ("sat_value", c_f32)]
+
+
 # exported symbol -> (restype, argtypes); every symbol include/mxq_hip.h declares
 SIGNATURES = {
     "mxq_last_error": (ctypes.c_char_p, []),
@@ -39,6 +45,8 @@ SIGNATURES = {
     "mxq_block_quantize": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64,
                                    ctypes.POINTER(BlockSpec), c_ptr]),
     "mxq_block_dequantize": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr]),
+    "mxq_systolic": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,
+                             ctypes.POINTER(ArithSpec), c_ptr, c_i32, c_ptr]),
     "mxq_round_bits": (c_i32, [c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i32, c_ptr]),
     "mxq_round_int": (c_i32, [c_ptr, c_i32, c_ptr, c_i64, c_i32, c_ptr]),
     "mxq_bf16": (c_i32, [c_ptr, c_ptr, c_i64, c_ptr]),
@@ -57,6 +65,7 @@ ELEM_NONE, ELEM_QTORCH, ELEM_IEEE, ELEM_OCP, ELEM_MICROSOFT = 0, 1, 2, 3, 4
 MODE_CODE = {"ties_away": 0, "rne": 1, "truncate": 2}
 MS_MODE_CODE = {"nearest": 0, "even": 1, "floor": 2}
 GRID_CODE = {"qtorch": 0, "ieee": 1, "ocp": 2}
+ARITH_MXGEMMINI, ARITH_MXQUANT = 0, 1
 
 
 def load(path: str = LIB_PATH) -> ctypes.CDLL:

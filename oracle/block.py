@@ -68,7 +68,7 @@ def mxquant_quantize(V, fmt, axis=0, block_size=BLOCK):
     if f is None:
         return compose(V, None, None, axis, block_size)
     e, m = nx.FORMATS[f][:2]
-    return compose(V, nx.scale_mxquant, lambda z: nx.float_em(z, e, m), axis, block_size)
+    return compose(V, nx.scale_mxquant, lambda z: nx.float_em(nx.canon_nan(z), e, m), axis, block_size)
 
 
 def mxgemmini_quantize(V, fmt, axis=0, block_size=BLOCK, rounding_mode="ties_away",

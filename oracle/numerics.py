@@ -49,6 +49,13 @@ def from_bits(q):
     return q.view(F32)
 
 
+def canon_nan(x):
+    """NaN payloads are outside the spec: a NaN made by arithmetic becomes the quiet NaN 0x7FC00000 before a
+    rounding that reads its bits (the qtorch grid)."""
+    x = f32(x)
+    return np.where(np.isnan(x), np.array(0x7FC00000, dtype=np.uint32).view(F32), x).astype(F32)
+
+
 def tsign(x):
     """torch.sign: (0 < x) - (x < 0); 0 for +-0 and NaN."""
     return ((x > 0).astype(x.dtype) - (x < 0).astype(x.dtype))
@@ -408,11 +415,11 @@ class MXQUANT:
 
     def product(self, a, b):
         with np.errstate(all="ignore"):
-            return self.q(f32(a) * f32(b), self.prod_e, self.prod_m)
+            return self.q(canon_nan(f32(a) * f32(b)), self.prod_e, self.prod_m)
 
     def acc_add(self, S, p, e, m):
         with np.errstate(all="ignore"):
-            return self.q(f32(S) + f32(p), e, m)
+            return self.q(canon_nan(f32(S) + f32(p)), e, m)
 
     def tile_add(self, C, tile):
         with np.errstate(all="ignore"):

@@ -1,0 +1,158 @@
+"""matmul.systolic on the GPU, bit for bit against the oracle's step-by-step reducer."""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_bits_equal, special_f32
+from oracle import block as ob
+from oracle import numerics as nx
+from oracle import systolic as osys
+
+pytestmark = pytest.mark.gpu
+
+HW_FINAL = osys.HW_FINAL
+
+
+def _codes(rng, K, n, fmt="MXFP8_E4M3", mode="ties_away", floor=1e-38, scale=1.0):
+    V = (rng.standard_normal((K, n)) * scale).astype(np.float32)
+    return ob.mxgemmini_quantize(V, fmt, 0, 32, mode, floor)
+
+
+def _run(P_A, X_A, P_B, X_B, arith, schedule, size=16, block_size=32, force_general=False):
+    from mxq import matmul
+    t = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in (P_A, X_A, P_B, X_B)]
+    return matmul.systolic(*t, arith, schedule, size, block_size, force_general=force_general).cpu().numpy()
+
+
+def _arith(name, *a):
+    from mxq import matmul
+    return getattr(matmul, name)(*a), getattr(nx, name)(*a)
+
+
+@pytest.mark.parametrize("shape", [(256, 64, 64), (4100 // 4, 40, 72), (96, 130, 70), (32, 1, 1), (5, 3, 9)])
+@pytest.mark.parametrize("force", [False, True])
+def test_mxgemmini_hw_final(cuda, shape, force):
+    K, M, N = shape
+    rng = np.random.default_rng(K * 7 + M)
+    P_A, X_A = _codes(rng, K, M)
+    P_B, X_B = _codes(rng, K, N, scale=0.02)
+    ar, orc = _arith("MXGEMMINI")
+    got = _run(P_A, X_A, P_B, X_B, ar, HW_FINAL, force_general=force)
+    want = osys.systolic(P_A, X_A, P_B, X_B, orc, HW_FINAL)
+    assert_bits_equal(got, want, f"mxgemmini {shape} force={force}")
+
+
+def test_mxgemmini_tapeout_operands(cuda):
+    """rne operands, hardware floor 2^-23: the recipe of the tapeout."""
+    rng = np.random.default_rng(5)
+    P_A, X_A = _codes(rng, 512, 48, mode="rne", floor=2.0 ** -23)
+    P_B, X_B = _codes(rng, 512, 80, mode="rne", floor=2.0 ** -23, scale=0.02)
+    ar, orc = _arith("MXGEMMINI")
+    assert_bits_equal(_run(P_A, X_A, P_B, X_B, ar, HW_FINAL), osys.systolic(P_A, X_A, P_B, X_B, orc, HW_FINAL), "tapeout")
+
+
+def _wild_codes(rng, K, n):
+    """Codes off every grid: large (saturating), specials, subnormals; scales incl. non-powers of two, Inf, NaN."""
+    P = (rng.standard_normal((K, n)) * np.exp2(rng.integers(-20, 12, (K, n)))).astype(np.float32)
+    sp = special_f32()
+    idx = rng.choice(P.size, size=min(P.size // 6, sp.size), replace=False)
+    P.flat[idx] = sp[: idx.size]
+    nb = -(-K // 32)
+    X = np.exp2(rng.integers(-30, 30, (nb, n))).astype(np.float32)
+    X[0, 0] = np.float32(1e-38)
+    if n > 3:
+        X[-1, 1] = np.inf
+        X[0, 2] = np.nan
+        X[-1, 3] = np.float32(2.0 ** 120)
+    return P, X
+
+
+@pytest.mark.parametrize("arith_args", [("MXGEMMINI",), ("MXGEMMINI", 4, 3, None), ("MXGEMMINI", 5, 2),
+                                        ("MXGEMMINI", 4, 4), ("MXGEMMINI", 3, 4), ("MXQUANT", 4, 3),
+                                        ("MXQUANT", 5, 10), ("MXQUANT", 8, 7)])
+def test_general_codes(cuda, arith_args):
+    rng = np.random.default_rng(hash(arith_args) % 1000)
+    K, M, N = 80, 33, 40
+    P_A, X_A = _wild_codes(rng, K, M)
+    P_B, X_B = _wild_codes(rng, K, N)
+    ar, orc = _arith(*arith_args)
+    for sched in (HW_FINAL, [(8, 23)] * 16, [(4, 3)] * 16, [(5, 10)] * 8 + [(8, 7)] * 8):
+        got = _run(P_A, X_A, P_B, X_B, ar, sched)
+        want = osys.systolic(P_A, X_A, P_B, X_B, orc, sched)
+        assert_bits_equal(got, want, f"{arith_args} {sched[:2]}")
+
+
+def test_random_ladders(cuda):
+    rng = np.random.default_rng(77)
+    K, M, N = 64, 24, 20
+    P_A, X_A = _codes(rng, K, M, scale=3.0)
+    P_B, X_B = _codes(rng, K, N)
+    for trial in range(8):
+        sched = [(int(rng.integers(1, 9)), int(rng.integers(1, 23))) for _ in range(16)]
+        for name in ("MXGEMMINI", "MXQUANT"):
+            ar, orc = _arith(name, 4, 3) if name == "MXQUANT" else _arith(name)
+            got = _run(P_A, X_A, P_B, X_B, ar, sched)
+            want = osys.systolic(P_A, X_A, P_B, X_B, orc, sched)
+            assert_bits_equal(got, want, f"{name} ladder {sched}")
+
+
+@pytest.mark.parametrize("K,size,bs", [(5, 16, 32), (17, 16, 32), (33, 16, 32), (48, 16, 48), (40, 8, 16),
+                                       (70, 4, 32), (31, 32, 32), (100, 2, 10)])
+def test_tails_and_sizes(cuda, K, size, bs):
+    rng = np.random.default_rng(K + size)
+    V1 = rng.standard_normal((K, 20)).astype(np.float32)
+    V2 = rng.standard_normal((K, 36)).astype(np.float32)
+    P_A, X_A = ob.mxgemmini_quantize(V1, "MXFP8_E4M3", 0, bs)
+    P_B, X_B = ob.mxgemmini_quantize(V2, "MXFP8_E4M3", 0, bs)
+    sched = (HW_FINAL if size == 16 else [(4, 4)] * (size - 1) + [(8, 7)])
+    for name in ("MXGEMMINI", "MXQUANT"):
+        ar, orc = _arith(name, 4, 3) if name == "MXQUANT" else _arith(name)
+        got = _run(P_A, X_A, P_B, X_B, ar, sched, size, bs)
+        want = osys.systolic(P_A, X_A, P_B, X_B, orc, sched, size, bs)
+        assert_bits_equal(got, want, f"{name} K={K} size={size} bs={bs}")
+
+
+def test_compiled_and_scheme(cuda):
+    from functools import partial
+
+    from mxq import Scheme, block, matmul
+    rng = np.random.default_rng(9)
+    A = torch.from_numpy(rng.standard_normal((96, 16)).astype(np.float32)).cuda()
+    B = torch.from_numpy(rng.standard_normal((96, 24)).astype(np.float32)).cuda()
+    q = partial(block.mxgemmini.quantize, fmt="MXFP8_E4M3", axis=0)
+    ar = matmul.compiled(matmul.MXGEMMINI())
+    assert ar.name == "compiled(mxgemmini(prod=e4m3))"
+    s = Scheme("hw", a=q, b=q, reduce=partial(matmul.systolic, arith=ar, schedule=matmul.HW_FINAL))
+    got = s.matmul(A, B).cpu().numpy()
+    P_A, X_A = ob.mxgemmini_quantize(A.cpu().numpy(), "MXFP8_E4M3", 0)
+    P_B, X_B = ob.mxgemmini_quantize(B.cpu().numpy(), "MXFP8_E4M3", 0)
+    assert_bits_equal(got, osys.systolic(P_A, X_A, P_B, X_B, nx.MXGEMMINI(), HW_FINAL), "scheme")
+
+
+def test_hand_made_arithmetic_runs_reference_loop(cuda):
+    """An Arithmetic of arbitrary callables (no kernel) runs the reference's loop on the device tensors."""
+    from mxq import matmul
+    base = matmul.MXGEMMINI()
+    hand = matmul.Arithmetic("hand", base.product, base.acc_add, base.tile_add)
+    rng = np.random.default_rng(10)
+    P_A, X_A = _codes(rng, 40, 8)
+    P_B, X_B = _codes(rng, 40, 12)
+    got = _run(P_A, X_A, P_B, X_B, hand, HW_FINAL)
+    assert_bits_equal(got, osys.systolic(P_A, X_A, P_B, X_B, nx.MXGEMMINI(), HW_FINAL), "hand-made")
+
+
+def test_c2_shape_column_slice(cuda):
+    """The benchmark's shape (M=512, N=4096, K=4096): the full GPU result, checked on a 32-column slice
+    (output columns are independent chains) and two rows of the oracle over all columns."""
+    from mxq import block, matmul
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(512, 4096, generator=g)
+    W = torch.randn(4096, 4096, generator=g) * 0.02
+    P_A, X_A = block.mxgemmini.quantize(x.t().contiguous().cuda(), "MXFP8_E4M3", axis=0)
+    P_B, X_B = block.mxgemmini.quantize(W.t().contiguous().cuda(), "MXFP8_E4M3", axis=0)
+    Y = matmul.systolic(P_A, X_A, P_B, X_B, matmul.MXGEMMINI(), matmul.HW_FINAL).cpu().numpy()
+    cols = slice(1000, 1032)
+    pa, xa = P_A.cpu().numpy(), X_A.cpu().numpy()
+    pb, xb = P_B.cpu().numpy()[:, cols], X_B.cpu().numpy()[:, cols]
+    want = osys.systolic(pa, xa, pb, xb, nx.MXGEMMINI(), HW_FINAL)
+    assert_bits_equal(Y[:, cols], want, "C2 column slice")
