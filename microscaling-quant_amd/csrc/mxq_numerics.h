@@ -30,7 +30,7 @@ enum { MXQ_TIES_AWAY = 0, MXQ_RNE = 1, MXQ_TRUNC = 2 };
 enum { MXQ_GRID_QTORCH = 0, MXQ_GRID_IEEE = 1, MXQ_GRID_OCP = 2 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
-__constant__ uint32_t mxq_log2_edge_dev[277] = {MXQ_LOG2_EDGE_LIST};
+static __constant__ uint32_t mxq_log2_edge_dev[277] = {MXQ_LOG2_EDGE_LIST};
 #define MXQ_LOG2_EDGE(i) mxq_log2_edge_dev[(i)]
 #else
 static const uint32_t mxq_log2_edge_host[277] = {MXQ_LOG2_EDGE_LIST};
@@ -89,6 +89,16 @@ MXQ_HD uint32_t round_bits32(uint32_t bits, int keep, int mode) {
   if (mode == MXQ_TIES_AWAY) return (bits + half) & ~mask;
   if (mode == MXQ_RNE) return (bits + (half - 1u) + ((bits >> drop) & 1u)) & ~mask;
   return bits & ~mask;
+}
+
+// The same with the mode fixed at compile time.
+template <int MODE>
+MXQ_HD uint32_t round_bits32_t(uint32_t bits, int keep) {
+  const int drop = 23 - keep;
+  const uint32_t mask = (1u << drop) - 1u, half = 1u << (drop - 1);
+  if constexpr (MODE == MXQ_TIES_AWAY) return (bits + half) & ~mask;
+  else if constexpr (MODE == MXQ_RNE) return (bits + (half - 1u) + ((bits >> drop) & 1u)) & ~mask;
+  else return bits & ~mask;
 }
 
 // mxq/rounding/__init__.py:64-85 `bf16`: bit RNE at 7 fraction bits, NaN passes unchanged.
@@ -269,31 +279,39 @@ MXQ_HD float float_em_quantize64(double z, int e, int m, int mode, int grid, flo
 // float exponent format (exp_bits > 0), allow_denorm=True.  The float32 operations are the reference's, in its
 // order: private_exp = floor(log2(|A| + (A == 0))) clipped at min_exp; out = A / 2^pe * 2^(bits-2); round;
 // out / 2^(bits-2) * 2^pe; saturate (clamp) or overflow to Inf; +-Inf inputs restored.
-MXQ_HD float ms_round_mantissa(float A, int mode) {
+template <int MODE>
+MXQ_HD float ms_round_mantissa_t(float A) {
   const float absA = fabsf(A);
   const float sgn = (A > 0.0f) ? 1.0f : ((A < 0.0f) ? -1.0f : 0.0f);   // torch.sign (0 for NaN and +-0)
-  if (mode == MXQ_TRUNC) return sgn * floorf(absA);
-  if (mode == MXQ_TIES_AWAY) return sgn * floorf(absA + 0.5f);
-  // "even": (absA - 0.5) % 2 == 0 subtracts one.  torch.remainder(t, 2) is 0 exactly when t is an even
-  // integer, i.e. when t / 2 (exact: t is a multiple of 2^-25 here) is an integer.
-  const float t = absA - 0.5f;
-  const float h = t * 0.5f;
-  const float maskA = (floorf(h) == h) ? 1.0f : 0.0f;
-  return sgn * (floorf(absA + 0.5f) - maskA);
+  if constexpr (MODE == MXQ_TRUNC) {
+    return sgn * floorf(absA);
+  } else if constexpr (MODE == MXQ_TIES_AWAY) {
+    return sgn * floorf(absA + 0.5f);
+  } else {
+    // "even": (absA - 0.5) % 2 == 0 subtracts one.  torch.remainder(t, 2) is 0 exactly when t is an even
+    // integer, i.e. when t / 2 (exact: t is a multiple of 2^-25 here) is an integer.
+    const float t = absA - 0.5f;
+    const float h = t * 0.5f;
+    const float maskA = (floorf(h) == h) ? 1.0f : 0.0f;
+    return sgn * (floorf(absA + 0.5f) - maskA);
+  }
 }
 
-MXQ_HD float microsoft_quantize(float A, int ebits, int mbits, float max_norm, int mode, bool saturate) {
+template <int MODE>
+MXQ_HD float microsoft_quantize_t(float A, int ebits, int mbits, float max_norm, bool saturate) {
   const uint32_t ua = f2u(A), aa = ua & 0x7FFFFFFFu;
-  if (aa > 0x7F800000u) return A;                        // NaN: every step keeps NaN
-  if (aa == 0x7F800000u) return A;                       // +-Inf restored at the end
+  if (aa >= 0x7F800000u) return A;                       // NaN stays NaN; +-Inf is restored at the end
   const int min_exp = -(1 << (ebits - 1)) + 2;
   int pe = (aa == 0u) ? 0 : floor_log2_pos(u2f(aa));
   if (pe < min_exp) pe = min_exp;
-  const float p2 = pow2f(pe);                            // 2 ** private_exp, exact
-  float out = A / p2;
+  // A / 2^pe and x / 2^(bits-2) as products with the exact reciprocal powers of two: the same correctly
+  // rounded values as the reference's divisions while 2^pe is finite (pe <= 127).  pe = 128 (the log2
+  // round-up band below FLT_MAX) makes 2^pe = Inf and the reference's A / Inf = 0 then 0 * Inf = NaN.
+  const float p2 = pow2f(pe);                            // 2 ** private_exp, exact or Inf
+  float out = (pe <= 127) ? A * pow2f(-pe) : A / p2;
   out = out * (float)(1 << (mbits - 2));
-  out = ms_round_mantissa(out, mode);
-  out = out / (float)(1 << (mbits - 2));
+  out = ms_round_mantissa_t<MODE>(out);
+  out = out * pow2f(2 - mbits);
   out = out * p2;
   if (saturate) {
     if (is_nan_f(out)) return out;
@@ -303,6 +321,18 @@ MXQ_HD float microsoft_quantize(float A, int ebits, int mbits, float max_norm, i
     out = (out > 0.0f) ? f_inf() : -f_inf();
   }
   return out;
+}
+
+MXQ_HD float ms_round_mantissa(float A, int mode) {
+  if (mode == MXQ_TRUNC) return ms_round_mantissa_t<MXQ_TRUNC>(A);
+  if (mode == MXQ_TIES_AWAY) return ms_round_mantissa_t<MXQ_TIES_AWAY>(A);
+  return ms_round_mantissa_t<MXQ_RNE>(A);
+}
+
+MXQ_HD float microsoft_quantize(float A, int ebits, int mbits, float max_norm, int mode, bool saturate) {
+  if (mode == MXQ_TRUNC) return microsoft_quantize_t<MXQ_TRUNC>(A, ebits, mbits, max_norm, saturate);
+  if (mode == MXQ_TIES_AWAY) return microsoft_quantize_t<MXQ_TIES_AWAY>(A, ebits, mbits, max_norm, saturate);
+  return microsoft_quantize_t<MXQ_RNE>(A, ebits, mbits, max_norm, saturate);
 }
 
 // ---------------------------------------------------------------------------------------- scale factors
@@ -473,32 +503,37 @@ MXQ_HD Div make_div(float X) {
 }
 MXQ_HD float apply_div(float v, const Div& d) { return d.inv != 0.0f ? v * d.inv : v / d.X; }
 
-// The OCP element grid (float_em.py:113-134) for e <= 5, m <= 3 on a float32 z.  Normal range: the
-// significand rounded at m fraction bits on the bit pattern (the carry runs into the exponent); below the
-// format's min normal: k = round(|z| / step) evaluated in float32 exactly as round_int does (ties_away adds
-// 0.5 in float32), times the step; then the max_norm clamp and the sign.
-MXQ_HD float ocp_grid_fast(float z, int e, int m, int mode, float max_norm) {
+// The OCP element grid (float_em.py:113-134) for e <= 5, m <= 3 on a float32 z, both paths computed and one
+// selected.  At or above the format's min normal: the significand rounded at m fraction bits on the bit
+// pattern (the carry runs into the exponent).  Below it: k = round(|z| / step) evaluated in float32 exactly as
+// round_int does (ties_away adds 0.5 in float32), times the step.  Then the max_norm clamp and the sign;
+// an exact +-0 gives +0, Inf and NaN pass.
+template <int MODE>
+MXQ_HD float ocp_grid_t(float z, int e, int m, float max_norm) {
   const uint32_t u = f2u(z), a = u & 0x7FFFFFFFu;
-  if (a == 0u) return 0.0f;
-  if (a >= 0x7F800000u) return z;
   const int emin = 2 - (1 << (e - 1));
-  float mag;
-  if (a >= (uint32_t)(emin + 127) << 23) {
-    mag = u2f(round_bits32(a, m, mode));
-  } else {
-    const float k = u2f(a) * pow2f(m - emin);
-    float r;
-    if (mode == MXQ_RNE) r = rintf(k);
-    else if (mode == MXQ_TIES_AWAY) r = floorf(k + 0.5f);
-    else r = truncf(k);
-    mag = r * pow2f(emin - m);
-  }
-  if (mag > max_norm) mag = max_norm;
-  return copysign_f(mag, z);
+  const uint32_t rn = round_bits32_t<MODE>(a, m);
+  const float k = u2f(a) * pow2f(m - emin);
+  float r;
+  if constexpr (MODE == MXQ_RNE) r = rintf(k);
+  else if constexpr (MODE == MXQ_TIES_AWAY) r = floorf(k + 0.5f);
+  else r = truncf(k);
+  const float rs = r * pow2f(emin - m);
+  float mag = (a >= ((uint32_t)(emin + 127) << 23)) ? u2f(rn) : rs;
+  mag = (mag > max_norm) ? max_norm : mag;
+  const float out = (a == 0u) ? 0.0f : copysign_f(mag, z);
+  return (a >= 0x7F800000u) ? z : out;
 }
 
-template <int ELEM>
-MXQ_HD float elem_q(float z, const mxq_block_spec& s) {
+MXQ_HD float ocp_grid_fast(float z, int e, int m, int mode, float max_norm) {
+  if (mode == MXQ_RNE) return ocp_grid_t<MXQ_RNE>(z, e, m, max_norm);
+  if (mode == MXQ_TIES_AWAY) return ocp_grid_t<MXQ_TIES_AWAY>(z, e, m, max_norm);
+  return ocp_grid_t<MXQ_TRUNC>(z, e, m, max_norm);
+}
+
+// Step 2 of a block spec.  MODE >= 0 fixes the rounding mode at compile time; MODE < 0 reads s.rounding.
+template <int ELEM, int MODE>
+MXQ_HD float elem_qm(float z, const mxq_block_spec& s) {
   if constexpr (ELEM == MXQ_ELEM_QTORCH) {
     // a NaN made by the division is taken as the canonical quiet NaN before the bit rounding
     return (s.e == 8 && s.m == 23) ? z : qtorch_round(canon_nan(z), s.e, s.m, s.rounding);
@@ -506,11 +541,16 @@ MXQ_HD float elem_q(float z, const mxq_block_spec& s) {
     return float_em_quantize32(z, s.e, s.m, s.rounding, MXQ_GRID_IEEE, 0.0f);
   } else if constexpr (ELEM == MXQ_ELEM_OCP) {
     if (s.via_e) z = float_em_quantize32(z, s.via_e, s.via_m, s.rounding, MXQ_GRID_IEEE, 0.0f);
-    return ocp_grid_fast(z, s.e, s.m, s.rounding, s.max_norm);
+    if constexpr (MODE < 0) return ocp_grid_fast(z, s.e, s.m, s.rounding, s.max_norm);
+    else return ocp_grid_t<MODE>(z, s.e, s.m, s.max_norm);
   } else if constexpr (ELEM == MXQ_ELEM_MICROSOFT) {
-    return microsoft_quantize(z, s.e, s.m, s.max_norm, s.rounding, true);
+    if constexpr (MODE < 0) return microsoft_quantize(z, s.e, s.m, s.max_norm, s.rounding, true);
+    else return microsoft_quantize_t<MODE>(z, s.e, s.m, s.max_norm, true);
   } else {
     return z;
   }
 }
+
+template <int ELEM>
+MXQ_HD float elem_q(float z, const mxq_block_spec& s) { return elem_qm<ELEM, -1>(z, s); }
 

@@ -1,0 +1,7 @@
+// Block-quantize kernels for bf16_t inputs (one translation unit per input type, compiled in parallel).
+#include "quantize_impl.h"
+
+int mxq_quantize_bf16(const void* V, float* P, float* X, int64_t outer, int64_t n, int64_t inner, int64_t bs,
+                      const mxq_block_spec& q, hipStream_t st) {
+  return mxq_quant::dispatch_elem(static_cast<const mxq_quant::bf16_t*>(V), P, X, outer, n, inner, bs, q, st);
+}

@@ -53,17 +53,35 @@ __global__ void k_zero2(uint32_t* s) {
 }
 
 __global__ void __launch_bounds__(256) k_stats(const float* __restrict__ x, int64_t n, uint32_t* out) {
+  __shared__ uint32_t red[4];
   uint32_t mx = 0u;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n4 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) ? n / 4 : 0;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  for (int64_t i = gid; i < n4; i += stride) {
+    const float4 v = x4[i];
+    const uint32_t a = f2u(v.x) & 0x7FFFFFFFu, b = f2u(v.y) & 0x7FFFFFFFu, c = f2u(v.z) & 0x7FFFFFFFu,
+                   d = f2u(v.w) & 0x7FFFFFFFu;
+    const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
+    const uint32_t m4 = ab > cd ? ab : cd;
+    mx = m4 > mx ? m4 : mx;
+  }
+  for (int64_t i = n4 * 4 + gid; i < n; i += stride) {
     const uint32_t u = f2u(x[i]) & 0x7FFFFFFFu;
     mx = u > mx ? u : mx;
   }
-  // wave reduction, then one atomic per wave
   for (int off = 32; off > 0; off >>= 1) {
     const uint32_t o = (uint32_t)__shfl_xor((int)mx, off, 64);
     mx = o > mx ? o : mx;
   }
-  if ((threadIdx.x & 63) == 0) atomicMax(out, mx);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t m = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = red[w] > m ? red[w] : m;
+    atomicMax(out, m);
+  }
 }
 
 __device__ __forceinline__ bool fast_ok(const uint32_t* stats) {
@@ -451,8 +469,9 @@ extern "C" int mxq_systolic(const float* P_A, const float* X_A, const float* P_B
   if (fast_lanes) {
     // statistics decide on the device between the fast and the general kernel; each exits unless it is chosen
     k_zero2<<<1, 64, 0, st>>>(workspace);
-    k_stats<<<1024, 256, 0, st>>>(P_A, K * M, workspace);
-    k_stats<<<1024, 256, 0, st>>>(P_B, K * N, workspace + 1);
+    auto sgrid = [](int64_t n) { int64_t b = mxq::ceil_div(n / 4 + 1, 256); return (unsigned)(b < 2048 ? b : 2048); };
+    k_stats<<<sgrid(K * M), 256, 0, st>>>(P_A, K * M, workspace);
+    k_stats<<<sgrid(K * N), 256, 0, st>>>(P_B, K * N, workspace + 1);
     if (int rc = mxq::check_launch("mxq_systolic stats")) return rc;
     k_systolic_fast<64, 64, 4, 4><<<grid_f, 256, 0, st>>>(a);
     if (int rc = mxq::check_launch("mxq_systolic fast")) return rc;

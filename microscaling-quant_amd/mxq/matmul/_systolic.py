@@ -51,9 +51,9 @@ def systolic(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: torch
         _lanes_check(kernel, schedule, min(size, K))
     dev = _lib.compute_device(P_A)
     ops = [_lib.to_device(t.detach(), dev).contiguous() for t in (P_A, X_A, P_B, X_B)]
-    C = torch.zeros((M, N), dtype=torch.float32, device=dev)
     if K == 0 or M == 0 or N == 0:
-        return _lib.back(C, P_A)
+        return _lib.back(torch.zeros((M, N), dtype=torch.float32, device=dev), P_A)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)          # every element is written
     import ctypes
     le = (ctypes.c_int32 * size)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
