@@ -90,6 +90,36 @@ int mxq_systolic(const float* P_A, const float* X_A, const float* P_B, const flo
                  int32_t block_size, const mxq_arith_spec* arith, uint32_t* workspace, int32_t force_general,
                  mxq_stream_t stream);
 
+/* ---- MX-Gemmini look-up tables (K x n float32 block codes, one 16-entry table per 2^group columns) ------ */
+
+/* lut.tables: per column group, the counts of each distinct code value, then weighted k-means in float64
+ * (quantile seeds, Lloyd passes until numpy.allclose or max_iters), snap to the finder-safe values, pad with
+ * unused safe values smallest magnitude first (safe_order: indices of `safe` sorted by |value|, negative
+ * first), sort.  grid: the format's nv distinct finite values ascending; safe: its ns finder-safe values
+ * ascending.  T: ceil(n / 2^group) x 16 float32.  workspace: int32 of ceil(n/2^group) * nv + 1 elements; its
+ * last element is set nonzero when P holds a value that is not a code (the caller reports it).
+ * Replaces mxq/lut/kmeans.py:46-122. */
+int mxq_lut_tables(const float* P, int64_t K, int64_t n, int32_t group, int32_t max_iters, const float* grid,
+                   int32_t nv, const float* safe, int32_t ns, const int32_t* safe_order, float* T,
+                   int32_t* workspace, mxq_stream_t stream);
+
+/* lut.pick: each code's nearest entry of its group's ascending table of `width` entries, ties to the lower
+ * index; writes int64 indices to I, or (I NULL) the entries themselves to P_lut (pick then lookup, fused).
+ * Replaces mxq/lut/kmeans.py:125-138 (and :141-146 when fused). */
+int mxq_lut_pick(const float* P, int64_t K, int64_t n, int32_t group, const float* T, int32_t width, int64_t* I,
+                 float* P_lut, mxq_stream_t stream);
+
+/* lut.lookup: out[k][j] = T[j >> group][I[k][j]] (indices already checked in range by the caller).
+ * Replaces mxq/lut/kmeans.py:141-146. */
+int mxq_lut_lookup(const int64_t* I, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,
+                   float* out, mxq_stream_t stream);
+
+/* lut.finder: fx_all[c] is element code c's fixed point (ncodes entries), lut_fx the fixed points of each
+ * group's 16 entries (ceil(n/2^group) x 16); out = argmin over entries of |fx - lut_fx| & mask (mask 0: none),
+ * first minimum.  Codes already checked in range by the caller.  Replaces mxq/lut/formats.py:140-159. */
+int mxq_lut_finder(const int64_t* codes, int64_t K, int64_t n, int32_t group, const int64_t* fx_all,
+                   int32_t ncodes, const int64_t* lut_fx, int64_t mask, int64_t* out, mxq_stream_t stream);
+
 /* ---- elementwise primitives over flat arrays of n elements (the caller broadcasts) ---------------------- */
 
 /* rounding.round_bits on int64 arrays of uint32 patterns; keep per element (int64 array) or, when keep is

@@ -1,0 +1,351 @@
+// MX-Gemmini look-up tables on gfx950 (mxq/lut/kmeans.py:27-152, mxq/lut/formats.py:140-159).
+//
+//   k_lut_hist    counts of each distinct code value per column group: the group's columns of a K-row stripe
+//                 are binned into an LDS histogram (binary search in the sorted value grid, exact-match check),
+//                 then added into the global counts with one atomic per nonzero bin
+//   k_lut_kmeans  one wavefront per group: quantile seeds (or the present values when 16 or fewer), weighted
+//                 Lloyd passes in float64 until two passes agree (numpy.allclose's tolerances) or max_iters,
+//                 snap to the nearest finder-safe value, pad with unused safe values smallest magnitude first,
+//                 sort.  Lanes own grid bins for the assignment step; the sums are exact in float64 (counts times
+//                 grid values have few significant bits), so their order does not matter
+//   k_lut_pick    nearest table entry per code (ties to the lower index), int64 index or the entry's value
+//   k_lut_lookup  the entries named by int64 indices
+//   k_lut_finder  the chip's finder: nearest in fixed point with the format's |difference| mask, first index
+#include "mxq_common.h"
+#include "mxq_numerics.h"
+
+namespace {
+
+constexpr int kSize = 16;            // entries per table
+constexpr int kMaxGrid = 256;        // distinct finite values of the largest LUT format (E5M2: 247)
+
+// lower_bound in a sorted float array: the first index with a[i] >= v (NaN compares false: count of a[i] < v)
+__device__ __forceinline__ int lower_bound_f(const float* a, int n, float v) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] < v) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// blockDim = 256; CB columns per block, 256 / CB row lanes per column; rows [k0, k0 + rows_per_block).
+__global__ void __launch_bounds__(256) k_lut_hist(const float* __restrict__ P, int64_t K, int64_t n, int group,
+                                                  const float* __restrict__ grid, int nv, int CB,
+                                                  int64_t rows_per_block, int* __restrict__ counts,
+                                                  int* __restrict__ err) {
+  extern __shared__ int hist[];                      // (CB >> group, at least 1) x nv
+  __shared__ float g_s[kMaxGrid];
+  const int64_t c0 = (int64_t)blockIdx.x * CB;
+  const int64_t k0 = (int64_t)blockIdx.y * rows_per_block;
+  const int gpb = (CB >> group) > 0 ? (CB >> group) : 1;
+  for (int i = threadIdx.x; i < gpb * nv; i += blockDim.x) hist[i] = 0;
+  for (int i = threadIdx.x; i < nv; i += blockDim.x) g_s[i] = grid[i];
+  __syncthreads();
+  const int col = threadIdx.x % CB, rl = threadIdx.x / CB, nrl = blockDim.x / CB;
+  const int64_t j = c0 + col;
+  const int64_t g0 = c0 >> group;
+  bool bad = false;
+  if (j < n) {
+    const int64_t kend = (k0 + rows_per_block < K) ? k0 + rows_per_block : K;
+    for (int64_t k = k0 + rl; k < kend; k += nrl) {
+      const float v = P[k * n + j];
+      const int b = lower_bound_f(g_s, nv, v);
+      if (b >= nv || !(g_s[b] == v)) {
+        bad = true;
+        continue;
+      }
+      atomicAdd(&hist[(int)((j >> group) - g0) * nv + b], 1);
+    }
+  }
+  if (bad) atomicOr(err, 1);
+  __syncthreads();
+  const int64_t ng = (n + (1 << group) - 1) >> group;
+  for (int i = threadIdx.x; i < gpb * nv; i += blockDim.x) {
+    const int c = hist[i];
+    const int64_t g = g0 + i / nv;
+    if (c && g < ng) atomicAdd(&counts[g * nv + (i % nv)], c);
+  }
+}
+
+// sort 16 doubles ascending (insertion sort; +inf last), then duplicates -> +inf and sort again
+__device__ void dedupe16(double* c) {
+  for (int i = 1; i < kSize; ++i) {
+    const double x = c[i];
+    int j = i - 1;
+    while (j >= 0 && c[j] > x) { c[j + 1] = c[j]; --j; }
+    c[j + 1] = x;
+  }
+  bool dup[kSize];
+  dup[0] = false;
+  for (int i = 1; i < kSize; ++i) dup[i] = c[i] == c[i - 1];
+  for (int i = 1; i < kSize; ++i) if (dup[i]) c[i] = d_inf();
+  for (int i = 1; i < kSize; ++i) {
+    const double x = c[i];
+    int j = i - 1;
+    while (j >= 0 && c[j] > x) { c[j + 1] = c[j]; --j; }
+    c[j + 1] = x;
+  }
+}
+
+__device__ __forceinline__ bool is_finite_d(double x) { return (d2u(x) & 0x7FF0000000000000ull) != 0x7FF0000000000000ull; }
+
+// one 64-lane workgroup per table
+__global__ void __launch_bounds__(64) k_lut_kmeans(const int* __restrict__ counts, int nv, const float* __restrict__ grid,
+                                                   const float* __restrict__ safe, int ns,
+                                                   const int* __restrict__ safe_order, int max_iters,
+                                                   float* __restrict__ T) {
+  __shared__ double x_s[kMaxGrid];
+  __shared__ double w_s[kMaxGrid];
+  __shared__ double C[kSize], Cn[kSize];
+  __shared__ double sums[kSize], wsum[kSize];
+  __shared__ unsigned char member[kMaxGrid];
+  __shared__ int stop;
+  const int g = blockIdx.x, lane = threadIdx.x;
+  for (int i = lane; i < nv; i += 64) {
+    x_s[i] = (double)grid[i];
+    w_s[i] = (double)counts[(int64_t)g * nv + i];
+  }
+  __syncthreads();
+  if (lane == 0) {
+    int npres = 0;
+    for (int i = 0; i < nv; ++i) npres += (w_s[i] > 0.0);
+    for (int i = 0; i < kSize; ++i) C[i] = d_inf();
+    if (npres <= kSize) {
+      int r = 0;
+      for (int i = 0; i < nv; ++i) if (w_s[i] > 0.0) C[r++] = x_s[i];
+      stop = 1;
+    } else {
+      // quantile seeds: first bin whose cumulative weight reaches (i + 0.5) / 16 of the total
+      double total = 0.0;
+      for (int i = 0; i < nv; ++i) total += w_s[i];
+      int s = 0;
+      double cum = 0.0;
+      int b = 0;
+      for (int i = 0; i < kSize; ++i) {
+        const double probe = ((double)i + 0.5) / (double)kSize;
+        // advance to the first b with cdf[b] >= probe (cdf is non-decreasing; cum holds cumsum up to b)
+        while (b < nv) {
+          const double cdf = (cum + w_s[b]) / total;
+          if (cdf >= probe) break;
+          cum += w_s[b];
+          ++b;
+        }
+        s = b < nv ? b : nv - 1;
+        C[i] = x_s[s];
+      }
+      dedupe16(C);
+      stop = max_iters > 0 ? 0 : 1;
+    }
+  }
+  __syncthreads();
+  for (int it = 0; it < max_iters && !stop; ++it) {
+    if (lane < kSize) { sums[lane] = 0.0; wsum[lane] = 0.0; }
+    __syncthreads();
+    for (int i = lane; i < nv; i += 64) {
+      const double xv = x_s[i];
+      int best = 0;
+      double bd = fabs(xv - C[0]);
+      for (int c = 1; c < kSize; ++c) {
+        const double d = fabs(xv - C[c]);
+        if (d < bd) { bd = d; best = c; }                        // first minimum (NaN never wins)
+      }
+      if (!(bd == bd)) best = 0;                                   // every centre infinite: argmin of NaNs -> 0
+      const double wv = w_s[i];
+      if (wv != 0.0) {
+        atomicAdd(&sums[best], wv * xv);
+        atomicAdd(&wsum[best], wv);
+      }
+    }
+    __syncthreads();
+    if (lane == 0) {
+      for (int c = 0; c < kSize; ++c) Cn[c] = (wsum[c] > 0.0) ? sums[c] / wsum[c] : C[c];
+      dedupe16(Cn);
+      bool same = true;
+      for (int c = 0; c < kSize; ++c) {
+        const bool valid = is_finite_d(C[c]);
+        if (is_finite_d(Cn[c]) != valid) same = false;
+        if (valid) {
+          const double tol = 1e-8 + 1e-5 * fabs(C[c]);
+          if (!(fabs(Cn[c] - C[c]) <= tol)) same = false;
+        }
+      }
+      if (same) stop = 1;
+      else for (int c = 0; c < kSize; ++c) C[c] = Cn[c];
+    }
+    __syncthreads();
+  }
+  if (lane == 0) {
+    // snap each finite centre to the nearest safe value (first minimum: the smaller one on a tie)
+    for (int i = 0; i < ns; ++i) member[i] = 0;
+    int cnt = 0;
+    for (int c = 0; c < kSize; ++c) {
+      if (!is_finite_d(C[c])) continue;
+      int best = 0;
+      double bd = fabs(C[c] - (double)safe[0]);
+      for (int i = 1; i < ns; ++i) {
+        const double d = fabs(C[c] - (double)safe[i]);
+        if (d < bd) { bd = d; best = i; }
+      }
+      if (!member[best]) { member[best] = 1; ++cnt; }
+    }
+    // pad with unused safe values, smallest magnitude first (negative before positive)
+    int need = kSize - cnt;
+    for (int q = 0; q < ns && need > 0; ++q) {
+      const int i = safe_order[q];
+      if (!member[i]) { member[i] = 1; --need; }
+    }
+    int r = 0;
+    for (int i = 0; i < ns && r < kSize; ++i) if (member[i]) T[(int64_t)g * kSize + r++] = safe[i];
+    for (; r < kSize; ++r) T[(int64_t)g * kSize + r] = f_inf();
+  }
+}
+
+// Nearest entry of each code's group table (ascending; ties to the lower index).  mode 0: int64 index to I;
+// mode 1: the entry's value to Pout.  One thread per column walks a stripe of rows; the block's tables in LDS.
+__global__ void __launch_bounds__(256) k_lut_pick(const float* __restrict__ P, int64_t K, int64_t n, int group,
+                                                  const float* __restrict__ T, int width, int64_t rows_per_block,
+                                                  int64_t* __restrict__ I, float* __restrict__ Pout) {
+  extern __shared__ float rows_s[];                 // (256 >> group, at least 1) x width
+  const int64_t c0 = (int64_t)blockIdx.x * 256;
+  const int64_t g0 = c0 >> group;
+  const int64_t ng = (n + (1 << group) - 1) >> group;
+  const int gpb = (256 >> group) > 0 ? (256 >> group) : 1;
+  for (int i = threadIdx.x; i < gpb * width; i += blockDim.x) {
+    const int64_t g = g0 + i / width;
+    rows_s[i] = g < ng ? T[g * width + (i % width)] : 0.0f;
+  }
+  __syncthreads();
+  const int64_t j = c0 + threadIdx.x;
+  if (j >= n) return;
+  const float* row = rows_s + (int)((j >> group) - g0) * width;
+  const int64_t k0 = (int64_t)blockIdx.y * rows_per_block;
+  const int64_t kend = (k0 + rows_per_block < K) ? k0 + rows_per_block : K;
+  for (int64_t k = k0; k < kend; ++k) {
+    const float v = P[k * n + j];
+    int hi = lower_bound_f(row, width, v);
+    hi = hi < 1 ? 1 : (hi > width - 1 ? width - 1 : hi);
+    const int lo = hi - 1;
+    const float d_lo = fabsf(v - row[lo]);
+    const float d_hi = fabsf(row[hi] - v);
+    const int pick = (d_lo <= d_hi) ? lo : hi;
+    if (I) I[k * n + j] = pick;
+    else Pout[k * n + j] = row[pick];
+  }
+}
+
+__global__ void __launch_bounds__(256) k_lut_lookup(const int64_t* __restrict__ I, int64_t K, int64_t n, int group,
+                                                    const float* __restrict__ T, int width, float* __restrict__ out) {
+  const int64_t total = K * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t j = e % n;
+    out[e] = T[(j >> group) * width + I[e]];
+  }
+}
+
+__global__ void __launch_bounds__(256) k_lut_finder(const int64_t* __restrict__ codes, int64_t K, int64_t n, int group,
+                                                    const int64_t* __restrict__ fx_all, int ncodes,
+                                                    const int64_t* __restrict__ lut_fx, int64_t mask,
+                                                    int64_t* __restrict__ out) {
+  __shared__ int64_t fx_s[kMaxGrid];
+  for (int i = threadIdx.x; i < ncodes; i += blockDim.x) fx_s[i] = fx_all[i];
+  __syncthreads();
+  const int64_t total = K * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t j = e % n;
+    const int64_t f = fx_s[codes[e]];
+    const int64_t* lf = lut_fx + (j >> group) * kSize;
+    int best = 0;
+    int64_t bd = f - lf[0];
+    bd = bd < 0 ? -bd : bd;
+    if (mask) bd &= mask;
+    for (int i = 1; i < kSize; ++i) {
+      int64_t d = f - lf[i];
+      d = d < 0 ? -d : d;
+      if (mask) d &= mask;
+      if (d < bd) { bd = d; best = i; }
+    }
+    out[e] = best;
+  }
+}
+
+__global__ void k_fill_i32(int* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+}  // namespace
+
+extern "C" int mxq_lut_tables(const float* P, int64_t K, int64_t n, int32_t group, int32_t max_iters,
+                              const float* grid, int32_t nv, const float* safe, int32_t ns, const int32_t* safe_order,
+                              float* T, int32_t* workspace, mxq_stream_t stream) {
+  if (K < 0 || n < 0 || group < 0 || group > 30 || max_iters < 0) return mxq::invalid("mxq_lut_tables: bad arguments");
+  if (nv < 1 || nv > kMaxGrid || ns < 1 || ns > kMaxGrid) return mxq::invalid("mxq_lut_tables: bad grid sizes");
+  if (n == 0) return MXQ_OK;
+  const int64_t ng = (n + (int64_t(1) << group) - 1) >> group;
+  hipStream_t st = mxq::as_stream(stream);
+  int* counts = workspace;                              // ng * nv, then one error flag
+  int* err = workspace + ng * nv;
+  {
+    int64_t nz = ng * nv + 1, blocks = mxq::ceil_div(nz, 256);
+    k_fill_i32<<<dim3((unsigned)(blocks < 4096 ? blocks : 4096)), 256, 0, st>>>(workspace, nz);
+  }
+  if (K > 0) {
+    // columns per block: the LDS histogram (groups x nv ints) within 64 KiB
+    int CB = 256;
+    while (CB > 1 && (int64_t)(((CB >> group) > 0 ? (CB >> group) : 1)) * nv * 4 > 65536) CB >>= 1;
+    const int64_t col_blocks = mxq::ceil_div(n, CB);
+    int64_t row_blocks = mxq::ceil_div(4096, col_blocks);             // aim at several thousand blocks in all
+    if (row_blocks > K) row_blocks = K;
+    if (row_blocks < 1) row_blocks = 1;
+    if (row_blocks > 65535) row_blocks = 65535;
+    const int64_t rpb = mxq::ceil_div(K, row_blocks);
+    row_blocks = mxq::ceil_div(K, rpb);
+    const size_t lds = (size_t)((CB >> group) > 0 ? (CB >> group) : 1) * nv * sizeof(int);
+    k_lut_hist<<<dim3((unsigned)col_blocks, (unsigned)row_blocks), 256, lds, st>>>(P, K, n, group, grid, nv, CB, rpb,
+                                                                                     counts, err);
+    if (int rc = mxq::check_launch("mxq_lut_tables histogram")) return rc;
+  }
+  k_lut_kmeans<<<dim3((unsigned)ng), 64, 0, st>>>(counts, nv, grid, safe, ns, safe_order, max_iters, T);
+  return mxq::check_launch("mxq_lut_tables k-means");
+}
+
+extern "C" int mxq_lut_pick(const float* P, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,
+                            int64_t* I, float* P_lut, mxq_stream_t stream) {
+  if (K < 0 || n < 0 || group < 0 || group > 30 || width < 2 || width > 4096) return mxq::invalid("mxq_lut_pick: bad arguments");
+  if ((I == nullptr) == (P_lut == nullptr)) return mxq::invalid("mxq_lut_pick: exactly one of I and P_lut");
+  if (K == 0 || n == 0) return MXQ_OK;
+  const size_t lds = (size_t)((256 >> group) > 0 ? (256 >> group) : 1) * width * sizeof(float);
+  if (lds > 65536) return mxq::invalid("mxq_lut_pick: tables too wide");
+  const int64_t col_blocks = mxq::ceil_div(n, 256);
+  int64_t row_blocks = mxq::ceil_div(8192, col_blocks);
+  if (row_blocks > K) row_blocks = K;
+  if (row_blocks > 65535) row_blocks = 65535;
+  const int64_t rpb = mxq::ceil_div(K, row_blocks);
+  row_blocks = mxq::ceil_div(K, rpb);
+  k_lut_pick<<<dim3((unsigned)col_blocks, (unsigned)row_blocks), 256, lds, mxq::as_stream(stream)>>>(
+      P, K, n, group, T, width, rpb, I, P_lut);
+  return mxq::check_launch("mxq_lut_pick");
+}
+
+extern "C" int mxq_lut_lookup(const int64_t* I, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,
+                              float* out, mxq_stream_t stream) {
+  if (K < 0 || n < 0 || group < 0 || group > 30 || width < 1) return mxq::invalid("mxq_lut_lookup: bad arguments");
+  if (K == 0 || n == 0) return MXQ_OK;
+  int64_t blocks = mxq::ceil_div(K * n, 256);
+  if (blocks > 65536) blocks = 65536;
+  k_lut_lookup<<<dim3((unsigned)blocks), 256, 0, mxq::as_stream(stream)>>>(I, K, n, group, T, width, out);
+  return mxq::check_launch("mxq_lut_lookup");
+}
+
+extern "C" int mxq_lut_finder(const int64_t* codes, int64_t K, int64_t n, int32_t group, const int64_t* fx_all,
+                              int32_t ncodes, const int64_t* lut_fx, int64_t mask, int64_t* out, mxq_stream_t stream) {
+  if (K < 0 || n < 0 || group < 0 || group > 30 || ncodes < 1 || ncodes > kMaxGrid)
+    return mxq::invalid("mxq_lut_finder: bad arguments");
+  if (K == 0 || n == 0) return MXQ_OK;
+  int64_t blocks = mxq::ceil_div(K * n, 256);
+  if (blocks > 65536) blocks = 65536;
+  k_lut_finder<<<dim3((unsigned)blocks), 256, 0, mxq::as_stream(stream)>>>(codes, K, n, group, fx_all, ncodes, lut_fx,
+                                                                           mask, out);
+  return mxq::check_launch("mxq_lut_finder");
+}

@@ -47,6 +47,11 @@ SIGNATURES = {
     "mxq_block_dequantize": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr]),
     "mxq_systolic": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,
                              ctypes.POINTER(ArithSpec), c_ptr, c_i32, c_ptr]),
+    "mxq_lut_tables": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr,
+                               c_ptr]),
+    "mxq_lut_pick": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr]),
+    "mxq_lut_lookup": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr]),
+    "mxq_lut_finder": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_i64, c_ptr, c_ptr]),
     "mxq_round_bits": (c_i32, [c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i32, c_ptr]),
     "mxq_round_int": (c_i32, [c_ptr, c_i32, c_ptr, c_i64, c_i32, c_ptr]),
     "mxq_bf16": (c_i32, [c_ptr, c_ptr, c_i64, c_ptr]),

@@ -10,6 +10,6 @@
     lut          mxgemmini + mxq.lut tables                       MX-Gemmini's LUT operand
 """
 from ._driver import BLOCK, compose, dequantize
-from . import mxquant, mxgemmini, ocp
+from . import mxquant, mxgemmini, ocp, lut
 
-__all__ = ["BLOCK", "compose", "dequantize", "mxquant", "mxgemmini", "ocp"]
+__all__ = ["BLOCK", "compose", "dequantize", "mxquant", "mxgemmini", "ocp", "lut"]

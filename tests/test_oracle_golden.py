@@ -1,0 +1,85 @@
+"""The oracle against the fixtures the reference itself wrote (tests/golden/make_golden.py): the functions only
+an import of the reference pins -- LUT tables, safe sets and finder, ocp_no_clip, microxcaling "even", the
+composed systolic datapaths."""
+import os
+
+import numpy as np
+import pytest
+
+from _util import assert_bits_equal
+from oracle import block as ob
+from oracle import lut as ol
+from oracle import numerics as nx
+from oracle import systolic as osys
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _load(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+@pytest.mark.parametrize("fmt", ol.FORMATS)
+def test_lut_formats(fmt):
+    z = _load(f"lut_{fmt}.npz")
+    vals, _, safe = ol.tables_of(fmt)
+    assert_bits_equal(safe, z["values"], f"values {fmt}")
+    assert_bits_equal(vals[z["decode_codes"]], z["decode"], f"decode {fmt}")
+
+
+@pytest.mark.parametrize("fmt", ol.FORMATS)
+def test_lut_tables_pick_lookup_finder(fmt):
+    z = _load(f"lut_{fmt}.npz")
+    keys = sorted(k[:-2] for k in z.files if k.endswith("_T"))
+    assert keys
+    for key in keys:
+        G = int(key.split("_g")[1].split("_")[0])
+        iters = int(key.split("_i")[1])
+        P = z[f"{key}_P"]
+        T = ol.tables(P, fmt, G, iters)
+        assert_bits_equal(T, z[f"{key}_T"], f"tables {fmt} {key}")
+        I = ol.pick(P, T, G)
+        assert np.array_equal(I, z[f"{key}_I"]), f"pick {fmt} {key}"
+        assert_bits_equal(ol.lookup(I, T, G), z[f"{key}_L"], f"lookup {fmt} {key}")
+        if f"{key}_codes" in z.files:
+            F = ol.finder(z[f"{key}_codes"], T, fmt, G)
+            assert np.array_equal(F, z[f"{key}_F"]), f"finder {fmt} {key}"
+
+
+def test_block_lut():
+    z = _load("blocklut.npz")
+    for i, (fmt, G, axis) in enumerate([("MXFP6_E3M2", 1, 0), ("MXFP6_E2M3", 0, 1), ("MXFP8_E5M2", 2, 0),
+                                        ("MXFP8_E4M3", 1, 1)]):
+        P, X = ol.lut_quantize(z[f"c{i}_V"], fmt, axis, 32, "rne", 2.0 ** -23, G, 50)
+        assert_bits_equal(P, z[f"c{i}_P"], f"block.lut P {fmt}")
+        assert_bits_equal(X, z[f"c{i}_X"], f"block.lut X {fmt}")
+
+
+def test_ocp_no_clip():
+    z = _load("noclip.npz")
+    for fmt in nx.FORMATS:
+        for mode in ("even", "nearest", "floor"):
+            assert_bits_equal(nx.scale_ocp_no_clip(z["amax"], fmt, mode), z[f"{fmt}_{mode}"], f"no_clip {fmt} {mode}")
+        P, X = ob.ocp_quantize(z[f"{fmt}_V"], fmt, 0, 32, "even", 8, "no_clip")
+        assert_bits_equal(P, z[f"{fmt}_P"], f"ocp no_clip P {fmt}")
+        assert_bits_equal(X, z[f"{fmt}_X"], f"ocp no_clip X {fmt}")
+
+
+def test_microsoft_even():
+    z = _load("ms_even.npz")
+    for fmt in nx.FORMATS:
+        assert_bits_equal(nx.microsoft_fmt(z[f"{fmt}_z"], fmt, "even"), z[f"{fmt}_even"], f"microsoft even {fmt}")
+
+
+def test_systolic_end_to_end():
+    z = _load("systolic.npz")
+    cases = [("hw", nx.MXGEMMINI(), osys.HW_FINAL, 16, 32), ("hw_tail", nx.MXGEMMINI(), osys.HW_FINAL, 16, 32),
+             ("hw_e5m2", nx.MXGEMMINI(5, 2), osys.HW_FINAL, 16, 32),
+             ("hw_noflush", nx.MXGEMMINI(4, 3, None), [(4, 3)] * 8 + [(8, 7)] * 8, 16, 32),
+             ("mxquant", nx.MXQUANT(4, 3), osys.HW_FINAL, 16, 32),
+             ("mxquant_e5m10", nx.MXQUANT(5, 10), [(6, 9)] * 16, 16, 32),
+             ("fp32_lanes", nx.MXGEMMINI(), [(8, 23)] * 16, 16, 32),
+             ("size8", nx.MXGEMMINI(), [(4, 4)] * 7 + [(8, 7)], 8, 32)]
+    for name, ar, sched, size, bs in cases:
+        Y = osys.systolic(z[f"{name}_PA"], z[f"{name}_XA"], z[f"{name}_PB"], z[f"{name}_XB"], ar, sched, size, bs)
+        assert_bits_equal(Y, z[f"{name}_Y"], f"systolic {name}")
