@@ -20,11 +20,11 @@ __version__ = "0.1.0"
 
 import torch  # noqa: F401  (first: libmxq_hip.so binds to the HIP runtime torch loads)
 
-from . import rounding, arith, schedule, scale_factor, element_quant, lut, block, matmul, scheme
+from . import rounding, arith, schedule, scale_factor, element_quant, lut, block, matmul, scheme, nn
 from .block import BLOCK
 from ._fp64_accum import fp64_accum
 from .element_quant.formats import Format
 from .scheme import Scheme
 
-__all__ = ["rounding", "arith", "schedule", "scale_factor", "element_quant", "lut", "block", "matmul", "scheme",
+__all__ = ["rounding", "arith", "schedule", "scale_factor", "element_quant", "lut", "block", "matmul", "scheme", "nn",
            "BLOCK", "Format", "Scheme", "fp64_accum"]

@@ -1,0 +1,170 @@
+"""mxq.nn on the GPU: attend, MXLinear and patch with Schemes built from the gfx950 kernels.
+
+attend: S and O bit for bit against oracle/attend.py run with the oracle's quantizers and systolic reducer and
+with the same torch.softmax on the same GPU; against the reference's own outputs (tests/golden/attend.npz,
+written with torch's CPU softmax) the only difference allowed is what the two softmax implementations leave:
+at most 2% of outputs may differ, none by more than 2^-4 of the largest |output|.
+"""
+import math
+import os
+from functools import partial
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from _util import assert_bits_equal
+from oracle import attend as oatt
+from oracle import block as ob
+from oracle import lut as ol
+from oracle import numerics as nx
+from oracle import systolic as osys
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _hw(mxq):
+    from mxq import Scheme, block, matmul, schedule
+    q = partial(block.mxgemmini.quantize, fmt="MXFP8_E4M3", axis=0)
+    return Scheme("hw", a=q, b=q, reduce=partial(matmul.systolic, arith=matmul.MXGEMMINI(), schedule=schedule.HW_FINAL))
+
+
+def _hw_oracle():
+    q = lambda V: ob.mxgemmini_quantize(V, "MXFP8_E4M3", 0)                       # noqa: E731
+    return oatt.Side(q, q, lambda *ops: osys.systolic(*ops, nx.MXGEMMINI(), osys.HW_FINAL))
+
+
+def _lut(mxq):
+    from mxq import Scheme, block, matmul, schedule
+    a = partial(block.lut.quantize, fmt="MXFP6_E3M2", axis=0, block_size=32, rounding_mode="rne",
+                scale_floor=2.0 ** -23, group=1, max_iters=50)
+    b = partial(block.mxgemmini.quantize, fmt="MXFP8_E4M3", axis=0)
+    return Scheme("lut", a=a, b=b, rows=2,
+                  reduce=partial(matmul.systolic, arith=matmul.MXGEMMINI(), schedule=schedule.HW_FINAL))
+
+
+def _lut_oracle():
+    a = lambda V: ol.lut_quantize(V, "MXFP6_E3M2", 0, 32, "rne", 2.0 ** -23, 1, 50)  # noqa: E731
+    b = lambda V: ob.mxgemmini_quantize(V, "MXFP8_E4M3", 0)                           # noqa: E731
+    return oatt.Side(a, b, lambda *ops: osys.systolic(*ops, nx.MXGEMMINI(), osys.HW_FINAL), rows=2)
+
+
+def _gpu_softmax(S):
+    return torch.softmax(torch.from_numpy(np.ascontiguousarray(S)).cuda(), dim=-1).cpu().numpy()
+
+
+def _causal(B, Tq, Tk):
+    m = torch.triu(torch.full((Tq, Tk), torch.finfo(torch.float32).min), Tk - Tq + 1)
+    return m[None, None].repeat(B, 1, 1, 1)
+
+
+def _fixture_cases():
+    z = np.load(os.path.join(GOLDEN, "attend.npz"), allow_pickle=False)
+    for i in range(len([k for k in z.files if k.endswith("_meta")])):
+        B, H, Hkv, T, D, masked, chunk = (int(x) for x in z[f"c{i}_meta"])
+        yield (i, z[f"c{i}_q"], z[f"c{i}_k"], z[f"c{i}_v"], z[f"c{i}_mask"] if masked else None,
+               None if chunk < 0 else chunk, z[f"c{i}_o"])
+
+
+@pytest.mark.parametrize("case", list(_fixture_cases()), ids=lambda c: f"c{c[0]}")
+def test_attend_fixture_shapes(cuda, case):
+    import mxq
+    i, q, k, v, mask, chunk, o_ref = case
+    D = q.shape[-1]
+    t = lambda a: None if a is None else torch.from_numpy(a).cuda()                   # noqa: E731
+    got = mxq.nn.attend(t(q), t(k), t(v), t(mask), D ** -0.5, _hw(mxq), _hw(mxq), chunk=chunk).cpu().numpy()
+    want = oatt.attend(q, k, v, mask, D ** -0.5, _hw_oracle(), _hw_oracle(), _gpu_softmax, chunk=chunk)
+    assert_bits_equal(got, want, f"attend c{i} vs oracle")
+    differ = got != o_ref
+    assert differ.mean() <= 0.02, f"c{i}: {differ.mean():.3%} of outputs differ from the reference's"
+    assert np.abs(got - o_ref).max() <= np.abs(o_ref).max() * 2.0 ** -4
+
+
+@pytest.mark.parametrize("case", [(1, 4, 1, 70, 32, 16, "hw"), (1, 2, 2, 66, 64, None, "lut"),
+                                  (2, 2, 1, 40, 32, 8, "lut"), (1, 2, 2, 512, 128, None, "hw")],
+                         ids=["gqa4_tails", "lut_rows2", "lut_chunks", "llama_head_512"])
+def test_attend_against_oracle(cuda, case):
+    import mxq
+    B, H, Hkv, T, D, chunk, kind = case
+    g = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn(B, h, T, D, generator=g) for h in (H, Hkv, Hkv))
+    mask = _causal(B, T, T)
+    s, so = (_hw(mxq), _hw_oracle()) if kind == "hw" else (_lut(mxq), _lut_oracle())
+    hw, hwo = _hw(mxq), _hw_oracle()
+    got = mxq.nn.attend(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), D ** -0.5, s, hw, chunk=chunk).cpu().numpy()
+    want = oatt.attend(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), D ** -0.5, so, hwo, _gpu_softmax, chunk=chunk)
+    assert_bits_equal(got, want, f"attend {case}")
+
+
+def test_attend_vector_bf16(cuda):
+    """vector="bf16": every softmax step rounded; the bf16 rounding is the library's kernel."""
+    import mxq
+    from mxq.nn._vector import softmax
+    g = torch.Generator().manual_seed(5)
+    S = (torch.randn(64, 96, generator=g) * 4).cuda()
+    P = softmax(S, "bf16")
+    r = lambda x: x.to(torch.bfloat16).float()                                         # noqa: E731
+    e = r(torch.exp(r(S - S.amax(-1, keepdim=True))))
+    assert torch.equal(P, r(e / r(e.sum(-1, keepdim=True))))
+    q, k, v = (torch.randn(1, 2, 64, 32, generator=g).cuda() for _ in range(3))
+    o = mxq.nn.attend(q, k, v, _causal(1, 64, 64).cuda(), 32 ** -0.5, _hw(mxq), _hw(mxq), vector="bf16")
+    assert torch.isfinite(o).all()
+
+
+def test_mxlinear_against_oracle(cuda):
+    import mxq
+    torch.manual_seed(4)
+    lin = nn.Linear(96, 48).cuda()
+    m = mxq.nn.MXLinear(lin, _hw(mxq))
+    x = torch.randn(3, 7, 96, device="cuda", dtype=torch.bfloat16)
+    y = m(x)
+    A = x.reshape(-1, 96).float().t().contiguous().cpu().numpy()
+    W = lin.weight.detach().float().t().contiguous().cpu().numpy()
+    so = _hw_oracle()
+    Y = osys.systolic(*so.a(A), *so.b(W), nx.MXGEMMINI(), osys.HW_FINAL)
+    Y = (torch.from_numpy(Y) + lin.bias.detach().float().cpu()).to(torch.bfloat16).reshape(3, 7, 48)
+    assert y.dtype == torch.bfloat16 and torch.equal(y.cpu(), Y)
+    assert torch.equal(mxq.nn.MXLinear(lin, _hw(mxq), chunk=5)(x), y)
+
+
+def _tiny_llama(seed):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(vocab_size=64, hidden_size=64, intermediate_size=96, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=128)
+    torch.manual_seed(seed)
+    return LlamaForCausalLM(cfg).eval().cuda()
+
+
+def test_patch_on_gpu(cuda):
+    import mxq
+    from mxq.nn import is_attention, patch
+    model = _tiny_llama(0)
+    ids = torch.randint(0, 64, (2, 20), generator=torch.Generator().manual_seed(0)).cuda()
+    before = model(ids).logits
+    hw = _hw(mxq)
+    h = patch(model, [("lm_head", None), (is_attention, None), (nn.Linear, hw),
+                      ("model.layers.0.self_attn", (hw, hw))], vector="bf16")
+    assert isinstance(model.model.layers[0].mlp.up_proj, mxq.nn.MXLinear)
+    assert {name: names for name, _, names in h.cores} == {"model.layers.0.self_attn": ("hw", "hw"),
+                                                           "model.layers.1.self_attn": ("exact", "exact")}
+    assert len(h.norms) == 5
+    out = model(ids).logits
+    assert torch.isfinite(out).all() and not torch.equal(out, before)
+    h.revert()
+    assert torch.equal(model(ids).logits, before)
+
+
+def test_exact_core_matches_eager(cuda):
+    """The EXACT core (fp32 operands, float64 sums) against transformers' eager attention."""
+    from mxq.nn import patch
+    from mxq.nn._vector import EXACT
+    model = _tiny_llama(2)
+    ids = torch.randint(0, 64, (2, 14), generator=torch.Generator().manual_seed(2)).cuda()
+    model.set_attn_implementation("eager")
+    eager = model(ids).logits
+    h = patch(model, [(lambda name, mod, parent: True, (EXACT, EXACT))])
+    torch.testing.assert_close(model(ids).logits, eager, rtol=1e-4, atol=1e-4)
+    h.revert()

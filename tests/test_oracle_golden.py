@@ -83,3 +83,32 @@ def test_systolic_end_to_end():
     for name, ar, sched, size, bs in cases:
         Y = osys.systolic(z[f"{name}_PA"], z[f"{name}_XA"], z[f"{name}_PB"], z[f"{name}_XB"], ar, sched, size, bs)
         assert_bits_equal(Y, z[f"{name}_Y"], f"systolic {name}")
+
+
+def _hw_side():
+    from oracle import attend as oatt
+    q = lambda V: ob.mxgemmini_quantize(V, "MXFP8_E4M3", 0)                       # noqa: E731
+    return oatt.Side(q, q, lambda *ops: osys.systolic(*ops, nx.MXGEMMINI(), osys.HW_FINAL))
+
+
+def _torch_cpu_softmax(S):
+    import torch
+    return torch.softmax(torch.from_numpy(np.ascontiguousarray(S)), dim=-1).numpy()
+
+
+def attend_cases():
+    z = _load("attend.npz")
+    for i in range(len([k for k in z.files if k.endswith("_meta")])):
+        B, H, Hkv, T, D, masked, chunk = (int(x) for x in z[f"c{i}_meta"])
+        yield (i, z[f"c{i}_q"], z[f"c{i}_k"], z[f"c{i}_v"], z[f"c{i}_mask"] if masked else None, D ** -0.5,
+               None if chunk < 0 else chunk, z[f"c{i}_o"])
+
+
+@pytest.mark.parametrize("case", list(attend_cases()), ids=lambda c: f"c{c[0]}")
+def test_attend(case):
+    """The reference's attend (CPU softmax) on GQA, chunked, masked and unmasked shapes, bit for bit."""
+    from oracle import attend as oatt
+    i, q, k, v, mask, scale, chunk, o = case
+    side = _hw_side()
+    got = oatt.attend(q, k, v, mask, scale, side, side, _torch_cpu_softmax, chunk=chunk)
+    assert_bits_equal(got, o, f"attend c{i}")
