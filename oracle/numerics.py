@@ -6,14 +6,15 @@ Each function restates one reference function in numpy, in the reference's opera
 (or float64 where the reference uses float64).  numpy float32 arithmetic, floor, trunc, rint, frexp, ldexp
 and remainder round exactly as torch's CPU kernels do.  Two torch calls have no exact numpy twin and are
 restated:
-  * torch.log2 on float32: taken as the correctly rounded log2 (float64 log2 rounded to float32); pinned
-    against torch.log2 itself at every binade's round-up threshold (tests/test_oracle_numerics.py).
+  * torch.log2 on float32, which the reference only ever floors: taken as the correctly rounded log2
+    (float64 log2 rounded to float32); its floor is pinned against torch.log2's, with the round-up band
+    below every power of two (tests/test_oracle_pins.py).
   * torch.exp2 / torch.pow(2, .) of integer-valued floats: exact powers of two, via ldexp; pinned against torch.
 
 Pins: rounding.* and bf16 against torch casts; float_em ieee/ocp against brute-force nearest-value search over
 the enumerated grid and torch float8 casts; qtorch by its grid properties; exact_add, truncate, flush and
 saturate against exact rationals (oracle/brute.py); microsoft "even", ocp_no_clip by fixtures the reference
-wrote (tests/golden/).
+wrote (tests/golden/); all in tests/test_oracle_pins.py and tests/test_oracle_golden.py.
 """
 import numpy as np
 

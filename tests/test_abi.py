@@ -1,0 +1,56 @@
+"""The C-ABI library: it loads without a GPU, exports every function include/mxq_hip.h declares, and the host
+side's argument table covers exactly those functions.  No compute calls (they need a GPU)."""
+import ctypes
+import os
+import re
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "mxq_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(mxq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared()
+    assert "mxq_systolic" in names and "mxq_block_quantize" in names and "mxq_lut_tables" in names
+    assert len(names) >= 19
+
+
+def test_library_exports_every_declared_symbol():
+    from mxq import _lib
+    lib = _lib.load()
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, f"declared in include/mxq_hip.h but not exported: {missing}"
+
+
+def test_signature_table_matches_header():
+    from mxq import _lib
+    assert sorted(_lib.SIGNATURES) == _declared()
+
+
+def test_version_and_error_without_gpu():
+    """mxq_version and mxq_last_error touch no device."""
+    from mxq import _lib
+    lib = _lib.load()
+    assert lib.mxq_version() >= 1
+    lib.mxq_last_error.restype = ctypes.c_char_p
+    assert isinstance(lib.mxq_last_error(), bytes)
+
+
+def test_structs_match_header():
+    """ctypes layouts of mxq_block_spec / mxq_arith_spec against the header's field lists."""
+    from mxq import _lib
+    text = open(HEADER).read()
+    for struct, py in (("mxq_block_spec", _lib.BlockSpec), ("mxq_arith_spec", _lib.ArithSpec)):
+        body = re.search(r"typedef struct " + struct + r"\s*\{(.*?)\}\s*" + struct + ";", text, flags=re.S).group(1)
+        body = re.sub(r"/\*.*?\*/|//[^\n]*", "", body, flags=re.S)
+        fields = [(t, n.strip()) for t, names in re.findall(r"\b(int32_t|float|double|int64_t)\s+([a-z_0-9, ]+);", body)
+                  for n in names.split(",")]
+        ctypes_of = {"int32_t": ctypes.c_int32, "float": ctypes.c_float, "double": ctypes.c_double,
+                     "int64_t": ctypes.c_int64}
+        assert [(n, ctypes_of[t]) for t, n in fields] == [(n, t) for n, t in py._fields_], struct
