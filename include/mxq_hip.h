@@ -82,7 +82,7 @@ int mxq_block_dequantize(const float* P, const float* X, float* out, int64_t out
  * (ceil(K/block_size) x M), X_B (ceil(K/block_size) x N), all float32 row-major.  Per block of K the scale map
  * X_A[g] (x) X_B[g]; per reduction of `size` k a fresh sum accumulated lane by lane (lane i has the format
  * (lane_e[i], lane_m[i]), host arrays of `size` entries), rescaled and added into C; K tails as the reference.
- * size must divide block_size and 32.  `workspace` is device memory of at least 8 bytes (operand statistics
+ * size must divide block_size and 32.  `workspace` is device memory of at least 16 bytes (operand statistics
  * that select the kernel on the device; the call makes no host synchronisation).  force_general = 1 skips the
  * fast kernel.  Replaces mxq/matmul/_systolic.py:23-62 with mxq/matmul/_arithmetic.py:64-134. */
 int mxq_systolic(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C, int64_t K,

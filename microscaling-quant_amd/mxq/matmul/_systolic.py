@@ -57,7 +57,7 @@ def systolic(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: torch
     import ctypes
     le = (ctypes.c_int32 * size)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
-    work = torch.empty(2, dtype=torch.int32, device=dev)
+    work = torch.empty(4, dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_systolic", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, le, lm, size, block_size,
                  kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))

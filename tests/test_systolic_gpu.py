@@ -112,6 +112,54 @@ def test_tails_and_sizes(cuda, K, size, bs):
         assert_bits_equal(got, want, f"{name} K={K} size={size} bs={bs}")
 
 
+FAST_LADDERS = [
+    (16, [(4, 4)] * 8 + [(4, 5)] * 2 + [(4, 6)] * 5 + [(8, 7)], (4, 3)),      # HW_FINAL
+    (16, [(4, 3)] * 4 + [(4, 5)] * 4 + [(4, 7)] * 7 + [(8, 7)], (4, 3)),      # two-step rises, m = 7 into bf16
+    (16, [(4, 4)] * 6 + [(4, 9)] * 10, (4, 3)),                              # no bf16 lane, m up to 9
+    (8, [(4, 3)] * 7 + [(8, 7)], (4, 2)),                                    # prod_m 2
+    (4, [(4, 1), (4, 2), (4, 3), (8, 7)], (4, 1)),                           # rises every lane, m from 1
+    (32, [(4, 4)] * 16 + [(4, 6)] * 15 + [(8, 7)], (4, 3)),
+    (32, [(4, 8)] * 32, (4, 3)),
+]
+
+
+@pytest.mark.parametrize("case", FAST_LADDERS, ids=[f"l{i}" for i in range(len(FAST_LADDERS))])
+@pytest.mark.parametrize("K", [64, 77])
+def test_fast_ladders(cuda, case, K):
+    """Ladders the fast kernel takes (e4 lanes of non-decreasing m, optional bf16 last lane), against the
+    oracle and against the general kernel, with K tails that end mid-reduction."""
+    size, sched, (pe, pm) = case
+    rng = np.random.default_rng(size + K)
+    P_A, X_A = _codes(rng, K, 70, scale=2.0)
+    P_B, X_B = _codes(rng, K, 66, scale=0.3)
+    ar, orc = _arith("MXGEMMINI", pe, pm)
+    want = osys.systolic(P_A, X_A, P_B, X_B, orc, sched, size)
+    assert_bits_equal(_run(P_A, X_A, P_B, X_B, ar, sched, size), want, f"fast {sched}")
+    assert_bits_equal(_run(P_A, X_A, P_B, X_B, ar, sched, size, force_general=True), want, f"general {sched}")
+
+
+def test_fast_guards(cuda):
+    """Operands outside the fast kernel's case go to the general kernel: non-finite scales, a code of 2^110
+    against tiny ones, products above 8, subnormal float32 codes, codes that are not on a code grid."""
+    rng = np.random.default_rng(5)
+    K, M, N = 64, 20, 24
+    P_A, X_A = _codes(rng, K, M)
+    P_B, X_B = _codes(rng, K, N)
+    ar, orc = _arith("MXGEMMINI")
+    cases = []
+    XA = X_A.copy(); XA[1, 3] = np.nan; cases.append((P_A, XA, P_B, X_B, "nan scale"))
+    XB = X_B.copy(); XB[0, 5] = np.inf; cases.append((P_A, X_A, P_B, XB, "inf scale"))
+    XA = X_A.copy(); XA[0, :] = np.float32(2.0 ** 100); cases.append((P_A, XA, P_B, X_B, "scale product overflows"))
+    PA = P_A.copy(); PA[3, 2] = np.float32(2.0 ** 110)
+    PB = (P_B * np.float32(2.0 ** -120)).astype(np.float32); cases.append((PA, X_A, PB, X_B, "huge a, tiny b"))
+    PA = P_A.copy(); PA[5, 5] = 448.0; cases.append((PA, X_A, P_B, X_B, "products above 8"))
+    PA = P_A.copy(); PA[7, 1] = np.float32(1e-40); cases.append((PA, X_A, P_B, X_B, "subnormal code"))
+    PA = (P_A + np.float32(1e-3)).astype(np.float32); cases.append((PA, X_A, P_B, X_B, "off-grid codes"))
+    for pa, xa, pb, xb, what in cases:
+        want = osys.systolic(pa, xa, pb, xb, orc, HW_FINAL)
+        assert_bits_equal(_run(pa, xa, pb, xb, ar, HW_FINAL), want, what)
+
+
 def test_compiled_and_scheme(cuda):
     from functools import partial
 
