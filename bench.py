@@ -1,12 +1,15 @@
 """Benchmark: emulated MX GEMM throughput of matmul.systolic (bit-exact MXGEMMINI, HW_FINAL ladder) on one GPU,
-plus block-quantize HBM throughput, each next to its roofline and the oracle's CPU rate.
+plus block-quantize HBM throughput, the LUT pipeline and the attention core, each next to its roofline and the
+oracle's CPU rate.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+    python bench.py --copy-calibration        # only a 256 MiB device copy, 5 times (counter calibration)
 
 A step is one systolic call over the benchmark workload (A = x^T with x 512 x 4096 ~ N(0,1), B = W^T with
-W 4096 x 4096 ~ N(0, 0.02), both block.mxgemmini MXFP8_E4M3 codes along K, M = 512, N = 4096, K = 4096),
-with operands and scales resident in HBM.  `value` is emulated GEMM ops per second (2 per MAC).
-One JSON line is printed.
+W 4096 x 4096 ~ N(0, 0.02), both block.mxgemmini MXFP8_E4M3 codes along K: M = 512, N = 4096, K = 4096),
+operands and scales resident in HBM.  `value` is emulated GEMM ops per second (2 per MAC) over the timed
+steps.  `roofline.achieved` uses the fast systolic kernel's own average duration, timed with HIP events the
+library records around each of its launches on the launch's stream.  One JSON line is printed.
 """
 import argparse
 import json
@@ -38,6 +41,23 @@ def _events_ms(fn, steps, stream):
     return start.elapsed_time(end) / steps
 
 
+def _kernel_ms(fn, steps, kernel):
+    """Average duration of the library kernel `kernel` over `steps` calls of fn (library HIP events)."""
+    import torch
+
+    from mxq import _lib
+    torch.cuda.synchronize()
+    _lib.timer_read(kernel)                                  # drop anything recorded before
+    _lib.timer_enable(True)
+    try:
+        for _ in range(steps):
+            fn()
+    finally:
+        _lib.timer_enable(False)
+    total, n = _lib.timer_read(kernel)
+    return total / n if n else None, n
+
+
 def _traffic(name):
     """HBM bytes per launch for `name` from profiles/<name>_traffic.txt ("bytes_per_launch: N"), else None."""
     path = os.path.join(REPO, "profiles", f"{name}_traffic.txt")
@@ -51,9 +71,10 @@ def _traffic(name):
     return None
 
 
-def cpu_baseline_systolic(P_A, X_A, P_B, X_B, cols, budget_s=20.0):
-    """The oracle (numpy port of the reference's reducer) on a column slice of the same operands."""
-    import numpy as np
+def cpu_baseline_systolic(P_A, X_A, P_B, X_B, cols):
+    """The oracle (numpy port of the reference's reducer) on a column slice of the same operands; output
+    columns are independent chains, so the slice is a fair sample of the whole."""
+    import numpy as np  # noqa: F401
 
     from oracle import numerics as nx
     from oracle import systolic as osys
@@ -65,8 +86,9 @@ def cpu_baseline_systolic(P_A, X_A, P_B, X_B, cols, budget_s=20.0):
     dt = time.perf_counter() - t0
     macs = K * M * cols
     return {"value": round(2 * macs / dt / 1e9, 4), "unit": "GOP/s", "cores": 1, "kind": "port",
-            "sample": f"oracle systolic MXGEMMINI HW_FINAL on M={M} x N={cols} columns x K={K} "
-                      f"({macs / 1e6:.1f} M MAC, {dt:.1f} s, numpy single thread, {platform.processor() or 'x86_64'})"}
+            "sample": f"oracle systolic MXGEMMINI HW_FINAL on the same operands, M={M} x N={cols} columns x "
+                      f"K={K} ({macs / 1e6:.1f} M MAC, {dt:.1f} s, numpy single thread, "
+                      f"{platform.processor() or platform.machine()})"}
 
 
 def quantize_lines(torch, steps):
@@ -80,15 +102,17 @@ def quantize_lines(torch, steps):
     t.view(-1)[idx] *= 100
     V = t.to(torch.bfloat16).to(dev)
     s = torch.cuda.current_stream(dev)
-    out = {}
+    out, kern = {}, {}
     bytes_c3 = 8192 * 8192 * 2 + 8192 * 8192 * 4 + 256 * 8192 * 4
     for fmt in ("MXFP8_E4M3", "MXFP8_E5M2", "MXFP6_E3M2", "MXFP6_E2M3", "MXFP4"):
         fn = lambda: block.mxgemmini.quantize(V, fmt, axis=0, rounding_mode="rne")   # noqa: E731
         fn()
         ms = _events_ms(fn, steps, s)
         out[fmt] = round(bytes_c3 / ms / 1e6, 1)
+        kms, _ = _kernel_ms(fn, steps, "block_quantize")
+        kern[fmt] = round(bytes_c3 / kms / 1e6, 1) if kms else None
     del V
-    # C1: 17 MB per call -- rotate over 64 inputs (1.1 GB with outputs) so HBM, not the cache, serves them
+    # 17 MB per call: rotate over 64 inputs (1.1 GB with outputs) so HBM, not the cache, serves them
     rot = [torch.randn(4096, 512, device=dev) for _ in range(64)]
     bytes_c1 = 4096 * 512 * 4 * 2 + 128 * 512 * 4
     i = [0]
@@ -98,12 +122,73 @@ def quantize_lines(torch, steps):
         i[0] += 1
     q1()
     ms1 = _events_ms(q1, 64, s)
+    kms1, _ = _kernel_ms(q1, 64, "block_quantize")
     P, X = block.ocp.quantize(rot[0], "MXFP8_E4M3", axis=0)
     ms1d = _events_ms(lambda: block.ocp.dequantize(P, X, axis=0), 64, s)
-    return {"mxgemmini_bf16_8192x8192_rne_GBs": out, "mxgemmini_bytes_per_call": bytes_c3,
+    return {"mxgemmini_bf16_8192x8192_rne_GBs": out, "mxgemmini_bf16_8192x8192_rne_kernel_GBs": kern,
+            "mxgemmini_bytes_per_call": bytes_c3,
             "ocp_e4m3_4096x512_quantize_GBs": round(bytes_c1 / ms1 / 1e6, 1),
+            "ocp_e4m3_4096x512_quantize_kernel_GBs": round(bytes_c1 / kms1 / 1e6, 1) if kms1 else None,
             "ocp_e4m3_4096x512_dequantize_GBs_cache_resident": round(bytes_c1 / ms1d / 1e6, 1),
             "peak_GBs": HBM_PEAK_GBS}
+
+
+def lut_line(torch, steps):
+    """block.lut MXFP6_E3M2 (rne, 2^-23, group 1, 50 iterations) on two fp32 4096 x 4096 operands, then the
+    systolic MXGEMMINI HW_FINAL product of the two LUT operands (K = M = N = 4096)."""
+    from mxq import block, matmul
+    dev = torch.device("cuda", 0)
+    s = torch.cuda.current_stream(dev)
+    A = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0)).to(dev)
+    B = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(1)).to(dev)
+    q = lambda V: block.lut.quantize(V, "MXFP6_E3M2", 0, 32, rounding_mode="rne", scale_floor=2.0 ** -23,  # noqa
+                                     group=1, max_iters=50)
+    PA, XA = q(A)
+    PB, XB = q(B)
+    ms_q = _events_ms(lambda: q(A), steps, s)
+    mm = lambda: matmul.systolic(PA, XA, PB, XB, matmul.MXGEMMINI(), matmul.HW_FINAL)        # noqa: E731
+    mm()
+    ms_mm = _events_ms(mm, steps, s)
+    kms, _ = _kernel_ms(mm, steps, "systolic_fast")
+    macs = 4096 ** 3
+    return {"workload": "block.lut MXFP6_E3M2 4096x4096 (tables, pick, lookup) + systolic 4096^3",
+            "lut_quantize_ms": round(ms_q, 3), "systolic_ms": round(ms_mm, 3),
+            "systolic_TOPs": round(2 * macs / ms_mm / 1e9, 3),
+            "systolic_kernel_TOPs": round(2 * macs / kms / 1e9, 3) if kms else None}
+
+
+def attend_line(torch, steps):
+    """mxq.nn.attend, Llama-3-8B-shaped: 1 x 32 heads x 2048 x 128, causal HF eager mask, Q K^T and P V through
+    the MXGEMMINI MXFP8_E4M3 Scheme, softmax in fp32."""
+    from functools import partial
+
+    import mxq
+    from mxq import Scheme, block, matmul
+    dev = torch.device("cuda", 0)
+    s = torch.cuda.current_stream(dev)
+    qz = partial(block.mxgemmini.quantize, fmt="MXFP8_E4M3", axis=0)
+    hw = Scheme("hw", a=qz, b=qz, reduce=partial(matmul.systolic, arith=matmul.MXGEMMINI(), schedule=matmul.HW_FINAL))
+    q, k, v = (torch.randn(1, 32, 2048, 128, generator=torch.Generator().manual_seed(i)).to(dev) for i in range(3))
+    mask = torch.triu(torch.full((2048, 2048), torch.finfo(torch.float32).min), 1)[None, None].to(dev)
+    fn = lambda: mxq.nn.attend(q, k, v, mask, 128 ** -0.5, hw, hw)                      # noqa: E731
+    fn()
+    ms = _events_ms(fn, steps, s)
+    macs = 2 * 32 * 2048 * 2048 * 128
+    return {"workload": "nn.attend 1x32x2048x128 causal, MXGEMMINI MXFP8_E4M3 Scheme for QK^T and PV",
+            "ms": round(ms, 3), "emulated_TOPs": round(2 * macs / ms / 1e9, 3)}
+
+
+def copy_calibration():
+    """A plain device copy of 256 MiB, five times: the reference point for the FETCH_SIZE / WRITE_SIZE
+    counters (each launch reads and writes 262144 KiB)."""
+    import torch
+    x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    x.fill_(1.0)
+    for _ in range(5):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": x.numel() * 4, "launches": 5}), flush=True)
 
 
 def main():
@@ -112,16 +197,20 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-quantize", action="store_true", help="skip the quantize lines")
+    ap.add_argument("--no-extra", action="store_true", help="only the systolic line (no quantize, LUT, attend)")
+    ap.add_argument("--copy-calibration", action="store_true", help="run only the counter-calibration copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the systolic path "
-              "shards over output columns with no exchange but a final gather; see the design notes)", file=sys.stderr)
+              "would shard over output columns with one final all-gather)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     import torch
 
-    import mxq
+    import mxq  # noqa: F401
     from mxq import block, matmul
     dev = torch.device("cuda", 0)
     M, N, K = 512, 4096, 4096
@@ -139,8 +228,10 @@ def main():
     t0 = time.perf_counter()
     ms = _events_ms(step, args.steps, s)
     wall = time.perf_counter() - t0
+    kms, launches = _kernel_ms(step, args.steps, "systolic_fast")
     macs = M * N * K
     gops = 2 * macs / (ms / 1e3) / 1e9
+    k_tops = 2 * macs / (kms / 1e3) / 1e12 if kms else None
     line = {
         "metric": METRIC, "value": round(gops, 2), "unit": "GOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -148,16 +239,23 @@ def main():
         "config": {"workload": "matmul.systolic MXGEMMINI HW_FINAL on block.mxgemmini MXFP8_E4M3 codes, "
                                "A = x^T (x 512x4096), B = W^T (W 4096x4096)", "M": M, "N": N, "K": K,
                    "emulated_macs_per_step": macs, "timed_wall_s": round(wall, 3)},
-        "roofline": {"bound": "valu", "achieved": round(gops / 1e3, 4), "peak": round(VALU_ROOF_TOPS, 3),
-                     "unit": "TOP/s", "frac": round(gops / 1e3 / VALU_ROOF_TOPS, 4),
+        "roofline": {"bound": "valu", "achieved": round(k_tops, 4) if k_tops else None,
+                     "peak": round(VALU_ROOF_TOPS, 3), "unit": "TOP/s",
+                     "frac": round(k_tops / VALU_ROOF_TOPS, 4) if k_tops else None,
                      "traffic": _traffic("systolic_fast_c2"),
-                     "note": "emulated ops (2 per MAC) per second over the systolic call's events; peak = 256 CUs x "
-                             "64 lanes x 2.4 GHz / 10 lane-ops per emulated MAC x 2"},
+                     "kernel": "k_systolic_fast<16, true>", "kernel_ms": round(kms, 4) if kms else None,
+                     "kernel_launches_timed": launches,
+                     "note": "VALU-bound emulation (neither HBM nor MFMA): achieved = 2 x 8,589,934,592 emulated "
+                             "MACs / the fast kernel's average duration; peak = 256 CUs x 64 lanes x 2.4 GHz / "
+                             "10 lane-ops per emulated MAC (the datapath's primitive count) x 2; the kernel "
+                             "spends about 8.3 VALU instructions per MAC, so frac can exceed 1"},
     }
-    if not args.no_quantize:
+    if not args.no_extra:
         line["quantize"] = quantize_lines(torch, max(5, args.steps // 2))
+        line["lut_c4"] = lut_line(torch, 3)
+        line["attend_c5"] = attend_line(torch, 3)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline_systolic(P_A, X_A, P_B, X_B, cols=32)
+        line["cpu_baseline"] = cpu_baseline_systolic(P_A, X_A, P_B, X_B, cols=160)
     print(json.dumps(line), flush=True)
 
 

@@ -66,6 +66,14 @@ typedef struct mxq_arith_spec {
 const char* mxq_last_error(void);
 int mxq_version(void);
 
+/* Kernel timing for measurement tools; no counterpart in the reference (the benchmark's roofline needs the
+ * dominant kernel's own duration, not the whole call's).  With mxq_timer_enable(1), every later launch of a
+ * timed kernel records a pair of HIP events on its stream.  mxq_timer_read waits for the pairs recorded under
+ * `kernel`, returns their summed milliseconds and their number, and forgets them.  Timed kernels:
+ * "systolic_fast", "systolic_general", "block_quantize", "lut_kmeans".  Not for use under graph capture. */
+int mxq_timer_enable(int32_t on);
+int mxq_timer_read(const char* kernel, double* total_ms, int64_t* launches);
+
 /* Fused block quantization: per block, amax -> scale X (step 1) -> z = block / X -> P = element rule (step 2).
  * V: (outer, n, inner) of type v_dtype; P: float32, same shape; X: float32 (outer, ceil(n/bs), inner).
  * The last block along n is zero-padded for the amax.

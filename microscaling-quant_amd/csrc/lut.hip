@@ -306,7 +306,10 @@ extern "C" int mxq_lut_tables(const float* P, int64_t K, int64_t n, int32_t grou
                                                                                      counts, err);
     if (int rc = mxq::check_launch("mxq_lut_tables histogram")) return rc;
   }
-  k_lut_kmeans<<<dim3((unsigned)ng), 64, 0, st>>>(counts, nv, grid, safe, ns, safe_order, max_iters, T);
+  {
+    mxq::KernelTimer timer("lut_kmeans", st);
+    k_lut_kmeans<<<dim3((unsigned)ng), 64, 0, st>>>(counts, nv, grid, safe, ns, safe_order, max_iters, T);
+  }
   return mxq::check_launch("mxq_lut_tables k-means");
 }
 

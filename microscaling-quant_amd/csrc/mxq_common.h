@@ -25,4 +25,19 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // One-dimensional grid of `threads` threads in blocks of `block`; grid.x caps at 2^31 - 1 blocks.
 inline dim3 grid_for(int64_t threads, int block) { return dim3((unsigned)ceil_div(threads, block)); }
 
+// While mxq_timer_enable(1) is in force, an object of this type brackets one kernel launch with a pair of
+// HIP events on the launch's stream, filed under `name` for mxq_timer_read.  Otherwise it does nothing.
+class KernelTimer {
+ public:
+  KernelTimer(const char* name, hipStream_t stream);
+  ~KernelTimer();
+  KernelTimer(const KernelTimer&) = delete;
+  KernelTimer& operator=(const KernelTimer&) = delete;
+
+ private:
+  const char* name_;
+  hipStream_t stream_;
+  hipEvent_t start_ = nullptr;
+};
+
 }  // namespace mxq

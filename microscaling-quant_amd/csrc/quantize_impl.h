@@ -269,6 +269,7 @@ inline int validate(const mxq_block_spec& s) {
 template <typename T, int ELEM, int MODE>
 int launch_quant(const T* V, float* P, float* X, int64_t outer, int64_t n, int64_t inner, int64_t bs,
                  const mxq_block_spec& q, hipStream_t st) {
+  mxq::KernelTimer timer("block_quantize", st);
   const int64_t nb = mxq::ceil_div(n, bs);
   const uintptr_t av = reinterpret_cast<uintptr_t>(V), ap = reinterpret_cast<uintptr_t>(P),
                   ax = reinterpret_cast<uintptr_t>(X);

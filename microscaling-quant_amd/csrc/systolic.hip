@@ -578,10 +578,15 @@ extern "C" int mxq_systolic(const float* P_A, const float* X_A, const float* P_B
     k_zero4<<<1, 64, 0, st>>>(workspace);
     k_stats<<<dim3((unsigned)sb, 4), 256, 0, st>>>(src, workspace);
     if (int rc = mxq::check_launch("mxq_systolic stats")) return rc;
-    launch_fast(size, lane_e[size - 1] == 8, grid_f, st, a, make_fast_lanes(lane_e, lane_m, size, *arith));
+    {
+      mxq::KernelTimer timer("systolic_fast", st);
+      launch_fast(size, lane_e[size - 1] == 8, grid_f, st, a, make_fast_lanes(lane_e, lane_m, size, *arith));
+    }
     if (int rc = mxq::check_launch("mxq_systolic fast")) return rc;
+    mxq::KernelTimer timer("systolic_general", st);
     k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a, 0);
   } else {
+    mxq::KernelTimer timer("systolic_general", st);
     k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a, 1);
   }
   return mxq::check_launch("mxq_systolic");

@@ -42,6 +42,8 @@ class ArithSpec(ctypes.Structure):
 SIGNATURES = {
     "mxq_last_error": (ctypes.c_char_p, []),
     "mxq_version": (c_i32, []),
+    "mxq_timer_enable": (c_i32, [c_i32]),
+    "mxq_timer_read": (c_i32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_i64)]),
     "mxq_block_quantize": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64,
                                    ctypes.POINTER(BlockSpec), c_ptr]),
     "mxq_block_dequantize": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr]),
@@ -140,3 +142,15 @@ def ew_prepare(x: torch.Tensor, dtype: torch.dtype):
     dev = compute_device(x)
     xd = to_device(x.detach(), dev).to(dtype).contiguous()
     return dev, xd
+
+
+def timer_enable(on: bool) -> None:
+    """Start (True) or stop timing the library's kernel launches with HIP events (see mxq_timer_enable)."""
+    run("mxq_timer_enable", 1 if on else 0)
+
+
+def timer_read(kernel: str):
+    """(summed milliseconds, launches) of the timed launches of `kernel` since the last read; waits for them."""
+    ms, n = ctypes.c_double(0.0), c_i64(0)
+    run("mxq_timer_read", kernel.encode(), ctypes.byref(ms), ctypes.byref(n))
+    return ms.value, n.value
