@@ -1,0 +1,141 @@
+"""The Python API's validation, on the CPU: every check runs before any device work, raising the exception type
+and message the reference's callers see (mxq/matmul/_common.py:8-29, mxq/element_quant/formats.py:50,
+float_em.py:40-49, block/ocp.py:39-40, block/lut.py:27, block/_driver.py:24-25, lut/kmeans.py:31-62,
+lut/formats.py:79-152, scheme.py:50-60, schedule.py:36-48, scale_factor.py:77, rounding/__init__.py:36-60).
+And without a GPU, a valid call fails loudly instead of computing anywhere else."""
+import os
+
+import pytest
+import torch
+
+import mxq
+from mxq import Scheme, block, lut, matmul, rounding, scale_factor, schedule
+from mxq.element_quant import float_em, formats, microsoft
+
+
+def _ops(K=64, M=3, N=4, nb=2):
+    return (torch.zeros(K, M), torch.ones(nb, M), torch.zeros(K, N), torch.ones(nb, N))
+
+
+def test_systolic_checks():
+    ar = matmul.MXGEMMINI()
+    P_A, X_A, P_B, X_B = _ops()
+    with pytest.raises(ValueError, match="must be 2-D"):
+        matmul.systolic(P_A[None], X_A, P_B, X_B, ar, matmul.HW_FINAL)
+    with pytest.raises(ValueError, match="contraction lengths differ"):
+        matmul.systolic(P_A, X_A, P_B[:32], X_B, ar, matmul.HW_FINAL)
+    with pytest.raises(ValueError, match="scales must be 2×3 and 2×4"):
+        matmul.systolic(P_A, X_A[:1], P_B, X_B, ar, matmul.HW_FINAL)
+    with pytest.raises(ValueError, match="must be float32"):
+        matmul.systolic(P_A.double(), X_A, P_B, X_B, ar, matmul.HW_FINAL)
+    with pytest.raises(ValueError, match="schedule has 15 rows"):
+        matmul.systolic(P_A, X_A, P_B, X_B, ar, matmul.HW_FINAL[:15])
+    with pytest.raises(ValueError, match="size 12 must divide block size 32"):
+        matmul.systolic(P_A, X_A, P_B, X_B, ar, [(4, 4)] * 12, 12)
+
+
+def test_formats_and_grids():
+    with pytest.raises(ValueError, match="Unknown format 'FP7'"):
+        formats.get("FP7")
+    assert formats.get("fp32") is None and formats.get("e4m3").name == "MXFP8_E4M3"
+    with pytest.raises(ValueError, match="rounding_mode must be one of"):
+        float_em.quantize(torch.zeros(3), 4, 3, rounding_mode="up")
+    with pytest.raises(ValueError, match="grid must be one of"):
+        float_em.quantize(torch.zeros(3), 4, 3, grid="posit")
+    with pytest.raises(ValueError, match="unsupported widths"):
+        float_em.quantize(torch.zeros(3), 9, 3)
+    with pytest.raises(ValueError, match="grid='ocp' is defined only"):
+        float_em.quantize(torch.zeros(3), 4, 4, grid="ocp")
+    with pytest.raises(ValueError, match="pass-through"):
+        microsoft.quantize(torch.zeros(3), "FP32")
+    with pytest.raises(ValueError, match="pass-through"):
+        scale_factor.ocp_no_clip(torch.ones(3), "FP32")
+
+
+def test_rounding_checks():
+    with pytest.raises(ValueError, match="keep must be in"):
+        rounding.round_bits(torch.zeros(3, dtype=torch.int64), 23, "rne")
+    with pytest.raises(ValueError, match="mode must be one of"):
+        rounding.round_bits(torch.zeros(3, dtype=torch.int64), 3, "odd")
+
+
+def test_block_checks():
+    V = torch.zeros(64, 8)
+    with pytest.raises(IndexError, match="axis 2 out of range"):
+        block.mxgemmini.quantize(V, "MXFP8_E4M3", axis=2)
+    with pytest.raises(ValueError, match="Unknown format"):
+        block.mxquant.quantize(V, "NOPE")
+    with pytest.raises(ValueError, match="placement must be one of"):
+        block.ocp.quantize(V, "MXFP8_E4M3", placement="middle")
+    with pytest.raises(ValueError, match="block.lut: V must be 2-D"):
+        block.lut.quantize(V[None], "MXFP6_E3M2", 0, 32, rounding_mode="rne", scale_floor=2.0 ** -23, group=1,
+                           max_iters=5)
+    with pytest.raises(ValueError, match="not a LUT format"):
+        block.lut.quantize(V, "MXFP4", 0, 32, rounding_mode="rne", scale_floor=2.0 ** -23, group=1, max_iters=5)
+
+
+def test_lut_checks():
+    with pytest.raises(ValueError, match="expects a K×n tensor"):
+        lut.tables(torch.zeros(3), "MXFP6_E3M2", group=0, max_iters=3)
+    with pytest.raises(ValueError, match="group -1 must be a non-negative integer"):
+        lut.tables(torch.zeros(4, 4), "MXFP6_E3M2", group=-1, max_iters=3)
+    with pytest.raises(ValueError, match="max_iters -2 must be a non-negative integer"):
+        lut.tables(torch.zeros(4, 4), "MXFP6_E3M2", group=0, max_iters=-2)
+    with pytest.raises(ValueError, match="is not an exact MXFP6_E3M2 value"):
+        lut.encode(torch.tensor([0.3]), "MXFP6_E3M2")
+    with pytest.raises(ValueError, match="need 2 tables, got 1"):
+        lut.finder(torch.zeros(4, 4, dtype=torch.int64), torch.zeros(1, 16), "MXFP6_E3M2", group=1)
+
+
+def test_scheme_and_schedule_checks(tmp_path):
+    q = lambda V: (V, torch.ones(1, V.shape[1]))                                       # noqa: E731
+    with pytest.raises(ValueError, match="rows 0 must be a positive integer"):
+        Scheme("s", a=q, b=q, reduce=None, rows=0)
+    with pytest.raises(ValueError, match="block_size True must be a positive integer"):
+        Scheme("s", a=q, b=q, reduce=None, block_size=True)
+    s = Scheme("s", a=q, b=q, reduce=lambda *ops: None)
+    with pytest.raises(ValueError, match="scale rows for K = 64"):
+        s.matmul(torch.zeros(64, 2), torch.zeros(64, 2))
+    p = tmp_path / "s.csv"
+    p.write_text("position,e,m\n0,4,4\n1,4,4\n")
+    assert schedule.load(str(p), rows=2) == [(4, 4), (4, 4)]
+    p.write_text("0,4,4\n0,4,5\n")
+    with pytest.raises(ValueError, match="position 0 given twice"):
+        schedule.load(str(p), rows=2)
+    p.write_text("0,4,4\n")
+    with pytest.raises(ValueError, match=r"missing positions \[1\]"):
+        schedule.load(str(p), rows=2)
+    p.write_text("0,4,4\n5,4,4\n")
+    with pytest.raises(ValueError, match="position 5 outside 0..1"):
+        schedule.load(str(p), rows=2)
+    assert schedule.fixed(4, 3, rows=3) == [(4, 3)] * 3
+    assert schedule.HW_FINAL == [(4, 4)] * 8 + [(4, 5)] * 2 + [(4, 6)] * 5 + [(8, 7)]
+
+
+def test_arithmetic_names():
+    assert matmul.MXGEMMINI().name == "mxgemmini(prod=e4m3)"
+    assert matmul.MXQUANT(4, 3).name == "mxquant(prod=e4m3)"
+    assert matmul.compiled(matmul.MXGEMMINI()).name.startswith("compiled(")
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour without a GPU")
+def test_no_gpu_fails_loudly():
+    """No CPU fallback: with no GPU every compute entry raises, naming the missing device."""
+    P_A, X_A, P_B, X_B = _ops()
+    calls = [lambda: block.mxgemmini.quantize(torch.randn(64, 8), "MXFP8_E4M3"),
+             lambda: matmul.systolic(P_A, X_A, P_B, X_B, matmul.MXGEMMINI(), matmul.HW_FINAL),
+             lambda: rounding.bf16(torch.randn(8)),
+             lambda: mxq.fp64_accum(P_A, X_A, P_B, X_B)]
+    for call in calls:
+        with pytest.raises(RuntimeError, match="no GPU"):
+            call()
+
+
+def test_product_does_not_import_the_oracle():
+    """The mxq package never reaches into oracle/ (test infrastructure only)."""
+    root = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "microscaling-quant_amd")
+    for dirpath, _, files in os.walk(root):
+        for f in files:
+            if f.endswith(".py"):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "import oracle" not in text and "from oracle" not in text, f

@@ -283,3 +283,36 @@ def test_scale_mxquant_properties():
     assert_bits_equal(X, want, "mxquant scale")
     H = nx.scale_mxquant(amax, 2.0 ** -23)
     assert (H >= F32(2.0 ** -23)).all()
+
+
+def test_compose_layout_invariants():
+    """Shapes, the zero-padded last block, P * expand(X) == dequantize, FP32 pass-through (X = 1, P = V), and
+    step 2 applied to V / X per block."""
+    V = (RNG.standard_normal((5, 70, 3)) * 3).astype(F32)
+    V[0, 64:, 0] = 100.0                                                    # the short last block's own amax
+    P, X = ob.compose(V, lambda a: nx.scale_mxquant(a), None, axis=1, block_size=32)
+    assert P.shape == V.shape and X.shape == (5, 3, 3)
+    amax_last = np.abs(V[:, 64:, :]).max(axis=1)
+    assert_bits_equal(X[:, 2, :], nx.scale_mxquant(amax_last), "last block scaled by its own 6 rows")
+    Xe = np.repeat(X, 32, axis=1)[:, :70, :]
+    assert_bits_equal(P, (V / Xe).astype(F32), "P = V / X without a step 2")
+    assert_bits_equal(ob.dequantize(P, X, axis=1), (P * Xe).astype(F32), "dequantize = P * expand(X)")
+    P1, X1 = ob.mxgemmini_quantize(V[0], None, 0)
+    assert_bits_equal(P1, V[0], "FP32 pass-through codes") and (X1 == 1).all()
+    P2, X2 = ob.mxquant_quantize(V[0], "MXFP8_E4M3", 0)
+    Xe2 = np.repeat(X2, 32, axis=0)[:70]
+    assert_bits_equal(P2, nx.float_em((V[0] / Xe2).astype(F32), 4, 3, "ties_away", "qtorch"), "mxquant = qtorch(V/X)")
+
+
+def test_scale_ocp_properties():
+    """shared = floor(log2 amax) - emax as an exponent (E8M0): NaN above 127, clamped at -127; amax 0 reads
+    the float32 minimum normal."""
+    amax = np.abs(np.concatenate([_random_finite_f32(20000, -140, 127), np.array([0.0], F32)]))
+    for emax in (8, 15, 2, 4):
+        X = nx.scale_ocp(amax, emax)
+        a = np.where(amax == 0, F32(2.0 ** -126), amax)
+        ex = np.frexp(a)[1] - 1
+        ex = np.where(nx.log2_f32(a) == ex + 1, ex + 1, ex) - emax
+        want = np.where(ex > 127, np.nan, np.ldexp(np.ones_like(a, dtype=F64), np.maximum(ex, -127))).astype(F32)
+        assert_bits_equal(X, want, f"scale_ocp emax={emax}")
+        assert_bits_equal(nx.scale_ocp_below_top(amax, emax + 1), X, "below_top is emax - 1")
