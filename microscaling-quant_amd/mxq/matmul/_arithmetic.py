@@ -21,6 +21,7 @@ for direct use and for reducers other than systolic.  An Arithmetic made by hand
 `compiled(arith)` returns the same Arithmetic under the name "compiled(...)": the HIP path is already one
 fused kernel per call, so there is nothing left for torch.compile to fuse (and no Triton is used).
 """
+import math
 from dataclasses import dataclass
 from typing import Callable, Hashable, Optional, Sequence, Tuple
 
@@ -72,53 +73,84 @@ def _canon(x: Tensor) -> Tensor:
     return torch.where(torch.isnan(x), torch.full_like(x, float("nan")), x)
 
 
+class _QtorchStages:
+    """MXQuant's rounding points: qtorch nearest (ties away) on the float32 product and on the float32 lane sum,
+    plain float32 block adds."""
+
+    def __init__(self, prod_e: int, prod_m: int):
+        float_em.check(prod_e, prod_m, "ties_away", "qtorch")
+        self.prod = (prod_e, prod_m)
+
+    @staticmethod
+    def _q(x: Tensor, e: int, m: int) -> Tensor:
+        return float_em.quantize(_canon(x), e, m, rounding_mode="ties_away", grid="qtorch")
+
+    def product(self, a: Tensor, b: Tensor) -> Tensor:
+        return self._q(a * b, *self.prod)
+
+    def acc_add(self, S: Tensor, p: Tensor, e: int, m: int) -> Tensor:
+        return self._q(S + p, e, m)
+
+    @staticmethod
+    def tile_add(C: Tensor, tile: Tensor) -> Tensor:
+        return C + tile
+
+
 def MXQUANT(prod_e: int, prod_m: int) -> Arithmetic:
-    """MXQuant's `_simulate_atw` datapath: qtorch "nearest" on the fp32 product, on the fp32 lane sum; fp32 block add."""
-    q = lambda x, e, m: float_em.quantize(_canon(x), e, m, rounding_mode="ties_away", grid="qtorch")  # noqa: E731
-    float_em.check(prod_e, prod_m, "ties_away", "qtorch")
-    return Arithmetic(
-        name=f"mxquant(prod=e{prod_e}m{prod_m})",
-        product=lambda a, b: q(a * b, prod_e, prod_m),
-        acc_add=lambda S, p, e, m: q(S + p, e, m),
-        tile_add=lambda C, tile: C + tile,
-        kernel=KernelArith(_lib.ARITH_MXQUANT, prod_e, prod_m),
-    )
+    """MXQuant's `_simulate_atw` datapath (mxq/matmul/_arithmetic.py:64-73)."""
+    st = _QtorchStages(prod_e, prod_m)
+    return Arithmetic(name=f"mxquant(prod=e{prod_e}m{prod_m})", product=st.product, acc_add=st.acc_add,
+                      tile_add=st.tile_add, kernel=KernelArith(_lib.ARITH_MXQUANT, prod_e, prod_m))
 
 
 def _saturation(prod_e: int, prod_m: int) -> Tuple[float, float]:
-    """(limit, value) of spike's product saturation (mx_fp_math.h:42-56): above max_normal -> sign * sat_val.
-    max_normal: e4m3 448 (mantissa 2^m - 2 at exponent b + 1), else 2^b * (2 - 2^-m);
-    sat_val: 2^(b + 1) * (1 + (2^m - 2) / 2^m); Inf when beyond float32."""
+    """(limit, value) of the chip model's product saturation (mxq/matmul/_arithmetic.py:88-102): a product above
+    `limit` becomes sign * `value`.  value = 2^(b+1) (2 - 2^(1-m)) (E4M3's 448), limit = value for E4M3 and the
+    IEEE largest normal 2^b (2 - 2^-m) otherwise; a value beyond float32 is Inf."""
     b = float_em.bias(prod_e)
-    fp8 = (prod_e, prod_m) == (4, 3)
-    limit = 2.0 ** (b + 1 if fp8 else b) * (1 + ((2 ** prod_m - 2) if fp8 else (2 ** prod_m - 1)) / 2 ** prod_m)
-    value = 2.0 ** (b + 1) * (1 + (2 ** prod_m - 2) / 2 ** prod_m)
-    if value > torch.finfo(torch.float32).max:
-        value = float("inf")
-    return limit, value
+    value = math.ldexp(2.0 - math.ldexp(1.0, 1 - prod_m), b + 1)
+    limit = value if (prod_e, prod_m) == (4, 3) else math.ldexp(2.0 - math.ldexp(1.0, -prod_m), b)
+    return limit, (value if value <= torch.finfo(torch.float32).max else math.inf)
 
 
 def _unsigned_zero(x: Tensor) -> Tensor:
-    """-0 becomes +0: spike's lane and bf16 roundings never return a negative zero."""
+    """-0 becomes +0: the chip model's lane and bf16 roundings never return a negative zero."""
     return torch.where(x == 0, torch.zeros_like(x), x)
 
 
+class _GemminiStages:
+    """MX-Gemmini's PE column: the product's significand truncated to prod_m bits, flushed below 2^prod_floor
+    (None: no flush), saturated; a lane add rounds both addends to the lane's float(e, m) (bf16 on the bit
+    pattern), adds exactly and rounds once; the block add is the same in bf16.  Zeros come out as +0."""
+
+    def __init__(self, prod_e: int, prod_m: int, prod_floor: Optional[int]):
+        self.prod_m, self.prod_floor = prod_m, prod_floor
+        self.limit, self.value = _saturation(prod_e, prod_m)
+
+    @staticmethod
+    def lane(x: Tensor, e: int, m: int) -> Tensor:
+        r = rounding.bf16(x) if (e, m) == (8, 7) else float_em.quantize(x, e, m, rounding_mode="rne", grid="ieee")
+        return _unsigned_zero(r)
+
+    def product(self, a: Tensor, b: Tensor) -> Tensor:
+        t = arith.truncate_significand(a * b, self.prod_m)
+        if self.prod_floor is not None:
+            t = arith.flush_product(t, self.prod_floor)
+        return arith.saturate(t, self.limit, self.value)
+
+    def acc_add(self, S: Tensor, p: Tensor, e: int, m: int) -> Tensor:
+        return arith.exact_add(self.lane(S, e, m), self.lane(p, e, m), e, m)
+
+    def tile_add(self, C: Tensor, tile: Tensor) -> Tensor:
+        return self.acc_add(C, tile, 8, 7)
+
+
 def MXGEMMINI(prod_e: int = 4, prod_m: int = 3, prod_floor: Optional[int] = PROD_FLOOR) -> Arithmetic:
-    """MX-Gemmini's PE column as spike computes it: product significand truncated to prod_m bits, flushed below
-    2^prod_floor (None: no flush), saturated; both addends rounded rne to the lane, added exactly, rounded once;
-    across blocks the same in bf16.  Every lane and bf16 rounding returns +0 for a zero."""
-    limit, value = _saturation(prod_e, prod_m)
-    rne = lambda x, e, m: (rounding.bf16(x) if (e, m) == (8, 7)                            # noqa: E731
-                           else float_em.quantize(x, e, m, rounding_mode="rne", grid="ieee"))
-    lane = lambda x, e, m: _unsigned_zero(rne(x, e, m))                                     # noqa: E731
-    flush = (lambda x: x) if prod_floor is None else (lambda x: arith.flush_product(x, prod_floor))
-    return Arithmetic(
-        name=f"mxgemmini(prod=e{prod_e}m{prod_m})",
-        product=lambda a, b: arith.saturate(flush(arith.truncate_significand(a * b, prod_m)), limit, value),
-        acc_add=lambda S, p, e, m: arith.exact_add(lane(S, e, m), lane(p, e, m), e, m),
-        tile_add=lambda C, tile: arith.exact_add(lane(C, 8, 7), lane(tile, 8, 7), 8, 7),
-        kernel=KernelArith(_lib.ARITH_MXGEMMINI, prod_e, prod_m, prod_floor, limit, value),
-    )
+    """MX-Gemmini's PE column as the chip's reference model computes it (mxq/matmul/_arithmetic.py:111-134)."""
+    st = _GemminiStages(prod_e, prod_m, prod_floor)
+    return Arithmetic(name=f"mxgemmini(prod=e{prod_e}m{prod_m})", product=st.product, acc_add=st.acc_add,
+                      tile_add=st.tile_add,
+                      kernel=KernelArith(_lib.ARITH_MXGEMMINI, prod_e, prod_m, prod_floor, st.limit, st.value))
 
 
 def compiled(arith_: Arithmetic) -> Arithmetic:
