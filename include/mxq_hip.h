@@ -90,13 +90,38 @@ int mxq_block_dequantize(const float* P, const float* X, float* out, int64_t out
  * (ceil(K/block_size) x M), X_B (ceil(K/block_size) x N), all float32 row-major.  Per block of K the scale map
  * X_A[g] (x) X_B[g]; per reduction of `size` k a fresh sum accumulated lane by lane (lane i has the format
  * (lane_e[i], lane_m[i]), host arrays of `size` entries), rescaled and added into C; K tails as the reference.
- * size must divide block_size and 32.  `workspace` is device memory of at least 16 bytes (operand statistics
- * that select the kernel on the device; the call makes no host synchronisation).  force_general = 1 skips the
- * fast kernel.  Replaces mxq/matmul/_systolic.py:23-62 with mxq/matmul/_arithmetic.py:64-134. */
+ * size must divide block_size and 32.  `workspace` is device memory of mxq_systolic_workspace(M, N, 1) uint32
+ * (which kernel computes each output tile is decided on the device; the call makes no host synchronisation).
+ * force_general = 1 skips the fast kernel.  Replaces mxq/matmul/_systolic.py:23-62 with
+ * mxq/matmul/_arithmetic.py:64-134. */
 int mxq_systolic(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C, int64_t K,
                  int64_t M, int64_t N, const int32_t* lane_e, const int32_t* lane_m, int32_t size,
                  int32_t block_size, const mxq_arith_spec* arith, uint32_t* workspace, int32_t force_general,
                  mxq_stream_t stream);
+
+/* Row strides (ld_*) and problem strides (batch_*) in elements: element (r, c) of problem z of an operand is
+ * at base + z * batch + r * ld + c. */
+typedef struct mxq_systolic_layout {
+  int64_t ld_a, batch_a;    /* codes A, K x M   */
+  int64_t ld_xa, batch_xa;  /* scales X_A, nb x M */
+  int64_t ld_b, batch_b;    /* codes B, K x N   */
+  int64_t ld_xb, batch_xb;  /* scales X_B, nb x N */
+  int64_t ld_c, batch_c;    /* C, M x N (problems may not overlap) */
+} mxq_systolic_layout;
+
+/* `count` independent systolic problems of one shape in one launch, operands addressed through `layout` (any
+ * column slice of a larger matrix, any spacing of the problems).  Each problem's result is bit-identical to
+ * mxq_systolic on that problem alone.  workspace: mxq_systolic_workspace(M, N, count) uint32.  The reference
+ * calls matmul.systolic once per problem (mxq/nn/_attention.py:108-141, once per head and query chunk);
+ * this is that loop as one launch. */
+int mxq_systolic_batched(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C,
+                         const mxq_systolic_layout* layout, int64_t count, int64_t K, int64_t M, int64_t N,
+                         const int32_t* lane_e, const int32_t* lane_m, int32_t size, int32_t block_size,
+                         const mxq_arith_spec* arith, uint32_t* workspace, int32_t force_general,
+                         mxq_stream_t stream);
+
+/* uint32 elements of workspace mxq_systolic / mxq_systolic_batched need (at least 1). */
+int64_t mxq_systolic_workspace(int64_t M, int64_t N, int64_t count);
 
 /* ---- MX-Gemmini look-up tables (K x n float32 block codes, one 16-entry table per 2^group columns) ------ */
 

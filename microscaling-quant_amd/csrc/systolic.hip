@@ -3,17 +3,17 @@
 //   for each block of K: scale map X_A[g] (x) X_B[g]
 //     for each reduction of `size` k: S = 0; S = acc_add(S, product(a_k, b_k), lane k % size)
 //       C = tile_add(C, S * scale)
-// Parallelism is over M x N only; nothing is split along K, so no summation order changes.  The work is
-// VALU (integer and float32 bit manipulation), not MFMA: the matrix cores' accumulation would not round
-// where the datapath does.
+// Parallelism is over M x N (and a batch of independent problems); nothing is split along K, so no summation
+// order changes.  The work is VALU (integer and float32 bit manipulation), not MFMA: the matrix cores'
+// accumulation would not round where the datapath does.
 //
-// Three kernels:
-//   k_stats         max |x| bit pattern of A, B, X_A and X_B (atomic max on the patterns of |x|: patterns of
-//                   non-negative floats order like their values; >= 0x7F800000 means Inf or NaN present)
+// Operands are strided and batched: element (r, c) of problem z of an operand sits at base + z*batch + r*ld + c.
+//
+// Two kernels, both launched:
 //   k_systolic_fast MXGEMMINI with size in {4, 8, 16, 32}, lanes (4, m <= 9) of non-decreasing m, optionally a
-//                   last (8, 7) lane, prod_m <= every e4 lane's m, when the stats show finite codes and scales,
-//                   max|a| < 2^100 and max|a| * max|b| <= 8.  A's rows are staged into LDS times 2^(6 + m) of
-//                   their lane, so an e4 lane works in units of its subnormal step 2^-(6+m):
+//                   last (8, 7) lane, prod_m <= every e4 lane's m (checked on the host).  A's rows are staged
+//                   into LDS times 2^(6 + m) of their lane, so an e4 lane works in units of its subnormal step
+//                   2^-(6+m):
 //                      p = rint(trunc(a' * b))      float32 multiply, mask the dropped significand bits,
 //                                                   round to an integer = lane(p) (the flush below
 //                                                   2^prod_floor is under half a step, so it is subsumed)
@@ -23,9 +23,12 @@
 //                   lane and the tile add are one float32 add of two values of at most 8 significant bits
 //                   followed by bit RNE to bf16, which equals the reference's exact add with one rounding
 //                   (double rounding through 24 bits is harmless for 8-bit operands: 24 >= 2*8 + 1).
-//   k_systolic_gen  every other case: the full per-step rule for any codes, any lanes (e <= 8), MXGEMMINI or
-//                   MXQUANT, NaN/Inf/saturation/overflow included.
-// Both compute kernels run; each reads the stats and returns at once unless the case is its own.
+//                   While it computes, each workgroup keeps the largest |a|, |b| and scale it has read.  Its
+//                   results are exact when those are finite, max|a| < 2^100 and max|a| * max|b| stays under
+//                   the ladder's overflow bound; then it writes its tile and a 0 flag, otherwise only a 1 flag.
+//   k_systolic_gen  the full per-step rule for any codes, any lanes (e <= 8), MXGEMMINI or MXQUANT, NaN, Inf,
+//                   saturation and overflow included.  After the fast kernel it computes only the tiles whose
+//                   flag is 1; alone (no fast case, or forced) it computes everything.
 #include <cmath>
 
 #include "mxq_common.h"
@@ -35,14 +38,21 @@ namespace {
 
 constexpr int kMaxLanes = 64;
 constexpr uint32_t kFastAMaxBits = 0x71800000u;   // 2^100: A's rows are staged times up to 2^15
+constexpr int FBN = 64;                           // the fast kernel's tile width (its height is 64 or 32)
+
+struct Operand {
+  const float* p;
+  int64_t ld;     // elements between rows
+  int64_t batch;  // elements between problems
+};
 
 struct SysArgs {
-  const float* A;   // K x M
-  const float* XA;  // nb x M
-  const float* B;   // K x N
-  const float* XB;  // nb x N
-  float* C;         // M x N
-  const uint32_t* stats;  // [max |A| bits, max |B| bits]
+  Operand A, XA, B, XB;   // A: K x M, XA: nb x M, B: K x N, XB: nb x N
+  float* C;
+  int64_t ldc, batch_c;   // C: M x N
+  uint32_t* flags;        // one per fast tile per problem (1: the general kernel computes it)
+  int64_t tiles_x, tiles_y;
+  int fbm;                // the fast kernel's tile height
   int64_t K, M, N;
   int size, block_size;
   mxq_arith_spec ar;
@@ -50,60 +60,6 @@ struct SysArgs {
   int8_t lane_m[kMaxLanes];
   float fast_prod_max;    // the fast kernel's bound on max|a| * max|b| (see fast_prod_bound)
 };
-
-// ---------------------------------------------------------------------------------------------- stats
-// stats[j] = max |x| bit pattern over A, B, X_A, X_B (j = 0..3): patterns of non-negative floats order like
-// their values, and >= 0x7F800000 means Inf or NaN is present.
-struct StatSrc {
-  const float* p[4];
-  int64_t n[4];
-};
-
-__global__ void k_zero4(uint32_t* s) {
-  if (threadIdx.x < 4) s[threadIdx.x] = 0u;
-}
-
-__global__ void __launch_bounds__(256) k_stats(const StatSrc src, uint32_t* out) {
-  __shared__ uint32_t red[4];
-  const int which = blockIdx.y;
-  const float* __restrict__ x = src.p[which];
-  const int64_t n = src.n[which];
-  uint32_t mx = 0u;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t n4 = (reinterpret_cast<uintptr_t>(x) % 16 == 0) ? n / 4 : 0;
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  for (int64_t i = gid; i < n4; i += stride) {
-    const float4 v = x4[i];
-    const uint32_t a = f2u(v.x) & 0x7FFFFFFFu, b = f2u(v.y) & 0x7FFFFFFFu, c = f2u(v.z) & 0x7FFFFFFFu,
-                   d = f2u(v.w) & 0x7FFFFFFFu;
-    const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
-    const uint32_t m4 = ab > cd ? ab : cd;
-    mx = m4 > mx ? m4 : mx;
-  }
-  for (int64_t i = n4 * 4 + gid; i < n; i += stride) {
-    const uint32_t u = f2u(x[i]) & 0x7FFFFFFFu;
-    mx = u > mx ? u : mx;
-  }
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)mx, off, 64);
-    mx = o > mx ? o : mx;
-  }
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t m = red[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) m = red[w] > m ? red[w] : m;
-    if (m) atomicMax(out + which, m);
-  }
-}
-
-// The fast kernel's case: finite codes and scales, max|a| < 2^100, max|a| * max|b| <= the lane bound.
-__device__ __forceinline__ bool fast_ok(const uint32_t* stats, float prod_max) {
-  const uint32_t ua = stats[0], ub = stats[1];
-  if (ua >= kFastAMaxBits || ub >= 0x7F800000u || stats[2] >= 0x7F800000u || stats[3] >= 0x7F800000u) return false;
-  return u2f(ua) * u2f(ub) <= prod_max;
-}
 
 // ------------------------------------------------------------------------------------- tile staging
 // Workgroup tile BM x BN outputs, K staged 32 rows at a time through LDS (two buffers).
@@ -115,27 +71,27 @@ struct Smem {
   float b[2][KT][BN];
 };
 
-// Load rows [k0, k0 + KT) x cols [c0, c0 + W) of a row-major R x L matrix into registers (zero outside).
+// Loads rows [k0, k0 + KT) x cols [c0, c0 + W) of an R x L matrix with row stride ld into registers (zero
+// outside the matrix).  vec_ok: ld and the base are multiples of 4 floats / 16 bytes.
 template <int W, int NT>
 struct TileLoader {
   static constexpr int PER = KT * W / NT;  // floats per thread
   float v[PER];
-  __device__ __forceinline__ void load(const float* __restrict__ src, int64_t R, int64_t L, int64_t k0, int64_t c0,
-                                       bool vec_ok) {
+  __device__ __forceinline__ void load(const float* __restrict__ src, int64_t ld, int64_t R, int64_t L, int64_t k0,
+                                       int64_t c0, bool vec_ok) {
     const int t = threadIdx.x;
     if (vec_ok) {
-      // PER / 4 float4 loads per thread: row = (t * 4 + j * NT * 4) / W
 #pragma unroll
       for (int j = 0; j < PER / 4; ++j) {
         const int e = (t + j * NT) * 4;
         const int r = e / W, c = e % W;
         const int64_t gr = k0 + r, gc = c0 + c;
         float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (gr < R && gc + 3 < L) q = *reinterpret_cast<const float4*>(src + gr * L + gc);
+        if (gr < R && gc + 3 < L) q = *reinterpret_cast<const float4*>(src + gr * ld + gc);
         else if (gr < R) {
-          if (gc < L) q.x = src[gr * L + gc];
-          if (gc + 1 < L) q.y = src[gr * L + gc + 1];
-          if (gc + 2 < L) q.z = src[gr * L + gc + 2];
+          if (gc < L) q.x = src[gr * ld + gc];
+          if (gc + 1 < L) q.y = src[gr * ld + gc + 1];
+          if (gc + 2 < L) q.z = src[gr * ld + gc + 2];
         }
         v[j * 4 + 0] = q.x; v[j * 4 + 1] = q.y; v[j * 4 + 2] = q.z; v[j * 4 + 3] = q.w;
       }
@@ -145,7 +101,7 @@ struct TileLoader {
         const int e = t + j * NT;
         const int r = e / W, c = e % W;
         const int64_t gr = k0 + r, gc = c0 + c;
-        v[j] = (gr < R && gc < L) ? src[gr * L + gc] : 0.0f;
+        v[j] = (gr < R && gc < L) ? src[gr * ld + gc] : 0.0f;
       }
     }
   }
@@ -165,7 +121,23 @@ struct TileLoader {
       }
     }
   }
+  // the largest |x| bit pattern among the staged values (patterns of non-negative floats order like values)
+  __device__ __forceinline__ uint32_t max_bits() const {
+    uint32_t mx = 0u;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const uint32_t u = f2u(v[j]) & 0x7FFFFFFFu;
+      mx = u > mx ? u : mx;
+    }
+    return mx;
+  }
 };
+
+__device__ __forceinline__ bool vec_ok(const Operand& o, const float* base) {
+  return o.ld % 4 == 0 && reinterpret_cast<uintptr_t>(base) % 16 == 0;
+}
+
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
 
 // ---------------------------------------------------------------------------------- fast datapath
 // Per-lane constants of the fast kernel, built on the host from the schedule (see make_fast_lanes).
@@ -182,24 +154,24 @@ struct FastLanes {
 
 // RNE of a float32 bit pattern at 7 fraction bits (bf16).  Finite values, infinities and the quiet NaNs the
 // ALU makes (0x7FC00000, 0xFFC00000) map as bf16_rne does; a NaN whose low 16 bits would carry is never
-// present here (codes and scales are finite, every NaN is produced by the ALU).
+// present (the workgroup's codes and scales are finite whenever its results are kept; every NaN is made by
+// the ALU).
 __device__ __forceinline__ float bf16_bits(float x) {
   const uint32_t u = f2u(x);
   return u2f((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
 }
 
-// Loads A's stage rows like TileLoader and scales each row by 2^a_exp[lane of the row] on the way to LDS.
-// A thread always stages the same rows of a stage (stages start at multiples of 32 and SIZE | 32), so the
-// exponents are fixed per thread.
+// Scales a thread's staged A rows by 2^a_exp[lane of the row] on the way to LDS.  A thread always stages the
+// same rows of a stage (stages start at multiples of 32 and SIZE | 32), so the exponents are fixed per thread.
 template <int W, int NT, int SIZE>
 struct ScaledRows {
   static constexpr int PER = KT * W / NT;
   int ex[PER];
-  __device__ __forceinline__ void init(const FastLanes& fl, bool vec_ok) {
+  __device__ __forceinline__ void init(const FastLanes& fl, bool vec) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const int e = vec_ok ? (t + (j / 4) * NT) * 4 + (j % 4) : t + j * NT;
+      const int e = vec ? (t + (j / 4) * NT) * 4 + (j % 4) : t + j * NT;
       ex[j] = fl.a_exp[(e / W) % SIZE];
     }
   }
@@ -209,17 +181,23 @@ struct ScaledRows {
   }
 };
 
-template <int SIZE, bool BF16_LAST>
+// BM = 64: 4 x 4 outputs per thread; BM = 32: 2 x 4, for problems with too few 64 x 64 tiles to fill the chip.
+template <int SIZE, bool BF16_LAST, int BM>
 __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const FastLanes fl) {
-  constexpr int BM = 64, BN = 64, TM = 4, TN = 4, NT = 256;
-  if (!fast_ok(args.stats, args.fast_prod_max)) return;
+  constexpr int BN = FBN, TM = BM / 16, TN = 4, NT = 256;
+  static_assert((BM / TM) * (BN / TN) == NT, "256 threads");
   __shared__ __align__(16) Smem<BM, BN> sm;
+  __shared__ uint32_t red[3][4];
   const int tn = threadIdx.x % (BN / TN), tm = threadIdx.x / (BN / TN);
+  const int64_t z = blockIdx.z;
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
-  const bool va = (args.M % 4 == 0) && (reinterpret_cast<uintptr_t>(args.A) % 16 == 0);
-  const bool vb = (args.N % 4 == 0) && (reinterpret_cast<uintptr_t>(args.B) % 16 == 0);
+  const float* A = args.A.p + z * args.A.batch;
+  const float* B = args.B.p + z * args.B.batch;
+  const float* XA = args.XA.p + z * args.XA.batch;
+  const float* XB = args.XB.p + z * args.XB.batch;
+  const bool va = vec_ok(args.A, A), vb = vec_ok(args.B, B);
   const int bs = args.block_size;
-  const int64_t K = args.K;
+  const int64_t K = args.K, M = args.M, N = args.N;
 
   float C[TM][TN];
 #pragma unroll
@@ -227,13 +205,16 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 #pragma unroll
     for (int y = 0; y < TN; ++y) C[x][y] = 0.0f;
 
+  uint32_t max_a = 0u, max_b = 0u, max_x = 0u;   // largest |a|, |b| and scale this thread has read
   TileLoader<BM, NT> la;
   TileLoader<BN, NT> lb;
   ScaledRows<BM, NT, SIZE> rows;
   rows.init(fl, va);
   int buf = 0;
-  la.load(args.A, K, args.M, 0, m0, va);
-  lb.load(args.B, K, args.N, 0, n0, vb);
+  la.load(A, args.A.ld, K, M, 0, m0, va);
+  lb.load(B, args.B.ld, K, N, 0, n0, vb);
+  max_a = umax(max_a, la.max_bits());
+  max_b = umax(max_b, lb.max_bits());
   rows.apply(la.v);
   la.store(sm.a[0], va);
   lb.store(sm.b[0], vb);
@@ -245,8 +226,8 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   for (int64_t k0 = 0; k0 < K; k0 += KT) {
     const bool more = k0 + KT < K;
     if (more) {
-      la.load(args.A, K, args.M, k0 + KT, m0, va);
-      lb.load(args.B, K, args.N, k0 + KT, n0, vb);
+      la.load(A, args.A.ld, K, M, k0 + KT, m0, va);
+      lb.load(B, args.B.ld, K, N, k0 + KT, n0, vb);
     }
     const int kend = (int)((K - k0 < KT) ? (K - k0) : KT);
     // rows past K are zero in LDS: their products are +0 and leave every lane's sum unchanged, so a short
@@ -257,12 +238,14 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 #pragma unroll
         for (int x = 0; x < TM; ++x) {
           const int64_t mm = m0 + tm * TM + x;
-          xa[x] = mm < args.M ? args.XA[g * args.M + mm] : 0.0f;
+          xa[x] = mm < M ? XA[g * args.XA.ld + mm] : 0.0f;
+          max_x = umax(max_x, f2u(xa[x]) & 0x7FFFFFFFu);
         }
 #pragma unroll
         for (int y = 0; y < TN; ++y) {
           const int64_t nn = n0 + tn * TN + y;
-          xb[y] = nn < args.N ? args.XB[g * args.N + nn] : 0.0f;
+          xb[y] = nn < N ? XB[g * args.XB.ld + nn] : 0.0f;
+          max_x = umax(max_x, f2u(xb[y]) & 0x7FFFFFFFu);
         }
 #pragma unroll
         for (int x = 0; x < TM; ++x)
@@ -276,14 +259,19 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
         for (int y = 0; y < TN; ++y) S[x][y] = 0.0f;
 #pragma unroll
       for (int i = 0; i < SIZE; ++i) {
-        const float4 a4 = *reinterpret_cast<const float4*>(&sm.a[buf][r0 + i][tm * TM]);
+        float a[TM];
+        if constexpr (TM == 4) {
+          const float4 a4 = *reinterpret_cast<const float4*>(&sm.a[buf][r0 + i][tm * TM]);
+          a[0] = a4.x; a[1] = a4.y; a[2] = a4.z; a[3] = a4.w;
+        } else {
+          const float2 a2 = *reinterpret_cast<const float2*>(&sm.a[buf][r0 + i][tm * TM]);
+          a[0] = a2.x; a[1] = a2.y;
+        }
         const float4 b4 = *reinterpret_cast<const float4*>(&sm.b[buf][r0 + i][tn * TN]);
-        const float a[TM] = {a4.x, a4.y, a4.z, a4.w};
         const float b[TN] = {b4.x, b4.y, b4.z, b4.w};
         if (BF16_LAST && i == SIZE - 1) {
           // bf16 lane: S (an e4 value, at most 8 significant bits) plus the truncated, flushed product
-          // (prod_m + 1 <= 8 bits), one float32 add and bit RNE to bf16: rounding an exact sum of two 8-bit
-          // precision values first to 24 bits and then to 8 equals rounding it once to 8 (24 >= 2*8 + 1).
+          // (prod_m + 1 <= 8 bits), one float32 add and bit RNE to bf16
 #pragma unroll
           for (int x = 0; x < TM; ++x)
 #pragma unroll
@@ -299,9 +287,7 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 #pragma unroll
               for (int y = 0; y < TN; ++y) S[x][y] *= fl.rescale[i];
           }
-          // e4 lane, in units of the lane's subnormal step 2^-(6+m): the truncated product rounded to an
-          // integer is lane(p); the sum is exact below 2^24; bit RNE at m fraction bits is the lane rounding
-          // (an identity under 2^m, the lane's subnormal range)
+          // e4 lane in units of the lane's subnormal step 2^-(6+m)
           const uint32_t half = fl.half_m1[i], mask = fl.lmask[i], d = fl.dsh[i];
 #pragma unroll
           for (int x = 0; x < TM; ++x)
@@ -319,7 +305,7 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 #pragma unroll
           for (int y = 0; y < TN; ++y) S[x][y] *= fl.out_scale;
       }
-      // tile_add: C (a bf16 value, never -0) plus bf16(S * scale), one rounding to bf16 (same argument)
+      // tile_add: C (a bf16 value, never -0) plus bf16(S * scale), one rounding to bf16
 #pragma unroll
       for (int x = 0; x < TM; ++x)
 #pragma unroll
@@ -331,6 +317,8 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
       }
     }
     if (more) {
+      max_a = umax(max_a, la.max_bits());
+      max_b = umax(max_b, lb.max_bits());
       rows.apply(la.v);
       la.store(sm.a[buf ^ 1], va);
       lb.store(sm.b[buf ^ 1], vb);
@@ -338,14 +326,37 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
     __syncthreads();
     buf ^= 1;
   }
+
+  // the workgroup's verdict: its maxima over everything it read
+  for (int off = 32; off > 0; off >>= 1) {
+    max_a = umax(max_a, (uint32_t)__shfl_xor((int)max_a, off, 64));
+    max_b = umax(max_b, (uint32_t)__shfl_xor((int)max_b, off, 64));
+    max_x = umax(max_x, (uint32_t)__shfl_xor((int)max_x, off, 64));
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[0][wave] = max_a;
+    red[1][wave] = max_b;
+    red[2][wave] = max_x;
+  }
+  __syncthreads();
+  const uint32_t wa = umax(umax(red[0][0], red[0][1]), umax(red[0][2], red[0][3]));
+  const uint32_t wb = umax(umax(red[1][0], red[1][1]), umax(red[1][2], red[1][3]));
+  const uint32_t wx = umax(umax(red[2][0], red[2][1]), umax(red[2][2], red[2][3]));
+  const bool ok = wa < kFastAMaxBits && wb < 0x7F800000u && wx < 0x7F800000u &&
+                  u2f(wa) * u2f(wb) <= args.fast_prod_max;
+  if (threadIdx.x == 0)
+    args.flags[(z * args.tiles_y + blockIdx.y) * args.tiles_x + blockIdx.x] = ok ? 0u : 1u;
+  if (!ok) return;
+  float* Cz = args.C + z * args.batch_c;
 #pragma unroll
   for (int x = 0; x < TM; ++x) {
     const int64_t mm = m0 + tm * TM + x;
-    if (mm >= args.M) continue;
+    if (mm >= M) continue;
 #pragma unroll
     for (int y = 0; y < TN; ++y) {
       const int64_t nn = n0 + tn * TN + y;
-      if (nn < args.N) args.C[mm * args.N + nn] = C[x][y];
+      if (nn < N) Cz[mm * args.ldc + nn] = C[x][y];
     }
   }
 }
@@ -364,16 +375,26 @@ __device__ __forceinline__ float gen_tile(float C, float tile, const mxq_arith_s
   return mxg_tile_add(C, tile);
 }
 
+// only_flagged: compute just the outputs whose fast tile has its flag set (the fast kernel ran first).
 template <int BM, int BN, int TM, int TN>
-__global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const SysArgs args, int force) {
+__global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const SysArgs args, int only_flagged) {
+  static_assert(32 % BM == 0 && FBN % BN == 0, "a general tile lies inside one fast tile");
   constexpr int NT = (BM / TM) * (BN / TN);
-  if (!force && fast_ok(args.stats, args.fast_prod_max)) return;
+  const int64_t z = blockIdx.z;
+  if (only_flagged) {
+    const int64_t fy = (int64_t)blockIdx.y * BM / args.fbm, fx = (int64_t)blockIdx.x * BN / FBN;
+    if (args.flags[(z * args.tiles_y + fy) * args.tiles_x + fx] == 0u) return;
+  }
   __shared__ Smem<BM, BN> sm;
   const int tn = threadIdx.x % (BN / TN), tm = threadIdx.x / (BN / TN);
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
-  const bool va = (args.M % 4 == 0) && (reinterpret_cast<uintptr_t>(args.A) % 16 == 0);
-  const bool vb = (args.N % 4 == 0) && (reinterpret_cast<uintptr_t>(args.B) % 16 == 0);
+  const float* A = args.A.p + z * args.A.batch;
+  const float* B = args.B.p + z * args.B.batch;
+  const float* XA = args.XA.p + z * args.XA.batch;
+  const float* XB = args.XB.p + z * args.XB.batch;
+  const bool va = vec_ok(args.A, A), vb = vec_ok(args.B, B);
   const int size = args.size, bs = args.block_size;
+  const int64_t K = args.K, M = args.M, N = args.N;
   float C[TM][TN];
 #pragma unroll
   for (int x = 0; x < TM; ++x)
@@ -381,41 +402,40 @@ __global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const Sy
     for (int y = 0; y < TN; ++y) C[x][y] = 0.0f;
   TileLoader<BM, NT> la;
   TileLoader<BN, NT> lb;
-  const int64_t K = args.K;
   int buf = 0;
-  la.load(args.A, K, args.M, 0, m0, va);
-  lb.load(args.B, K, args.N, 0, n0, vb);
+  la.load(A, args.A.ld, K, M, 0, m0, va);
+  lb.load(B, args.B.ld, K, N, 0, n0, vb);
   la.store(sm.a[0], va);
   lb.store(sm.b[0], vb);
   __syncthreads();
   float scale[TM][TN];
+  int in_block = 0;
+  int64_t g = 0;
   for (int64_t k0 = 0; k0 < K; k0 += KT) {
     const bool more = k0 + KT < K;
     if (more) {
-      la.load(args.A, K, args.M, k0 + KT, m0, va);
-      lb.load(args.B, K, args.N, k0 + KT, n0, vb);
+      la.load(A, args.A.ld, K, M, k0 + KT, m0, va);
+      lb.load(B, args.B.ld, K, N, k0 + KT, n0, vb);
     }
     const int kend = (int)((K - k0 < KT) ? (K - k0) : KT);
     for (int r0 = 0; r0 < kend; r0 += size) {
-      const int64_t kb = k0 + r0;
-      if (kb % bs == 0) {
-        const int64_t g = kb / bs;
+      if (in_block == 0) {
 #pragma unroll
         for (int x = 0; x < TM; ++x) {
           const int64_t mm = m0 + tm * TM + x;
-          const float xa = mm < args.M ? args.XA[g * args.M + mm] : 0.0f;
+          const float xa = mm < M ? XA[g * args.XA.ld + mm] : 0.0f;
 #pragma unroll
           for (int y = 0; y < TN; ++y) {
             const int64_t nn = n0 + tn * TN + y;
-            const float xb = nn < args.N ? args.XB[g * args.N + nn] : 0.0f;
+            const float xb = nn < N ? XB[g * args.XB.ld + nn] : 0.0f;
             scale[x][y] = xa * xb;
           }
         }
       }
-      const int64_t blk_end = (kb / bs + 1) * bs;
+      // the reduction ends at its size, the block's end or K's end, whichever is first
       int cnt = size;
-      if (kb + cnt > blk_end) cnt = (int)(blk_end - kb);
-      if (kb + cnt > K) cnt = (int)(K - kb);
+      if (in_block + cnt > bs) cnt = bs - in_block;
+      if (k0 + r0 + cnt > K) cnt = (int)(K - k0 - r0);
       float S[TM][TN];
 #pragma unroll
       for (int x = 0; x < TM; ++x)
@@ -438,6 +458,11 @@ __global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const Sy
       for (int x = 0; x < TM; ++x)
 #pragma unroll
         for (int y = 0; y < TN; ++y) C[x][y] = gen_tile(C[x][y], S[x][y] * scale[x][y], args.ar);
+      in_block += size;
+      if (in_block >= bs) {
+        in_block = 0;
+        ++g;
+      }
     }
     if (more) {
       la.store(sm.a[buf ^ 1], va);
@@ -446,18 +471,20 @@ __global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const Sy
     __syncthreads();
     buf ^= 1;
   }
+  float* Cz = args.C + z * args.batch_c;
 #pragma unroll
   for (int x = 0; x < TM; ++x) {
     const int64_t mm = m0 + tm * TM + x;
-    if (mm >= args.M) continue;
+    if (mm >= M) continue;
 #pragma unroll
     for (int y = 0; y < TN; ++y) {
       const int64_t nn = n0 + tn * TN + y;
-      if (nn < args.N) args.C[mm * args.N + nn] = C[x][y];
+      if (nn < N) Cz[mm * args.ldc + nn] = C[x][y];
     }
   }
 }
 
+// ------------------------------------------------------------------------------------------- host side
 // A bound on |product| under which no e4 lane can overflow: with n e4 lanes of at least m_min fraction bits,
 // a rounding in the normal range grows a value by a factor of at most 1 + u, u = 2^-(m_min+1), and one in the
 // lane's subnormal range by at most 2^-7 absolute, so |S_k| <= P n (1 + u)^(n+1) + n 2^-7; the lanes stay
@@ -519,8 +546,13 @@ FastLanes make_fast_lanes(const int32_t* e, const int32_t* m, int size, const mx
 
 template <int SIZE>
 void launch_fast_size(bool bf16_last, dim3 grid, hipStream_t st, const SysArgs& a, const FastLanes& fl) {
-  if (bf16_last) k_systolic_fast<SIZE, true><<<grid, 256, 0, st>>>(a, fl);
-  else k_systolic_fast<SIZE, false><<<grid, 256, 0, st>>>(a, fl);
+  if (a.fbm == 64) {
+    if (bf16_last) k_systolic_fast<SIZE, true, 64><<<grid, 256, 0, st>>>(a, fl);
+    else k_systolic_fast<SIZE, false, 64><<<grid, 256, 0, st>>>(a, fl);
+  } else {
+    if (bf16_last) k_systolic_fast<SIZE, true, 32><<<grid, 256, 0, st>>>(a, fl);
+    else k_systolic_fast<SIZE, false, 32><<<grid, 256, 0, st>>>(a, fl);
+  }
 }
 
 void launch_fast(int size, bool bf16_last, dim3 grid, hipStream_t st, const SysArgs& a, const FastLanes& fl) {
@@ -532,13 +564,55 @@ void launch_fast(int size, bool bf16_last, dim3 grid, hipStream_t st, const SysA
   }
 }
 
-bool lanes_valid(const int32_t* e, const int32_t* m, int size, int kind) {
+bool lanes_valid(const int32_t* e, const int32_t* m, int size) {
   for (int i = 0; i < size; ++i) {
     const bool ok = (e[i] == 8 && m[i] == 23) || (e[i] >= 1 && e[i] <= 8 && m[i] >= 1 && m[i] <= 22);
     if (!ok) return false;
   }
-  (void)kind;
   return true;
+}
+
+int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane_m, int64_t count,
+                 int32_t force_general, hipStream_t st) {
+  const mxq_arith_spec& ar = base.ar;
+  SysArgs a = base;
+  for (int i = 0; i < a.size; ++i) { a.lane_e[i] = (int8_t)lane_e[i]; a.lane_m[i] = (int8_t)lane_m[i]; }
+  a.tiles_x = mxq::ceil_div(a.N, FBN);
+  // 64-row tiles while they give every CU at least 8 workgroups, else 32-row tiles (twice the waves)
+  a.fbm = (mxq::ceil_div(a.M, 64) * a.tiles_x * count >= 8 * 256) ? 64 : 32;
+  a.tiles_y = mxq::ceil_div(a.M, a.fbm);
+  a.fast_prod_max = 0.0f;
+  const bool fast_lanes = !force_general && a.K > 0 && lanes_fast(lane_e, lane_m, a.size, ar);
+  const dim3 grid_f((unsigned)a.tiles_x, (unsigned)a.tiles_y, (unsigned)count);
+  const dim3 grid_g((unsigned)mxq::ceil_div(a.N, 32), (unsigned)mxq::ceil_div(a.M, 32), (unsigned)count);
+  if (fast_lanes) {
+    a.fast_prod_max = fast_prod_bound(lane_e, lane_m, a.size);
+    {
+      mxq::KernelTimer timer("systolic_fast", st);
+      launch_fast(a.size, lane_e[a.size - 1] == 8, grid_f, st, a, make_fast_lanes(lane_e, lane_m, a.size, ar));
+    }
+    if (int rc = mxq::check_launch("mxq_systolic fast")) return rc;
+    mxq::KernelTimer timer("systolic_general", st);
+    k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a, 1);
+  } else {
+    mxq::KernelTimer timer("systolic_general", st);
+    k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a, 0);
+  }
+  return mxq::check_launch("mxq_systolic");
+}
+
+int check_common(int64_t K, int64_t M, int64_t N, int64_t count, const int32_t* lane_e, const int32_t* lane_m,
+                 int32_t size, int32_t block_size, const mxq_arith_spec* arith) {
+  if (!arith || !lane_e || !lane_m) return mxq::invalid("mxq_systolic: NULL spec or lanes");
+  if (K < 0 || M < 0 || N < 0 || count < 0) return mxq::invalid("mxq_systolic: negative shape");
+  if (mxq::ceil_div(M, 32) > 65535 || count > 65535) return mxq::invalid("mxq_systolic: M or batch too large");
+  if (size < 1 || size > kMaxLanes) return mxq::invalid("mxq_systolic: size must be in [1, 64]");
+  if (block_size < 1 || block_size % size) return mxq::invalid("mxq_systolic: size must divide block_size");
+  if (KT % size) return mxq::invalid("mxq_systolic: size must divide 32");
+  if (arith->kind != MXQ_ARITH_MXGEMMINI && arith->kind != MXQ_ARITH_MXQUANT)
+    return mxq::invalid("mxq_systolic: bad arithmetic");
+  if (!lanes_valid(lane_e, lane_m, size)) return mxq::invalid("mxq_systolic: unsupported lane widths");
+  return MXQ_OK;
 }
 
 }  // namespace
@@ -547,47 +621,41 @@ extern "C" int mxq_systolic(const float* P_A, const float* X_A, const float* P_B
                             int64_t K, int64_t M, int64_t N, const int32_t* lane_e, const int32_t* lane_m,
                             int32_t size, int32_t block_size, const mxq_arith_spec* arith, uint32_t* workspace,
                             int32_t force_general, mxq_stream_t stream) {
-  if (!arith || !lane_e || !lane_m) return mxq::invalid("mxq_systolic: NULL spec or lanes");
-  if (K < 0 || M < 0 || N < 0) return mxq::invalid("mxq_systolic: negative shape");
-  if (size < 1 || size > kMaxLanes) return mxq::invalid("mxq_systolic: size must be in [1, 64]");
-  if (block_size < 1 || block_size % size) return mxq::invalid("mxq_systolic: size must divide block_size");
-  if (KT % size) return mxq::invalid("mxq_systolic: size must divide 32");
-  if (arith->kind != MXQ_ARITH_MXGEMMINI && arith->kind != MXQ_ARITH_MXQUANT) return mxq::invalid("mxq_systolic: bad arithmetic");
-  if (!lanes_valid(lane_e, lane_m, size, arith->kind)) return mxq::invalid("mxq_systolic: unsupported lane widths");
+  if (int rc = check_common(K, M, N, 1, lane_e, lane_m, size, block_size, arith)) return rc;
   if (M == 0 || N == 0) return MXQ_OK;
   if (!P_A || !X_A || !P_B || !X_B || !C || !workspace) return mxq::invalid("mxq_systolic: NULL pointer");
-  hipStream_t st = mxq::as_stream(stream);
-
   SysArgs a{};
-  a.A = P_A; a.XA = X_A; a.B = P_B; a.XB = X_B; a.C = C; a.stats = workspace;
+  a.A = {P_A, M, 0}; a.XA = {X_A, M, 0}; a.B = {P_B, N, 0}; a.XB = {X_B, N, 0};
+  a.C = C; a.ldc = N; a.batch_c = 0; a.flags = workspace;
   a.K = K; a.M = M; a.N = N; a.size = size; a.block_size = block_size; a.ar = *arith;
-  for (int i = 0; i < size; ++i) { a.lane_e[i] = (int8_t)lane_e[i]; a.lane_m[i] = (int8_t)lane_m[i]; }
-  a.fast_prod_max = 0.0f;
+  return run_systolic(a, lane_e, lane_m, 1, force_general, mxq::as_stream(stream));
+}
 
-  const bool fast_lanes = !force_general && K > 0 && lanes_fast(lane_e, lane_m, size, *arith);
-  const dim3 grid_f((unsigned)mxq::ceil_div(N, 64), (unsigned)mxq::ceil_div(M, 64));
-  const dim3 grid_g((unsigned)mxq::ceil_div(N, 32), (unsigned)mxq::ceil_div(M, 32));
-  if (fast_lanes) {
-    a.fast_prod_max = fast_prod_bound(lane_e, lane_m, size);
-    // statistics decide on the device between the fast and the general kernel; each exits unless it is chosen
-    const int64_t nb = mxq::ceil_div(K, block_size);
-    StatSrc src{{P_A, P_B, X_A, X_B}, {K * M, K * N, nb * M, nb * N}};
-    const int64_t most = K * (M > N ? M : N);
-    int64_t sb = mxq::ceil_div(most / 4 + 1, 256);
-    sb = sb < 2048 ? sb : 2048;
-    k_zero4<<<1, 64, 0, st>>>(workspace);
-    k_stats<<<dim3((unsigned)sb, 4), 256, 0, st>>>(src, workspace);
-    if (int rc = mxq::check_launch("mxq_systolic stats")) return rc;
-    {
-      mxq::KernelTimer timer("systolic_fast", st);
-      launch_fast(size, lane_e[size - 1] == 8, grid_f, st, a, make_fast_lanes(lane_e, lane_m, size, *arith));
-    }
-    if (int rc = mxq::check_launch("mxq_systolic fast")) return rc;
-    mxq::KernelTimer timer("systolic_general", st);
-    k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a, 0);
-  } else {
-    mxq::KernelTimer timer("systolic_general", st);
-    k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a, 1);
-  }
-  return mxq::check_launch("mxq_systolic");
+extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const float* P_B, const float* X_B,
+                                    float* C, const mxq_systolic_layout* layout, int64_t count, int64_t K,
+                                    int64_t M, int64_t N, const int32_t* lane_e, const int32_t* lane_m, int32_t size,
+                                    int32_t block_size, const mxq_arith_spec* arith, uint32_t* workspace,
+                                    int32_t force_general, mxq_stream_t stream) {
+  if (int rc = check_common(K, M, N, count, lane_e, lane_m, size, block_size, arith)) return rc;
+  if (!layout) return mxq::invalid("mxq_systolic_batched: NULL layout");
+  const mxq_systolic_layout& L = *layout;
+  if (L.ld_a < M || L.ld_b < N || L.ld_xa < M || L.ld_xb < N || L.ld_c < N)
+    return mxq::invalid("mxq_systolic_batched: a row stride is shorter than its row");
+  if (L.batch_a < 0 || L.batch_b < 0 || L.batch_xa < 0 || L.batch_xb < 0 || L.batch_c < 0)
+    return mxq::invalid("mxq_systolic_batched: negative batch stride");
+  if (count > 1 && M > 0 && N > 0 && L.batch_c < (M - 1) * L.ld_c + N)
+    return mxq::invalid("mxq_systolic_batched: outputs of two problems overlap");
+  if (M == 0 || N == 0 || count == 0) return MXQ_OK;
+  if (!P_A || !X_A || !P_B || !X_B || !C || !workspace) return mxq::invalid("mxq_systolic_batched: NULL pointer");
+  SysArgs a{};
+  a.A = {P_A, L.ld_a, L.batch_a}; a.XA = {X_A, L.ld_xa, L.batch_xa};
+  a.B = {P_B, L.ld_b, L.batch_b}; a.XB = {X_B, L.ld_xb, L.batch_xb};
+  a.C = C; a.ldc = L.ld_c; a.batch_c = L.batch_c; a.flags = workspace;
+  a.K = K; a.M = M; a.N = N; a.size = size; a.block_size = block_size; a.ar = *arith;
+  return run_systolic(a, lane_e, lane_m, count, force_general, mxq::as_stream(stream));
+}
+
+extern "C" int64_t mxq_systolic_workspace(int64_t M, int64_t N, int64_t count) {
+  if (M <= 0 || N <= 0 || count <= 0) return 1;
+  return mxq::ceil_div(M, 32) * mxq::ceil_div(N, FBN) * count;   // the smaller of the two fast tiles
 }

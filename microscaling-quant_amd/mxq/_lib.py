@@ -38,6 +38,12 @@ class ArithSpec(ctypes.Structure):
                 ("sat_limit", c_f32), ("sat_value", c_f32)]
 
 
+class SystolicLayout(ctypes.Structure):
+    """mxq_systolic_layout (include/mxq_hip.h): row and problem strides of the five operands, in elements."""
+    _fields_ = [(n, c_i64) for n in ("ld_a", "batch_a", "ld_xa", "batch_xa", "ld_b", "batch_b", "ld_xb", "batch_xb",
+                                     "ld_c", "batch_c")]
+
+
 # exported symbol -> (restype, argtypes); every symbol include/mxq_hip.h declares
 SIGNATURES = {
     "mxq_last_error": (ctypes.c_char_p, []),
@@ -49,6 +55,10 @@ SIGNATURES = {
     "mxq_block_dequantize": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr]),
     "mxq_systolic": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,
                              ctypes.POINTER(ArithSpec), c_ptr, c_i32, c_ptr]),
+    "mxq_systolic_batched": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, ctypes.POINTER(SystolicLayout), c_i64,
+                                     c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32, ctypes.POINTER(ArithSpec),
+                                     c_ptr, c_i32, c_ptr]),
+    "mxq_systolic_workspace": (c_i64, [c_i64, c_i64, c_i64]),
     "mxq_lut_tables": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr,
                                c_ptr]),
     "mxq_lut_pick": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr]),

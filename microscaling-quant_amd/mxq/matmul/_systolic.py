@@ -57,11 +57,43 @@ def systolic(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: torch
     import ctypes
     le = (ctypes.c_int32 * size)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
-    work = torch.empty(4, dtype=torch.int32, device=dev)
+    work = torch.empty(workspace_elements(M, N, 1), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_systolic", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, le, lm, size, block_size,
                  kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))
     return _lib.back(C, P_A)
+
+
+def workspace_elements(M: int, N: int, count: int) -> int:
+    """int32 elements of device workspace a systolic launch of `count` M x N problems needs."""
+    return int(_lib.load().mxq_systolic_workspace(M, N, count))
+
+
+def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: int, N: int, C: torch.Tensor,
+                     arith: Arithmetic, schedule: Sequence[Tuple[int, int]], size: int = 16,
+                     block_size: int = BLOCK) -> None:
+    """`count` problems of one shape in one launch, written into C (mxq_systolic_batched).  ops: the four
+    device tensors the layout's strides address (codes A, scales X_A, codes B, scales X_B), float32 on C's
+    device.  Each problem's result equals systolic() on that problem alone.  The Arithmetic must carry a
+    kernel description (MXGEMMINI, MXQUANT, compiled)."""
+    import ctypes
+    kernel = getattr(arith, "kernel", None)
+    if kernel is None or size > 64 or 32 % size != 0 or block_size % size != 0:
+        raise ValueError("systolic_batched needs a kernel Arithmetic and size dividing 32 and block_size")
+    check_schedule(schedule, size)
+    if count == 0 or M == 0 or N == 0:
+        return
+    if K > 0:
+        _lanes_check(kernel, schedule, min(size, K))
+    dev = C.device
+    if any(t.device != dev or t.dtype != torch.float32 for t in ops) or C.dtype != torch.float32:
+        raise ValueError("codes, scales and C must be float32 on one device")
+    le = (ctypes.c_int32 * size)(*[int(e) for e, _ in schedule])
+    lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
+    work = torch.empty(workspace_elements(M, N, count), dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.run("mxq_systolic_batched", *(_lib.ptr(t) for t in ops), _lib.ptr(C), ctypes.byref(layout), count,
+                 K, M, N, le, lm, size, block_size, kernel.ctype(), _lib.ptr(work), 0, _lib.stream(dev))
 
 
 def _reference_loop(P_A, X_A, P_B, X_B, arith, schedule, size, block_size, K, M, N):

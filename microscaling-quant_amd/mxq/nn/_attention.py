@@ -23,6 +23,7 @@ P V then runs over the same key blocks, provided P is exactly zero on every key 
 all keys.  Outside keys contribute whole all-zero blocks, which add nothing to any reducer's tile sum.
 """
 from dataclasses import dataclass
+from functools import partial
 from typing import Iterator, Optional, Tuple
 
 import torch
@@ -109,52 +110,250 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[tor
     step = chunk or max(rows, ELEMENTS_PER_STEP // (dims.group * dims.Tk) // rows * rows)
     rnd = rounder(vector)
     out = q.new_empty(dims.B, dims.Tq, dims.H, dims.D)
+    bias = None                                                                   # Bm x Tq x Tk, Bm = 1 or B
+    if mask is not None:
+        bias = mask[:, 0, :, :dims.Tk].to(torch.float32)
+        bias = bias.expand(bias.shape[0], dims.Tq, dims.Tk) if bias.shape[1] == 1 else bias
+    batch = _Batched.of(qk, pv, q)
+    if batch is not None:
+        batch.run(q, k, v, bias, scale, step, vector, rnd, dims, out)
+        return out
     for b in range(dims.B):
-        bias = None
-        if mask is not None:
-            bias = mask[b if mask.shape[0] > 1 else 0, 0, :, :dims.Tk].to(torch.float32)
-            bias = bias.expand(dims.Tq, dims.Tk) if bias.shape[0] == 1 else bias
+        bias_b = None if bias is None else bias[b if bias.shape[0] > 1 else 0]
         for h in range(dims.Hkv):
-            _one_kv_head(q[b], k[b, h], v[b, h], bias, scale, qk, pv, step, rows, vector, rnd, dims,
-                         range(h * dims.group, (h + 1) * dims.group), out[b])
+            ops = _KVOperands.quantize(k[b, h], v[b, h], qk, pv, bias_b is not None)
+            for hs, s0, e0 in _calls(range(h * dims.group, (h + 1) * dims.group), dims.Tq, step, rows):
+                _one_call(q[b], ops, bias_b, scale, qk, pv, vector, rnd, dims, hs, s0, e0, out[b])
     return out
 
 
-def _one_kv_head(q_b, k_h, v_h, bias, scale, qk: Scheme, pv: Scheme, step, rows, vector, rnd, dims: _Dims,
-                 heads: range, out_b):
+@dataclass
+class _KVOperands:
+    """One KV head's quantized K^T (D x Tk) and V (Tk x D), and K's per-row code maxima for the skip bound."""
+    KT_P: torch.Tensor
+    KT_X: torch.Tensor
+    V_P: torch.Tensor
+    V_X: torch.Tensor
+    k_amax: Optional[torch.Tensor]
+
+    @staticmethod
+    def quantize(k_h, v_h, qk: Scheme, pv: Scheme, masked: bool) -> "_KVOperands":
+        KT_P, KT_X = qk.b(k_h.to(torch.float32).t().contiguous())
+        V_P, V_X = pv.b(v_h.to(torch.float32).contiguous())
+        return _KVOperands.checked(KT_P, KT_X, V_P, V_X, qk, pv, masked)
+
+    @staticmethod
+    def checked(KT_P, KT_X, V_P, V_X, qk: Scheme, pv: Scheme, masked: bool) -> "_KVOperands":
+        qk.check_scales(KT_X, KT_P.shape[0], "b (Kᵀ)")
+        pv.check_scales(V_X, V_P.shape[0], "b (V)")
+        return _KVOperands(KT_P, KT_X, V_P, V_X, _code_amax(KT_P, KT_X, qk.block_size) if masked else None)
+
+
+def _one_call(q_b, ops: _KVOperands, bias, scale, qk: Scheme, pv: Scheme, vector, rnd, dims: _Dims, hs: range,
+              s0: int, e0: int, out_b) -> None:
+    """One call of the reference's loop: query heads hs, queries [s0, e0) against one KV head."""
     Tk, D = dims.Tk, dims.D
-    KT_P, KT_X = qk.b(k_h.to(torch.float32).t().contiguous())                    # D x Tk
-    V_P, V_X = pv.b(v_h.to(torch.float32).contiguous())                          # Tk x D
-    qk.check_scales(KT_X, D, "b (Kᵀ)")
-    pv.check_scales(V_X, Tk, "b (V)")
-    k_amax = _code_amax(KT_P, KT_X, qk.block_size) if bias is not None else None
     bv = pv.block_size
-    tiny = torch.finfo(torch.float32).tiny
-    for hs, s0, e0 in _calls(heads, dims.Tq, step, rows):
-        n, m = len(hs), e0 - s0
-        Q_T = q_b[hs.start:hs.stop, s0:e0].to(torch.float32).reshape(n * m, D).t().contiguous()
-        A_P, A_X = qk.a(Q_T)
-        lo, hi = 0, Tk
-        rows_bias = None
+    n, m = len(hs), e0 - s0
+    Q_T = q_b[hs.start:hs.stop, s0:e0].to(torch.float32).reshape(n * m, D).t().contiguous()
+    A_P, A_X = qk.a(Q_T)
+    lo, hi = 0, Tk
+    rows_bias = None
+    if bias is not None:
+        rows_bias = bias[s0:e0]                                                   # m x Tk
+        bound = SLACK * abs(scale) * float((_code_amax(A_P, A_X, qk.block_size) * ops.k_amax).sum())
+        lo, hi = _live_span(rows_bias, max(bound, torch.finfo(torch.float32).tiny), bv)
+    S_live = rnd(qk.reduce(A_P, A_X, ops.KT_P[:, lo:hi], ops.KT_X[:, lo:hi]) * scale)   # n*m x (hi - lo)
+    if rows_bias is not None:
+        S_live = rnd(S_live.view(n, m, hi - lo) + rows_bias[:, lo:hi]).view(n * m, hi - lo)
+    if hi - lo == Tk:
+        S = S_live
+    else:
+        S = rnd(rows_bias).repeat(n, 1)                                           # absorbed keys: the mask
+        S.view(n, m, Tk)[:, :, lo:hi] = S_live.view(n, m, hi - lo)
+    P = softmax(S, vector)
+    if hi - lo != Tk and (P[:, :lo].any() or P[:, hi:].any()):
+        lo, hi = 0, Tk                                                            # some row has no live key
+    PT_P, PT_X = pv.a(P.t().contiguous())                                         # Tk x n*m, blocks along keys
+    blocks = slice(lo // bv, -(-hi // bv))
+    O = pv.reduce(PT_P[lo:hi], PT_X[blocks], ops.V_P[lo:hi], ops.V_X[blocks])     # n*m x D
+    out_b[s0:e0, hs.start:hs.stop] = O.view(n, m, D).transpose(0, 1).to(out_b.dtype)
+
+
+# ------------------------------------------------------------------------------------------ batched path
+#: score entries per batched launch (problems x n*m x Tk float32): 4 GiB
+ELEMENTS_PER_LAUNCH = 1 << 30
+
+
+def _columnwise(quantizer, block_size: int) -> bool:
+    """A library block quantizer with blocks along axis 0: every column is quantized on its own, so the columns
+    of many calls quantized side by side get exactly the codes and scales each call would get."""
+    from ..block import mxgemmini, mxquant, ocp
+    if not isinstance(quantizer, partial) or quantizer.args:
+        return False
+    if quantizer.func not in (mxgemmini.quantize, mxquant.quantize, ocp.quantize):
+        return False
+    kw = quantizer.keywords
+    return "fmt" in kw and kw.get("axis", 0) in (0, -2) and kw.get("block_size", block_size) == block_size
+
+
+def _systolic_reducer(reduce, block_size: int):
+    """(arith, schedule, size) when `reduce` is matmul.systolic bound to an Arithmetic the kernel runs."""
+    from ..matmul import _systolic
+    if not isinstance(reduce, partial) or reduce.args or reduce.func is not _systolic.systolic:
+        return None
+    kw = reduce.keywords
+    if set(kw) - {"arith", "schedule", "size", "block_size"} or "arith" not in kw or "schedule" not in kw:
+        return None
+    size = kw.get("size", 16)
+    if getattr(kw["arith"], "kernel", None) is None or kw.get("block_size", 32) != block_size:
+        return None
+    if size > 64 or 32 % size or block_size % size or len(kw["schedule"]) != size:
+        return None
+    return kw["arith"], kw["schedule"], size
+
+
+def _column_group_amax(codes: torch.Tensor, scales: torch.Tensor, block_size: int, groups: int) -> torch.Tensor:
+    """_code_amax of each of `groups` equal column groups side by side: K x groups, float64."""
+    per_row = scales.repeat_interleave(block_size, dim=0)[:codes.shape[0]]
+    prod = codes.abs() * per_row
+    return prod.view(codes.shape[0], groups, -1).amax(dim=2).to(torch.float64)
+
+
+@dataclass
+class _Batched:
+    """attend built from the library's own pieces (column-wise block quantizers, matmul.systolic with a kernel
+    Arithmetic, no LUT rows) runs a query chunk of every (batch row, KV head) pair as one quantize call per
+    operand and one launch per matmul.  Each pair's codes, scales, scores and outputs are those its own call
+    gives: the quantizers treat columns independently, a batched launch computes each problem as a single one,
+    and softmax works row by row.  A chunk in which some pair would skip masked keys goes through the
+    reference's per-pair loop instead, on the same codes."""
+    qk: Scheme
+    pv: Scheme
+    qk_red: tuple
+    pv_red: tuple
+
+    @staticmethod
+    def of(qk: Scheme, pv: Scheme, q: torch.Tensor) -> Optional["_Batched"]:
+        if q.device.type != "cuda" or qk.rows != 1 or pv.rows != 1:
+            return None
+        if not all(_columnwise(f, s.block_size) for s, f in ((qk, qk.a), (qk, qk.b), (pv, pv.a), (pv, pv.b))):
+            return None
+        qk_red, pv_red = _systolic_reducer(qk.reduce, qk.block_size), _systolic_reducer(pv.reduce, pv.block_size)
+        if qk_red is None or pv_red is None:
+            return None
+        return _Batched(qk, pv, qk_red, pv_red)
+
+    def run(self, q, k, v, bias, scale, step, vector, rnd, dims: _Dims, out) -> None:
+        qk, pv = self.qk, self.pv
+        B, Hkv, Tk, D, n = dims.B, dims.Hkv, dims.Tk, dims.D, dims.group
+        Z = B * Hkv
+        # pair z = b * Hkv + h: its K^T in columns [z*Tk, (z+1)*Tk), its V in columns [z*D, (z+1)*D)
+        KT_P, KT_X = qk.b(k.to(torch.float32).permute(3, 0, 1, 2).reshape(D, Z * Tk))
+        V_P, V_X = pv.b(v.to(torch.float32).permute(2, 0, 1, 3).reshape(Tk, Z * D))
+        qk.check_scales(KT_X, D, "b (Kᵀ)")
+        pv.check_scales(V_X, Tk, "b (V)")
+        kv = (KT_P, KT_X, V_P, V_X)
+        k_amax = _column_group_amax(KT_P, KT_X, qk.block_size, Z) if bias is not None else None
+        qg = q.reshape(Z, n, dims.Tq, D)
+        for s0 in range(0, dims.Tq, step):
+            e0 = min(s0 + step, dims.Tq)
+            for z0, z1 in _launch_ranges(B, Hkv, max(1, ELEMENTS_PER_LAUNCH // (n * (e0 - s0) * Tk))):
+                if not self._chunk(qg, bias, kv, k_amax, scale, vector, rnd, dims, z0, z1, s0, e0, out):
+                    self._per_pair(q, bias, kv, scale, vector, rnd, dims, z0, z1, s0, e0, out)
+
+    def _chunk(self, qg, bias, kv, k_amax, scale, vector, rnd, dims: _Dims, z0, z1, s0, e0, out) -> bool:
+        from .. import _lib
+        from ..matmul._systolic import systolic_batched
+        qk, pv = self.qk, self.pv
+        KT_P, KT_X, V_P, V_X = kv
+        Zc, n, m, Tk, D, Hkv = z1 - z0, dims.group, e0 - s0, dims.Tk, dims.D, dims.Hkv
+        cols = n * m                                                              # one call's columns
+        A_P, A_X = qk.a(qg[z0:z1, :, s0:e0].to(torch.float32).permute(3, 0, 1, 2).reshape(D, Zc * cols))
         if bias is not None:
-            rows_bias = bias[s0:e0]                                               # m x Tk
-            bound = SLACK * abs(scale) * float((_code_amax(A_P, A_X, qk.block_size) * k_amax).sum())
-            lo, hi = _live_span(rows_bias, max(bound, tiny), bv)
-        S_live = rnd(qk.reduce(A_P, A_X, KT_P[:, lo:hi], KT_X[:, lo:hi]) * scale)  # n*m x (hi - lo)
-        if rows_bias is not None:
-            S_live = rnd(S_live.view(n, m, hi - lo) + rows_bias[:, lo:hi]).view(n * m, hi - lo)
-        if hi - lo == Tk:
-            S = S_live
-        else:
-            S = rnd(rows_bias).repeat(n, 1)                                       # absorbed keys: the mask
-            S.view(n, m, Tk)[:, :, lo:hi] = S_live.view(n, m, hi - lo)
+            bound = SLACK * abs(scale) * (_column_group_amax(A_P, A_X, qk.block_size, Zc) * k_amax[:, z0:z1]).sum(0)
+            b_of = torch.arange(z0, z1, device=qg.device) // Hkv if bias.shape[0] > 1 else \
+                torch.zeros(Zc, dtype=torch.int64, device=qg.device)
+            if not _windows_full(bias[:, s0:e0], b_of, bound.clamp(min=torch.finfo(torch.float32).tiny),
+                                 pv.block_size):
+                return False
+        arith, sched, size = self.qk_red
+        S = torch.empty(Zc, cols, Tk, dtype=torch.float32, device=qg.device)
+        systolic_batched((A_P, A_X, KT_P[:, z0 * Tk:], KT_X[:, z0 * Tk:]),
+                         _lib.SystolicLayout(ld_a=Zc * cols, batch_a=cols, ld_xa=Zc * cols, batch_xa=cols,
+                                             ld_b=KT_P.shape[1], batch_b=Tk, ld_xb=KT_X.shape[1], batch_xb=Tk,
+                                             ld_c=Tk, batch_c=cols * Tk),
+                         Zc, D, cols, Tk, S, arith, sched, size, qk.block_size)
+        S = rnd(S * scale)
+        if bias is not None:
+            rows = _mask_rows(bias, z0, z1, Hkv, s0, e0)
+            S = rnd((S.view(-1, Hkv, n, m, Tk) if rows.dim() == 5 else S.view(Zc, n, m, Tk)) + rows)
+            S = S.view(Zc, cols, Tk)
         P = softmax(S, vector)
-        if hi - lo != Tk and (P[:, :lo].any() or P[:, hi:].any()):
-            lo, hi = 0, Tk                                                        # some row has no live key
-        PT_P, PT_X = pv.a(P.t().contiguous())                                     # Tk x n*m, blocks along keys
-        blocks = slice(lo // bv, -(-hi // bv))
-        O = pv.reduce(PT_P[lo:hi], PT_X[blocks], V_P[lo:hi], V_X[blocks])         # n*m x D
-        out_b[s0:e0, hs.start:hs.stop] = O.view(n, m, D).transpose(0, 1).to(out_b.dtype)
+        PT_P, PT_X = pv.a(P.permute(2, 0, 1).reshape(Tk, Zc * cols))             # every call's P^T side by side
+        arith, sched, size = self.pv_red
+        O = torch.empty(Zc, cols, D, dtype=torch.float32, device=qg.device)
+        systolic_batched((PT_P, PT_X, V_P[:, z0 * D:], V_X[:, z0 * D:]),
+                         _lib.SystolicLayout(ld_a=Zc * cols, batch_a=cols, ld_xa=Zc * cols, batch_xa=cols,
+                                             ld_b=V_P.shape[1], batch_b=D, ld_xb=V_X.shape[1], batch_xb=D,
+                                             ld_c=D, batch_c=cols * D),
+                         Zc, Tk, cols, D, O, arith, sched, size, pv.block_size)
+        O = O.view(Zc, n, m, D)
+        for b in range(z0 // Hkv, (z1 - 1) // Hkv + 1):                          # pairs into B x Tq x H x D
+            h0, h1 = max(z0, b * Hkv) - b * Hkv, min(z1, (b + 1) * Hkv) - b * Hkv
+            part = O[b * Hkv + h0 - z0:b * Hkv + h1 - z0]                         # (h1 - h0) x n x m x D
+            out[b, s0:e0, h0 * n:h1 * n] = part.permute(2, 0, 1, 3).reshape(m, (h1 - h0) * n, D).to(out.dtype)
+        return True
+
+    def _per_pair(self, q, bias, kv, scale, vector, rnd, dims: _Dims, z0, z1, s0, e0, out) -> None:
+        KT_P, KT_X, V_P, V_X = kv
+        Tk, D, n = dims.Tk, dims.D, dims.group
+        for z in range(z0, z1):
+            b, h = divmod(z, dims.Hkv)
+            ops = _KVOperands.checked(KT_P[:, z * Tk:(z + 1) * Tk], KT_X[:, z * Tk:(z + 1) * Tk],
+                                      V_P[:, z * D:(z + 1) * D], V_X[:, z * D:(z + 1) * D], self.qk, self.pv,
+                                      bias is not None)
+            bias_b = None if bias is None else bias[b if bias.shape[0] > 1 else 0]
+            _one_call(q[b], ops, bias_b, scale, self.qk, self.pv, vector, rnd, dims, range(h * n, (h + 1) * n),
+                      s0, e0, out[b])
+
+
+def _launch_ranges(B: int, Hkv: int, per_launch: int):
+    """Pair ranges [z0, z1) of at most per_launch pairs: whole batch rows when a launch holds one or more,
+    else pieces of one batch row."""
+    if per_launch >= Hkv:
+        per_launch -= per_launch % Hkv
+        return [(z0, min(B * Hkv, z0 + per_launch)) for z0 in range(0, B * Hkv, per_launch)]
+    return [(b * Hkv + h0, b * Hkv + min(Hkv, h0 + per_launch)) for b in range(B) for h0 in range(0, Hkv, per_launch)]
+
+
+def _mask_rows(bias: torch.Tensor, z0: int, z1: int, Hkv: int, s0: int, e0: int) -> torch.Tensor:
+    """The mask rows [s0, e0) of pairs z0..z1 as a view: (1, 1, m, Tk) when they share one row of the mask,
+    else (batch rows, 1, 1, m, Tk) against scores shaped (batch rows, Hkv, n, m, Tk)."""
+    if bias.shape[0] == 1:
+        return bias[0, s0:e0][None, None]
+    b0, b1 = z0 // Hkv, (z1 - 1) // Hkv + 1
+    if b1 - b0 == 1:
+        return bias[b0, s0:e0][None, None]
+    return bias[b0:b1, None, None, s0:e0]
+
+
+def _windows_full(rows: torch.Tensor, b_of: torch.Tensor, bound: torch.Tensor, block: int) -> bool:
+    """Would every call keep all its keys (_live_span = [0, Tk))?  rows: Bm x m x Tk mask rows, b_of: each
+    call's row of `rows`, bound: each call's float64 bound.  A call keeps all keys when some query sees a key
+    of the first block and one of the last (a single block always stays whole)."""
+    Tk = rows.shape[2]
+    if Tk <= block:
+        return True
+    b32 = bound.to(torch.float32)[:, None, None]
+
+    def live(cols: torch.Tensor) -> torch.Tensor:
+        c = cols[b_of]                                                            # calls x m x block
+        absorbed = ((c + b32) == c) & ((c - b32) == c)
+        return (~absorbed.all(dim=1)).any(dim=1)
+
+    last0 = (Tk - 1) // block * block
+    return bool((live(rows[:, :, :block]) & live(rows[:, :, last0:])).all())
 
 
 def _mxq_attention(module, query, key, value, attention_mask, dropout: float = 0.0, scaling: Optional[float] = None,

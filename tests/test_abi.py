@@ -46,7 +46,8 @@ def test_structs_match_header():
     """ctypes layouts of mxq_block_spec / mxq_arith_spec against the header's field lists."""
     from mxq import _lib
     text = open(HEADER).read()
-    for struct, py in (("mxq_block_spec", _lib.BlockSpec), ("mxq_arith_spec", _lib.ArithSpec)):
+    for struct, py in (("mxq_block_spec", _lib.BlockSpec), ("mxq_arith_spec", _lib.ArithSpec),
+                       ("mxq_systolic_layout", _lib.SystolicLayout)):
         body = re.search(r"typedef struct " + struct + r"\s*\{(.*?)\}\s*" + struct + ";", text, flags=re.S).group(1)
         body = re.sub(r"/\*.*?\*/|//[^\n]*", "", body, flags=re.S)
         fields = [(t, n.strip()) for t, names in re.findall(r"\b(int32_t|float|double|int64_t)\s+([a-z_0-9, ]+);", body)

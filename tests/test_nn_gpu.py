@@ -168,3 +168,22 @@ def test_exact_core_matches_eager(cuda):
     h = patch(model, [(lambda name, mod, parent: True, (EXACT, EXACT))])
     torch.testing.assert_close(model(ids).logits, eager, rtol=1e-4, atol=1e-4)
     h.revert()
+
+
+def test_attend_batched_launch_ranges(cuda, monkeypatch):
+    """The batched path split into launches of fewer pairs than a batch row holds, two batch rows with their
+    own left-padding masks, GQA 2:1: bit for bit against the oracle's per-call loop."""
+    import mxq
+    from mxq.nn import _attention
+    monkeypatch.setattr(_attention, "ELEMENTS_PER_LAUNCH", 3 * 2 * 48 * 48)
+    B, H, Hkv, T, D = 2, 8, 4, 48, 32
+    g = torch.Generator().manual_seed(9)
+    q, k, v = (torch.randn(B, h, T, D, generator=g) for h in (H, Hkv, Hkv))
+    mask = _causal(B, T, T)
+    mask[0, :, :, :5] = torch.finfo(torch.float32).min
+    mask[1, :, :, :11] = torch.finfo(torch.float32).min
+    hw, hwo = _hw(mxq), _hw_oracle()
+    got = mxq.nn.attend(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), D ** -0.5, hw, hw).cpu().numpy()
+    want = oatt.attend(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), D ** -0.5, hwo, hwo, _gpu_softmax)
+    assert_bits_equal(got, want, "batched launch ranges")
+    assert _attention._Batched.of(hw, hw, q.cuda()) is not None, "the hw scheme takes the batched path"

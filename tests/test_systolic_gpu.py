@@ -204,3 +204,47 @@ def test_c2_shape_column_slice(cuda):
     pb, xb = P_B.cpu().numpy()[:, cols], X_B.cpu().numpy()[:, cols]
     want = osys.systolic(pa, xa, pb, xb, nx.MXGEMMINI(), HW_FINAL)
     assert_bits_equal(Y[:, cols], want, "C2 column slice")
+
+
+@pytest.mark.parametrize("sched_name", ["hw", "general"])
+def test_batched_matches_single(cuda, sched_name):
+    """mxq_systolic_batched over strided column slices of shared matrices equals one systolic call per problem;
+    one problem carries codes outside the fast kernel's case, so its tiles go to the general kernel."""
+    from mxq import _lib, matmul
+    from mxq.matmul._systolic import systolic_batched
+    rng = np.random.default_rng(3)
+    count, K, M, N, gap = 5, 70, 40, 72, 8
+    P_A, X_A = _codes(rng, K, count * (M + gap), scale=2.0)
+    P_B, X_B = _codes(rng, K, count * N)
+    P_A[5, 2 * (M + gap) + 7] = 448.0                                      # problem 2: products above the bound
+    sched = HW_FINAL if sched_name == "hw" else [(5, 6)] * 16
+    ar = matmul.MXGEMMINI()
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()          # noqa: E731
+    ops = (t(P_A), t(X_A), t(P_B), t(X_B))
+    C = torch.full((count, M, N + 3), float("nan"), device="cuda")
+    lay = _lib.SystolicLayout(ld_a=P_A.shape[1], batch_a=M + gap, ld_xa=X_A.shape[1], batch_xa=M + gap,
+                              ld_b=P_B.shape[1], batch_b=N, ld_xb=X_B.shape[1], batch_xb=N,
+                              ld_c=N + 3, batch_c=M * (N + 3))
+    systolic_batched(ops, lay, count, K, M, N, C, ar, sched)
+    for z in range(count):
+        a = slice(z * (M + gap), z * (M + gap) + M)
+        b = slice(z * N, (z + 1) * N)
+        want = _run(P_A[:, a], X_A[:, a], P_B[:, b], X_B[:, b], ar, sched)
+        assert_bits_equal(C[z, :, :N].cpu().numpy(), want, f"problem {z}")
+        assert torch.isnan(C[z, :, N:]).all(), "columns past N are left alone"
+
+
+def test_both_fast_tile_heights(cuda):
+    """2048 x 4096 outputs run on 64-row fast tiles, 512 x 4096 on 32-row ones (too few 64-row tiles to fill
+    the chip); both against the oracle on column slices (columns are independent chains)."""
+    from mxq import matmul
+    rng = np.random.default_rng(8)
+    for M in (2048, 512):
+        K, N = 64, 4096
+        P_A, X_A = _codes(rng, K, M)
+        P_B, X_B = _codes(rng, K, N, scale=0.1)
+        t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()      # noqa: E731
+        Y = matmul.systolic(t(P_A), t(X_A), t(P_B), t(X_B), matmul.MXGEMMINI(), matmul.HW_FINAL).cpu().numpy()
+        for cols in (slice(0, 8), slice(4090, 4096)):
+            want = osys.systolic(P_A, X_A, P_B[:, cols], X_B[:, cols], nx.MXGEMMINI(), HW_FINAL)
+            assert_bits_equal(Y[:, cols], want, f"M={M} cols {cols}")
