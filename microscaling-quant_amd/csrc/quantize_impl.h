@@ -45,6 +45,19 @@ __device__ __forceinline__ void store_vec(float* p, const float (&in)[VEC]) {
   *reinterpret_cast<VecT<float, VEC>*>(p) = r;
 }
 
+// Codes are written once and not read back by this kernel: streaming (non-temporal) stores.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <int VEC>
+__device__ __forceinline__ void store_vec_nt(float* p, const float (&in)[VEC]) {
+  if constexpr (VEC == 4) {
+    f32x4 r = {in[0], in[1], in[2], in[3]};
+    __builtin_nontemporal_store(r, reinterpret_cast<f32x4*>(p));
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) __builtin_nontemporal_store(in[j], p + j);
+  }
+}
+
 // (o, b, column group) of a flat thread index over outer * nb * groups.
 __device__ __forceinline__ void split_index(int64_t t, int64_t groups, int64_t nb, int64_t& o, int64_t& b,
                                             int64_t& g) {
@@ -107,7 +120,7 @@ __global__ void __launch_bounds__(256) k_quant_strided(const T* __restrict__ V, 
     load_vec<T, VEC>(V + off + r * inner, v);
 #pragma unroll
     for (int j = 0; j < VEC; ++j) q[j] = elem_qm<ELEM, MODE>(s.scale_rule ? apply_div(v[j], d[j]) : v[j], s);
-    store_vec<VEC>(P + off + r * inner, q);
+    store_vec_nt<VEC>(P + off + r * inner, q);
   }
   store_vec<VEC>(X + (o * nb + b) * inner + g * VEC, xs);
 }
@@ -182,7 +195,7 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, fl
       float q[VEC];
 #pragma unroll
       for (int j = 0; j < VEC; ++j) q[j] = elem_qm<ELEM, MODE>(v[i][j], s);
-      store_vec<VEC>(P + off + (int64_t)row * inner, q);
+      store_vec_nt<VEC>(P + off + (int64_t)row * inner, q);
     }
   }
   if (r == 0) store_vec<VEC>(X + (o * nb + b) * inner + cg * VEC, xs);
@@ -211,7 +224,7 @@ __global__ void __launch_bounds__(256) k_quant_contig32(const T* __restrict__ V,
   float q[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) q[j] = elem_qm<ELEM, MODE>(s.scale_rule ? apply_div(v[j], d) : v[j], s);
-  store_vec<4>(P + off, q);
+  store_vec_nt<4>(P + off, q);
   if ((t & 7) == 0) X[blk] = xs;
 }
 
@@ -238,7 +251,7 @@ __global__ void __launch_bounds__(256) k_dequant_strided(const float* __restrict
     load_vec<float, VEC>(P + off + r * inner, v);
 #pragma unroll
     for (int j = 0; j < VEC; ++j) v[j] = v[j] * xs[j];
-    store_vec<VEC>(out + off + r * inner, v);
+    store_vec_nt<VEC>(out + off + r * inner, v);
   }
 }
 

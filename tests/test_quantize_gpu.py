@@ -75,13 +75,20 @@ def test_ocp(cuda, fmt, placement):
 def test_low_precision_inputs(cuda, dtype):
     from mxq import block
     rng = np.random.default_rng(4)
-    V = torch.from_numpy(_edge_matrix(rng, 512, 256) * 3).to(dtype)
-    V32 = V.to(torch.float32).numpy()
-    for fmt in FMTS:
-        P, X = block.mxgemmini.quantize(V.cuda(), fmt, axis=0, rounding_mode="rne")
-        wP, wX = ob.mxgemmini_quantize(V32, fmt, 0, 32, "rne")
-        assert_bits_equal(P.cpu().numpy(), wP, f"P {dtype} {fmt}")
-        assert_bits_equal(X.cpu().numpy(), wX, f"X {dtype} {fmt}")
+    for shape in ((512, 256), (100, 260), (70, 24)):            # 8, 4 and 8 columns per lane; short last block
+        V = torch.from_numpy(_edge_matrix(rng, *shape) * 3).to(dtype)
+        V32 = V.to(torch.float32).numpy()
+        for fmt in FMTS:
+            P, X = block.mxgemmini.quantize(V.cuda(), fmt, axis=0, rounding_mode="rne")
+            wP, wX = ob.mxgemmini_quantize(V32, fmt, 0, 32, "rne")
+            assert_bits_equal(P.cpu().numpy(), wP, f"P {dtype} {fmt} {shape}")
+            assert_bits_equal(X.cpu().numpy(), wX, f"X {dtype} {fmt} {shape}")
+        P, X = block.ocp.quantize(V.cuda(), "MXFP8_E4M3", axis=0)
+        wP, wX = ob.ocp_quantize(V32, "MXFP8_E4M3", 0)
+        assert_bits_equal(P.cpu().numpy(), wP, f"ocp P {dtype} {shape}")
+        P, X = block.mxquant.quantize(V.cuda(), "MXFP6_E3M2", axis=0, block_size=16)
+        wP, wX = ob.mxquant_quantize(V32, "MXFP6_E3M2", 0, 16)
+        assert_bits_equal(P.cpu().numpy(), wP, f"mxquant bs16 P {dtype} {shape}")
 
 
 def test_contiguous_block_layout(cuda):
