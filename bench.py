@@ -1,6 +1,6 @@
 """Benchmark: emulated MX GEMM throughput of matmul.systolic (bit-exact MXGEMMINI, HW_FINAL ladder) on one GPU,
-plus block-quantize HBM throughput, the LUT pipeline and the attention core, each next to its roofline and the
-oracle's CPU rate.
+plus block-quantize HBM throughput, the LUT pipeline, the attention core and the matrix-core comparison product,
+each next to its roofline, and the oracle's CPU rate.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
     python bench.py --copy-calibration        # only a 256 MiB device copy, 5 times (counter calibration)
@@ -31,6 +31,7 @@ HBM_PEAK_GBS = 8000.0
 VALU_LANE_OPS = 157.3e12 / 2
 OPS_PER_MAC_MODEL = 10                      # canonical datapath primitives per emulated MAC
 VALU_ROOF_TOPS = VALU_LANE_OPS / OPS_PER_MAC_MODEL * 2 / 1e12   # 15.73 TOP/s emulated
+FP8_PEAK_TFLOPS = 5000.0                    # MI355X dense FP8 matrix-core peak
 
 
 def _events_ms(fn, steps, stream):
@@ -182,6 +183,25 @@ def attend_line(torch, steps):
             "ms": round(ms, 3), "emulated_TOPs": round(2 * macs / ms / 1e9, 3)}
 
 
+def mfma_line(torch, steps, P_A, X_A, P_B, X_B):
+    """mfma_accum (the matrix-core comparison product) on the benchmark's own codes: pack both operands to FP8
+    and E8M0 bytes, then V_MFMA_SCALE_F32_32X32X64_F8F6F4.  The kernel rate is held against MI355X's dense FP8
+    peak, 5.0 PFLOP/s."""
+    import mxq
+    dev = P_A.device
+    s = torch.cuda.current_stream(dev)
+    fn = lambda: mxq.mfma_accum(P_A, X_A, P_B, X_B, "MXFP8_E4M3")                # noqa: E731
+    fn()
+    ms = _events_ms(fn, steps, s)
+    kms, _ = _kernel_ms(fn, steps, "mx_mfma")
+    flops = 2 * P_A.shape[0] * P_A.shape[1] * P_B.shape[1]
+    k_tf = flops / (kms / 1e3) / 1e12 if kms else None
+    return {"workload": "mfma_accum on the same MXFP8_E4M3 codes (M = 512, N = 4096, K = 4096)",
+            "ms": round(ms, 4), "kernel": "k_mx_mfma<0, 0>", "kernel_ms": round(kms, 4) if kms else None,
+            "kernel_TFLOPs": round(k_tf, 2) if k_tf else None, "peak_TFLOPs": FP8_PEAK_TFLOPS,
+            "frac": round(k_tf / FP8_PEAK_TFLOPS, 4) if k_tf else None}
+
+
 def copy_calibration():
     """A plain device copy of 256 MiB, five times: the reference point for the FETCH_SIZE / WRITE_SIZE
     counters (each launch reads and writes 262144 KiB)."""
@@ -259,6 +279,7 @@ def main():
         line["quantize"] = quantize_lines(torch, max(5, args.steps // 2))
         line["lut_c4"] = lut_line(torch, 3)
         line["attend_c5"] = attend_line(torch, 3)
+        line["mfma_c2"] = mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_systolic(P_A, X_A, P_B, X_B, cols=160)
     print(json.dumps(line), flush=True)

@@ -59,6 +59,8 @@ SIGNATURES = {
                                      c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32, ctypes.POINTER(ArithSpec),
                                      c_ptr, c_i32, c_ptr]),
     "mxq_systolic_workspace": (c_i64, [c_i64, c_i64, c_i64]),
+    "mxq_mx_pack": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mxq_mx_mfma": (c_i32, [c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr]),
     "mxq_lut_tables": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr,
                                c_ptr]),
     "mxq_lut_pick": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr]),
