@@ -160,6 +160,29 @@ def test_fast_guards(cuda):
         assert_bits_equal(_run(pa, xa, pb, xb, ar, HW_FINAL), want, what)
 
 
+@pytest.mark.parametrize("prod_floor,edge", [(-16, 53), (-40, 41), (-126, 53)])
+def test_tile_add_scale_ranges(cuda, prod_floor, edge):
+    """The fast kernel adds S * scale into C without rounding S * scale first only for blocks whose scales are
+    powers of two within 2^-L .. 2^L (L = 53 for the default product floor 2^-16, 41 for 2^-40, none for
+    2^-126).  Blocks at, just beyond and far beyond that edge, non-power-of-two scales on some columns, and
+    zero scales: against the oracle and the general kernel."""
+    rng = np.random.default_rng(-prod_floor)
+    K, M, N = 256, 40, 72
+    P_A, X_A = _codes(rng, K, M)
+    P_B, X_B = _codes(rng, K, N, scale=0.02)
+    shift = np.array([0, edge, -edge, edge + 1, -(edge + 1), 60, -60, 0], dtype=np.float64)
+    XA = (X_A * np.exp2(shift)[:, None]).astype(np.float32)
+    XB = X_B.copy()
+    XB[6] = np.float32(2.0 ** -edge)
+    XB[7, :5] = np.float32(0.3)
+    XB[7, 5:9] = 0.0
+    XB[1, 40:] = np.float32(3.0)
+    ar, orc = _arith("MXGEMMINI", 4, 3, prod_floor)
+    want = osys.systolic(P_A, XA, P_B, XB, orc, HW_FINAL)
+    assert_bits_equal(_run(P_A, XA, P_B, XB, ar, HW_FINAL), want, f"fast, floor 2^{prod_floor}")
+    assert_bits_equal(_run(P_A, XA, P_B, XB, ar, HW_FINAL, force_general=True), want, "general")
+
+
 def test_compiled_and_scheme(cuda):
     from functools import partial
 
