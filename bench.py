@@ -26,7 +26,7 @@ METRIC = "emulated MX GEMM GOP/s (systolic, bit-exact) + quantize GB/s vs HBM ro
 HBM_PEAK_GBS = 8000.0
 # MI355X's published vector FP32 peak, 157.3 TFLOP/s, is 78.6 T FMA lane-operations per second: the rate at which
 # its 1024 SIMDs retire 32-bit VALU lanes (256 CUs x 128 lanes/clk x 2.4 GHz).  The fast systolic kernel is
-# measured above the single-issue 64 lanes/clk/CU figure (SQ_INSTS_VALU x 64 / duration = 42.6 T lane-ops/s),
+# measured above the single-issue 64 lanes/clk/CU figure (SQ_INSTS_VALU x 64 / duration = 45.5 T lane-ops/s),
 # so the 128-lane rate is the ceiling it is held against.
 VALU_LANE_OPS = 157.3e12 / 2
 OPS_PER_MAC_MODEL = 10                      # canonical datapath primitives per emulated MAC
@@ -272,7 +272,7 @@ def main():
                      "note": "VALU-bound emulation (neither HBM nor MFMA): achieved = 2 x 8,589,934,592 emulated "
                              "MACs / the fast kernel's average duration; peak = MI355X vector FP32 157.3 TFLOP/s "
                              "= 78.6 T 32-bit lane-ops/s, / 10 lane-ops per emulated MAC (the datapath's primitive "
-                             "count) x 2 ops per MAC; the kernel executes 8.6 VALU lane-ops per MAC "
+                             "count) x 2 ops per MAC; the kernel executes 7.8 VALU lane-ops per MAC "
                              "(SQ_INSTS_VALU, profiles/systolic_fast_c2_valu.txt)"},
     }
     if not args.no_extra:
