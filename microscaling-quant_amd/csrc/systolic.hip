@@ -34,18 +34,16 @@
 
 #include "mxq_common.h"
 #include "mxq_numerics.h"
+#include "reducer_common.h"
 
 namespace {
+
+using namespace mxq_red;
 
 constexpr int kMaxLanes = 64;
 constexpr uint32_t kFastAMaxBits = 0x71800000u;   // 2^100: A's rows are staged times up to 2^15
 constexpr int FBN = 64;                           // the fast kernel's tile width (its height is 64 or 32)
 
-struct Operand {
-  const float* p;
-  int64_t ld;     // elements between rows
-  int64_t batch;  // elements between problems
-};
 
 struct SysArgs {
   Operand A, XA, B, XB;   // A: K x M, XA: nb x M, B: K x N, XB: nb x N
@@ -61,84 +59,6 @@ struct SysArgs {
   int8_t lane_m[kMaxLanes];
   float fast_prod_max;    // the fast kernel's bound on max|a| * max|b| (see fast_prod_bound)
 };
-
-// ------------------------------------------------------------------------------------- tile staging
-// Workgroup tile BM x BN outputs, K staged 32 rows at a time through LDS (two buffers).
-constexpr int KT = 32;
-
-template <int BM, int BN>
-struct Smem {
-  float a[2][KT][BM];
-  float b[2][KT][BN];
-};
-
-// Loads rows [k0, k0 + KT) x cols [c0, c0 + W) of an R x L matrix with row stride ld into registers (zero
-// outside the matrix).  vec_ok: ld and the base are multiples of 4 floats / 16 bytes.
-template <int W, int NT>
-struct TileLoader {
-  static constexpr int PER = KT * W / NT;  // floats per thread
-  float v[PER];
-  __device__ __forceinline__ void load(const float* __restrict__ src, int64_t ld, int64_t R, int64_t L, int64_t k0,
-                                       int64_t c0, bool vec_ok) {
-    const int t = threadIdx.x;
-    if (vec_ok) {
-#pragma unroll
-      for (int j = 0; j < PER / 4; ++j) {
-        const int e = (t + j * NT) * 4;
-        const int r = e / W, c = e % W;
-        const int64_t gr = k0 + r, gc = c0 + c;
-        float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (gr < R && gc + 3 < L) q = *reinterpret_cast<const float4*>(src + gr * ld + gc);
-        else if (gr < R) {
-          if (gc < L) q.x = src[gr * ld + gc];
-          if (gc + 1 < L) q.y = src[gr * ld + gc + 1];
-          if (gc + 2 < L) q.z = src[gr * ld + gc + 2];
-        }
-        v[j * 4 + 0] = q.x; v[j * 4 + 1] = q.y; v[j * 4 + 2] = q.z; v[j * 4 + 3] = q.w;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        const int e = t + j * NT;
-        const int r = e / W, c = e % W;
-        const int64_t gr = k0 + r, gc = c0 + c;
-        v[j] = (gr < R && gc < L) ? src[gr * ld + gc] : 0.0f;
-      }
-    }
-  }
-  __device__ __forceinline__ void store(float (*dst)[W], bool vec_ok) const {
-    const int t = threadIdx.x;
-    if (vec_ok) {
-#pragma unroll
-      for (int j = 0; j < PER / 4; ++j) {
-        const int e = (t + j * NT) * 4;
-        *reinterpret_cast<float4*>(&dst[e / W][e % W]) = make_float4(v[j * 4], v[j * 4 + 1], v[j * 4 + 2], v[j * 4 + 3]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        const int e = t + j * NT;
-        dst[e / W][e % W] = v[j];
-      }
-    }
-  }
-  // the largest |x| bit pattern among the staged values (patterns of non-negative floats order like values)
-  __device__ __forceinline__ uint32_t max_bits() const {
-    uint32_t mx = 0u;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const uint32_t u = f2u(v[j]) & 0x7FFFFFFFu;
-      mx = u > mx ? u : mx;
-    }
-    return mx;
-  }
-};
-
-__device__ __forceinline__ bool vec_ok(const Operand& o, const float* base) {
-  return o.ld % 4 == 0 && reinterpret_cast<uintptr_t>(base) % 16 == 0;
-}
-
-__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
 
 // ---------------------------------------------------------------------------------- fast datapath
 // Per-lane constants of the fast kernel, built on the host from the schedule (see make_fast_lanes).
@@ -429,19 +349,6 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 }
 
 // ------------------------------------------------------------------------------- general datapath
-__device__ __forceinline__ float gen_product(float a, float b, const mxq_arith_spec& ar) {
-  if (ar.kind == MXQ_ARITH_MXQUANT) return mxq_q(a * b, ar.prod_e, ar.prod_m);
-  return mxg_product(a, b, ar.prod_m, ar.has_floor != 0, ar.flush_thr, ar.sat_limit, ar.sat_value);
-}
-__device__ __forceinline__ float gen_acc(float S, float p, int e, int m, const mxq_arith_spec& ar) {
-  if (ar.kind == MXQ_ARITH_MXQUANT) return mxq_q(S + p, e, m);
-  return mxg_acc_add(S, p, e, m);
-}
-__device__ __forceinline__ float gen_tile(float C, float tile, const mxq_arith_spec& ar) {
-  if (ar.kind == MXQ_ARITH_MXQUANT) return C + tile;
-  return mxg_tile_add(C, tile);
-}
-
 // only_flagged: compute just the outputs whose fast tile has its flag set (the fast kernel ran first).
 template <int BM, int BN, int TM, int TN>
 __global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const SysArgs args, int only_flagged) {

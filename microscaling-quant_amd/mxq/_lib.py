@@ -44,6 +44,11 @@ class SystolicLayout(ctypes.Structure):
                                      "ld_c", "batch_c")]
 
 
+class AnchorSpec(ctypes.Structure):
+    """mxq_anchor_spec (include/mxq_hip.h)."""
+    _fields_ = [(n, c_i32) for n in ("width", "drop", "headroom", "has_emin", "emin", "nbits")]
+
+
 # exported symbol -> (restype, argtypes); every symbol include/mxq_hip.h declares
 SIGNATURES = {
     "mxq_last_error": (ctypes.c_char_p, []),
@@ -59,6 +64,10 @@ SIGNATURES = {
                                      c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32, ctypes.POINTER(ArithSpec),
                                      c_ptr, c_i32, c_ptr]),
     "mxq_systolic_workspace": (c_i64, [c_i64, c_i64, c_i64]),
+    "mxq_adder_tree": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,
+                               ctypes.POINTER(ArithSpec), c_ptr]),
+    "mxq_anchor_tree": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i32,
+                                c_i32, ctypes.POINTER(AnchorSpec), ctypes.POINTER(ArithSpec), c_ptr]),
     "mxq_mx_pack": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_ptr, c_ptr]),
     "mxq_mx_mfma": (c_i32, [c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr]),
     "mxq_lut_tables": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr,

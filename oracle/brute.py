@@ -5,7 +5,7 @@ TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 Nothing here shares a formula with oracle/numerics.py: rounding is a search for the nearest member of an
 enumerated grid (ties by the grid index, which alternates parity exactly as the significand's last bit does),
 sums are exact (float64 where every operand sits on a narrow grid, fractions.Fraction otherwise), and the
-systolic model walks one output at a time in Python scalars.  A slip in the oracle's step, exponent, tie or
+systolic, adder-tree and anchor-tree models walk one output at a time in Python scalars.  A slip in the oracle's step, exponent, tie or
 sign handling makes one of them disagree.
 """
 from fractions import Fraction
@@ -200,6 +200,124 @@ def systolic_mxgemmini(P_A, X_A, P_B, X_B, schedule, size=16, block_size=32):
                     tile = float(F32(F32(S) * sc))
                     c = exact_add(lane(c, 8, 7), lane(tile, 8, 7), 8, 7)
             C[i, j] = c
+    return C
+
+
+def _mxg_lane(x, e, m):
+    """An MXGEMMINI lane value: x on the ieee(e, m) grid, nearest, ties even; zeros unsigned."""
+    r = exact_round_fraction(Fraction(float(x)), e, m) if np.isfinite(x) else float(x)
+    return 0.0 if r == 0 else r
+
+
+def _mxg_acc(a, b, e, m):
+    return exact_add(_mxg_lane(a, e, m), _mxg_lane(b, e, m), e, m)
+
+
+def _bf16_tile(c, S, sc):
+    tile = float(F32(F32(S) * sc))
+    return exact_add(_mxg_lane(c, 8, 7), _mxg_lane(tile, 8, 7), 8, 7)
+
+
+def _blocks(K, size, block_size):
+    """(first k of the block, first k of the reduction, its product count) in the reducers' order."""
+    for g0 in range(0, K, block_size):
+        for k0 in range(g0, min(g0 + block_size, K), size):
+            yield g0, k0, min(k0 + size, g0 + block_size, K) - k0
+
+
+def adder_tree_mxgemmini(P_A, X_A, P_B, X_B, schedule, size=16, block_size=32):
+    """The MXGEMMINI adder tree one output at a time: a reduction's `size` exact-scalar products (zeros past a
+    tail) halved level by level, each pair summed exactly and rounded once to its level's format."""
+    P_A, X_A, P_B, X_B = (np.asarray(t, F32) for t in (P_A, X_A, P_B, X_B))
+    K, M = P_A.shape
+    N = P_B.shape[1]
+    C = np.zeros((M, N), F32)
+    for i in range(M):
+        for j in range(N):
+            c = 0.0
+            for g0, k0, n in _blocks(K, size, block_size):
+                sc = F32(X_A[g0 // block_size, i]) * F32(X_B[g0 // block_size, j])
+                vals = [mxgemmini_product(P_A[k, i], P_B[k, j]) for k in range(k0, k0 + n)] + [0.0] * (size - n)
+                for e, m in schedule:
+                    vals = [_mxg_acc(vals[2 * q], vals[2 * q + 1], e, m) for q in range(len(vals) // 2)]
+                c = _bf16_tile(c, vals[0], sc)
+            C[i, j] = c
+    return C
+
+
+def _exp_label(x):
+    """floor(log2|x|) of a finite nonzero float from its exact binary expansion; -1 for zero and non-finite
+    values (they never decide an anchor through it)."""
+    x = float(x)
+    if x == 0 or not np.isfinite(x):
+        return -1
+    q = abs(Fraction(x))
+    E = q.numerator.bit_length() - q.denominator.bit_length()
+    while Fraction(2) ** E > q:
+        E -= 1
+    while Fraction(2) ** (E + 1) <= q:
+        E += 1
+    return E
+
+
+def _drop_to_int(q, drop):
+    """An exact rational made an integer: toward zero, or nearest with ties to even."""
+    if drop == "truncate":
+        return Fraction(int(q))                       # int() of a Fraction truncates toward zero
+    fl = q.numerator // q.denominator
+    rem = q - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    return Fraction(fl)
+
+
+def anchor_tree_mxgemmini(P_A, X_A, P_B, X_B, schedule, size, width, bits_of, drop, headroom, emin=None,
+                          block_size=32):
+    """The MXGEMMINI anchor tree one output at a time in exact rationals.  bits_of(m) gives a tree's level
+    widths.  Per tree: the anchor is the largest label among its nonzero products (code-exponent sum, at least
+    emin per code when given) and the running sum c (its exponent minus one), plus headroom; every term is cut
+    to an integer multiple of 2^(anchor + 2 - bits[0]); terms are summed in adjacent pairs, products first and
+    c last, an odd one carried up, and cut again where the level width falls; the root is rounded to float32,
+    then to the tree's lane."""
+    P_A, X_A, P_B, X_B = (np.asarray(t, F32) for t in (P_A, X_A, P_B, X_B))
+    K, M = P_A.shape
+    N = P_B.shape[1]
+
+    def label(x):
+        lab = _exp_label(x)
+        return lab if emin is None else max(lab, emin)
+
+    C = np.zeros((M, N), F32)
+    for i in range(M):
+        for j in range(N):
+            cacc = 0.0
+            for g0, k0, n in _blocks(K, size, block_size):
+                sc = F32(X_A[g0 // block_size, i]) * F32(X_B[g0 // block_size, j])
+                c = 0.0
+                for t, (e, m) in enumerate(schedule):
+                    bits = bits_of(m)
+                    ks = [k for k in range(k0 + t * width, k0 + (t + 1) * width) if k < k0 + n]
+                    prods = [mxgemmini_product(P_A[k, i], P_B[k, j]) for k in ks]
+                    labs = [label(P_A[k, i]) + label(P_B[k, j]) for k in ks]
+                    cands = [lb for pv, lb in zip(prods, labs) if pv != 0]
+                    if c != 0:
+                        cands.append(_exp_label(c) - 1)
+                    anchor = (max(cands) if cands else 0) + headroom
+                    step = Fraction(2) ** (anchor + 2 - bits[0])
+                    terms = prods + [0.0] * (width - len(prods)) + [c]
+                    x = [_drop_to_int(Fraction(float(v)) / step, drop) for v in terms]
+                    for lvl in range(1, len(bits)):
+                        nxt = [x[2 * q] + x[2 * q + 1] for q in range(len(x) // 2)]
+                        if len(x) % 2:
+                            nxt.append(x[-1])
+                        if bits[lvl] != bits[lvl - 1]:
+                            nxt = [_drop_to_int(v / Fraction(2) ** (bits[lvl - 1] - bits[lvl]), drop) for v in nxt]
+                        x = nxt
+                    root = x[0] * Fraction(2) ** (anchor + 2 - bits[-1])
+                    assert Fraction(float(root)) == root            # an integer below 2^53 times a power of two
+                    c = _mxg_lane(float(F32(float(root))), e, m)   # one rounding to float32, then the lane
+                cacc = _bf16_tile(cacc, c, sc)
+            C[i, j] = cacc
     return C
 
 

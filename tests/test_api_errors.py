@@ -34,6 +34,40 @@ def test_systolic_checks():
         matmul.systolic(P_A, X_A, P_B, X_B, ar, [(4, 4)] * 12, 12)
 
 
+def test_tree_checks():
+    """mxq/matmul/_adder.py:58-63 and mxq/matmul/_anchor.py:101-124, in that order."""
+    ar = matmul.MXGEMMINI()
+    P_A, X_A, P_B, X_B = _ops()
+    with pytest.raises(ValueError, match="contraction lengths differ"):
+        matmul.adder_tree(P_A, X_A, P_B[:32], X_B, ar, [(8, 7)] * 4)
+    with pytest.raises(ValueError, match="size 12 must be a power of two >= 2"):
+        matmul.adder_tree(P_A, X_A, P_B, X_B, ar, [(8, 7)] * 3, 12)
+    with pytest.raises(ValueError, match="size 1 must be a power of two >= 2"):
+        matmul.adder_tree(P_A, X_A, P_B, X_B, ar, [], 1)
+    with pytest.raises(ValueError, match="size 64 must divide block size 32"):
+        matmul.adder_tree(P_A, X_A, P_B, X_B, ar, [(8, 7)] * 6, 64)
+    with pytest.raises(ValueError, match="schedule has 3 rows, reducer has 4"):
+        matmul.adder_tree(P_A, X_A, P_B, X_B, ar, [(8, 7)] * 3)
+    with pytest.raises(ValueError, match="scales must be"):
+        matmul.anchor_tree(P_A, X_A[:1], P_B, X_B, ar)
+    with pytest.raises(ValueError, match="width 3 must divide size 16, and size must divide block size 32"):
+        matmul.anchor_tree(P_A, X_A, P_B, X_B, ar, width=3)
+    with pytest.raises(ValueError, match="width 8 must divide size 24, and size must divide block size 32"):
+        matmul.anchor_tree(P_A, X_A, P_B, X_B, ar, None, 24, width=8)
+    with pytest.raises(ValueError, match="schedule has 1 rows, reducer has 2"):
+        matmul.anchor_tree(P_A, X_A, P_B, X_B, ar, [(8, 7)], width=8)
+    with pytest.raises(ValueError, match="drop must be one of"):
+        matmul.anchor_tree(P_A, X_A, P_B, X_B, ar, drop="floor")
+    with pytest.raises(ValueError, match="headroom 4 < 6: the sum of 17 terms could overflow"):
+        matmul.anchor_tree(P_A, X_A, P_B, X_B, ar, headroom=4)
+    with pytest.raises(ValueError, match=r"bits needs 6 non-increasing entries, each <= 24; got \[36, 36"):
+        matmul.anchor_tree(P_A, X_A, P_B, X_B, ar, [(8, 23)])
+    with pytest.raises(ValueError, match=r"bits needs 6 non-increasing entries"):
+        matmul.anchor_tree(P_A, X_A, P_B, X_B, ar, bits=[10, 12, 10, 10, 10, 10])
+    with pytest.raises(ValueError, match=r"bits needs 6 non-increasing entries"):
+        matmul.anchor_tree(P_A, X_A, P_B, X_B, ar, bits=[10] * 5)
+
+
 def test_formats_and_grids():
     with pytest.raises(ValueError, match="Unknown format 'FP7'"):
         formats.get("FP7")
