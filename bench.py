@@ -1,6 +1,6 @@
 """Benchmark: emulated MX GEMM throughput of matmul.systolic (bit-exact MXGEMMINI, HW_FINAL ladder) on one GPU,
-plus block-quantize HBM throughput, the LUT pipeline, the attention core and the matrix-core comparison product,
-each next to its roofline, and the oracle's CPU rate.
+plus block-quantize HBM throughput, the LUT pipeline, the attention core, the adder and anchor trees and the
+matrix-core comparison product, each next to its roofline, and the oracle's CPU rate.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
     python bench.py --copy-calibration        # only a 256 MiB device copy, 5 times (counter calibration)
@@ -183,6 +183,26 @@ def attend_line(torch, steps):
             "ms": round(ms, 3), "emulated_TOPs": round(2 * macs / ms / 1e9, 3)}
 
 
+def trees_line(torch, steps, P_A, X_A, P_B, X_B):
+    """The other two reducers on the benchmark's own codes (M = 512, N = 4096, K = 4096): matmul.adder_tree with
+    MXGEMMINI and bf16 at every level (size 16), matmul.anchor_tree with MXGEMMINI and its defaults (one
+    16-product tree per reduction, bf16 out, truncating 19-bit levels).  Emulated ops as for systolic."""
+    from mxq import matmul
+    dev = P_A.device
+    s = torch.cuda.current_stream(dev)
+    ar = matmul.MXGEMMINI()
+    macs = P_A.shape[0] * P_A.shape[1] * P_B.shape[1]
+    out = {"workload": "adder_tree (size 16, bf16 levels) and anchor_tree (defaults), MXGEMMINI, C2 codes"}
+    for name, fn in (("adder_tree", lambda: matmul.adder_tree(P_A, X_A, P_B, X_B, ar, [(8, 7)] * 4)),
+                     ("anchor_tree", lambda: matmul.anchor_tree(P_A, X_A, P_B, X_B, ar))):
+        fn()
+        ms = _events_ms(fn, steps, s)
+        kms, _ = _kernel_ms(fn, steps, name)
+        out[name] = {"ms": round(ms, 3), "kernel_ms": round(kms, 3) if kms else None,
+                     "emulated_TOPs": round(2 * macs / (kms or ms) / 1e9, 3)}
+    return out
+
+
 def mfma_line(torch, steps, P_A, X_A, P_B, X_B):
     """mfma_accum (the matrix-core comparison product) on the benchmark's own codes: pack both operands to FP8
     and E8M0 bytes, then V_MFMA_SCALE_F32_32X32X64_F8F6F4.  The kernel rate is held against MI355X's dense FP8
@@ -280,6 +300,7 @@ def main():
         line["lut_c4"] = lut_line(torch, 3)
         line["attend_c5"] = attend_line(torch, 3)
         line["mfma_c2"] = mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B)
+        line["trees_c2"] = trees_line(torch, 3, P_A, X_A, P_B, X_B)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_systolic(P_A, X_A, P_B, X_B, cols=160)
     print(json.dumps(line), flush=True)

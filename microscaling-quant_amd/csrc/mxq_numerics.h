@@ -460,12 +460,25 @@ MXQ_HD float mxg_lane(float x, int e, int m) {
   return unsigned_zero(r);
 }
 
+// exact_add of two lane values of a bf16 (8, 7) or float32 (8, 23) lane.  Both operands already sit on the
+// lane's grid, so the float32 sum rounded to the lane is the exact sum rounded once: for (8, 23) the float32 add
+// is that rounding; for bf16 a float32 add then RNE to 8 significant bits is a double rounding that cannot
+// differ from one (24 >= 2 * 8 + 1), bf16 subnormal sums are exact in float32, and overflow goes to Inf either
+// way.  Zeros short-circuit as exact_add's do.
+MXQ_HD float wide_lane_add(float a, float b, int m) {
+  if (a == 0.0f) return b;
+  if (b == 0.0f) return a;
+  const float s = a + b;
+  return m == 7 ? bf16_rne(s) : s;
+}
+
 // MXGEMMINI acc_add (mxq/matmul/_arithmetic.py:132) and tile_add (:133).
 MXQ_HD float mxg_acc_add(float S, float p, int e, int m) {
+  if (e == 8 && (m == 7 || m == 23)) return wide_lane_add(mxg_lane(S, e, m), mxg_lane(p, e, m), m);
   return exact_add(mxg_lane(S, e, m), mxg_lane(p, e, m), e, m, MXQ_RNE, MXQ_GRID_IEEE, 0.0f);
 }
 MXQ_HD float mxg_tile_add(float C, float tile) {
-  return exact_add(mxg_lane(C, 8, 7), mxg_lane(tile, 8, 7), 8, 7, MXQ_RNE, MXQ_GRID_IEEE, 0.0f);
+  return wide_lane_add(mxg_lane(C, 8, 7), mxg_lane(tile, 8, 7), 7);
 }
 // MXGEMMINI product (mxq/matmul/_arithmetic.py:131): saturate(flush(truncate(a * b, prod_m))).
 MXQ_HD float mxg_product(float a, float b, int prod_m, bool do_flush, float flush_thr, float limit, float value) {

@@ -11,7 +11,7 @@
 //   k_anchor_tree<WIDTH> one output per thread.  Per tree of the reduction: pass 1 takes the anchor, the
 //                        largest label among the nonzero products (code-exponent sums, frexp's, clamped at
 //                        emin when asked) and the running sum c (its exponent minus one), plus headroom;
-//                        pass 2 recomputes the products, cuts each and c to integers on the grid
+//                        pass 2 cuts each product (kept in registers from pass 1) and c to integers on the grid
 //                        2^(anchor + 2 - bits[0]) (toward zero or to nearest even), then adds adjacent pairs
 //                        level by level in float64 (exact: integers below 2^25), c last, an odd term passed up,
 //                        regridding where the level width falls; the root goes to float32 once and through the
@@ -205,13 +205,16 @@ __global__ void __launch_bounds__(256) k_anchor_tree(const TreeArgs args) {
       float c = 0.0f;
       for (int t = 0; t < trees; ++t) {
         const int base = r0 + t * WIDTH;
-        // S1: the anchor
+        // S1: the anchor (the products are kept for S2)
         int top = c != 0.0f ? frexp_label(c) - 1 : INT_MIN;
+        float pv[WIDTH];
 #pragma unroll
         for (int j = 0; j < WIDTH; ++j) {
+          pv[j] = 0.0f;
           if (t * WIDTH + j >= cnt) continue;
           const float a = sm.a[buf][base + j][tm], b = sm.b[buf][base + j][tn];
-          if (gen_product(a, b, args.ar) == 0.0f) continue;
+          pv[j] = gen_product(a, b, args.ar);
+          if (pv[j] == 0.0f) continue;
           int lab = frexp_label(a), lbb = frexp_label(b);
           if (args.has_emin) {
             lab = max(lab, args.emin);
@@ -224,11 +227,7 @@ __global__ void __launch_bounds__(256) k_anchor_tree(const TreeArgs args) {
         const int g0 = anchor + 2 - args.bits[t][0];
         double x[NTERMS];
 #pragma unroll
-        for (int j = 0; j < WIDTH; ++j) {
-          const float a = sm.a[buf][base + j][tm], b = sm.b[buf][base + j][tn];
-          const float p = t * WIDTH + j < cnt ? gen_product(a, b, args.ar) : 0.0f;
-          x[j] = keep(ldexp((double)p, -g0), rne);
-        }
+        for (int j = 0; j < WIDTH; ++j) x[j] = keep(ldexp((double)pv[j], -g0), rne);
         x[WIDTH] = keep(ldexp((double)c, -g0), rne);
         // S3: adjacent pairs level by level, an odd last term passed up, regridding where the width falls
         int n = NTERMS;
