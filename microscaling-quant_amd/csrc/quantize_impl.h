@@ -130,50 +130,69 @@ __global__ void __launch_bounds__(256) k_quant_strided(const T* __restrict__ V, 
 // partial maxima meet through cross-lane exchanges.  Few values per lane keep many waves resident, which is
 // what hides the HBM latency here (measured on MI355X: R = 8, VEC = 4 is the fastest layout on 8192 x 8192
 // bf16 and on 4096 x 512 float32).
+//   * The wave's index is uniform, so the (outer, block, column-group) split of it runs in scalar registers.
+//   * A whole block (all but a tail) loads without per-row conditions; lanes past the last column group read
+//     column group 0 (valid memory) and store nothing.
+//   * The block maximum is the largest |v| bit pattern (non-negative floats order like their patterns, and
+//     every NaN pattern lies above +Inf, so a NaN wins as torch.amax's does).
+//   * The R lanes of a column group hold the same maxima after the exchanges; lane r < VEC computes the scale
+//     of column r alone and the others read it (one scale rule evaluation per lane instead of VEC).
 template <typename T, int ELEM, int MODE, int VEC, int R>
 __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, float* __restrict__ P,
                                                      float* __restrict__ X, int64_t outer, int64_t n, int64_t inner,
                                                      int64_t nb, int64_t waves_per_row, mxq_block_spec s) {
   constexpr int CPW = 64 / R;          // column groups per wave
   constexpr int ROWS = 32 / R;         // rows per lane
+  static_assert(VEC <= R, "one scale-computing lane per column");
   const int64_t groups = inner / VEC;
   const int lane = threadIdx.x & 63;
-  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t wave = (int64_t)blockIdx.x * (256 / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wave >= outer * nb * waves_per_row) return;    // whole waves only: the exchanges below see every lane
   const int64_t wr = wave / waves_per_row;           // (o, b) flattened
-  const int64_t cg = (wave - wr * waves_per_row) * CPW + (lane % CPW);
-  const int r = lane / CPW;
-  const int64_t o = wr / nb, b = wr - (wr / nb) * nb;
-  const bool live = cg < groups;
+  const int64_t o = wr / nb, b = wr - o * nb;
   const int64_t k0 = b * 32;
-  const int64_t rows = (n - k0 < 32) ? n - k0 : 32;
-  const int64_t off = (o * n + k0) * inner + cg * VEC;
+  const int rows = (int)((n - k0 < 32) ? n - k0 : 32);
+  const int c = lane % CPW, r = lane / CPW;
+  const int64_t cg = (wave - wr * waves_per_row) * CPW + c;
+  const bool live = cg < groups;
+  const T* src = V + (o * n + k0 + r * ROWS) * inner + (live ? cg : 0) * VEC;
 
   float v[ROWS][VEC];
-  float amax[VEC];
+  uint32_t am[VEC];
 #pragma unroll
-  for (int j = 0; j < VEC; ++j) amax[j] = 0.0f;
+  for (int j = 0; j < VEC; ++j) am[j] = 0u;
+  if (rows == 32) {
 #pragma unroll
-  for (int i = 0; i < ROWS; ++i) {
-    const int row = r * ROWS + i;
-    if (live && row < rows) {
-      load_vec<T, VEC>(V + off + (int64_t)row * inner, v[i]);
-    } else {
+    for (int i = 0; i < ROWS; ++i) load_vec<T, VEC>(src + (int64_t)i * inner, v[i]);
+  } else {
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) v[i][j] = 0.0f;
+    for (int i = 0; i < ROWS; ++i) {
+      if (r * ROWS + i < rows) {
+        load_vec<T, VEC>(src + (int64_t)i * inner, v[i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) v[i][j] = 0.0f;
+      }
     }
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) amax[j] = amax_combine(amax[j], fabsf(v[i][j]));
   }
+#pragma unroll
+  for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) am[j] = max(am[j], f2u(v[i][j]) & 0x7FFFFFFFu);
 #pragma unroll
   for (int step = CPW; step < 64; step <<= 1)
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) amax[j] = amax_combine(amax[j], __shfl_xor(amax[j], step, 64));
-  Div d[VEC];
+    for (int j = 0; j < VEC; ++j) am[j] = max(am[j], (uint32_t)__shfl_xor((int)am[j], step, 64));
+  // lane r < VEC: the scale of column r of its group; every lane then reads column j's from lane c + j * CPW
+  uint32_t mine = am[0];
+#pragma unroll
+  for (int j = 1; j < VEC; ++j) mine = (r == j) ? am[j] : mine;
+  const float own = block_scale(u2f(mine), s);
   float xs[VEC];
+  Div d[VEC];
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
-    xs[j] = block_scale(amax[j], s);
+    xs[j] = __shfl(own, c + j * CPW, 64);
     d[j] = make_div(xs[j]);
   }
   if (s.scale_rule && wave_needs_div<VEC>(d)) {
@@ -188,14 +207,14 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, fl
       for (int j = 0; j < VEC; ++j) v[i][j] = v[i][j] * d[j].inv;
   }
   if (!live) return;
+  float* dst = P + (o * n + k0 + r * ROWS) * inner + cg * VEC;
 #pragma unroll
   for (int i = 0; i < ROWS; ++i) {
-    const int row = r * ROWS + i;
-    if (row < rows) {
+    if (rows == 32 || r * ROWS + i < rows) {
       float q[VEC];
 #pragma unroll
       for (int j = 0; j < VEC; ++j) q[j] = elem_qm<ELEM, MODE>(v[i][j], s);
-      store_vec_nt<VEC>(P + off + (int64_t)row * inner, q);
+      store_vec_nt<VEC>(dst + (int64_t)i * inner, q);
     }
   }
   if (r == 0) store_vec<VEC>(X + (o * nb + b) * inner + cg * VEC, xs);
