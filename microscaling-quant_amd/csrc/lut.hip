@@ -30,33 +30,85 @@ __device__ __forceinline__ int lower_bound_f(const float* a, int n, float v) {
   return lo;
 }
 
+// Grid values of the LUT formats have at most 4 significand bits past the leading one, so a value's top
+// 9 + kGridKeyBits bits (sign, exponent, first mantissa bits) name its grid index; the low bits must be zero.
+constexpr int kGridKeyBits = 4;
+constexpr int kGridKeys = 1 << (9 + kGridKeyBits);
+
 // blockDim = 256; CB columns per block, 256 / CB row lanes per column; rows [k0, k0 + rows_per_block).
+// Each code is placed by its key in an LDS table built from the grid (one load), when every grid value has at
+// most kGridKeyBits fraction bits; otherwise by binary search.  A value is counted only when it equals a grid
+// value (-0 counts as the 0 bin, as == says); anything else sets the error flag.
 __global__ void __launch_bounds__(256) k_lut_hist(const float* __restrict__ P, int64_t K, int64_t n, int group,
                                                   const float* __restrict__ grid, int nv, int CB,
                                                   int64_t rows_per_block, int* __restrict__ counts,
                                                   int* __restrict__ err) {
-  extern __shared__ int hist[];                      // (CB >> group, at least 1) x nv
+  extern __shared__ int hist[];                      // (CB >> group, at least 1) x nv, then the key table
   __shared__ float g_s[kMaxGrid];
+  __shared__ int frac_bits;
   const int64_t c0 = (int64_t)blockIdx.x * CB;
   const int64_t k0 = (int64_t)blockIdx.y * rows_per_block;
   const int gpb = (CB >> group) > 0 ? (CB >> group) : 1;
+  short* key = reinterpret_cast<short*>(hist + gpb * nv);
+  if (threadIdx.x == 0) frac_bits = 0;
   for (int i = threadIdx.x; i < gpb * nv; i += blockDim.x) hist[i] = 0;
-  for (int i = threadIdx.x; i < nv; i += blockDim.x) g_s[i] = grid[i];
+  // the key table is 16-byte aligned when gpb * nv is a multiple of 4; clear it 8 entries per store then
+  if ((gpb * nv) % 4 == 0) {
+    int4* k4 = reinterpret_cast<int4*>(key);
+    for (int i = threadIdx.x; i < kGridKeys / 8; i += blockDim.x) k4[i] = make_int4(-1, -1, -1, -1);
+  } else {
+    for (int i = threadIdx.x; i < kGridKeys; i += blockDim.x) key[i] = -1;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nv; i += blockDim.x) {
+    const float gv = grid[i];
+    g_s[i] = gv;
+    const uint32_t mant = f2u(gv) & 0x007FFFFFu;
+    atomicMax(&frac_bits, mant ? 23 - __builtin_ctz(mant) : 0);
+  }
+  __syncthreads();
+  const bool keyed = frac_bits <= kGridKeyBits;
+  constexpr int sh = 23 - kGridKeyBits;
+  if (keyed) {
+    for (int i = threadIdx.x; i < nv; i += blockDim.x) {
+      key[f2u(g_s[i]) >> sh] = (short)i;
+      if (g_s[i] == 0.0f) {                            // the grid's zero (either sign) takes +0 and -0
+        key[0u] = (short)i;
+        key[0x80000000u >> sh] = (short)i;
+      }
+    }
+  }
   __syncthreads();
   const int col = threadIdx.x % CB, rl = threadIdx.x / CB, nrl = blockDim.x / CB;
   const int64_t j = c0 + col;
   const int64_t g0 = c0 >> group;
+  int* h = hist + (int)((j >> group) - g0) * nv;
   bool bad = false;
   if (j < n) {
     const int64_t kend = (k0 + rows_per_block < K) ? k0 + rows_per_block : K;
-    for (int64_t k = k0 + rl; k < kend; k += nrl) {
-      const float v = P[k * n + j];
-      const int b = lower_bound_f(g_s, nv, v);
-      if (b >= nv || !(g_s[b] == v)) {
-        bad = true;
-        continue;
+    constexpr int U = 16;                              // loads in flight per thread before binning them
+    for (int64_t kb = k0 + rl; kb < kend; kb += (int64_t)U * nrl) {
+      float v[U];
+#pragma unroll
+      for (int t = 0; t < U; ++t) {
+        const int64_t k = kb + (int64_t)t * nrl;
+        v[t] = k < kend ? P[k * n + j] : 0.0f;
       }
-      atomicAdd(&hist[(int)((j >> group) - g0) * nv + b], 1);
+#pragma unroll
+      for (int t = 0; t < U; ++t) {
+        if (kb + (int64_t)t * nrl >= kend) break;
+        int b;
+        if (keyed) {
+          const uint32_t u = f2u(v[t]);
+          b = key[u >> sh];
+          if (b < 0 || (u & ((1u << sh) - 1u))) b = -1;
+        } else {
+          b = lower_bound_f(g_s, nv, v[t]);
+          if (b >= nv || !(g_s[b] == v[t])) b = -1;
+        }
+        if (b < 0) bad = true;
+        else atomicAdd(&h[b], 1);
+      }
     }
   }
   if (bad) atomicOr(err, 1);
@@ -69,77 +121,141 @@ __global__ void __launch_bounds__(256) k_lut_hist(const float* __restrict__ P, i
   }
 }
 
-// sort 16 doubles ascending (insertion sort; +inf last), then duplicates -> +inf and sort again
-__device__ void dedupe16(double* c) {
-  for (int i = 1; i < kSize; ++i) {
-    const double x = c[i];
-    int j = i - 1;
-    while (j >= 0 && c[j] > x) { c[j + 1] = c[j]; --j; }
-    c[j + 1] = x;
+// The 16 values held by lanes 0..15 sorted ascending across those lanes (bitonic network), equal values kept
+// in lane order, as a stable sort leaves them.  Lanes 16..63 take part in
+// their own 16-lane groups and are ignored.
+__device__ __forceinline__ double sort16_lanes(double v, int lane) {
+  int idx = lane;
+#pragma unroll
+  for (int k = 2; k <= kSize; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const double pv = __shfl_xor(v, j, 64);
+      const int pi = __shfl_xor(idx, j, 64);
+      const bool up = (lane & k) == 0;                     // this pair sorts ascending
+      const bool lower = (lane & j) == 0;                  // this lane is the pair's lower position
+      const bool p_first = pv < v || (pv == v && pi < idx);
+      // the lower position of an ascending pair takes the first of the two; the upper takes the second
+      const bool take = (lower == up) ? p_first : !p_first;
+      if (take) {
+        v = pv;
+        idx = pi;
+      }
+    }
   }
-  bool dup[kSize];
-  dup[0] = false;
-  for (int i = 1; i < kSize; ++i) dup[i] = c[i] == c[i - 1];
-  for (int i = 1; i < kSize; ++i) if (dup[i]) c[i] = d_inf();
-  for (int i = 1; i < kSize; ++i) {
-    const double x = c[i];
-    int j = i - 1;
-    while (j >= 0 && c[j] > x) { c[j + 1] = c[j]; --j; }
-    c[j + 1] = x;
-  }
+  return v;
 }
 
 __device__ __forceinline__ bool is_finite_d(double x) { return (d2u(x) & 0x7FF0000000000000ull) != 0x7FF0000000000000ull; }
 
-// one 64-lane workgroup per table
+// Wave-wide helpers for the table kernel (one 64-lane wavefront per table).
+// Number of lanes below this one whose flag is set.
+__device__ __forceinline__ int lanes_below(bool flag, int lane) {
+  const unsigned long long m = __ballot(flag);
+  return __popcll(m & ((1ull << lane) - 1ull));
+}
+// Inclusive prefix sum of one double per lane (exact here: integer counts).
+__device__ __forceinline__ double wave_scan(double v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const double u = __shfl_up(v, off, 64);
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+
+// One 64-lane workgroup per table; lane i handles grid bins i, i + 64, ... (nv <= 256: four rounds).
+//   seeds   the present values when 16 or fewer (in grid order); else the quantile seeds: bin cdf =
+//           cumsum(counts) / total (exact integer prefix sums, the same float64 division per bin), seed i the
+//           first bin whose cdf reaches (i + 0.5) / 16, found with ballots; then a sort, duplicate
+//           removal and sort, across lanes 0..15
+//   Lloyd   lanes own bins for the nearest-centre step (first minimum), float64 LDS sums (exact, so their
+//           order does not matter), lane c < 16 updates centre c, the same dedupe, allclose by wave vote
+//   snap    lane c < 16: the nearest safe value to centre c (first minimum); the distinct ones are the table's
+//           members; the unused safe values in safe_order order fill it to 16 (ranks by ballot); the members
+//           are written in ascending order, +Inf past them
 __global__ void __launch_bounds__(64) k_lut_kmeans(const int* __restrict__ counts, int nv, const float* __restrict__ grid,
                                                    const float* __restrict__ safe, int ns,
                                                    const int* __restrict__ safe_order, int max_iters,
                                                    float* __restrict__ T) {
+  constexpr int kRounds = kMaxGrid / 64;
   __shared__ double x_s[kMaxGrid];
   __shared__ double w_s[kMaxGrid];
-  __shared__ double C[kSize], Cn[kSize];
+  __shared__ double C[kSize];
   __shared__ double sums[kSize], wsum[kSize];
+  __shared__ float safe_s[kMaxGrid];
+  __shared__ int order_s[kMaxGrid];
   __shared__ unsigned char member[kMaxGrid];
-  __shared__ int stop;
   const int g = blockIdx.x, lane = threadIdx.x;
   for (int i = lane; i < nv; i += 64) {
     x_s[i] = (double)grid[i];
     w_s[i] = (double)counts[(int64_t)g * nv + i];
   }
-  __syncthreads();
-  if (lane == 0) {
-    int npres = 0;
-    for (int i = 0; i < nv; ++i) npres += (w_s[i] > 0.0);
-    for (int i = 0; i < kSize; ++i) C[i] = d_inf();
-    if (npres <= kSize) {
-      int r = 0;
-      for (int i = 0; i < nv; ++i) if (w_s[i] > 0.0) C[r++] = x_s[i];
-      stop = 1;
-    } else {
-      // quantile seeds: first bin whose cumulative weight reaches (i + 0.5) / 16 of the total
-      double total = 0.0;
-      for (int i = 0; i < nv; ++i) total += w_s[i];
-      int s = 0;
-      double cum = 0.0;
-      int b = 0;
-      for (int i = 0; i < kSize; ++i) {
-        const double probe = ((double)i + 0.5) / (double)kSize;
-        // advance to the first b with cdf[b] >= probe (cdf is non-decreasing; cum holds cumsum up to b)
-        while (b < nv) {
-          const double cdf = (cum + w_s[b]) / total;
-          if (cdf >= probe) break;
-          cum += w_s[b];
-          ++b;
-        }
-        s = b < nv ? b : nv - 1;
-        C[i] = x_s[s];
-      }
-      dedupe16(C);
-      stop = max_iters > 0 ? 0 : 1;
-    }
+  for (int i = lane; i < ns; i += 64) {
+    safe_s[i] = safe[i];
+    order_s[i] = safe_order[i];
+    member[i] = 0;
   }
   __syncthreads();
+
+  // ---- seeds
+  int npres = 0;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int i = r * 64 + lane;
+    npres += __popcll(__ballot(i < nv && w_s[i] > 0.0));
+  }
+  double cen = d_inf();                                // lane c < 16: centre c
+  bool stop;
+  if (npres <= kSize) {
+    int base = 0;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      const int i = r * 64 + lane;
+      const bool pres = i < nv && w_s[i] > 0.0;
+      const int rank = base + lanes_below(pres, lane);
+      if (pres) C[rank] = x_s[i];
+      base += __popcll(__ballot(pres));
+    }
+    if (lane >= npres && lane < kSize) C[lane] = d_inf();
+    __syncthreads();
+    if (lane < kSize) cen = C[lane];
+    stop = true;
+  } else {
+    double cum[kRounds];
+    double carry = 0.0;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      const int i = r * 64 + lane;
+      const double incl = wave_scan(i < nv ? w_s[i] : 0.0, lane) + carry;
+      cum[r] = incl;
+      carry = __shfl(incl, 63, 64);
+    }
+    const double total = carry;
+    double cdf[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) cdf[r] = cum[r] / total;
+    for (int q = 0; q < kSize; ++q) {
+      const double probe = ((double)q + 0.5) / (double)kSize;
+      int first = nv;                                  // no bin reaches the probe: the last bin
+#pragma unroll
+      for (int r = kRounds - 1; r >= 0; --r) {
+        const int i = r * 64 + lane;
+        const unsigned long long m = __ballot(i < nv && cdf[r] >= probe);
+        if (m) first = r * 64 + __ffsll((long long)m) - 1;
+      }
+      if (lane == q) cen = x_s[first < nv ? first : nv - 1];
+    }
+    cen = sort16_lanes(cen, lane);
+    const double below = __shfl_up(cen, 1, 64);
+    if (lane > 0 && lane < kSize && cen == below) cen = d_inf();
+    cen = sort16_lanes(cen, lane);
+    if (lane < kSize) C[lane] = cen;
+    stop = max_iters <= 0;
+  }
+  __syncthreads();
+
+  // ---- Lloyd passes
   for (int it = 0; it < max_iters && !stop; ++it) {
     if (lane < kSize) { sums[lane] = 0.0; wsum[lane] = 0.0; }
     __syncthreads();
@@ -159,47 +275,74 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(const int* __restrict__ count
       }
     }
     __syncthreads();
-    if (lane == 0) {
-      for (int c = 0; c < kSize; ++c) Cn[c] = (wsum[c] > 0.0) ? sums[c] / wsum[c] : C[c];
-      dedupe16(Cn);
-      bool same = true;
-      for (int c = 0; c < kSize; ++c) {
-        const bool valid = is_finite_d(C[c]);
-        if (is_finite_d(Cn[c]) != valid) same = false;
-        if (valid) {
-          const double tol = 1e-8 + 1e-5 * fabs(C[c]);
-          if (!(fabs(Cn[c] - C[c]) <= tol)) same = false;
-        }
-      }
-      if (same) stop = 1;
-      else for (int c = 0; c < kSize; ++c) C[c] = Cn[c];
+    // lane c < 16: the new centre c (the old one when its cluster is empty), the dedupe, allclose by vote
+    double cn = d_inf();
+    if (lane < kSize) cn = (wsum[lane] > 0.0) ? sums[lane] / wsum[lane] : C[lane];
+    cn = sort16_lanes(cn, lane);
+    const double below = __shfl_up(cn, 1, 64);
+    if (lane > 0 && lane < kSize && cn == below) cn = d_inf();
+    cn = sort16_lanes(cn, lane);
+    bool same = true;
+    if (lane < kSize) {
+      const double old_c = C[lane];
+      const bool valid = is_finite_d(old_c);
+      if (is_finite_d(cn) != valid) same = false;
+      if (valid && !(fabs(cn - old_c) <= 1e-8 + 1e-5 * fabs(old_c))) same = false;
     }
+    stop = __all(same);
+    __syncthreads();                                   // every lane has read C
+    if (!stop && lane < kSize) C[lane] = cn;
     __syncthreads();
   }
-  if (lane == 0) {
-    // snap each finite centre to the nearest safe value (first minimum: the smaller one on a tie)
-    for (int i = 0; i < ns; ++i) member[i] = 0;
-    int cnt = 0;
-    for (int c = 0; c < kSize; ++c) {
-      if (!is_finite_d(C[c])) continue;
+
+  // ---- snap to the safe values, pad, write in ascending order
+  if (lane < kSize) {
+    const double c = C[lane];
+    if (is_finite_d(c)) {
       int best = 0;
-      double bd = fabs(C[c] - (double)safe[0]);
+      double bd = fabs(c - (double)safe_s[0]);
       for (int i = 1; i < ns; ++i) {
-        const double d = fabs(C[c] - (double)safe[i]);
+        const double d = fabs(c - (double)safe_s[i]);
         if (d < bd) { bd = d; best = i; }
       }
-      if (!member[best]) { member[best] = 1; ++cnt; }
+      member[best] = 1;
     }
-    // pad with unused safe values, smallest magnitude first (negative before positive)
-    int need = kSize - cnt;
-    for (int q = 0; q < ns && need > 0; ++q) {
-      const int i = safe_order[q];
-      if (!member[i]) { member[i] = 1; --need; }
-    }
-    int r = 0;
-    for (int i = 0; i < ns && r < kSize; ++i) if (member[i]) T[(int64_t)g * kSize + r++] = safe[i];
-    for (; r < kSize; ++r) T[(int64_t)g * kSize + r] = f_inf();
   }
+  __syncthreads();
+  int cnt = 0;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int i = r * 64 + lane;
+    cnt += __popcll(__ballot(i < ns && member[i]));
+  }
+  int need = kSize - cnt;
+  // unused safe values in safe_order order, the first `need` of them
+  bool take[kRounds];
+  int base = 0;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int q = r * 64 + lane;
+    const bool unused = q < ns && !member[order_s[q]];
+    take[r] = unused && base + lanes_below(unused, lane) < need;
+    base += __popcll(__ballot(unused));
+  }
+  __syncthreads();                                     // every lane has read member
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int q = r * 64 + lane;
+    if (take[r]) member[order_s[q]] = 1;
+  }
+  __syncthreads();
+  base = 0;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int i = r * 64 + lane;
+    const bool mem = i < ns && member[i];
+    const int rank = base + lanes_below(mem, lane);
+    if (mem && rank < kSize) T[(int64_t)g * kSize + rank] = safe_s[i];
+    base += __popcll(__ballot(mem));
+  }
+  if (lane >= base && lane < kSize) T[(int64_t)g * kSize + lane] = f_inf();
 }
 
 // Nearest entry of each code's group table (ascending; ties to the lower index).  mode 0: int64 index to I;
@@ -222,16 +365,24 @@ __global__ void __launch_bounds__(256) k_lut_pick(const float* __restrict__ P, i
   const float* row = rows_s + (int)((j >> group) - g0) * width;
   const int64_t k0 = (int64_t)blockIdx.y * rows_per_block;
   const int64_t kend = (k0 + rows_per_block < K) ? k0 + rows_per_block : K;
-  for (int64_t k = k0; k < kend; ++k) {
-    const float v = P[k * n + j];
-    int hi = lower_bound_f(row, width, v);
-    hi = hi < 1 ? 1 : (hi > width - 1 ? width - 1 : hi);
-    const int lo = hi - 1;
-    const float d_lo = fabsf(v - row[lo]);
-    const float d_hi = fabsf(row[hi] - v);
-    const int pick = (d_lo <= d_hi) ? lo : hi;
-    if (I) I[k * n + j] = pick;
-    else Pout[k * n + j] = row[pick];
+  constexpr int U = 8;                                 // loads in flight per thread
+  for (int64_t kb = k0; kb < kend; kb += U) {
+    float v[U];
+#pragma unroll
+    for (int t = 0; t < U; ++t) v[t] = kb + t < kend ? P[(kb + t) * n + j] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < U; ++t) {
+      const int64_t k = kb + t;
+      if (k >= kend) break;
+      int hi = lower_bound_f(row, width, v[t]);
+      hi = hi < 1 ? 1 : (hi > width - 1 ? width - 1 : hi);
+      const int lo = hi - 1;
+      const float d_lo = fabsf(v[t] - row[lo]);
+      const float d_hi = fabsf(row[hi] - v[t]);
+      const int pick = (d_lo <= d_hi) ? lo : hi;
+      if (I) I[k * n + j] = pick;
+      else Pout[k * n + j] = row[pick];
+    }
   }
 }
 
@@ -293,15 +444,17 @@ extern "C" int mxq_lut_tables(const float* P, int64_t K, int64_t n, int32_t grou
   if (K > 0) {
     // columns per block: the LDS histogram (groups x nv ints) within 64 KiB
     int CB = 256;
-    while (CB > 1 && (int64_t)(((CB >> group) > 0 ? (CB >> group) : 1)) * nv * 4 > 65536) CB >>= 1;
+    while (CB > 1 && (int64_t)(((CB >> group) > 0 ? (CB >> group) : 1)) * nv * 4 + kGridKeys * 2 > 65536) CB >>= 1;
     const int64_t col_blocks = mxq::ceil_div(n, CB);
-    int64_t row_blocks = mxq::ceil_div(4096, col_blocks);             // aim at several thousand blocks in all
+    // about two blocks per CU: every block adds its histogram into the global counts with one atomic per
+    // nonzero bin, so fewer, taller blocks (each thread bins a long stripe, 16 loads in flight) do best
+    int64_t row_blocks = mxq::ceil_div(512, col_blocks);
     if (row_blocks > K) row_blocks = K;
     if (row_blocks < 1) row_blocks = 1;
     if (row_blocks > 65535) row_blocks = 65535;
     const int64_t rpb = mxq::ceil_div(K, row_blocks);
     row_blocks = mxq::ceil_div(K, rpb);
-    const size_t lds = (size_t)((CB >> group) > 0 ? (CB >> group) : 1) * nv * sizeof(int);
+    const size_t lds = (size_t)((CB >> group) > 0 ? (CB >> group) : 1) * nv * sizeof(int) + kGridKeys * sizeof(short);
     k_lut_hist<<<dim3((unsigned)col_blocks, (unsigned)row_blocks), 256, lds, st>>>(P, K, n, group, grid, nv, CB, rpb,
                                                                                      counts, err);
     if (int rc = mxq::check_launch("mxq_lut_tables histogram")) return rc;
@@ -321,7 +474,7 @@ extern "C" int mxq_lut_pick(const float* P, int64_t K, int64_t n, int32_t group,
   const size_t lds = (size_t)((256 >> group) > 0 ? (256 >> group) : 1) * width * sizeof(float);
   if (lds > 65536) return mxq::invalid("mxq_lut_pick: tables too wide");
   const int64_t col_blocks = mxq::ceil_div(n, 256);
-  int64_t row_blocks = mxq::ceil_div(8192, col_blocks);
+  int64_t row_blocks = mxq::ceil_div(1024, col_blocks);             // about four blocks per CU, long stripes
   if (row_blocks > K) row_blocks = K;
   if (row_blocks > 65535) row_blocks = 65535;
   const int64_t rpb = mxq::ceil_div(K, row_blocks);
