@@ -187,3 +187,29 @@ def test_elementwise_scale_and_arith(cuda, corpus):
     assert_bits_equal(arith.truncate_significand(x, 3).cpu().numpy(), nx.truncate_significand(corpus, 3), "trunc")
     assert_bits_equal(arith.flush_product(x, -16).cpu().numpy(), nx.flush_product(corpus, -16), "flush")
     assert_bits_equal(arith.saturate(x, 448.0, 448.0).cpu().numpy(), nx.saturate(corpus, 448.0, 448.0), "sat")
+
+
+def test_c3_full_size_column_slices(cuda):
+    """The bf16 sweep at its full size, 8192 x 8192 (Student-t(3) x 0.5 with 0.1% of entries x 100): each
+    format's whole GPU result, checked bit for bit against the oracle on the first and the last 64 columns at
+    full height (axis-0 blocks keep columns independent), and the dequantized slice against P * X."""
+    from mxq import block
+    torch.manual_seed(2)
+    t = torch.distributions.StudentT(torch.tensor(3.0)).sample((8192, 8192)) * 0.5
+    idx = torch.randperm(8192 * 8192, generator=torch.Generator().manual_seed(2))[:67109]
+    t.view(-1)[idx] *= 100
+    V = t.to(torch.bfloat16)
+    del t
+    Vd = V.cuda()
+    cols = [slice(0, 64), slice(8128, 8192)]
+    V32 = [V[:, c].to(torch.float32).numpy() for c in cols]
+    for fmt in FMTS:
+        P, X = block.mxgemmini.quantize(Vd, fmt, axis=0, rounding_mode="rne")
+        assert P.shape == (8192, 8192) and X.shape == (256, 8192)
+        for c, v32 in zip(cols, V32):
+            wP, wX = ob.mxgemmini_quantize(v32, fmt, 0, 32, "rne")
+            assert_bits_equal(P[:, c].cpu().numpy(), wP, f"C3 P {fmt} {c}")
+            assert_bits_equal(X[:, c].cpu().numpy(), wX, f"C3 X {fmt} {c}")
+            D = block.mxgemmini.dequantize(P[:, c].contiguous(), X[:, c].contiguous(), axis=0).cpu().numpy()
+            assert_bits_equal(D, ob.dequantize(wP, wX, 0), f"C3 dequantize {fmt} {c}")
+        del P, X
