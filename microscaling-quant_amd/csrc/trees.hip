@@ -13,7 +13,7 @@
 //                        emin when asked) and the running sum c (its exponent minus one), plus headroom;
 //                        pass 2 cuts each product (kept in registers from pass 1) and c to integers on the grid
 //                        2^(anchor + 2 - bits[0]) (toward zero or to nearest even), then adds adjacent pairs
-//                        level by level in float64 (exact: integers below 2^25), c last, an odd term passed up,
+//                        level by level in float32 (exact: integers below 2^24), c last, an odd term passed up,
 //                        regridding where the level width falls; the root goes to float32 once and through the
 //                        Arithmetic's lane rounding (acc_add of +0 and the root).
 #include <climits>
@@ -156,17 +156,19 @@ __global__ void __launch_bounds__(256) k_adder_tree(const TreeArgs args) {
   }
 }
 
-// floor(log2|x|) as frexp gives it for a finite nonzero float; -1 for zero and non-finite values
-// (mxq/matmul/_anchor.py:36-42).
+// floor(log2|x|) as frexp gives it for a finite nonzero float (subnormals included); -1 for zero and non-finite
+// values (mxq/matmul/_anchor.py:36-42).
 __device__ __forceinline__ int frexp_label(float x) {
   const uint32_t a = f2u(x) & 0x7FFFFFFFu;
-  if (a == 0u || a >= 0x7F800000u) return -1;
-  const int be = (int)(a >> 23);
-  if (be > 0) return be - 127;
-  return -118 - __clz((int)a);                         // subnormal: 2^-149 times the significand bits
+  return (a == 0u || a >= 0x7F800000u) ? -1 : __builtin_amdgcn_frexp_expf(x) - 1;
 }
 
-__device__ __forceinline__ double keep(double x, bool rne) { return rne ? rint(x) : trunc(x); }
+// The grid terms as float32: every term is an integer below 2^(bits[0] - headroom) <= 2^23 (a term's label is at
+// most the anchor minus headroom and |term| < 2^(label + 2)), so are the width + 1 of them added in any order
+// (headroom >= ceil(log2(width + 1)) + 1), and regridding divides by powers of two: float32 holds all of it
+// exactly, as the reference's float64 does.  A term below 2^-126 after the shift rounds to an integer 0 either
+// way.  The root's scaling back is the one rounding, as the reference's float64-to-float32 cast.
+__device__ __forceinline__ float keep(float x, bool rne) { return rne ? rintf(x) : truncf(x); }
 
 template <int WIDTH>
 __global__ void __launch_bounds__(256) k_anchor_tree(const TreeArgs args) {
@@ -225,10 +227,10 @@ __global__ void __launch_bounds__(256) k_anchor_tree(const TreeArgs args) {
         const int anchor = (top == INT_MIN ? 0 : top) + args.headroom;
         // S2: every term on the grid 2^(anchor + 2 - bits[0]); products first, c last
         const int g0 = anchor + 2 - args.bits[t][0];
-        double x[NTERMS];
+        float x[NTERMS];
 #pragma unroll
-        for (int j = 0; j < WIDTH; ++j) x[j] = keep(ldexp((double)pv[j], -g0), rne);
-        x[WIDTH] = keep(ldexp((double)c, -g0), rne);
+        for (int j = 0; j < WIDTH; ++j) x[j] = keep(ldexpf(pv[j], -g0), rne);
+        x[WIDTH] = keep(ldexpf(c, -g0), rne);
         // S3: adjacent pairs level by level, an odd last term passed up, regridding where the width falls
         int n = NTERMS;
 #pragma unroll
@@ -242,11 +244,11 @@ __global__ void __launch_bounds__(256) k_anchor_tree(const TreeArgs args) {
           if (drop != 0) {
 #pragma unroll
             for (int i = 0; i < NTERMS; ++i)
-              if (i < n) x[i] = keep(ldexp(x[i], -drop), rne);
+              if (i < n) x[i] = keep(ldexpf(x[i], -drop), rne);
           }
         }
         // S4: one rounding to float32, then the tree's lane
-        const float s = (float)ldexp(x[0], anchor + 2 - args.bits[t][nb - 1]);
+        const float s = ldexpf(x[0], anchor + 2 - args.bits[t][nb - 1]);
         c = gen_acc(0.0f, s, args.fe[t], args.fm[t], args.ar);
       }
       C = gen_tile(C, c * scale, args.ar);
