@@ -124,6 +124,20 @@ int mxq_systolic_batched(const float* P_A, const float* X_A, const float* P_B, c
 /* uint32 elements of workspace mxq_systolic / mxq_systolic_batched need (at least 1). */
 int64_t mxq_systolic_workspace(int64_t M, int64_t N, int64_t count);
 
+/* attend's two elementwise steps on the scores, in place: S (Z problems x n heads x m queries x Tk keys, float32,
+ * contiguous) becomes r(r(S * scale) + mask_row), r the identity or (round_bf16 = 1) rounding.bf16; the add and its
+ * rounding are skipped when mask is NULL.  Query j of problem z reads the Tk contiguous floats at
+ * mask + (floor((z0 + z) / z_per_b) - floor(z0 / z_per_b)) * mask_b_stride + j * mask_row_stride: z0 is the first
+ * problem's global index, z_per_b the problems per batch row of the mask (mask_b_stride 0: one shared row set).
+ * Replaces mxq/nn/_attention.py:128-135 (`S = r(... * scale)`, `S = r(S + mb[...])`) for a batch of calls. */
+int mxq_scores_scale_mask(float* S, int64_t Z, int64_t n, int64_t m, int64_t Tk, float scale, const float* mask,
+                          int64_t mask_b_stride, int64_t mask_row_stride, int64_t z0, int64_t z_per_b,
+                          int32_t round_bf16, mxq_stream_t stream);
+
+/* out (C x R) = in (R x C) transposed, float32 row-major; in and out must not overlap.  Replaces the
+ * `P.t().contiguous()` of mxq/nn/_attention.py:139 for a batch of calls. */
+int mxq_transpose(const float* in, float* out, int64_t R, int64_t C, mxq_stream_t stream);
+
 /* The adder tree: the operands, Arithmetic, scales and output of mxq_systolic; each reduction of `size` products
  * (zeros past a K tail) summed by log2(size) levels of adjacent-pair acc_adds, level l in (level_e[l],
  * level_m[l]), the root rescaled and tile-added into C.  size: a power of two in [2, 32] dividing block_size.

@@ -64,6 +64,9 @@ SIGNATURES = {
                                      c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32, ctypes.POINTER(ArithSpec),
                                      c_ptr, c_i32, c_ptr]),
     "mxq_systolic_workspace": (c_i64, [c_i64, c_i64, c_i64]),
+    "mxq_scores_scale_mask": (c_i32, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64, c_i64, c_i64, c_i64,
+                                      c_i32, c_ptr]),
+    "mxq_transpose": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_ptr]),
     "mxq_adder_tree": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,
                                ctypes.POINTER(ArithSpec), c_ptr]),
     "mxq_anchor_tree": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i32,

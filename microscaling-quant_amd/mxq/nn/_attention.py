@@ -284,13 +284,12 @@ class _Batched:
                                              ld_b=KT_P.shape[1], batch_b=Tk, ld_xb=KT_X.shape[1], batch_xb=Tk,
                                              ld_c=Tk, batch_c=cols * Tk),
                          Zc, D, cols, Tk, S, arith, sched, size, qk.block_size)
-        S = rnd(S * scale)
-        if bias is not None:
-            rows = _mask_rows(bias, z0, z1, Hkv, s0, e0)
-            S = rnd((S.view(-1, Hkv, n, m, Tk) if rows.dim() == 5 else S.view(Zc, n, m, Tk)) + rows)
-            S = S.view(Zc, cols, Tk)
+        _scale_mask(S, bias, scale, vector, n, m, z0, Hkv, s0)
         P = softmax(S, vector)
-        PT_P, PT_X = pv.a(P.permute(2, 0, 1).reshape(Tk, Zc * cols))             # every call's P^T side by side
+        PT = torch.empty(Tk, Zc * cols, dtype=torch.float32, device=qg.device)   # every call's P^T side by side
+        with torch.cuda.device(qg.device):
+            _lib.run("mxq_transpose", _lib.ptr(P.contiguous()), _lib.ptr(PT), Zc * cols, Tk, _lib.stream(qg.device))
+        PT_P, PT_X = pv.a(PT)
         arith, sched, size = self.pv_red
         O = torch.empty(Zc, cols, D, dtype=torch.float32, device=qg.device)
         systolic_batched((PT_P, PT_X, V_P[:, z0 * D:], V_X[:, z0 * D:]),
@@ -327,15 +326,26 @@ def _launch_ranges(B: int, Hkv: int, per_launch: int):
     return [(b * Hkv + h0, b * Hkv + min(Hkv, h0 + per_launch)) for b in range(B) for h0 in range(0, Hkv, per_launch)]
 
 
-def _mask_rows(bias: torch.Tensor, z0: int, z1: int, Hkv: int, s0: int, e0: int) -> torch.Tensor:
-    """The mask rows [s0, e0) of pairs z0..z1 as a view: (1, 1, m, Tk) when they share one row of the mask,
-    else (batch rows, 1, 1, m, Tk) against scores shaped (batch rows, Hkv, n, m, Tk)."""
-    if bias.shape[0] == 1:
-        return bias[0, s0:e0][None, None]
-    b0, b1 = z0 // Hkv, (z1 - 1) // Hkv + 1
-    if b1 - b0 == 1:
-        return bias[b0, s0:e0][None, None]
-    return bias[b0:b1, None, None, s0:e0]
+def _scale_mask(S: torch.Tensor, bias: Optional[torch.Tensor], scale: float, vector: Optional[str], n: int, m: int,
+                z0: int, Hkv: int, s0: int) -> None:
+    """S (Zc x n*m x Tk scores of pairs z0.., queries s0..) <- r(r(S * scale) + mask rows) in place, one pass:
+    the reference's `r(S * scale)` and `r(S + mask)` (mxq/nn/_attention.py:128-135), float32 multiply and add
+    with the scale as float32, r the vector rounding.  Pair z's mask is bias[z // Hkv] (bias[0] when the mask has
+    one batch row), rows s0.., keys contiguous."""
+    from .. import _lib
+    Zc, _, Tk = S.shape
+    mask, b_stride, r_stride = None, 0, 0
+    if bias is not None:
+        if bias.stride(2) != 1:
+            bias = bias.contiguous()
+        b0 = z0 // Hkv if bias.shape[0] > 1 else 0
+        mask = bias[b0, s0]
+        b_stride = bias.stride(0) if bias.shape[0] > 1 else 0
+        r_stride = bias.stride(1)
+    with torch.cuda.device(S.device):
+        _lib.run("mxq_scores_scale_mask", _lib.ptr(S), Zc, n, m, Tk, float(scale), _lib.ptr(mask), b_stride,
+                 r_stride, z0, Hkv, int(vector == "bf16"),
+                 _lib.stream(S.device))
 
 
 def _windows_full(rows: torch.Tensor, b_of: torch.Tensor, bound: torch.Tensor, block: int) -> bool:
