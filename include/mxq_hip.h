@@ -83,6 +83,14 @@ int mxq_timer_read(const char* kernel, double* total_ms, int64_t* launches);
 int mxq_block_quantize(const void* V, int32_t v_dtype, float* P, float* X, int64_t outer, int64_t n,
                        int64_t inner, int64_t block_size, const mxq_block_spec* spec, mxq_stream_t stream);
 
+/* mxq_block_quantize of V = M^T along axis 0 (V: n x inner, blocks of block_size = 32 along n), reading M
+ * (inner x n, row-major, type v_dtype) as it lies: P (n x inner) and X (ceil(n/32) x inner) as mxq_block_quantize
+ * writes them for the contiguous V, with no copy of the transposed input.  Replaces the `.t().contiguous()` +
+ * quantize of mxq/nn/_attention.py:139 (`pv.a(P.t().contiguous())`) and any axis-0 quantize of a transposed
+ * view (mxq/block/_driver.py:45-66). */
+int mxq_block_quantize_t(const void* M, int32_t v_dtype, float* P, float* X, int64_t n, int64_t inner,
+                         int64_t block_size, const mxq_block_spec* spec, mxq_stream_t stream);
+
 /* out = P * expand(X) along n.  Replaces mxq/block/_driver.py:69-72 `dequantize`. */
 int mxq_block_dequantize(const float* P, const float* X, float* out, int64_t outer, int64_t n, int64_t inner,
                          int64_t block_size, mxq_stream_t stream);
@@ -124,6 +132,25 @@ int mxq_systolic_batched(const float* P_A, const float* X_A, const float* P_B, c
 /* uint32 elements of workspace mxq_systolic / mxq_systolic_batched need (at least 1). */
 int64_t mxq_systolic_workspace(int64_t M, int64_t N, int64_t count);
 
+/* Per contraction row k of codes P (K x cols) with scales X (ceil(K/block_size) x cols), float32 row-major, and
+ * per group g of cols/groups adjacent columns: out[k * groups + g] = max over the group of |P[k, c]| *
+ * X[k / block_size, c] (float32 products; NaN wins), as float64.  Replaces `_code_amax` of
+ * mxq/nn/_attention.py:65-67 for the calls of a batch side by side (one group per call). */
+int mxq_group_amax(const float* P, const float* X, int64_t K, int64_t cols, int64_t groups, int64_t block_size,
+                   double* out, mxq_stream_t stream);
+
+/* For each of Z attention calls, whether it keeps every key: bound = max(slack_scale * sum over d < D of
+ * amax_a[d * lda + z] * amax_k[d * ldk + z], FLT_MIN) (float64), b32 = float(bound); a mask value c absorbs
+ * the call's scores when c + b32 == c and c - b32 == c in float32.  flags (Z int32, zero on entry) gain bit 0
+ * when the first key block (`block` keys) holds a key that some of the call's m query rows does not absorb, bit
+ * 1 for the last block; Tk <= block sets both.  A call keeps every key iff its flag is 3.  Mask rows are
+ * addressed as in mxq_scores_scale_mask.  Replaces the bound and `_live_span` == (0, Tk) test of
+ * mxq/nn/_attention.py:117-127 for a batch of calls. */
+int mxq_attend_windows(const double* amax_a, int64_t lda, const double* amax_k, int64_t ldk, int64_t D, int64_t Z,
+                       double slack_scale, const float* mask, int64_t mask_b_stride, int64_t mask_row_stride,
+                       int64_t z0, int64_t z_per_b, int64_t m, int64_t Tk, int64_t block, int32_t* flags,
+                       mxq_stream_t stream);
+
 /* attend's two elementwise steps on the scores, in place: S (Z problems x n heads x m queries x Tk keys, float32,
  * contiguous) becomes r(r(S * scale) + mask_row), r the identity or (round_bf16 = 1) rounding.bf16; the add and its
  * rounding are skipped when mask is NULL.  Query j of problem z reads the Tk contiguous floats at
@@ -133,10 +160,6 @@ int64_t mxq_systolic_workspace(int64_t M, int64_t N, int64_t count);
 int mxq_scores_scale_mask(float* S, int64_t Z, int64_t n, int64_t m, int64_t Tk, float scale, const float* mask,
                           int64_t mask_b_stride, int64_t mask_row_stride, int64_t z0, int64_t z_per_b,
                           int32_t round_bf16, mxq_stream_t stream);
-
-/* out (C x R) = in (R x C) transposed, float32 row-major; in and out must not overlap.  Replaces the
- * `P.t().contiguous()` of mxq/nn/_attention.py:139 for a batch of calls. */
-int mxq_transpose(const float* in, float* out, int64_t R, int64_t C, mxq_stream_t stream);
 
 /* The adder tree: the operands, Arithmetic, scales and output of mxq_systolic; each reduction of `size` products
  * (zeros past a K tail) summed by log2(size) levels of adjacent-pair acc_adds, level l in (level_e[l],

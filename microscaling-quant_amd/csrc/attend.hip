@@ -1,92 +1,159 @@
-// Score glue of the batched attention path (mxq/nn/_attention.py:128-139): the steps between the two systolic
-// launches that are not matmuls, each one pass over the Z x n*m x Tk scores.
-//
-//   k_scores_scale_mask  S <- r(r(S * scale) + mask row), in place: the float32 multiply, the rounding r (none,
-//                        or bf16 RNE for vector precision "bf16"), the float32 add of the query's mask row, r
-//                        again -- the reference's two elementwise steps with their two roundings, read and
-//                        written once
-//   k_transpose          out (C x R) = in (R x C)^T through 64 x 64 LDS tiles (row padding against bank
-//                        conflicts): P^T for the P-side quantizer, whose blocks run along the keys
+// Glue of the batched attention path (mxq/nn/_attention.py:108-141), around the two systolic launches:
+//   k_group_amax         per contraction row, the max over each column group of |code| * its block scale (the
+//                        masked-key bound's factors, one group per call)
+//   k_attend_windows     per call, the masked-key bound and whether the call keeps every key (its first and last
+//                        key blocks each hold a key some query still sees)
+//   k_scores_scale_mask  S <- r(r(S * scale) + mask row) in place over the Z x n*m x Tk scores: the float32
+//                        multiply, the rounding r (none, or bf16 RNE for vector precision "bf16"), the float32
+//                        add of the query's mask row, r again -- the reference's two elementwise steps with their
+//                        two roundings, read and written once.
 #include "mxq_common.h"
 #include "mxq_numerics.h"
 
 namespace {
 
-constexpr int TT = 64;   // transpose tile
+constexpr int ZCH = 8;   // problems per thread
 
-// Scores in groups of G (G = 4: Tk % 4 == 0, one 16-byte load and store per thread; else G = 1), group index
-// of type I (uint32 when the scores fit it: cheap divisions).  mask: the row of query j of pair z is
-// mask + ((z0 + z) / z_per_b - z0 / z_per_b) * mask_b_stride + j * mask_row_stride (keys contiguous).
+// One thread per group of G scores (G = 4: Tk % 4 == 0, 16-byte loads and stores; else G = 1) of one row of the
+// n*m x Tk score matrix, for ZCH consecutive problems: the mask values are loaded once per batch row of the mask
+// and the ZCH score loads are issued together.  Index type I: uint32 when the counts fit it (cheap divisions).
+// The mask row of query j of problem z: mask + ((z0 + z) / z_per_b - z0 / z_per_b) * mask_b_stride
+// + j * mask_row_stride, keys contiguous.
 template <int G, typename I>
-__global__ void __launch_bounds__(256) k_scores_scale_mask(float* __restrict__ S, I groups, I Tk, I n, I m,
-                                                           float scale, const float* __restrict__ mask,
+__global__ void __launch_bounds__(256) k_scores_scale_mask(float* __restrict__ S, I per_problem, I Z, I Tk, I m,
+                                                           I zchunks, float scale, const float* __restrict__ mask,
                                                            int64_t mask_b_stride, int64_t mask_row_stride,
                                                            int64_t z0, int64_t z_per_b, int bf16) {
   const I t = (I)blockIdx.x * 256 + threadIdx.x;
-  if (t >= groups) return;
-  const I row = t / (Tk / G);                                     // row = (z * n + i) * m + j
-  float v[G];
-  float* s = S + (int64_t)t * G;
-  if constexpr (G == 4) {
-    const float4 q = *reinterpret_cast<const float4*>(s);
-    v[0] = q.x, v[1] = q.y, v[2] = q.z, v[3] = q.w;
-  } else {
-    v[0] = s[0];
-  }
+  if (t >= per_problem * zchunks) return;
+  const I zc = t / per_problem, g = t - zc * per_problem;   // g: group within one problem's n*m x Tk scores
+  const I row = g / (Tk / G), k = g * G - row * Tk;         // row = i * m + j
+  const I j = row % m;
+  const I zb = zc * ZCH;
+  float v[ZCH][G];
 #pragma unroll
-  for (int e = 0; e < G; ++e) {
-    v[e] = v[e] * scale;
-    if (bf16) v[e] = bf16_rne(v[e]);
-  }
-  if (mask) {
-    const I j = row % m, z = row / (n * m), k = (I)(t * G - row * Tk);
-    const float* mr = mask + ((z0 + (int64_t)z) / z_per_b - z0 / z_per_b) * mask_b_stride +
-                      (int64_t)j * mask_row_stride + k;
-#pragma unroll
-    for (int e = 0; e < G; ++e) {
-      v[e] = v[e] + mr[e];
-      if (bf16) v[e] = bf16_rne(v[e]);
+  for (int u = 0; u < ZCH; ++u) {
+    if (zb + u < Z) {
+      const float* s = S + ((int64_t)(zb + u) * per_problem + g) * G;
+      if constexpr (G == 4) {
+        const float4 q = *reinterpret_cast<const float4*>(s);
+        v[u][0] = q.x, v[u][1] = q.y, v[u][2] = q.z, v[u][3] = q.w;
+      } else {
+        v[u][0] = s[0];
+      }
     }
   }
-  if constexpr (G == 4) {
-    *reinterpret_cast<float4*>(s) = make_float4(v[0], v[1], v[2], v[3]);
-  } else {
-    s[0] = v[0];
+  float mv[G];
+  int64_t b_prev = -1;
+#pragma unroll
+  for (int u = 0; u < ZCH; ++u) {
+    if (zb + u >= Z) break;
+#pragma unroll
+    for (int e = 0; e < G; ++e) {
+      v[u][e] = v[u][e] * scale;
+      if (bf16) v[u][e] = bf16_rne(v[u][e]);
+    }
+    if (mask) {
+      const int64_t b = (z0 + (int64_t)(zb + u)) / z_per_b - z0 / z_per_b;
+      if (b != b_prev) {
+        const float* mr = mask + b * mask_b_stride + (int64_t)j * mask_row_stride + k;
+#pragma unroll
+        for (int e = 0; e < G; ++e) mv[e] = mr[e];
+        b_prev = b;
+      }
+#pragma unroll
+      for (int e = 0; e < G; ++e) {
+        v[u][e] = v[u][e] + mv[e];
+        if (bf16) v[u][e] = bf16_rne(v[u][e]);
+      }
+    }
+    float* s = S + ((int64_t)(zb + u) * per_problem + g) * G;
+    if constexpr (G == 4) {
+      *reinterpret_cast<float4*>(s) = make_float4(v[u][0], v[u][1], v[u][2], v[u][3]);
+    } else {
+      s[0] = v[u][0];
+    }
   }
 }
 
 template <typename I>
-void launch_scores(float* S, int64_t rows, int64_t n, int64_t m, int64_t Tk, float scale, const float* mask,
+void launch_scores(float* S, int64_t Z, int64_t n, int64_t m, int64_t Tk, float scale, const float* mask,
                    int64_t mbs, int64_t mrs, int64_t z0, int64_t zpb, int bf16, hipStream_t st) {
   const bool vec = Tk % 4 == 0 && reinterpret_cast<uintptr_t>(S) % 16 == 0;
-  const int64_t groups = rows * Tk / (vec ? 4 : 1);
-  const dim3 grid = mxq::grid_for(groups, 256);
+  const int64_t per_problem = n * m * Tk / (vec ? 4 : 1), zchunks = mxq::ceil_div(Z, ZCH);
+  const dim3 grid = mxq::grid_for(per_problem * zchunks, 256);
   if (vec)
-    k_scores_scale_mask<4, I><<<grid, 256, 0, st>>>(S, (I)groups, (I)Tk, (I)n, (I)m, scale, mask, mbs, mrs, z0, zpb,
-                                                    bf16);
+    k_scores_scale_mask<4, I><<<grid, 256, 0, st>>>(S, (I)per_problem, (I)Z, (I)Tk, (I)m, (I)zchunks, scale, mask,
+                                                    mbs, mrs, z0, zpb, bf16);
   else
-    k_scores_scale_mask<1, I><<<grid, 256, 0, st>>>(S, (I)groups, (I)Tk, (I)n, (I)m, scale, mask, mbs, mrs, z0, zpb,
-                                                    bf16);
+    k_scores_scale_mask<1, I><<<grid, 256, 0, st>>>(S, (I)per_problem, (I)Z, (I)Tk, (I)m, (I)zchunks, scale, mask,
+                                                    mbs, mrs, z0, zpb, bf16);
 }
 
-// One 64 x 64 tile per workgroup, tiles numbered row-major over the ceil(R/64) x ceil(C/64) tile grid.
-__global__ void __launch_bounds__(256) k_transpose(const float* __restrict__ in, float* __restrict__ out, int64_t R,
-                                                   int64_t C, int64_t tiles_c) {
-  __shared__ float tile[TT][TT + 1];
-  const int64_t tr = blockIdx.x / tiles_c, tc = blockIdx.x - tr * tiles_c;
-  const int64_t r0 = tr * TT, c0 = tc * TT;
-  const int tx = threadIdx.x % TT, ty = threadIdx.x / TT;          // 64 x 4 threads
+// One workgroup per (contraction row k, column group g): out[k * groups + g] = max over the group's columns c of
+// |P[k, c]| * X[k / bs, c] (float32 products, as float64).  The max is taken over the products' bit patterns:
+// non-negative floats order like their patterns and every NaN pattern lies above +Inf, so a NaN wins as
+// torch.amax's does.
+__global__ void __launch_bounds__(256) k_group_amax(const float* __restrict__ P, const float* __restrict__ X,
+                                                    int64_t cols, int64_t groups, int64_t bs, double* __restrict__ out) {
+  __shared__ uint32_t part[4];
+  const int64_t k = blockIdx.x / groups, g = blockIdx.x - k * groups;
+  const int64_t per = cols / groups;
+  const float* p = P + k * cols + g * per;
+  const float* x = X + (k / bs) * cols + g * per;
+  uint32_t am = 0u;
+  for (int64_t c = threadIdx.x; c < per; c += 256) am = max(am, f2u(fabsf(p[c]) * x[c]) & 0x7FFFFFFFu);
 #pragma unroll
-  for (int i = 0; i < TT; i += 4) {
-    const int64_t r = r0 + ty + i, c = c0 + tx;
-    if (r < R && c < C) tile[ty + i][tx] = in[r * C + c];
+  for (int off = 32; off >= 1; off >>= 1) am = max(am, (uint32_t)__shfl_xor((int)am, off, 64));
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = am;
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = (double)u2f(max(max(part[0], part[1]), max(part[2], part[3])));
+}
+
+// Workgroup (z, chunk) of the Z x chunks grid checks query rows [chunk * WROWS, +WROWS) of call z.  Its bound:
+// max(slack_scale * sum over d of amax_a[d, z] * amax_k[d, z], FLT_MIN) in float64, b32 = float(bound); a mask
+// value c absorbs the call's scores when c + b32 == c and c - b32 == c (float32).  flags[z] (zero on entry)
+// gains bit 0 when some checked row leaves a key of the first key block unabsorbed, bit 1 for the last block;
+// Tk <= block sets both.  The mask row of query j of call z as in k_scores_scale_mask.
+constexpr int WROWS = 64;
+
+__global__ void __launch_bounds__(256) k_attend_windows(const double* __restrict__ amax_a, int64_t lda,
+                                                        const double* __restrict__ amax_k, int64_t ldk, int64_t D,
+                                                        double slack_scale, const float* __restrict__ mask,
+                                                        int64_t mask_b_stride, int64_t mask_row_stride, int64_t z0,
+                                                        int m, int Tk, int block, int chunks,
+                                                        int64_t z_per_b, int32_t* __restrict__ flags) {
+  __shared__ float b32;
+  const int z = blockIdx.x / chunks, chunk = blockIdx.x - z * chunks;
+  if (Tk <= block) {
+    if (threadIdx.x == 0 && chunk == 0) atomicOr(flags + z, 3);
+    return;
+  }
+  if (threadIdx.x == 0) {
+    double sum = 0.0;
+    for (int64_t d = 0; d < D; ++d) sum += amax_a[d * lda + z] * amax_k[d * ldk + z];
+    double bound = slack_scale * sum;
+    if (bound < 1.1754943508222875e-38) bound = 1.1754943508222875e-38;     // NaN stays NaN
+    b32 = (float)bound;
   }
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < TT; i += 4) {
-    const int64_t c = c0 + ty + i, r = r0 + tx;
-    if (c < C && r < R) out[c * R + r] = tile[tx][ty + i];
+  const float bnd = b32;
+  const float* rows = mask + ((z0 + z) / z_per_b - z0 / z_per_b) * mask_b_stride;
+  const int last0 = (Tk - 1) / block * block, j0 = chunk * WROWS;
+  const int nrows = min(WROWS, m - j0);
+  int live = 0;
+  for (int i = threadIdx.x; i < nrows * block; i += 256) {
+    const int j = i / block, key = i - j * block;
+    const float* r = rows + (int64_t)(j0 + j) * mask_row_stride;
+    const float c = r[key];                                   // key < block < Tk
+    if (!((c + bnd) == c && (c - bnd) == c)) live |= 1;
+    if (last0 + key < Tk) {
+      const float e = r[last0 + key];
+      if (!((e + bnd) == e && (e - bnd) == e)) live |= 2;
+    }
   }
+  const int first = __syncthreads_or(live & 1), last = __syncthreads_or(live & 2);
+  if (threadIdx.x == 0 && (first || last)) atomicOr(flags + z, (first ? 1 : 0) | (last ? 2 : 0));
 }
 
 }  // namespace
@@ -99,24 +166,44 @@ extern "C" int mxq_scores_scale_mask(float* S, int64_t Z, int64_t n, int64_t m, 
   const int64_t rows = Z * n * m;
   if (rows == 0 || Tk == 0) return MXQ_OK;
   if (!S) return mxq::invalid("mxq_scores_scale_mask: NULL scores");
-  if (mxq::ceil_div(rows * Tk, 256) > INT32_MAX) return mxq::invalid("mxq_scores_scale_mask: too many scores");
+  if (mxq::ceil_div(n * m * Tk * mxq::ceil_div(Z, ZCH), 256) > INT32_MAX)
+    return mxq::invalid("mxq_scores_scale_mask: too many scores");
   if (mask && (mask_row_stride < 0 || mask_b_stride < 0))
     return mxq::invalid("mxq_scores_scale_mask: bad mask strides");
   if (rows * Tk < ((int64_t)1 << 31))             // thread indices stay far from uint32 wrap-around
-    launch_scores<uint32_t>(S, rows, n, m, Tk, scale, mask, mask_b_stride, mask_row_stride, z0, z_per_b,
+    launch_scores<uint32_t>(S, Z, n, m, Tk, scale, mask, mask_b_stride, mask_row_stride, z0, z_per_b,
                             round_bf16 ? 1 : 0, mxq::as_stream(stream));
   else
-    launch_scores<int64_t>(S, rows, n, m, Tk, scale, mask, mask_b_stride, mask_row_stride, z0, z_per_b,
+    launch_scores<int64_t>(S, Z, n, m, Tk, scale, mask, mask_b_stride, mask_row_stride, z0, z_per_b,
                            round_bf16 ? 1 : 0, mxq::as_stream(stream));
   return mxq::check_launch("mxq_scores_scale_mask");
 }
 
-extern "C" int mxq_transpose(const float* in, float* out, int64_t R, int64_t C, mxq_stream_t stream) {
-  if (R < 0 || C < 0) return mxq::invalid("mxq_transpose: bad shape");
-  if (R == 0 || C == 0) return MXQ_OK;
-  if (!in || !out) return mxq::invalid("mxq_transpose: NULL pointer");
-  const int64_t tiles_c = mxq::ceil_div(C, TT), tiles = mxq::ceil_div(R, TT) * tiles_c;
-  if (tiles > INT32_MAX) return mxq::invalid("mxq_transpose: matrix too large");
-  k_transpose<<<dim3((unsigned)tiles), 256, 0, mxq::as_stream(stream)>>>(in, out, R, C, tiles_c);
-  return mxq::check_launch("mxq_transpose");
+extern "C" int mxq_group_amax(const float* P, const float* X, int64_t K, int64_t cols, int64_t groups,
+                              int64_t block_size, double* out, mxq_stream_t stream) {
+  if (K < 0 || cols < 0 || groups < 1 || block_size < 1 || cols % groups)
+    return mxq::invalid("mxq_group_amax: bad shape");
+  if (K == 0) return MXQ_OK;
+  if (!P || !X || !out) return mxq::invalid("mxq_group_amax: NULL pointer");
+  if (K * groups > INT32_MAX) return mxq::invalid("mxq_group_amax: too many groups");
+  k_group_amax<<<dim3((unsigned)(K * groups)), 256, 0, mxq::as_stream(stream)>>>(P, X, cols, groups, block_size, out);
+  return mxq::check_launch("mxq_group_amax");
+}
+
+extern "C" int mxq_attend_windows(const double* amax_a, int64_t lda, const double* amax_k, int64_t ldk, int64_t D,
+                                  int64_t Z, double slack_scale, const float* mask, int64_t mask_b_stride,
+                                  int64_t mask_row_stride, int64_t z0, int64_t z_per_b, int64_t m, int64_t Tk,
+                                  int64_t block, int32_t* flags, mxq_stream_t stream) {
+  if (D < 0 || Z < 0 || m < 1 || Tk < 0 || block < 1 || z0 < 0 || z_per_b < 1 || lda < Z || ldk < Z ||
+      mask_b_stride < 0 || mask_row_stride < 0)
+    return mxq::invalid("mxq_attend_windows: bad shape");
+  if (Z == 0) return MXQ_OK;
+  if (!amax_a || !amax_k || !mask || !flags) return mxq::invalid("mxq_attend_windows: NULL pointer");
+  const int64_t chunks = mxq::ceil_div(m, WROWS);
+  if (Tk > INT32_MAX || m * block > INT32_MAX || Z * chunks > INT32_MAX)
+    return mxq::invalid("mxq_attend_windows: too large");
+  k_attend_windows<<<dim3((unsigned)(Z * chunks)), 256, 0, mxq::as_stream(stream)>>>(
+      amax_a, lda, amax_k, ldk, D, slack_scale, mask, mask_b_stride, mask_row_stride, z0, (int)m, (int)Tk,
+      (int)block, (int)chunks, z_per_b, flags);
+  return mxq::check_launch("mxq_attend_windows");
 }

@@ -24,6 +24,25 @@ extern "C" int mxq_block_quantize(const void* V, int32_t v_dtype, float* P, floa
   }
 }
 
+// The transposed layout goes through the same per-type dispatch, flagged by a negative block size.
+extern "C" int mxq_block_quantize_t(const void* M, int32_t v_dtype, float* P, float* X, int64_t n, int64_t inner,
+                                    int64_t block_size, const mxq_block_spec* spec, mxq_stream_t stream) {
+  if (!spec) return mxq::invalid("mxq_block_quantize_t: spec is NULL");
+  if (n < 0 || inner < 0) return mxq::invalid("mxq_block_quantize_t: bad shape");
+  if (block_size != 32) return mxq::invalid("mxq_block_quantize_t: block_size must be 32");
+  if (int rc = mxq_quant::validate(*spec)) return rc;
+  if (n == 0 || inner == 0) return MXQ_OK;
+  if (!M || !P || !X) return mxq::invalid("mxq_block_quantize_t: NULL pointer");
+  const mxq_block_spec q = *spec;
+  hipStream_t st = mxq::as_stream(stream);
+  switch (v_dtype) {
+    case MXQ_DT_F32: return mxq_quantize_f32(M, P, X, 1, n, inner, -32, q, st);
+    case MXQ_DT_BF16: return mxq_quantize_bf16(M, P, X, 1, n, inner, -32, q, st);
+    case MXQ_DT_F16: return mxq_quantize_f16(M, P, X, 1, n, inner, -32, q, st);
+    default: return mxq::invalid("mxq_block_quantize_t: unsupported input dtype");
+  }
+}
+
 extern "C" int mxq_block_dequantize(const float* P, const float* X, float* out, int64_t outer, int64_t n,
                                     int64_t inner, int64_t block_size, mxq_stream_t stream) {
   if (outer < 0 || n < 0 || inner < 0 || block_size < 1) return mxq::invalid("mxq_block_dequantize: bad shape");

@@ -247,6 +247,77 @@ __global__ void __launch_bounds__(256) k_quant_contig32(const T* __restrict__ V,
   if ((t & 7) == 0) X[blk] = xs;
 }
 
+// V = M^T with M (inner x n) row-major in memory, blocks of 32 along n: every block is 32 contiguous elements
+// of a row of M.  A workgroup quantizes a tile of 64 rows of M x 64 of n (two blocks per row): loads along M's
+// rows (coalesced), eight lanes of four elements per block whose maxima meet through exchanges, and the codes
+// pass through LDS to leave along P's rows (P is V-shaped: n x inner).  The same scale and element rules as
+// the other layouts, per block; no copy of the transposed input is made.
+constexpr int kTT = 64;
+
+template <typename T, int ELEM, int MODE>
+__global__ void __launch_bounds__(256) k_quant_t(const T* __restrict__ M, float* __restrict__ P,
+                                                 float* __restrict__ X, int64_t n, int64_t inner, int64_t tiles_k,
+                                                 int vec_in, int vec_out, mxq_block_spec s) {
+  __shared__ float tile[kTT][kTT + 1];               // [position along n][row of M]
+  const int64_t tc = blockIdx.x / tiles_k, tk = blockIdx.x - tc * tiles_k;
+  const int64_t c0 = tc * kTT, k0 = tk * kTT;
+  const bool full = c0 + kTT <= inner && k0 + kTT <= n;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int id = it * 256 + tid;
+    const int row = id >> 4, quad = id & 15;          // 8 consecutive lanes: one row, one block of 32
+    const int64_t c = c0 + row, k = k0 + quad * 4;
+    float v[4];
+    if (full && vec_in) {
+      load_vec<T, 4>(M + c * n + k, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (c < inner && k + e < n) ? to_f32(M[c * n + k + e]) : 0.0f;
+    }
+    uint32_t am = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) am = max(am, f2u(v[e]) & 0x7FFFFFFFu);
+    am = max(am, (uint32_t)__shfl_xor((int)am, 1, 8));
+    am = max(am, (uint32_t)__shfl_xor((int)am, 2, 8));
+    am = max(am, (uint32_t)__shfl_xor((int)am, 4, 8));
+    const float xs = block_scale(u2f(am), s);
+    const Div d = make_div(xs);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[quad * 4 + e][row] = elem_qm<ELEM, MODE>(s.scale_rule ? apply_div(v[e], d) : v[e], s);
+    if ((quad & 7) == 0 && c < inner && k < n) X[(k >> 5) * inner + c] = xs;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int id = it * 256 + tid;
+    const int key = id >> 4, cq = (id & 15) * 4;
+    const int64_t k = k0 + key, c = c0 + cq;
+    float q[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = tile[key][cq + e];
+    if (full && vec_out) {
+      store_vec_nt<4>(P + k * inner + c, q);
+    } else if (k < n) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c + e < inner) P[k * inner + c + e] = q[e];
+    }
+  }
+}
+
+template <typename T, int ELEM, int MODE>
+int launch_quant_t(const T* M, float* P, float* X, int64_t n, int64_t inner, const mxq_block_spec& q,
+                   hipStream_t st) {
+  mxq::KernelTimer timer("block_quantize", st);
+  const int64_t tiles_k = mxq::ceil_div(n, kTT), tiles = mxq::ceil_div(inner, kTT) * tiles_k;
+  if (tiles > INT32_MAX) return mxq::invalid("mxq_block_quantize_t: tensor too large");
+  const int vec_in = n % 4 == 0 && reinterpret_cast<uintptr_t>(M) % (4 * sizeof(T)) == 0;
+  const int vec_out = inner % 4 == 0 && reinterpret_cast<uintptr_t>(P) % 16 == 0;
+  k_quant_t<T, ELEM, MODE><<<dim3((unsigned)tiles), 256, 0, st>>>(M, P, X, n, inner, tiles_k, vec_in, vec_out, q);
+  return mxq::check_launch("mxq_block_quantize_t");
+}
+
 template <int VEC>
 __global__ void __launch_bounds__(256) k_dequant_strided(const float* __restrict__ P, const float* __restrict__ X,
                                                          float* __restrict__ out, int64_t outer, int64_t n,
@@ -298,9 +369,11 @@ inline int validate(const mxq_block_spec& s) {
   return MXQ_OK;
 }
 
+// bs < 0: the transposed layout (outer 1, block 32, V read as M^T), k_quant_t.
 template <typename T, int ELEM, int MODE>
 int launch_quant(const T* V, float* P, float* X, int64_t outer, int64_t n, int64_t inner, int64_t bs,
                  const mxq_block_spec& q, hipStream_t st) {
+  if (bs < 0) return launch_quant_t<T, ELEM, MODE>(V, P, X, n, inner, q, st);
   mxq::KernelTimer timer("block_quantize", st);
   const int64_t nb = mxq::ceil_div(n, bs);
   const uintptr_t av = reinterpret_cast<uintptr_t>(V), ap = reinterpret_cast<uintptr_t>(P),

@@ -57,6 +57,8 @@ SIGNATURES = {
     "mxq_timer_read": (c_i32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_i64)]),
     "mxq_block_quantize": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64,
                                    ctypes.POINTER(BlockSpec), c_ptr]),
+    "mxq_block_quantize_t": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, ctypes.POINTER(BlockSpec),
+                                     c_ptr]),
     "mxq_block_dequantize": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr]),
     "mxq_systolic": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,
                              ctypes.POINTER(ArithSpec), c_ptr, c_i32, c_ptr]),
@@ -66,7 +68,9 @@ SIGNATURES = {
     "mxq_systolic_workspace": (c_i64, [c_i64, c_i64, c_i64]),
     "mxq_scores_scale_mask": (c_i32, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64, c_i64, c_i64, c_i64,
                                       c_i32, c_ptr]),
-    "mxq_transpose": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_ptr]),
+    "mxq_group_amax": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
+    "mxq_attend_windows": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_f64, c_ptr, c_i64, c_i64, c_i64,
+                                   c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
     "mxq_adder_tree": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,
                                ctypes.POINTER(ArithSpec), c_ptr]),
     "mxq_anchor_tree": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i32,

@@ -50,6 +50,8 @@ def quantize_fused(V: torch.Tensor, axis: int, block_size: int, spec: _lib.Block
     Vd = _lib.to_device(V.detach(), dev)
     if Vd.dtype not in _NATIVE:
         Vd = Vd.to(torch.float32)                       # the reference's V.to(float32) (RNE from float64)
+    if _transposed_view(Vd, axis, block_size):
+        return _quantize_transposed(Vd, dev, spec, V)
     Vd = Vd.contiguous()
     outer, n, inner = _view3(Vd.shape, axis)
     nb = -(-n // block_size)
@@ -60,6 +62,23 @@ def quantize_fused(V: torch.Tensor, axis: int, block_size: int, spec: _lib.Block
     with torch.cuda.device(dev):
         _lib.run("mxq_block_quantize", _lib.ptr(Vd), _NATIVE[Vd.dtype], _lib.ptr(P), _lib.ptr(X), outer, n, inner,
                  block_size, spec, _lib.stream(dev))
+    return _lib.back(P, V), _lib.back(X, V)
+
+
+def _transposed_view(V: torch.Tensor, axis: int, block_size: int) -> bool:
+    """V (n x inner) is the transpose of a row-major matrix and is quantized along axis 0 in blocks of 32."""
+    return (V.ndim == 2 and axis == 0 and block_size == 32 and not V.is_contiguous()
+            and V.stride() == (1, V.shape[0]) and V.shape[0] > 1 and V.shape[1] > 1)
+
+
+def _quantize_transposed(Vd: torch.Tensor, dev: torch.device, spec: _lib.BlockSpec, V: torch.Tensor):
+    """quantize_fused of a transposed view, read as it lies (no copy of the input)."""
+    n, inner = Vd.shape
+    P = torch.empty((n, inner), dtype=torch.float32, device=dev)
+    X = torch.empty((-(-n // 32), inner), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.run("mxq_block_quantize_t", _lib.ptr(Vd), _NATIVE[Vd.dtype], _lib.ptr(P), _lib.ptr(X), n, inner, 32,
+                 spec, _lib.stream(dev))
     return _lib.back(P, V), _lib.back(X, V)
 
 

@@ -213,11 +213,39 @@ def _systolic_reducer(reduce, block_size: int):
     return kw["arith"], kw["schedule"], size
 
 
-def _column_group_amax(codes: torch.Tensor, scales: torch.Tensor, block_size: int, groups: int) -> torch.Tensor:
-    """_code_amax of each of `groups` equal column groups side by side: K x groups, float64."""
-    per_row = scales.repeat_interleave(block_size, dim=0)[:codes.shape[0]]
-    prod = codes.abs() * per_row
-    return prod.view(codes.shape[0], groups, -1).amax(dim=2).to(torch.float64)
+def _group_amax(codes: torch.Tensor, scales: torch.Tensor, block_size: int, groups: int) -> torch.Tensor:
+    """_code_amax of each of `groups` equal column groups side by side, one kernel: K x groups, float64."""
+    from .. import _lib
+    K, cols = codes.shape
+    out = torch.empty(K, groups, dtype=torch.float64, device=codes.device)
+    with torch.cuda.device(codes.device):
+        _lib.run("mxq_group_amax", _lib.ptr(codes.contiguous()), _lib.ptr(scales.contiguous()), K, cols, groups,
+                 block_size, _lib.ptr(out), _lib.stream(codes.device))
+    return out
+
+
+def _mask_rows(bias: torch.Tensor, z0: int, Hkv: int, s0: int):
+    """(pointer tensor, batch-row stride, row stride) of mask row s0 of pair z0, keys contiguous."""
+    if bias.stride(2) != 1:
+        bias = bias.contiguous()
+    batched = bias.shape[0] > 1
+    return bias[z0 // Hkv if batched else 0, s0], bias.stride(0) if batched else 0, bias.stride(1)
+
+
+def _windows(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale: float, bias: torch.Tensor,
+             Hkv: int, s0: int, m: int, block: int) -> torch.Tensor:
+    """Per pair z0..z0+Zc, 3 when its call keeps every key: the reference's bound (SLACK * |scale| * sum over
+    D of the two amax factors, at least FLT_MIN) and its live-key span == (0, Tk) (mxq/nn/_attention.py:117-127),
+    as int32 flags on the device (no host synchronisation)."""
+    from .. import _lib
+    D, Tk = a_amax.shape[0], bias.shape[2]
+    flags = torch.zeros(Zc, dtype=torch.int32, device=a_amax.device)
+    mask, b_stride, r_stride = _mask_rows(bias, z0, Hkv, s0)
+    with torch.cuda.device(a_amax.device):
+        _lib.run("mxq_attend_windows", _lib.ptr(a_amax), a_amax.shape[1], _lib.ptr(k_amax[:, z0:]), k_amax.shape[1],
+                 D, Zc, SLACK * abs(scale), _lib.ptr(mask), b_stride, r_stride, z0, Hkv, m, Tk, block,
+                 _lib.ptr(flags), _lib.stream(a_amax.device))
+    return flags
 
 
 @dataclass
@@ -248,21 +276,36 @@ class _Batched:
         qk, pv = self.qk, self.pv
         B, Hkv, Tk, D, n = dims.B, dims.Hkv, dims.Tk, dims.D, dims.group
         Z = B * Hkv
-        # pair z = b * Hkv + h: its K^T in columns [z*Tk, (z+1)*Tk), its V in columns [z*D, (z+1)*D)
+        # pair z = b * Hkv + h: its K^T in columns [z*Tk, (z+1)*Tk) (a transposed view of k: no copy), its V the
+        # z-th Tk x D slab (blocks along the keys, every column on its own, so the same codes as V alone)
         KT_P, KT_X = qk.b(k.to(torch.float32).permute(3, 0, 1, 2).reshape(D, Z * Tk))
-        V_P, V_X = pv.b(v.to(torch.float32).permute(2, 0, 1, 3).reshape(Tk, Z * D))
+        V_P, V_X = pv.b.func(v.to(torch.float32).reshape(Z, Tk, D), **{**pv.b.keywords, "axis": 1})
         qk.check_scales(KT_X, D, "b (Kᵀ)")
-        pv.check_scales(V_X, Tk, "b (V)")
+        pv.check_scales(V_X.transpose(0, 1), Tk, "b (V)")                         # Z x nb x D
         kv = (KT_P, KT_X, V_P, V_X)
-        k_amax = _column_group_amax(KT_P, KT_X, qk.block_size, Z) if bias is not None else None
+        k_amax = _group_amax(KT_P, KT_X, qk.block_size, Z) if bias is not None else None
         qg = q.reshape(Z, n, dims.Tq, D)
+        pending = []                                     # (flags, z0, s0, e0) of chunks run on the batched path
         for s0 in range(0, dims.Tq, step):
             e0 = min(s0 + step, dims.Tq)
             for z0, z1 in _launch_ranges(B, Hkv, max(1, ELEMENTS_PER_LAUNCH // (n * (e0 - s0) * Tk))):
-                if not self._chunk(qg, bias, kv, k_amax, scale, vector, rnd, dims, z0, z1, s0, e0, out):
-                    self._per_pair(q, bias, kv, scale, vector, rnd, dims, z0, z1, s0, e0, out)
+                flags = self._chunk(qg, bias, kv, k_amax, scale, vector, dims, z0, z1, s0, e0, out)
+                if flags is not None:
+                    pending.append((flags, z0, s0, e0))
+        # a pair that would skip masked keys gets the reference's own call, on the same codes, over its outputs
+        if pending:
+            every = torch.cat([f for f, _, _, _ in pending]).cpu().tolist()
+            at = 0
+            for flags, z0, s0, e0 in pending:
+                for z in range(flags.numel()):
+                    if every[at + z] != 3:
+                        self._per_pair(q, bias, kv, scale, vector, rnd, dims, z0 + z, z0 + z + 1, s0, e0, out)
+                at += flags.numel()
 
-    def _chunk(self, qg, bias, kv, k_amax, scale, vector, rnd, dims: _Dims, z0, z1, s0, e0, out) -> bool:
+    def _chunk(self, qg, bias, kv, k_amax, scale, vector, dims: _Dims, z0, z1, s0, e0, out) -> Optional[torch.Tensor]:
+        """Pairs z0..z1, queries s0..e0 as two batched launches.  With a mask, returns each pair's flag (int32 on
+        the device): 3 when its call keeps every key (the batched result is the reference's); otherwise the
+        caller must redo it through the reference's call."""
         from .. import _lib
         from ..matmul._systolic import systolic_batched
         qk, pv = self.qk, self.pv
@@ -270,13 +313,10 @@ class _Batched:
         Zc, n, m, Tk, D, Hkv = z1 - z0, dims.group, e0 - s0, dims.Tk, dims.D, dims.Hkv
         cols = n * m                                                              # one call's columns
         A_P, A_X = qk.a(qg[z0:z1, :, s0:e0].to(torch.float32).permute(3, 0, 1, 2).reshape(D, Zc * cols))
+        flags = None
         if bias is not None:
-            bound = SLACK * abs(scale) * (_column_group_amax(A_P, A_X, qk.block_size, Zc) * k_amax[:, z0:z1]).sum(0)
-            b_of = torch.arange(z0, z1, device=qg.device) // Hkv if bias.shape[0] > 1 else \
-                torch.zeros(Zc, dtype=torch.int64, device=qg.device)
-            if not _windows_full(bias[:, s0:e0], b_of, bound.clamp(min=torch.finfo(torch.float32).tiny),
-                                 pv.block_size):
-                return False
+            flags = _windows(_group_amax(A_P, A_X, qk.block_size, Zc), k_amax, z0, Zc, scale, bias, Hkv, s0, m,
+                             pv.block_size)
         arith, sched, size = self.qk_red
         S = torch.empty(Zc, cols, Tk, dtype=torch.float32, device=qg.device)
         systolic_batched((A_P, A_X, KT_P[:, z0 * Tk:], KT_X[:, z0 * Tk:]),
@@ -286,15 +326,13 @@ class _Batched:
                          Zc, D, cols, Tk, S, arith, sched, size, qk.block_size)
         _scale_mask(S, bias, scale, vector, n, m, z0, Hkv, s0)
         P = softmax(S, vector)
-        PT = torch.empty(Tk, Zc * cols, dtype=torch.float32, device=qg.device)   # every call's P^T side by side
-        with torch.cuda.device(qg.device):
-            _lib.run("mxq_transpose", _lib.ptr(P.contiguous()), _lib.ptr(PT), Zc * cols, Tk, _lib.stream(qg.device))
-        PT_P, PT_X = pv.a(PT)
+        # every call's P^T side by side, quantized from P as it lies (a transposed view: no copy)
+        PT_P, PT_X = pv.a(P.contiguous().view(Zc * cols, Tk).t())
         arith, sched, size = self.pv_red
         O = torch.empty(Zc, cols, D, dtype=torch.float32, device=qg.device)
-        systolic_batched((PT_P, PT_X, V_P[:, z0 * D:], V_X[:, z0 * D:]),
+        systolic_batched((PT_P, PT_X, V_P[z0:], V_X[z0:]),
                          _lib.SystolicLayout(ld_a=Zc * cols, batch_a=cols, ld_xa=Zc * cols, batch_xa=cols,
-                                             ld_b=V_P.shape[1], batch_b=D, ld_xb=V_X.shape[1], batch_xb=D,
+                                             ld_b=D, batch_b=Tk * D, ld_xb=D, batch_xb=V_X.shape[1] * D,
                                              ld_c=D, batch_c=cols * D),
                          Zc, Tk, cols, D, O, arith, sched, size, pv.block_size)
         O = O.view(Zc, n, m, D)
@@ -302,16 +340,15 @@ class _Batched:
             h0, h1 = max(z0, b * Hkv) - b * Hkv, min(z1, (b + 1) * Hkv) - b * Hkv
             part = O[b * Hkv + h0 - z0:b * Hkv + h1 - z0]                         # (h1 - h0) x n x m x D
             out[b, s0:e0, h0 * n:h1 * n] = part.permute(2, 0, 1, 3).reshape(m, (h1 - h0) * n, D).to(out.dtype)
-        return True
+        return flags
 
     def _per_pair(self, q, bias, kv, scale, vector, rnd, dims: _Dims, z0, z1, s0, e0, out) -> None:
         KT_P, KT_X, V_P, V_X = kv
         Tk, D, n = dims.Tk, dims.D, dims.group
         for z in range(z0, z1):
             b, h = divmod(z, dims.Hkv)
-            ops = _KVOperands.checked(KT_P[:, z * Tk:(z + 1) * Tk], KT_X[:, z * Tk:(z + 1) * Tk],
-                                      V_P[:, z * D:(z + 1) * D], V_X[:, z * D:(z + 1) * D], self.qk, self.pv,
-                                      bias is not None)
+            ops = _KVOperands.checked(KT_P[:, z * Tk:(z + 1) * Tk], KT_X[:, z * Tk:(z + 1) * Tk], V_P[z], V_X[z],
+                                      self.qk, self.pv, bias is not None)
             bias_b = None if bias is None else bias[b if bias.shape[0] > 1 else 0]
             _one_call(q[b], ops, bias_b, scale, self.qk, self.pv, vector, rnd, dims, range(h * n, (h + 1) * n),
                       s0, e0, out[b])
@@ -334,36 +371,11 @@ def _scale_mask(S: torch.Tensor, bias: Optional[torch.Tensor], scale: float, vec
     one batch row), rows s0.., keys contiguous."""
     from .. import _lib
     Zc, _, Tk = S.shape
-    mask, b_stride, r_stride = None, 0, 0
-    if bias is not None:
-        if bias.stride(2) != 1:
-            bias = bias.contiguous()
-        b0 = z0 // Hkv if bias.shape[0] > 1 else 0
-        mask = bias[b0, s0]
-        b_stride = bias.stride(0) if bias.shape[0] > 1 else 0
-        r_stride = bias.stride(1)
+    mask, b_stride, r_stride = (None, 0, 0) if bias is None else _mask_rows(bias, z0, Hkv, s0)
     with torch.cuda.device(S.device):
         _lib.run("mxq_scores_scale_mask", _lib.ptr(S), Zc, n, m, Tk, float(scale), _lib.ptr(mask), b_stride,
                  r_stride, z0, Hkv, int(vector == "bf16"),
                  _lib.stream(S.device))
-
-
-def _windows_full(rows: torch.Tensor, b_of: torch.Tensor, bound: torch.Tensor, block: int) -> bool:
-    """Would every call keep all its keys (_live_span = [0, Tk))?  rows: Bm x m x Tk mask rows, b_of: each
-    call's row of `rows`, bound: each call's float64 bound.  A call keeps all keys when some query sees a key
-    of the first block and one of the last (a single block always stays whole)."""
-    Tk = rows.shape[2]
-    if Tk <= block:
-        return True
-    b32 = bound.to(torch.float32)[:, None, None]
-
-    def live(cols: torch.Tensor) -> torch.Tensor:
-        c = cols[b_of]                                                            # calls x m x block
-        absorbed = ((c + b32) == c) & ((c - b32) == c)
-        return (~absorbed.all(dim=1)).any(dim=1)
-
-    last0 = (Tk - 1) // block * block
-    return bool((live(rows[:, :, :block]) & live(rows[:, :, last0:])).all())
 
 
 def _mxq_attention(module, query, key, value, attention_mask, dropout: float = 0.0, scaling: Optional[float] = None,

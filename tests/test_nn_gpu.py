@@ -187,3 +187,21 @@ def test_attend_batched_launch_ranges(cuda, monkeypatch):
     want = oatt.attend(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), D ** -0.5, hwo, hwo, _gpu_softmax)
     assert_bits_equal(got, want, "batched launch ranges")
     assert _attention._Batched.of(hw, hw, q.cuda()) is not None, "the hw scheme takes the batched path"
+
+
+def test_attend_batched_pairwise_fallback(cuda):
+    """In one batched launch, the pairs of batch row 1 (right padding: its last 40 keys masked for every query)
+    would skip keys and are redone through the per-call loop, those of row 0 (causal) are not; every output
+    bit for bit against the oracle.  An all-zero V block behind the padding checks that skipped keys add
+    nothing."""
+    import mxq
+    B, H, Hkv, T, D = 2, 4, 2, 96, 32
+    g = torch.Generator().manual_seed(21)
+    q, k, v = (torch.randn(B, h, T, D, generator=g) for h in (H, Hkv, Hkv))
+    mask = _causal(B, T, T)
+    mask[1, :, :, T - 40:] = torch.finfo(torch.float32).min
+    v[1, :, T - 32:] = 0.0
+    hw, hwo = _hw(mxq), _hw_oracle()
+    got = mxq.nn.attend(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), D ** -0.5, hw, hw).cpu().numpy()
+    want = oatt.attend(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), D ** -0.5, hwo, hwo, _gpu_softmax)
+    assert_bits_equal(got, want, "pairwise fallback")

@@ -105,6 +105,33 @@ def test_contiguous_block_layout(cuda):
             assert_bits_equal(X, wX, f"X {shape} {fn.__module__}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_transposed_view_layout(cuda, dtype):
+    """Axis 0 of a transposed view (V = M.t(), M row-major) runs the transposing kernel on M as it lies: the same
+    codes and scales as the oracle on V, for every rule; tiles cut by both edges, n and inner off multiples of 4
+    and of 32 (scalar loads and stores), and the aligned whole-tile path."""
+    from mxq import block
+    rng = np.random.default_rng(9)
+    quantizers = [(block.mxgemmini.quantize, lambda V, f: ob.mxgemmini_quantize(V, f, 0, 32, "rne"),
+                   dict(rounding_mode="rne")),
+                  (block.mxgemmini.quantize, lambda V, f: ob.mxgemmini_quantize(V, f, 0, 32, "truncate", 2.0 ** -23),
+                   dict(rounding_mode="truncate", scale_floor=2.0 ** -23)),
+                  (block.mxquant.quantize, lambda V, f: ob.mxquant_quantize(V, f, 0, 32), {}),
+                  (block.ocp.quantize, lambda V, f: ob.ocp_quantize(V, f, 0, 32, "nearest", 8, "top"),
+                   dict(rounding_mode="nearest"))]
+    for n, inner in [(2048, 256), (100, 70), (33, 130), (64, 3), (7, 65)]:
+        M = torch.from_numpy(_edge_matrix(rng, inner, n, scale=float(np.exp2(rng.integers(-10, 10))))).to(dtype)
+        V32 = M.to(torch.float32).numpy().T.copy()
+        Md = M.cuda()
+        for fn, ref, kw in quantizers:
+            for fmt in ("MXFP8_E4M3", "MXFP4", "MXFP6_E2M3"):
+                P, X = fn(Md.t(), fmt, axis=0, **kw)
+                wP, wX = ref(V32, fmt)
+                assert_bits_equal(P.cpu().numpy(), wP, f"P {dtype} {n}x{inner} {fmt} {kw}")
+                assert_bits_equal(X.cpu().numpy(), wX, f"X {dtype} {n}x{inner} {fmt} {kw}")
+                assert P.is_contiguous() and P.shape == (n, inner) and X.shape == (-(-n // 32), inner)
+
+
 def test_cpu_tensors_round_trip_through_gpu(cuda):
     from mxq import block
     V = torch.randn(64, 8)
