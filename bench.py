@@ -184,21 +184,29 @@ def attend_line(torch, steps):
 
 
 def trees_line(torch, steps, P_A, X_A, P_B, X_B):
-    """The other two reducers on the benchmark's own codes (M = 512, N = 4096, K = 4096): matmul.adder_tree with
-    MXGEMMINI and bf16 at every level (size 16), matmul.anchor_tree with MXGEMMINI and its defaults (one
-    16-product tree per reduction, bf16 out, truncating 19-bit levels).  Emulated ops as for systolic."""
+    """The other two reducers on the benchmark's own codes (M = 512, N = 4096, K = 4096), MXGEMMINI, size 16:
+    matmul.adder_tree with bf16 at every level and with the README's ladder [(4, 4), (4, 5), (4, 6), (8, 7)],
+    and matmul.anchor_tree with its defaults (one 16-product tree per reduction, bf16 out, truncating 20-bit
+    levels).  Emulated ops as for systolic, over the fast kernel's own duration (the general kernel that follows
+    it computes only flagged tiles: none on these codes)."""
     from mxq import matmul
     dev = P_A.device
     s = torch.cuda.current_stream(dev)
     ar = matmul.MXGEMMINI()
     macs = P_A.shape[0] * P_A.shape[1] * P_B.shape[1]
-    out = {"workload": "adder_tree (size 16, bf16 levels) and anchor_tree (defaults), MXGEMMINI, C2 codes"}
-    for name, fn in (("adder_tree", lambda: matmul.adder_tree(P_A, X_A, P_B, X_B, ar, [(8, 7)] * 4)),
-                     ("anchor_tree", lambda: matmul.anchor_tree(P_A, X_A, P_B, X_B, ar))):
+    out = {"workload": "adder_tree (size 16: bf16 levels; e4m4, e4m5, e4m6, bf16 levels) and anchor_tree "
+                       "(defaults), MXGEMMINI, on the systolic benchmark's codes"}
+    ladder = [(4, 4), (4, 5), (4, 6), (8, 7)]
+    for name, kernel, fn in (
+            ("adder_tree_bf16", "adder_fast", lambda: matmul.adder_tree(P_A, X_A, P_B, X_B, ar, [(8, 7)] * 4)),
+            ("adder_tree_ladder", "adder_fast", lambda: matmul.adder_tree(P_A, X_A, P_B, X_B, ar, ladder)),
+            ("anchor_tree", "anchor_fast", lambda: matmul.anchor_tree(P_A, X_A, P_B, X_B, ar))):
         fn()
         ms = _events_ms(fn, steps, s)
-        kms, _ = _kernel_ms(fn, steps, name)
-        out[name] = {"ms": round(ms, 3), "kernel_ms": round(kms, 3) if kms else None,
+        kms, _ = _kernel_ms(fn, steps, kernel)
+        gms, _ = _kernel_ms(fn, steps, kernel.replace("_fast", "_tree"))
+        out[name] = {"ms": round(ms, 3), "kernel": kernel, "kernel_ms": round(kms, 3) if kms else None,
+                     "general_kernel_ms": round(gms, 4) if gms else None,
                      "emulated_TOPs": round(2 * macs / (kms or ms) / 1e9, 3)}
     return out
 

@@ -70,8 +70,8 @@ int mxq_version(void);
  * dominant kernel's own duration, not the whole call's).  With mxq_timer_enable(1), every later launch of a
  * timed kernel records a pair of HIP events on its stream.  mxq_timer_read waits for the pairs recorded under
  * `kernel`, returns their summed milliseconds and their number, and forgets them.  Timed kernels:
- * "systolic_fast", "systolic_general", "block_quantize", "lut_kmeans", "mx_mfma", "adder_tree", "anchor_tree".
- * Not for use under graph capture. */
+ * "systolic_fast", "systolic_general", "block_quantize", "lut_kmeans", "mx_mfma", "adder_fast", "adder_tree",
+ * "anchor_fast", "anchor_tree".  Not for use under graph capture. */
 int mxq_timer_enable(int32_t on);
 int mxq_timer_read(const char* kernel, double* total_ms, int64_t* launches);
 
@@ -164,10 +164,13 @@ int mxq_scores_scale_mask(float* S, int64_t Z, int64_t n, int64_t m, int64_t Tk,
 /* The adder tree: the operands, Arithmetic, scales and output of mxq_systolic; each reduction of `size` products
  * (zeros past a K tail) summed by log2(size) levels of adjacent-pair acc_adds, level l in (level_e[l],
  * level_m[l]), the root rescaled and tile-added into C.  size: a power of two in [2, 32] dividing block_size.
+ * workspace: device memory of mxq_systolic_workspace(M, N, 1) uint32 (the fast kernel's tile flags).
+ * force_general: run the general kernel alone, also where the fast one applies (the two are bit-identical).
  * Replaces mxq/matmul/_adder.py:42-71 (the reduction of :24-32). */
 int mxq_adder_tree(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C, int64_t K,
                    int64_t M, int64_t N, const int32_t* level_e, const int32_t* level_m, int32_t size,
-                   int32_t block_size, const mxq_arith_spec* arith, mxq_stream_t stream);
+                   int32_t block_size, const mxq_arith_spec* arith, uint32_t* workspace, int32_t force_general,
+                   mxq_stream_t stream);
 
 /* The anchor tree's configuration (mxq/matmul/_anchor.py:96-124): width products per tree; drop 0 truncate,
  * 1 rne; headroom; emin applied to code labels when has_emin; nbits = ceil(log2(width + 1)) + 1 level widths
@@ -179,12 +182,13 @@ typedef struct mxq_anchor_spec {
 /* The anchor tree: each reduction of `size` products summed by size / width trees chained through a running
  * sum; a tree aligns its products and the sum to one anchor on an integer grid, adds adjacent pairs level by
  * level (tree_bits: trees x nbits widths, non-increasing, each <= 24) and rounds the root once to the tree's
- * lane (tree_e[t], tree_m[t]).  size must divide 32 and block_size, width must divide size.
+ * lane (tree_e[t], tree_m[t]).  size must divide 32 and block_size, width must divide size.  workspace and
+ * force_general as for mxq_adder_tree.
  * Replaces mxq/matmul/_anchor.py:96-138 (trees of :50-82). */
 int mxq_anchor_tree(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C, int64_t K,
                     int64_t M, int64_t N, const int32_t* tree_e, const int32_t* tree_m, const int32_t* tree_bits,
                     int32_t size, int32_t block_size, const mxq_anchor_spec* spec, const mxq_arith_spec* arith,
-                    mxq_stream_t stream);
+                    uint32_t* workspace, int32_t force_general, mxq_stream_t stream);
 
 /* ---- matrix-core comparison product (no counterpart in the reference, whose unrounded comparison is
  * fp64_accum, mxq/_fp64_accum.py:24-29) ---------------------------------------------------------------- */

@@ -5,7 +5,9 @@ the output.  The pairing is fixed, (0, 1), (2, 3), ..., since a floating-point t
 
 With MXGEMMINI or MXQUANT (or compiled(...) of them) and size <= 32 the whole call is one HIP launch
 (include/mxq_hip.h mxq_adder_tree): every output's reductions run in one thread, products entering a
-binary-counter stack of one pending sum per level.  A hand-made Arithmetic, or a larger size, runs the
+binary-counter stack of one pending sum per level.  For MXGEMMINI with e4 levels of non-decreasing m followed by
+bf16 levels (the README's [(4, 4), (4, 5), (4, 6), (8, 7)], or all bf16) a fast kernel runs first and the general
+one computes only the tiles whose codes it could not take.  A hand-made Arithmetic, or a larger size, runs the
 reference's loop with the Arithmetic's own callables on the operands' device.
 """
 from typing import Sequence, Tuple
@@ -16,16 +18,18 @@ from .. import _lib
 from ..block import BLOCK
 from ._arithmetic import Arithmetic
 from ._common import check_operands, check_schedule, scale_map
-from ._systolic import _lanes_check
+from ._systolic import _lanes_check, workspace_elements
 
 __all__ = ["adder_tree"]
 
 
 def adder_tree(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: torch.Tensor,
                arith: Arithmetic, schedule: Sequence[Tuple[int, int]], size: int = 16,
-               block_size: int = BLOCK) -> torch.Tensor:
+               block_size: int = BLOCK, *, force_general: bool = False) -> torch.Tensor:
     """Y = A^T B.  A: K x M codes, X_A: ceil(K/block_size) x M scales; B: K x N, X_B: ceil(K/block_size) x N.
-    One schedule entry per tree level, level 1 first; `size` a power of two dividing `block_size`."""
+    One schedule entry per tree level, level 1 first; `size` a power of two dividing `block_size`.
+    `force_general` (not in the reference) runs the general kernel even where the fast one applies; the two are
+    bit-identical."""
     K, M, N = check_operands(P_A, X_A, P_B, X_B, block_size)
     levels = size.bit_length() - 1
     if size < 2 or (1 << levels) != size:
@@ -46,9 +50,10 @@ def adder_tree(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: tor
     import ctypes
     le = (ctypes.c_int32 * levels)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * levels)(*[int(m) for _, m in schedule])
+    work = torch.empty(workspace_elements(M, N, 1), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_adder_tree", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, le, lm, size, block_size,
-                 kernel.ctype(), _lib.stream(dev))
+                 kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))
     return _lib.back(C, P_A)
 
 

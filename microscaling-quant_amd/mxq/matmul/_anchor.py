@@ -16,7 +16,8 @@ bits; drop "truncate".  K tail: missing products are zeros.
 
 With MXGEMMINI or MXQUANT (or compiled(...) of them), size dividing 32 and integer widths, the whole call is one
 HIP launch (include/mxq_hip.h mxq_anchor_tree): one thread per output, each tree's terms held in registers as
-exact float64 integers.  Otherwise the reference's loop runs with the Arithmetic's callables on the operands'
+exact integers.  For MXGEMMINI without emin, bf16 trees and equal level widths (the defaults) a fast kernel runs
+first and the general one computes only the tiles whose codes it could not take.  Otherwise the reference's loop runs with the Arithmetic's callables on the operands'
 device.
 """
 import math
@@ -28,7 +29,7 @@ from .. import _lib
 from ..block import BLOCK
 from ._arithmetic import Arithmetic
 from ._common import check_operands, check_schedule, scale_map
-from ._systolic import _lanes_check
+from ._systolic import _lanes_check, workspace_elements
 
 __all__ = ["anchor_tree", "DROPS"]
 
@@ -43,9 +44,11 @@ def _levels_for(width: int) -> int:
 def anchor_tree(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: torch.Tensor,
                 arith: Arithmetic, schedule: Optional[Sequence[Tuple[int, int]]] = None, size: int = 16,
                 block_size: int = BLOCK, *, width: Optional[int] = None, bits: Optional[Sequence[int]] = None,
-                drop: str = "truncate", headroom: Optional[int] = None, emin: Optional[int] = None) -> torch.Tensor:
+                drop: str = "truncate", headroom: Optional[int] = None, emin: Optional[int] = None,
+                force_general: bool = False) -> torch.Tensor:
     """Y = A^T B, each reduction of `size` products summed by chained anchor trees of `width` products.
-    `schedule`: one (e, m) per tree (default bf16)."""
+    `schedule`: one (e, m) per tree (default bf16).  `force_general` (not in the reference) runs the general
+    kernel even where the fast one applies; the two are bit-identical."""
     K, M, N = check_operands(P_A, X_A, P_B, X_B, block_size)
     width = size if width is None else width
     if width < 1 or size % width or block_size % size:
@@ -86,9 +89,10 @@ def anchor_tree(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: to
     tb = (ctypes.c_int32 * (trees * (lg + 1)))(*[int(b) for _, _, ws in per_tree for b in ws])
     spec = _lib.AnchorSpec(width=width, drop=DROPS.index(drop), headroom=head, has_emin=int(emin is not None),
                            emin=0 if emin is None else emin, nbits=lg + 1)
+    work = torch.empty(workspace_elements(M, N, 1), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_anchor_tree", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, te, tm, tb, size, block_size,
-                 ctypes.byref(spec), kernel.ctype(), _lib.stream(dev))
+                 ctypes.byref(spec), kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))
     return _lib.back(C, P_A)
 
 

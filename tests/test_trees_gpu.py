@@ -150,3 +150,124 @@ def test_trees_empty_and_zero_k(cuda):
         Y = fn(z(0, 5), z(0, 5), z(0, 7), z(0, 7))
         assert Y.shape == (5, 7) and torch.equal(Y, z(5, 7))
         assert fn(z(64, 0), z(2, 0), z(64, 7), z(2, 7)).shape == (0, 7)
+
+
+# ------------------------------------------------------------------------------------ fast kernels
+def _launches(kernel, fn):
+    """Runs fn with the library's kernel timer on; returns (fn's result, launches of `kernel`)."""
+    from mxq import _lib
+    torch.cuda.synchronize()
+    _lib.timer_read(kernel)
+    _lib.timer_enable(True)
+    try:
+        out = fn()
+    finally:
+        _lib.timer_enable(False)
+    return out, _lib.timer_read(kernel)[1]
+
+
+def _edge_columns(n, w=48):
+    """Column slices checked against the oracle: the first and last w columns (every tile position kind)."""
+    return [slice(0, min(w, n)), slice(max(0, n - w), n)]
+
+
+ADDER_FAST = [
+    (16, [(4, 4), (4, 5), (4, 6), (8, 7)], ("MXGEMMINI",)),
+    (16, [(8, 7)] * 4, ("MXGEMMINI",)),
+    (4, [(4, 3), (8, 7)], ("MXGEMMINI",)),
+    (8, [(4, 4), (4, 4), (4, 7)], ("MXGEMMINI",)),
+    (32, [(4, 4), (4, 5), (4, 6), (8, 7), (8, 7)], ("MXGEMMINI",)),
+    (16, [(4, 4), (4, 5), (4, 6), (8, 7)], ("MXGEMMINI", 4, 3, None)),
+    (16, [(4, 6), (4, 6), (4, 9), (4, 9)], ("MXGEMMINI",)),
+]
+
+
+@pytest.mark.parametrize("case", ADDER_FAST, ids=[f"af{i}" for i in range(len(ADDER_FAST))])
+@pytest.mark.parametrize("shape", [(256, 136, 200), (77, 40, 70), (64, 2944, 2944)])
+def test_adder_fast_kernel(cuda, case, shape):
+    """The fast adder kernel on its own configurations: every output equal to the general kernel's, and the
+    oracle's on edge column slices (columns are independent chains); 2944 x 2944 takes the 64 x 64 tiles."""
+    from mxq import matmul
+    size, sched, ar_args = case
+    K, M, N = shape
+    rng = np.random.default_rng(size * 13 + K + M)
+    PA, XA = _codes(rng, K, M)
+    PB, XB = _codes(rng, K, N, scale=0.02)
+    ar, orc = _arith(*ar_args)
+    ops = _t(PA, XA, PB, XB)
+    got, n = _launches("adder_fast", lambda: matmul.adder_tree(*ops, ar, sched, size))
+    assert n == 1, "the fast adder kernel did not run"
+    gen = matmul.adder_tree(*ops, ar, sched, size, force_general=True)
+    assert_bits_equal(got.cpu().numpy(), gen.cpu().numpy(), f"adder fast vs general {case} {shape}")
+    got = got.cpu().numpy()
+    for cs in _edge_columns(N):
+        want = ot.adder_tree(PA, XA, PB[:, cs], XB[:, cs], orc, sched, size)
+        assert_bits_equal(got[:, cs], want, f"adder fast vs oracle {case} {shape} {cs}")
+
+
+ANCHOR_FAST = [
+    # size, width, drop, headroom, bits, arithmetic
+    (16, None, "truncate", None, None, ("MXGEMMINI",)),
+    (16, 8, "truncate", None, None, ("MXGEMMINI",)),
+    (16, 4, "rne", None, None, ("MXGEMMINI",)),
+    (32, None, "rne", None, None, ("MXGEMMINI", 4, 3, None)),
+    (32, 16, "truncate", 7, [18] * 6, ("MXGEMMINI",)),
+    (8, 8, "rne", 5, [12] * 5, ("MXGEMMINI", 4, 3, -20)),
+]
+
+
+@pytest.mark.parametrize("case", ANCHOR_FAST, ids=[f"nf{i}" for i in range(len(ANCHOR_FAST))])
+@pytest.mark.parametrize("shape", [(256, 136, 200), (45, 40, 70), (64, 2944, 2944)])
+def test_anchor_fast_kernel(cuda, case, shape):
+    """The fast anchor kernel on its own configurations, against the general kernel everywhere and the oracle
+    on edge column slices.  Zero codes (a zero column, zero K rows) and a row of small codes, whose trees have
+    anchors too low for the fast path, send some tiles to the general kernel."""
+    from mxq import matmul
+    size, width, drop, head, bits, ar_args = case
+    K, M, N = shape
+    rng = np.random.default_rng(size * 5 + K + M)
+    PA, XA = _codes(rng, K, M)
+    PB, XB = _codes(rng, K, N, scale=0.3)
+    PA[:, 3] = 0.0
+    PA[min(5, K - 1), :] = 0.0
+    PA[:, 7] *= np.float32(2.0 ** -14)
+    ar, orc = _arith(*ar_args)
+    ops = _t(PA, XA, PB, XB)
+    kw = dict(width=width, bits=bits, drop=drop, headroom=head)
+    got, n = _launches("anchor_fast", lambda: matmul.anchor_tree(*ops, ar, None, size, **kw))
+    assert n == 1, "the fast anchor kernel did not run"
+    gen = matmul.anchor_tree(*ops, ar, None, size, force_general=True, **kw)
+    assert_bits_equal(got.cpu().numpy(), gen.cpu().numpy(), f"anchor fast vs general {case} {shape}")
+    got = got.cpu().numpy()
+    for cs in _edge_columns(N):
+        want = ot.anchor_tree(PA, XA, PB[:, cs], XB[:, cs], orc, None, size, 32, width, bits, drop, head)
+        assert_bits_equal(got[:, cs], want, f"anchor fast vs oracle {case} {shape} {cs}")
+
+
+@pytest.mark.parametrize("which", ["adder", "anchor"])
+def test_trees_fast_kernel_falls_back(cuda, which):
+    """Tiles whose codes the fast kernels cannot take (overflowing e4 levels, saturating products, Inf, NaN,
+    tiny anchors) are computed by the general kernel: the result equals the general kernel's alone."""
+    from mxq import matmul
+    rng = np.random.default_rng(23)
+    K, M, N = 96, 130, 140
+    PA, XA = _codes(rng, K, M)
+    PB, XB = _codes(rng, K, N)
+    PA[:, 70:] *= np.float32(64.0)            # products up to 256: beyond the e4 levels' bound
+    PB[10, 100] = np.inf
+    PB[40, 30] = np.nan
+    PA[:, 1] *= np.float32(2.0 ** -40)
+    XB[1, 5] = np.float32(0.3)
+    hw = matmul.MXGEMMINI()
+    ops = _t(PA, XA, PB, XB)
+    if which == "adder":
+        sched = [(4, 4), (4, 5), (4, 6), (8, 7)]
+        fn = lambda fg: matmul.adder_tree(*ops, hw, sched, force_general=fg)        # noqa: E731
+        want = ot.adder_tree(PA, XA, PB, XB, nx.MXGEMMINI(), sched)
+    else:
+        fn = lambda fg: matmul.anchor_tree(*ops, hw, force_general=fg)              # noqa: E731
+        want = ot.anchor_tree(PA, XA, PB, XB, nx.MXGEMMINI())
+    got, n = _launches(f"{which}_fast", lambda: fn(False))
+    assert n == 1
+    assert_bits_equal(got.cpu().numpy(), fn(True).cpu().numpy(), f"{which} fallback vs general")
+    assert_bits_equal(got.cpu().numpy(), want, f"{which} fallback vs oracle")
