@@ -42,7 +42,10 @@ using namespace mxq_red;
 
 constexpr int kMaxLanes = 64;
 constexpr uint32_t kFastAMaxBits = 0x71800000u;   // 2^100: A's rows are staged times up to 2^15
-constexpr int FBN = 64;                           // the fast kernel's tile width (its height is 64 or 32)
+// The fast kernel's tiles: 64 x 64, 32 x 64 or 32 x 32 outputs, the largest that still gives the chip at least
+// 8 workgroups per CU.  More waves per SIMD issue the VALU chains faster than more outputs per thread: on C2's
+// 512 x 4096 outputs, 32 x 32 tiles (2 x 2 per thread, 2048 workgroups) beat 32 x 64 (1024) by 3 %.  (Holding
+// the 32 x 32 instance to 64 VGPRs for 8 waves per SIMD made it spill and lose 3 %.)
 
 
 struct SysArgs {
@@ -51,7 +54,7 @@ struct SysArgs {
   int64_t ldc, batch_c;   // C: M x N
   uint32_t* flags;        // one per fast tile per problem (1: the general kernel computes it)
   int64_t tiles_x, tiles_y;
-  int fbm;                // the fast kernel's tile height
+  int fbm, fbn;           // the fast kernel's tile height and width
   int64_t K, M, N;
   int size, block_size;
   mxq_arith_spec ar;
@@ -146,11 +149,11 @@ struct ScaledRows {
   }
 };
 
-// BM = 64: 4 x 4 outputs per thread; BM = 32: 2 x 4, for problems with too few 64 x 64 tiles to fill the chip.
+// BM x BN outputs per workgroup, (BM / 16) x (BN / 16) per thread.
 // HWF: the lanes are HW_FINAL's (SIZE 16, bf16 last), whose constants are then immediates.
-template <int SIZE, bool BF16_LAST, int BM, bool HWF>
+template <int SIZE, bool BF16_LAST, int BM, int BN, bool HWF>
 __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const FastLanes fl) {
-  constexpr int BN = FBN, TM = BM / 16, TN = 4, NT = 256;
+  constexpr int TM = BM / 16, TN = BN / 16, NT = 256;
   static_assert(!HWF || (SIZE == 16 && BF16_LAST), "HW_FINAL has 16 lanes, the last bf16");
   const LaneConsts<HWF> lc{fl};
   static_assert((BM / TM) * (BN / TN) == NT, "256 threads");
@@ -240,8 +243,14 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
           const float2 a2 = *reinterpret_cast<const float2*>(&sm.a[buf][r0 + i][tm * TM]);
           a[0] = a2.x; a[1] = a2.y;
         }
-        const float4 b4 = *reinterpret_cast<const float4*>(&sm.b[buf][r0 + i][tn * TN]);
-        const float b[TN] = {b4.x, b4.y, b4.z, b4.w};
+        float b[TN];
+        if constexpr (TN == 4) {
+          const float4 b4 = *reinterpret_cast<const float4*>(&sm.b[buf][r0 + i][tn * TN]);
+          b[0] = b4.x; b[1] = b4.y; b[2] = b4.z; b[3] = b4.w;
+        } else {
+          const float2 b2 = *reinterpret_cast<const float2*>(&sm.b[buf][r0 + i][tn * TN]);
+          b[0] = b2.x; b[1] = b2.y;
+        }
         if (BF16_LAST && i == SIZE - 1) {
           // bf16 lane: S (an e4 value, at most 8 significant bits) plus the truncated, flushed product
           // (prod_m + 1 <= 8 bits), one float32 add and bit RNE to bf16
@@ -352,11 +361,11 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 // only_flagged: compute just the outputs whose fast tile has its flag set (the fast kernel ran first).
 template <int BM, int BN, int TM, int TN>
 __global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const SysArgs args, int only_flagged) {
-  static_assert(32 % BM == 0 && FBN % BN == 0, "a general tile lies inside one fast tile");
+  static_assert(32 % BM == 0 && 32 % BN == 0, "a general tile lies inside one fast tile");
   constexpr int NT = (BM / TM) * (BN / TN);
   const int64_t z = blockIdx.z;
   if (only_flagged) {
-    const int64_t fy = (int64_t)blockIdx.y * BM / args.fbm, fx = (int64_t)blockIdx.x * BN / FBN;
+    const int64_t fy = (int64_t)blockIdx.y * BM / args.fbm, fx = (int64_t)blockIdx.x * BN / args.fbn;
     if (args.flags[(z * args.tiles_y + fy) * args.tiles_x + fx] == 0u) return;
   }
   __shared__ Smem<BM, BN> sm;
@@ -532,15 +541,17 @@ FastLanes make_fast_lanes(const int32_t* e, const int32_t* m, int size, const mx
   return fl;
 }
 
+template <int SIZE, bool BF16_LAST, bool HWF>
+void launch_fast_tile(dim3 grid, hipStream_t st, const SysArgs& a, const FastLanes& fl) {
+  if (a.fbm == 64) k_systolic_fast<SIZE, BF16_LAST, 64, 64, HWF><<<grid, 256, 0, st>>>(a, fl);
+  else if (a.fbn == 64) k_systolic_fast<SIZE, BF16_LAST, 32, 64, HWF><<<grid, 256, 0, st>>>(a, fl);
+  else k_systolic_fast<SIZE, BF16_LAST, 32, 32, HWF><<<grid, 256, 0, st>>>(a, fl);
+}
+
 template <int SIZE>
 void launch_fast_size(bool bf16_last, dim3 grid, hipStream_t st, const SysArgs& a, const FastLanes& fl) {
-  if (a.fbm == 64) {
-    if (bf16_last) k_systolic_fast<SIZE, true, 64, false><<<grid, 256, 0, st>>>(a, fl);
-    else k_systolic_fast<SIZE, false, 64, false><<<grid, 256, 0, st>>>(a, fl);
-  } else {
-    if (bf16_last) k_systolic_fast<SIZE, true, 32, false><<<grid, 256, 0, st>>>(a, fl);
-    else k_systolic_fast<SIZE, false, 32, false><<<grid, 256, 0, st>>>(a, fl);
-  }
+  if (bf16_last) launch_fast_tile<SIZE, true, false>(grid, st, a, fl);
+  else launch_fast_tile<SIZE, false, false>(grid, st, a, fl);
 }
 
 bool is_hw_final(const int32_t* e, const int32_t* m, int size) {
@@ -553,8 +564,7 @@ bool is_hw_final(const int32_t* e, const int32_t* m, int size) {
 void launch_fast(int size, bool bf16_last, bool hwf, dim3 grid, hipStream_t st, const SysArgs& a,
                  const FastLanes& fl) {
   if (hwf) {
-    if (a.fbm == 64) k_systolic_fast<16, true, 64, true><<<grid, 256, 0, st>>>(a, fl);
-    else k_systolic_fast<16, true, 32, true><<<grid, 256, 0, st>>>(a, fl);
+    launch_fast_tile<16, true, true>(grid, st, a, fl);
     return;
   }
   switch (size) {
@@ -578,9 +588,12 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
   const mxq_arith_spec& ar = base.ar;
   SysArgs a = base;
   for (int i = 0; i < a.size; ++i) { a.lane_e[i] = (int8_t)lane_e[i]; a.lane_m[i] = (int8_t)lane_m[i]; }
-  a.tiles_x = mxq::ceil_div(a.N, FBN);
-  // 64-row tiles while they give every CU at least 8 workgroups, else 32-row tiles (twice the waves)
-  a.fbm = (mxq::ceil_div(a.M, 64) * a.tiles_x * count >= 8 * 256) ? 64 : 32;
+  // the largest fast tile that gives every CU at least 8 workgroups (else the smallest)
+  const int64_t want = 8 * 256;
+  if (mxq::ceil_div(a.M, 64) * mxq::ceil_div(a.N, 64) * count >= want) { a.fbm = 64; a.fbn = 64; }
+  else if (mxq::ceil_div(a.M, 32) * mxq::ceil_div(a.N, 64) * count >= want) { a.fbm = 32; a.fbn = 64; }
+  else { a.fbm = 32; a.fbn = 32; }
+  a.tiles_x = mxq::ceil_div(a.N, a.fbn);
   a.tiles_y = mxq::ceil_div(a.M, a.fbm);
   a.fast_prod_max = 0.0f;
   const bool fast_lanes = !force_general && a.K > 0 && lanes_fast(lane_e, lane_m, a.size, ar);
@@ -659,5 +672,5 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
 
 extern "C" int64_t mxq_systolic_workspace(int64_t M, int64_t N, int64_t count) {
   if (M <= 0 || N <= 0 || count <= 0) return 1;
-  return mxq::ceil_div(M, 32) * mxq::ceil_div(N, FBN) * count;   // the smaller of the two fast tiles
+  return mxq::ceil_div(M, 32) * mxq::ceil_div(N, 32) * count;    // the smallest fast tile
 }

@@ -257,17 +257,25 @@ def test_batched_matches_single(cuda, sched_name):
         assert torch.isnan(C[z, :, N:]).all(), "columns past N are left alone"
 
 
-def test_both_fast_tile_heights(cuda):
-    """2048 x 4096 outputs run on 64-row fast tiles, 512 x 4096 on 32-row ones (too few 64-row tiles to fill
-    the chip); both against the oracle on column slices (columns are independent chains)."""
+def test_all_fast_tile_shapes(cuda):
+    """The fast kernel's three tiles: 2048 x 4096 outputs run on 64 x 64 tiles, 1024 x 4096 on 32 x 64 and
+    500 x 4000 on 32 x 32 (too few larger tiles to give every CU 8 workgroups), with HW_FINAL's instance and a
+    generic ladder: every output equal to the general kernel's, edge column slices equal to the oracle's
+    (columns are independent chains)."""
     from mxq import matmul
     rng = np.random.default_rng(8)
-    for M in (2048, 512):
-        K, N = 64, 4096
+    ladder = [(4, 4)] * 6 + [(4, 5)] * 6 + [(4, 7)] * 3 + [(8, 7)]
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()          # noqa: E731
+    for M, N in ((2048, 4096), (1024, 4096), (500, 4000)):
+        K = 64
         P_A, X_A = _codes(rng, K, M)
         P_B, X_B = _codes(rng, K, N, scale=0.1)
-        t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()      # noqa: E731
-        Y = matmul.systolic(t(P_A), t(X_A), t(P_B), t(X_B), matmul.MXGEMMINI(), matmul.HW_FINAL).cpu().numpy()
-        for cols in (slice(0, 8), slice(4090, 4096)):
-            want = osys.systolic(P_A, X_A, P_B[:, cols], X_B[:, cols], nx.MXGEMMINI(), HW_FINAL)
-            assert_bits_equal(Y[:, cols], want, f"M={M} cols {cols}")
+        ops = [t(x) for x in (P_A, X_A, P_B, X_B)]
+        for sched in (HW_FINAL, ladder):
+            Y = matmul.systolic(*ops, matmul.MXGEMMINI(), sched)
+            G = matmul.systolic(*ops, matmul.MXGEMMINI(), sched, force_general=True)
+            assert_bits_equal(Y.cpu().numpy(), G.cpu().numpy(), f"{M}x{N} fast vs general")
+            Y = Y.cpu().numpy()
+            for cols in (slice(0, 8), slice(N - 6, N)):
+                want = osys.systolic(P_A, X_A, P_B[:, cols], X_B[:, cols], nx.MXGEMMINI(), sched)
+                assert_bits_equal(Y[:, cols], want, f"{M}x{N} cols {cols}")
