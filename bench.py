@@ -116,6 +116,17 @@ def quantize_lines(torch, steps):
         out[fmt] = round(bytes_c3 / ms / 1e6, 1)
         kms, _ = _kernel_ms(fn, steps, "block_quantize")
         kern[fmt] = round(bytes_c3 / kms / 1e6, 1) if kms else None
+    # the same quantize written as code and E8M0 bytes in one pass (mxq.packed, not in the reference)
+    import mxq
+    bytes_pk = 8192 * 8192 * 2 + 8192 * 8192 + 256 * 8192
+    pk, pk_kern = {}, {}
+    for fmt in ("MXFP8_E4M3", "MXFP8_E5M2", "MXFP6_E3M2", "MXFP6_E2M3", "MXFP4"):
+        fn = lambda: mxq.packed.quantize(V, fmt, rounding_mode="rne", check=False)            # noqa: E731
+        fn()
+        ms = _events_ms(fn, steps, s)
+        pk[fmt] = round(bytes_pk / ms / 1e6, 1)
+        kms, _ = _kernel_ms(fn, steps, "block_quantize")
+        pk_kern[fmt] = round(bytes_pk / kms / 1e6, 1) if kms else None
     del V
     # 17 MB per call: rotate over 64 inputs (1.1 GB with outputs) so HBM, not the cache, serves them
     rot = [torch.randn(4096, 512, device=dev) for _ in range(64)]
@@ -132,6 +143,8 @@ def quantize_lines(torch, steps):
     ms1d = _events_ms(lambda: block.ocp.dequantize(P, X, axis=0), 64, s)
     return {"mxgemmini_bf16_8192x8192_rne_GBs": out, "mxgemmini_bf16_8192x8192_rne_kernel_GBs": kern,
             "mxgemmini_bytes_per_call": bytes_c3,
+            "packed_bf16_8192x8192_rne_GBs": pk, "packed_bf16_8192x8192_rne_kernel_GBs": pk_kern,
+            "packed_bytes_per_call": bytes_pk,
             "ocp_e4m3_4096x512_quantize_GBs": round(bytes_c1 / ms1 / 1e6, 1),
             "ocp_e4m3_4096x512_quantize_kernel_GBs": round(bytes_c1 / kms1 / 1e6, 1) if kms1 else None,
             "ocp_e4m3_4096x512_dequantize_GBs_cache_resident": round(bytes_c1 / ms1d / 1e6, 1),

@@ -95,6 +95,36 @@ int mxq_block_quantize_t(const void* M, int32_t v_dtype, float* P, float* X, int
 int mxq_block_dequantize(const float* P, const float* X, float* out, int64_t outer, int64_t n, int64_t inner,
                          int64_t block_size, mxq_stream_t stream);
 
+/* ---- packed wire formats (no counterpart in the reference, whose codes and scales are float32 tensors) ----
+ * Element codes are bytes in the OCP MX layout, sign | e exponent bits | m mantissa bits with bias
+ * 2^(e-1) - 1 (the numbering of the reference's element codes, mxq/lut/formats.py:87-99, on every finite value;
+ * E5M2 keeps Inf and NaN, E4M3's NaN is S.1111.111, FP6 and FP4 have no specials); (e, m) is one of (4, 3),
+ * (5, 2), (3, 2), (2, 3), (2, 1).  Scales are E8M0 bytes: 2^k is k + 127 for k in [-127, 127], NaN is 0xFF; a
+ * block whose codes are all zero may have any scale (its values are 0 under any) and gets 0.  Codes are shaped
+ * like P and scales like X.  `err` is an int32 device word the caller clears: bit 0 is set when a code is not
+ * a value of the format, bit 1 when a scale of a nonzero block is not an E8M0 value. */
+
+/* mxq_block_quantize with the codes and scales written as bytes, in one pass (a quarter of the float32 output
+ * bytes).  The element rule must be the qtorch grid (mxquant), the ocp grid (mxgemmini) or the microxcaling step
+ * (block.ocp) of an OCP MX format; the code bytes are that format's. */
+int mxq_block_quantize_packed(const void* V, int32_t v_dtype, uint8_t* codes, uint8_t* scales, int32_t* err,
+                              int64_t outer, int64_t n, int64_t inner, int64_t block_size, const mxq_block_spec* spec,
+                              mxq_stream_t stream);
+
+/* float32 codes P and scales X of format (e, m) -> bytes. */
+int mxq_pack(const float* P, const float* X, uint8_t* codes, uint8_t* scales, int32_t* err, int64_t outer, int64_t n,
+             int64_t inner, int64_t block_size, int32_t e, int32_t m, mxq_stream_t stream);
+
+/* bytes -> float32 codes P and scales X (either may be NULL to skip it).  For a block whose scale mxq_pack or
+ * mxq_block_quantize_packed replaced (all-zero codes), X reads 2^-127. */
+int mxq_unpack(const uint8_t* codes, const uint8_t* scales, float* P, float* X, int64_t outer, int64_t n,
+               int64_t inner, int64_t block_size, int32_t e, int32_t m, mxq_stream_t stream);
+
+/* bytes -> the dequantized values P * expand(X), float32, without materialising P or X; bit-identical to
+ * mxq_block_dequantize of the float32 codes and scales the bytes hold. */
+int mxq_dequantize_packed(const uint8_t* codes, const uint8_t* scales, float* out, int64_t outer, int64_t n,
+                          int64_t inner, int64_t block_size, int32_t e, int32_t m, mxq_stream_t stream);
+
 /* The systolic PE column: C = A^T B (M x N float32) from codes A (K x M), B (K x N) and block scales X_A
  * (ceil(K/block_size) x M), X_B (ceil(K/block_size) x N), all float32 row-major.  Per block of K the scale map
  * X_A[g] (x) X_B[g]; per reduction of `size` k a fresh sum accumulated lane by lane (lane i has the format
@@ -235,6 +265,16 @@ int mxq_lut_pick(const float* P, int64_t K, int64_t n, int32_t group, const floa
  * Replaces mxq/lut/kmeans.py:141-146. */
 int mxq_lut_lookup(const int64_t* I, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,
                    float* out, mxq_stream_t stream);
+
+/* mxq_lut_pick's indices as the wire's 4-bit nibbles (no counterpart in the reference, which returns int64):
+ * row k's byte j / 2 holds column j's index in its low nibble (j even) and column j + 1's in its high one
+ * (0 past n); I4 is K x ceil(n / 2) bytes.  width <= 16. */
+int mxq_lut_pick_packed(const float* P, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,
+                        uint8_t* I4, mxq_stream_t stream);
+
+/* mxq_lut_lookup of 4-bit indices in mxq_lut_pick_packed's layout. */
+int mxq_lut_lookup_packed(const uint8_t* I4, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,
+                          float* out, mxq_stream_t stream);
 
 /* lut.finder: fx_all[c] is element code c's fixed point (ncodes entries), lut_fx the fixed points of each
  * group's 16 entries (ceil(n/2^group) x 16); out = argmin over entries of |fx - lut_fx| & mask (mask 0: none),

@@ -8,8 +8,10 @@
 //                 snap to the nearest finder-safe value, pad with unused safe values smallest magnitude first,
 //                 sort.  Lanes own grid bins for the assignment step; the sums are exact in float64 (counts times
 //                 grid values have few significant bits), so their order does not matter
-//   k_lut_pick    nearest table entry per code (ties to the lower index), int64 index or the entry's value
-//   k_lut_lookup  the entries named by int64 indices
+//   k_lut_pick    nearest table entry per code (ties to the lower index): int64 index, the entry's value, or
+//                 4-bit indices two to a byte (the wire format: adjacent lanes hold adjacent columns and pair
+//                 up through a shuffle)
+//   k_lut_lookup  the entries named by int64 indices; k_lut_lookup4 by 4-bit ones
 //   k_lut_finder  the chip's finder: nearest in fixed point with the format's |difference| mask, first index
 #include "mxq_common.h"
 #include "mxq_numerics.h"
@@ -347,9 +349,12 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(const int* __restrict__ count
 
 // Nearest entry of each code's group table (ascending; ties to the lower index).  mode 0: int64 index to I;
 // mode 1: the entry's value to Pout.  One thread per column walks a stripe of rows; the block's tables in LDS.
+// Exactly one of I, Pout, I4 is set.  I4: row k's byte j / 2 holds column j's index in its low nibble (j even)
+// and column j + 1's in its high one (0 past n).
 __global__ void __launch_bounds__(256) k_lut_pick(const float* __restrict__ P, int64_t K, int64_t n, int group,
                                                   const float* __restrict__ T, int width, int64_t rows_per_block,
-                                                  int64_t* __restrict__ I, float* __restrict__ Pout) {
+                                                  int64_t* __restrict__ I, float* __restrict__ Pout,
+                                                  uint8_t* __restrict__ I4) {
   extern __shared__ float rows_s[];                 // (256 >> group, at least 1) x width
   const int64_t c0 = (int64_t)blockIdx.x * 256;
   const int64_t g0 = c0 >> group;
@@ -361,15 +366,18 @@ __global__ void __launch_bounds__(256) k_lut_pick(const float* __restrict__ P, i
   }
   __syncthreads();
   const int64_t j = c0 + threadIdx.x;
-  if (j >= n) return;
-  const float* row = rows_s + (int)((j >> group) - g0) * width;
+  const bool live = j < n;
+  if (!live && !I4) return;                          // the nibble output keeps every lane for its shuffle
+  const int64_t jj = live ? j : n - 1;               // a column of this block (c0 < n)
+  const float* row = rows_s + (int)((jj >> group) - g0) * width;
+  const int64_t nbytes = (n + 1) >> 1;
   const int64_t k0 = (int64_t)blockIdx.y * rows_per_block;
   const int64_t kend = (k0 + rows_per_block < K) ? k0 + rows_per_block : K;
   constexpr int U = 8;                                 // loads in flight per thread
   for (int64_t kb = k0; kb < kend; kb += U) {
     float v[U];
 #pragma unroll
-    for (int t = 0; t < U; ++t) v[t] = kb + t < kend ? P[(kb + t) * n + j] : 0.0f;
+    for (int t = 0; t < U; ++t) v[t] = kb + t < kend ? P[(kb + t) * n + jj] : 0.0f;
 #pragma unroll
     for (int t = 0; t < U; ++t) {
       const int64_t k = kb + t;
@@ -380,8 +388,14 @@ __global__ void __launch_bounds__(256) k_lut_pick(const float* __restrict__ P, i
       const float d_lo = fabsf(v[t] - row[lo]);
       const float d_hi = fabsf(row[hi] - v[t]);
       const int pick = (d_lo <= d_hi) ? lo : hi;
-      if (I) I[k * n + j] = pick;
-      else Pout[k * n + j] = row[pick];
+      if (I4) {                                       // k < kend holds for the whole block: all lanes shuffle
+        const int next = __shfl_xor(pick, 1, 64);
+        if (live && (j & 1) == 0) I4[k * nbytes + (j >> 1)] = (uint8_t)(pick | ((j + 1 < n ? next : 0) << 4));
+      } else if (I) {
+        I[k * n + j] = pick;
+      } else {
+        Pout[k * n + j] = row[pick];
+      }
     }
   }
 }
@@ -392,6 +406,17 @@ __global__ void __launch_bounds__(256) k_lut_lookup(const int64_t* __restrict__ 
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t j = e % n;
     out[e] = T[(j >> group) * width + I[e]];
+  }
+}
+
+__global__ void __launch_bounds__(256) k_lut_lookup4(const uint8_t* __restrict__ I4, int64_t K, int64_t n,
+                                                     int group, const float* __restrict__ T, int width,
+                                                     float* __restrict__ out) {
+  const int64_t total = K * n, nbytes = (n + 1) >> 1;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = e / n, j = e - k * n;
+    const int idx = (I4[k * nbytes + (j >> 1)] >> ((j & 1) * 4)) & 0xF;
+    out[e] = T[(j >> group) * width + idx];
   }
 }
 
@@ -480,8 +505,38 @@ extern "C" int mxq_lut_pick(const float* P, int64_t K, int64_t n, int32_t group,
   const int64_t rpb = mxq::ceil_div(K, row_blocks);
   row_blocks = mxq::ceil_div(K, rpb);
   k_lut_pick<<<dim3((unsigned)col_blocks, (unsigned)row_blocks), 256, lds, mxq::as_stream(stream)>>>(
-      P, K, n, group, T, width, rpb, I, P_lut);
+      P, K, n, group, T, width, rpb, I, P_lut, nullptr);
   return mxq::check_launch("mxq_lut_pick");
+}
+
+extern "C" int mxq_lut_pick_packed(const float* P, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,
+                                   uint8_t* I4, mxq_stream_t stream) {
+  if (K < 0 || n < 0 || group < 0 || group > 30 || width < 2 || width > kSize)
+    return mxq::invalid("mxq_lut_pick_packed: bad arguments");
+  if (K == 0 || n == 0) return MXQ_OK;
+  if (!P || !T || !I4) return mxq::invalid("mxq_lut_pick_packed: NULL pointer");
+  const size_t lds = (size_t)((256 >> group) > 0 ? (256 >> group) : 1) * width * sizeof(float);
+  const int64_t col_blocks = mxq::ceil_div(n, 256);
+  int64_t row_blocks = mxq::ceil_div(1024, col_blocks);
+  if (row_blocks > K) row_blocks = K;
+  if (row_blocks > 65535) row_blocks = 65535;
+  const int64_t rpb = mxq::ceil_div(K, row_blocks);
+  row_blocks = mxq::ceil_div(K, rpb);
+  k_lut_pick<<<dim3((unsigned)col_blocks, (unsigned)row_blocks), 256, lds, mxq::as_stream(stream)>>>(
+      P, K, n, group, T, width, rpb, nullptr, nullptr, I4);
+  return mxq::check_launch("mxq_lut_pick_packed");
+}
+
+extern "C" int mxq_lut_lookup_packed(const uint8_t* I4, int64_t K, int64_t n, int32_t group, const float* T,
+                                     int32_t width, float* out, mxq_stream_t stream) {
+  if (K < 0 || n < 0 || group < 0 || group > 30 || width < 1 || width > kSize)
+    return mxq::invalid("mxq_lut_lookup_packed: bad arguments");
+  if (K == 0 || n == 0) return MXQ_OK;
+  if (!I4 || !T || !out) return mxq::invalid("mxq_lut_lookup_packed: NULL pointer");
+  int64_t blocks = mxq::ceil_div(K * n, 256);
+  if (blocks > 65536) blocks = 65536;
+  k_lut_lookup4<<<dim3((unsigned)blocks), 256, 0, mxq::as_stream(stream)>>>(I4, K, n, group, T, width, out);
+  return mxq::check_launch("mxq_lut_lookup_packed");
 }
 
 extern "C" int mxq_lut_lookup(const int64_t* I, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,

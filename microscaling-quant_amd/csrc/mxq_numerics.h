@@ -538,6 +538,29 @@ MXQ_HD float ocp_grid_t(float z, int e, int m, float max_norm) {
   return (a >= 0x7F800000u) ? z : out;
 }
 
+// ocp_grid_t's result as its element code (mx_encode's layout), from the same two roundings: the rounded
+// significand bits (normal: bits >> (23 - m), less the float32-to-format exponent bias difference) or the
+// rounded multiple of the subnormal step (whose 2^m is the code of the smallest normal), clamped at the
+// largest finite code `maxcode` as the grid clamps at max_norm.  An exact +-0 is +0, a value rounded to 0 keeps
+// its sign.  *good is cleared for Inf and NaN, which the grid passes through and mx_encode takes.
+template <int MODE>
+MXQ_HD uint32_t ocp_code_t(float z, int e, int m, uint32_t maxcode, bool* good) {
+  const uint32_t u = f2u(z), a = u & 0x7FFFFFFFu;
+  const int emin = 2 - (1 << (e - 1));
+  const uint32_t rn = round_bits32_t<MODE>(a, m);
+  const float k = u2f(a) * pow2f(m - emin);
+  float r;
+  if constexpr (MODE == MXQ_RNE) r = rintf(k);
+  else if constexpr (MODE == MXQ_TIES_AWAY) r = floorf(k + 0.5f);
+  else r = truncf(k);
+  const uint32_t nsub = (uint32_t)(128 - (1 << (e - 1))) << m;
+  const uint32_t cn = (rn >> (23 - m)) - nsub;
+  uint32_t mag = (a >= ((uint32_t)(emin + 127) << 23)) ? cn : (uint32_t)(int)r;
+  mag = mag < maxcode ? mag : maxcode;
+  *good = a < 0x7F800000u;
+  return (a == 0u) ? 0u : (mag | ((u >> 31) << (e + m)));
+}
+
 MXQ_HD float ocp_grid_fast(float z, int e, int m, int mode, float max_norm) {
   if (mode == MXQ_RNE) return ocp_grid_t<MXQ_RNE>(z, e, m, max_norm);
   if (mode == MXQ_TIES_AWAY) return ocp_grid_t<MXQ_TIES_AWAY>(z, e, m, max_norm);
@@ -567,3 +590,72 @@ MXQ_HD float elem_qm(float z, const mxq_block_spec& s) {
 template <int ELEM>
 MXQ_HD float elem_q(float z, const mxq_block_spec& s) { return elem_qm<ELEM, -1>(z, s); }
 
+
+// ----------------------------------------------------------------------------------- packed byte codes
+// Element codes in the OCP MX layout (OCP Microscaling Formats v1.0): sign | e exponent bits | m mantissa bits,
+// bias 2^(e-1) - 1, low bits of a byte.  For every finite value of the format this is the numbering of the
+// reference's element codes (mxq/lut/formats.py:87-99).  Specials: E5M2 keeps IEEE Inf (exponent all ones,
+// mantissa 0) and NaN (0x7F); E4M3's only special is NaN, S.1111.111 (so 480, its code in MX-Gemmini's
+// decoders, is not a value here); FP6 and FP4 have none.
+//
+// The code of a float32 value q; *ok is cleared when q is not exactly a value of the format (off its grid,
+// beyond its range, or a special it lacks).  -0 keeps its sign bit.
+MXQ_HD uint32_t mx_encode(float q, int e, int m, bool* ok) {
+  const uint32_t u = f2u(q), a = u & 0x7FFFFFFFu;
+  const uint32_t sbit = (u >> 31) << (e + m);
+  const bool e4m3 = e == 4 && m == 3, e5m2 = e == 5 && m == 2;
+  if (a == 0u) return sbit;
+  if (a >= 0x7F800000u) {                                         // Inf or NaN
+    if (e5m2) return sbit | (a == 0x7F800000u ? 0x7Cu : 0x7Fu);
+    if (e4m3 && a > 0x7F800000u) return sbit | 0x7Fu;
+    *ok = false;
+    return 0u;
+  }
+  const int bias = (1 << (e - 1)) - 1, emin = 1 - bias;
+  const int E = (int)(a >> 23) - 127;                              // -127 for a float32 subnormal
+  const uint32_t sig = (a & 0x7FFFFFu) | (E > -127 ? 0x800000u : 0u);   // 24-bit significand of a normal
+  uint32_t code;
+  if (E >= emin) {
+    if (a & ((1u << (23 - m)) - 1u)) *ok = false;                  // more than m fraction bits
+    const int be = E + bias;
+    code = ((uint32_t)be << m) | ((a >> (23 - m)) & ((1u << m) - 1u));
+    const int emax_field = (1 << e) - 1;
+    if (be > emax_field || (e5m2 && be == emax_field) || (e4m3 && code == 0x7Fu)) *ok = false;
+  } else {
+    // subnormal: q = mant * 2^(emin - m), 1 <= mant < 2^m, so 2^(emin - m) <= |q| < 2^emin
+    const int sh = 23 - (E - (emin - m));                          // sig >> sh = mant
+    if (E <= -127 || E < emin - m || sh > 23 || (sig & ((1u << sh) - 1u))) {
+      *ok = false;
+      return 0u;
+    }
+    code = sig >> sh;
+  }
+  return sbit | (code & ((1u << (e + m)) - 1u));
+}
+
+// The float32 value of a code (the inverse of mx_encode on its values).
+MXQ_HD float mx_decode(uint32_t code, int e, int m) {
+  const uint32_t s = (code >> (e + m)) & 1u, ex = (code >> m) & ((1u << e) - 1u), man = code & ((1u << m) - 1u);
+  const int bias = (1 << (e - 1)) - 1;
+  float v;
+  if (e == 5 && m == 2 && ex == 31u) v = man ? f_nan() : f_inf();
+  else if (e == 4 && m == 3 && ex == 15u && man == 7u) v = f_nan();
+  else if (ex == 0u) v = (float)man * pow2f(1 - bias - m);
+  else v = u2f(((uint32_t)((int)ex - bias + 127) << 23) | (man << (23 - m)));
+  return s ? -v : v;
+}
+
+// E8M0 scale byte of a block scale x: 2^(k) for k in [-127, 127] is k + 127, NaN is 0xFF.  A block whose codes
+// are all zero (zero_block) has the value 0 under any scale: a scale E8M0 lacks (the 1e-38 floor of a zero
+// block) becomes 0, i.e. 2^-127.  *ok is cleared for any other scale E8M0 lacks.
+MXQ_HD uint32_t e8m0_encode(float x, bool zero_block, bool* ok) {
+  const uint32_t u = f2u(x);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0xFFu;
+  const uint32_t ex = u >> 23;                                     // sign 0 for a positive scale
+  if ((u & 0x7FFFFFu) == 0u && ex >= 1u && ex <= 254u) return ex;  // 2^-126 .. 2^127
+  if (u == 0x00400000u) return 0u;                                 // 2^-127, a float32 subnormal
+  if (!zero_block) *ok = false;
+  return 0u;
+}
+
+MXQ_HD float e8m0_decode(uint32_t b) { return b == 0xFFu ? f_nan() : pow2f((int)b - 127); }

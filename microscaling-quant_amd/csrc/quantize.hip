@@ -5,6 +5,12 @@
 int mxq_quantize_f32(const void*, float*, float*, int64_t, int64_t, int64_t, int64_t, const mxq_block_spec&, hipStream_t);
 int mxq_quantize_bf16(const void*, float*, float*, int64_t, int64_t, int64_t, int64_t, const mxq_block_spec&, hipStream_t);
 int mxq_quantize_f16(const void*, float*, float*, int64_t, int64_t, int64_t, int64_t, const mxq_block_spec&, hipStream_t);
+int mxq_quantize_packed_f32(const void*, uint8_t*, uint8_t*, int32_t*, int, int, int64_t, int64_t, int64_t, int64_t,
+                            const mxq_block_spec&, hipStream_t);
+int mxq_quantize_packed_bf16(const void*, uint8_t*, uint8_t*, int32_t*, int, int, int64_t, int64_t, int64_t, int64_t,
+                             const mxq_block_spec&, hipStream_t);
+int mxq_quantize_packed_f16(const void*, uint8_t*, uint8_t*, int32_t*, int, int, int64_t, int64_t, int64_t, int64_t,
+                            const mxq_block_spec&, hipStream_t);
 
 extern "C" int mxq_block_quantize(const void* V, int32_t v_dtype, float* P, float* X, int64_t outer, int64_t n,
                                   int64_t inner, int64_t block_size, const mxq_block_spec* spec,
@@ -62,4 +68,35 @@ extern "C" int mxq_block_dequantize(const float* P, const float* X, float* out, 
   else
     mxq_quant::k_dequant_strided<1><<<mxq::grid_for(threads, 256), 256, 0, st>>>(P, X, out, outer, n, inner, block_size, nb);
   return mxq::check_launch("mxq_block_dequantize");
+}
+
+// The element format of the code bytes a spec's element rule produces: float_em's widths for the qtorch and ocp
+// grids, the microxcaling step's mbits less its sign and implicit bits; false unless it is an OCP MX format.
+static bool code_format(const mxq_block_spec& q, int* ce, int* cm) {
+  *ce = q.e;
+  *cm = q.elem == MXQ_ELEM_MICROSOFT ? q.m - 2 : q.m;
+  const int e = *ce, m = *cm;
+  return (e == 4 && m == 3) || (e == 5 && m == 2) || (e == 3 && m == 2) || (e == 2 && m == 3) || (e == 2 && m == 1);
+}
+
+extern "C" int mxq_block_quantize_packed(const void* V, int32_t v_dtype, uint8_t* codes, uint8_t* scales,
+                                         int32_t* err, int64_t outer, int64_t n, int64_t inner, int64_t block_size,
+                                         const mxq_block_spec* spec, mxq_stream_t stream) {
+  if (!spec) return mxq::invalid("mxq_block_quantize_packed: spec is NULL");
+  if (outer < 0 || n < 0 || inner < 0 || block_size < 1) return mxq::invalid("mxq_block_quantize_packed: bad shape");
+  if (int rc = mxq_quant::validate(*spec)) return rc;
+  int ce, cm;
+  if (spec->elem != MXQ_ELEM_QTORCH && spec->elem != MXQ_ELEM_OCP && spec->elem != MXQ_ELEM_MICROSOFT)
+    return mxq::invalid("mxq_block_quantize_packed: the element rule has no byte format");
+  if (!code_format(*spec, &ce, &cm)) return mxq::invalid("mxq_block_quantize_packed: not an OCP MX element format");
+  if (outer == 0 || n == 0 || inner == 0) return MXQ_OK;
+  if (!V || !codes || !scales || !err) return mxq::invalid("mxq_block_quantize_packed: NULL pointer");
+  const mxq_block_spec q = *spec;
+  hipStream_t st = mxq::as_stream(stream);
+  switch (v_dtype) {
+    case MXQ_DT_F32: return mxq_quantize_packed_f32(V, codes, scales, err, ce, cm, outer, n, inner, block_size, q, st);
+    case MXQ_DT_BF16: return mxq_quantize_packed_bf16(V, codes, scales, err, ce, cm, outer, n, inner, block_size, q, st);
+    case MXQ_DT_F16: return mxq_quantize_packed_f16(V, codes, scales, err, ce, cm, outer, n, inner, block_size, q, st);
+    default: return mxq::invalid("mxq_block_quantize_packed: unsupported input dtype");
+  }
 }

@@ -58,6 +58,138 @@ __device__ __forceinline__ void store_vec_nt(float* p, const float (&in)[VEC]) {
   }
 }
 
+// Where a kernel's codes and scales go; the sink also runs step 2 (the element rule) on the scaled values z.
+//   FloatSink  float32 P and X, the reference's outputs (codes written with streaming stores).
+//   ByteSink   one element-code byte per element and one E8M0 byte per scale (mx_encode, e8m0_encode); a value
+//              neither format holds sets *err (a zero block's scale is free, its value being 0 under any).
+// `at` is an element index of P (or X); VEC consecutive elements, VEC-aligned.
+struct FloatSink {
+  float* P;
+  float* X;
+  static constexpr int kBytes = 4;
+  template <int ELEM, int MODE, int VEC>
+  __device__ __forceinline__ void elems(int64_t at, const float (&z)[VEC], const mxq_block_spec& s) const {
+    float q[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) q[j] = elem_qm<ELEM, MODE>(z[j], s);
+    store_vec_nt<VEC>(P + at, q);
+  }
+  template <int VEC>
+  __device__ __forceinline__ void scales(int64_t at, const float (&xs)[VEC], const bool (&)[VEC]) const {
+    store_vec<VEC>(X + at, xs);
+  }
+  __device__ __forceinline__ uintptr_t p_addr() const { return reinterpret_cast<uintptr_t>(P); }
+  __device__ __forceinline__ uintptr_t x_addr() const { return reinterpret_cast<uintptr_t>(X); }
+};
+
+template <int VEC>
+__device__ __forceinline__ void store_bytes(uint8_t* p, uint32_t w) {
+  if constexpr (VEC == 4) __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(p));
+  else if constexpr (VEC == 2) *reinterpret_cast<uint16_t*>(p) = (uint16_t)w;
+  else *p = (uint8_t)w;
+}
+
+// The element format's constants for the byte sink's short encoder.
+struct CodeConsts {
+  uint32_t nmin;      // bit pattern of 2^emin, the smallest normal
+  uint32_t nshift;    // 23 - m
+  uint32_t nsub;      // (127 - bias) << m: float32 exponent bias to the format's, in code position
+  uint32_t lowmask;   // the float32 fraction bits below the format's m
+  uint32_t maxbits;   // bit pattern of the largest finite value
+  float sub_mul;      // 2^(m - emin): a subnormal value in units of the format's subnormal step
+  int sign_at;        // e + m
+};
+
+__host__ __device__ inline CodeConsts code_consts(int e, int m) {
+  CodeConsts k{};
+  const int bias = (1 << (e - 1)) - 1, emin = 1 - bias;
+  k.nmin = (uint32_t)(emin + 127) << 23;
+  k.nshift = (uint32_t)(23 - m);
+  k.nsub = (uint32_t)(127 - bias) << m;
+  k.lowmask = (1u << (23 - m)) - 1u;
+  int emax = (1 << e) - 1 - bias;                  // largest exponent field's exponent
+  uint32_t mmax = (1u << m) - 1u;                   // largest mantissa there
+  if (e == 5 && m == 2) emax -= 1;                  // E5M2: the top exponent field is Inf / NaN
+  if (e == 4 && m == 3) mmax -= 1;                  // E4M3: S.1111.111 is NaN
+  k.maxbits = ((uint32_t)(emax + 127) << 23) | (mmax << (23 - m));
+  k.sub_mul = __builtin_bit_cast(float, (uint32_t)(m - emin + 127) << 23);
+  k.sign_at = e + m;
+  return k;
+}
+
+// The code of a value the element rule put on the format's grid: normal, (bits >> (23 - m)) less the exponent
+// bias difference; subnormal (or zero), its multiple of the subnormal step.  `good` is false for anything
+// else (beyond the largest finite value, a special, or off the grid: the qtorch grid's smallest values), which
+// then takes mx_encode.
+__device__ __forceinline__ uint32_t short_encode(float q, const CodeConsts& k, bool& good) {
+  const uint32_t u = f2u(q), a = u & 0x7FFFFFFFu;
+  const bool nrm = a >= k.nmin;
+  const float t = u2f(a) * k.sub_mul;
+  const uint32_t cs = __float2uint_rz(t);            // saturating convert: any t is defined
+  const uint32_t mag = nrm ? (a >> k.nshift) - k.nsub : cs;
+  good = a <= k.maxbits && (nrm ? (a & k.lowmask) == 0u : (float)cs == t);
+  return mag | ((u >> 31) << k.sign_at);
+}
+
+struct ByteSink {
+  uint8_t* P;
+  uint8_t* X;
+  int32_t* err;
+  int e, m;
+  CodeConsts k;
+  uint32_t maxcode;    // the code of the largest finite value
+  static constexpr int kBytes = 1;
+  // mxgemmini's ocp grid without `via` yields the code from its own roundings (ocp_code_t); every other rule
+  // rounds to float32 and the code is read off the value (short_encode).  Specials, and values the grid made
+  // that the format lacks, take mx_encode.
+  template <int ELEM, int MODE, int VEC>
+  __device__ __forceinline__ void elems(int64_t at, const float (&z)[VEC], const mxq_block_spec& s) const {
+    uint32_t w = 0u;
+    bool all_good = true;
+    if constexpr (ELEM == MXQ_ELEM_OCP && MODE >= 0) {
+      if (s.via_e == 0) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          bool good;
+          w |= ocp_code_t<MODE>(z[j], e, m, maxcode, &good) << (8 * j);
+          all_good = all_good && good;
+        }
+        if (!all_good) w = general_codes<ELEM, MODE, VEC>(z, s);
+        store_bytes<VEC>(P + at, w);
+        return;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      bool good;
+      w |= short_encode(elem_qm<ELEM, MODE>(z[j], s), k, good) << (8 * j);
+      all_good = all_good && good;
+    }
+    if (!all_good) w = general_codes<ELEM, MODE, VEC>(z, s);
+    store_bytes<VEC>(P + at, w);
+  }
+  template <int ELEM, int MODE, int VEC>
+  __device__ __forceinline__ uint32_t general_codes(const float (&z)[VEC], const mxq_block_spec& s) const {
+    bool ok = true;
+    uint32_t w = 0u;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) w |= mx_encode(elem_qm<ELEM, MODE>(z[j], s), e, m, &ok) << (8 * j);
+    if (!ok) atomicOr(err, 1);
+    return w;
+  }
+  template <int VEC>
+  __device__ __forceinline__ void scales(int64_t at, const float (&xs)[VEC], const bool (&zero)[VEC]) const {
+    bool ok = true;
+    uint32_t w = 0u;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) w |= e8m0_encode(xs[j], zero[j], &ok) << (8 * j);
+    store_bytes<VEC>(X + at, w);
+    if (!ok) atomicOr(err, 2);
+  }
+  __device__ __forceinline__ uintptr_t p_addr() const { return reinterpret_cast<uintptr_t>(P); }
+  __device__ __forceinline__ uintptr_t x_addr() const { return reinterpret_cast<uintptr_t>(X); }
+};
+
 // (o, b, column group) of a flat thread index over outer * nb * groups.
 __device__ __forceinline__ void split_index(int64_t t, int64_t groups, int64_t nb, int64_t& o, int64_t& b,
                                             int64_t& g) {
@@ -87,10 +219,10 @@ __device__ __forceinline__ bool wave_needs_div(const Div (&d)[VEC]) {
 
 // Any block size (read twice: once for the amax, once for the elements), one thread per block column of
 // VEC adjacent columns.
-template <typename T, int ELEM, int MODE, int VEC>
-__global__ void __launch_bounds__(256) k_quant_strided(const T* __restrict__ V, float* __restrict__ P,
-                                                       float* __restrict__ X, int64_t outer, int64_t n,
-                                                       int64_t inner, int64_t bs, int64_t nb, mxq_block_spec s) {
+template <typename T, int ELEM, int MODE, int VEC, typename SINK>
+__global__ void __launch_bounds__(256) k_quant_strided(const T* __restrict__ V, const SINK out, int64_t outer,
+                                                       int64_t n, int64_t inner, int64_t bs, int64_t nb,
+                                                       mxq_block_spec s) {
   const int64_t groups = inner / VEC;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= outer * nb * groups) return;
@@ -116,13 +248,16 @@ __global__ void __launch_bounds__(256) k_quant_strided(const T* __restrict__ V, 
     d[j] = make_div(xs[j]);
   }
   for (int64_t r = 0; r < rows; ++r) {
-    float v[VEC], q[VEC];
+    float v[VEC], z[VEC];
     load_vec<T, VEC>(V + off + r * inner, v);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) q[j] = elem_qm<ELEM, MODE>(s.scale_rule ? apply_div(v[j], d[j]) : v[j], s);
-    store_vec_nt<VEC>(P + off + r * inner, q);
+    for (int j = 0; j < VEC; ++j) z[j] = s.scale_rule ? apply_div(v[j], d[j]) : v[j];
+    out.template elems<ELEM, MODE, VEC>(off + r * inner, z, s);
   }
-  store_vec<VEC>(X + (o * nb + b) * inner + g * VEC, xs);
+  bool zero[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) zero[j] = amax[j] == 0.0f;
+  out.template scales<VEC>((o * nb + b) * inner + g * VEC, xs, zero);
 }
 
 // Block size 32 with R lanes of one wavefront sharing a block column: lane l of a wave takes row part
@@ -137,10 +272,10 @@ __global__ void __launch_bounds__(256) k_quant_strided(const T* __restrict__ V, 
 //     every NaN pattern lies above +Inf, so a NaN wins as torch.amax's does).
 //   * The R lanes of a column group hold the same maxima after the exchanges; lane r < VEC computes the scale
 //     of column r alone and the others read it (one scale rule evaluation per lane instead of VEC).
-template <typename T, int ELEM, int MODE, int VEC, int R>
-__global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, float* __restrict__ P,
-                                                     float* __restrict__ X, int64_t outer, int64_t n, int64_t inner,
-                                                     int64_t nb, int64_t waves_per_row, mxq_block_spec s) {
+template <typename T, int ELEM, int MODE, int VEC, int R, typename SINK>
+__global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, const SINK out, int64_t outer,
+                                                     int64_t n, int64_t inner, int64_t nb, int64_t waves_per_row,
+                                                     mxq_block_spec s) {
   constexpr int CPW = 64 / R;          // column groups per wave
   constexpr int ROWS = 32 / R;         // rows per lane
   static_assert(VEC <= R, "one scale-computing lane per column");
@@ -207,23 +342,23 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, fl
       for (int j = 0; j < VEC; ++j) v[i][j] = v[i][j] * d[j].inv;
   }
   if (!live) return;
-  float* dst = P + (o * n + k0 + r * ROWS) * inner + cg * VEC;
+  const int64_t dst = (o * n + k0 + r * ROWS) * inner + cg * VEC;
 #pragma unroll
   for (int i = 0; i < ROWS; ++i) {
-    if (rows == 32 || r * ROWS + i < rows) {
-      float q[VEC];
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) q[j] = elem_qm<ELEM, MODE>(v[i][j], s);
-      store_vec_nt<VEC>(dst + (int64_t)i * inner, q);
-    }
+    if (rows == 32 || r * ROWS + i < rows) out.template elems<ELEM, MODE, VEC>(dst + (int64_t)i * inner, v[i], s);
   }
-  if (r == 0) store_vec<VEC>(X + (o * nb + b) * inner + cg * VEC, xs);
+  if (r == 0) {
+    bool zero[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) zero[j] = am[j] == 0u;
+    out.template scales<VEC>((o * nb + b) * inner + cg * VEC, xs, zero);
+  }
 }
 
 // inner == 1, blocks of 32 contiguous elements, n % 32 == 0: eight lanes per block, four elements per lane.
-template <typename T, int ELEM, int MODE>
-__global__ void __launch_bounds__(256) k_quant_contig32(const T* __restrict__ V, float* __restrict__ P,
-                                                        float* __restrict__ X, int64_t nblocks, mxq_block_spec s) {
+template <typename T, int ELEM, int MODE, typename SINK>
+__global__ void __launch_bounds__(256) k_quant_contig32(const T* __restrict__ V, const SINK out, int64_t nblocks,
+                                                        mxq_block_spec s) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t blk = t >> 3;
   const bool live = blk < nblocks;
@@ -240,11 +375,15 @@ __global__ void __launch_bounds__(256) k_quant_contig32(const T* __restrict__ V,
   if (!live) return;
   const float xs = block_scale(a, s);
   const Div d = make_div(xs);
-  float q[4];
+  float z[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) q[j] = elem_qm<ELEM, MODE>(s.scale_rule ? apply_div(v[j], d) : v[j], s);
-  store_vec_nt<4>(P + off, q);
-  if ((t & 7) == 0) X[blk] = xs;
+  for (int j = 0; j < 4; ++j) z[j] = s.scale_rule ? apply_div(v[j], d) : v[j];
+  out.template elems<ELEM, MODE, 4>(off, z, s);
+  if ((t & 7) == 0) {
+    const float x1[1] = {xs};
+    const bool z1[1] = {a == 0.0f};
+    out.template scales<1>(blk, x1, z1);
+  }
 }
 
 // V = M^T with M (inner x n) row-major in memory, blocks of 32 along n: every block is 32 contiguous elements
@@ -369,22 +508,27 @@ inline int validate(const mxq_block_spec& s) {
   return MXQ_OK;
 }
 
-// bs < 0: the transposed layout (outer 1, block 32, V read as M^T), k_quant_t.
-template <typename T, int ELEM, int MODE>
-int launch_quant(const T* V, float* P, float* X, int64_t outer, int64_t n, int64_t inner, int64_t bs,
+// bs < 0: the transposed layout (outer 1, block 32, V read as M^T), k_quant_t (float32 outputs only).
+template <typename T, int ELEM, int MODE, typename SINK>
+int launch_quant(const T* V, const SINK& out, int64_t outer, int64_t n, int64_t inner, int64_t bs,
                  const mxq_block_spec& q, hipStream_t st) {
-  if (bs < 0) return launch_quant_t<T, ELEM, MODE>(V, P, X, n, inner, q, st);
+  if constexpr (SINK::kBytes == 4) {
+    if (bs < 0) return launch_quant_t<T, ELEM, MODE>(V, out.P, out.X, n, inner, q, st);
+  } else if (bs < 0) {
+    return mxq::invalid("mxq_block_quantize_packed: no transposed layout");
+  }
   mxq::KernelTimer timer("block_quantize", st);
   const int64_t nb = mxq::ceil_div(n, bs);
-  const uintptr_t av = reinterpret_cast<uintptr_t>(V), ap = reinterpret_cast<uintptr_t>(P),
-                  ax = reinterpret_cast<uintptr_t>(X);
-  if (inner == 1 && bs == 32 && n % 32 == 0 && av % (4 * sizeof(T)) == 0 && ap % 16 == 0) {
+  const uintptr_t av = reinterpret_cast<uintptr_t>(V), ap = reinterpret_cast<uintptr_t>(out.P),
+                  ax = reinterpret_cast<uintptr_t>(out.X);
+  constexpr int OB = SINK::kBytes;
+  if (inner == 1 && bs == 32 && n % 32 == 0 && av % (4 * sizeof(T)) == 0 && ap % (4 * OB) == 0) {
     const int64_t nblocks = outer * nb;
-    k_quant_contig32<T, ELEM, MODE><<<mxq::grid_for(nblocks * 8, 256), 256, 0, st>>>(V, P, X, nblocks, q);
+    k_quant_contig32<T, ELEM, MODE, SINK><<<mxq::grid_for(nblocks * 8, 256), 256, 0, st>>>(V, out, nblocks, q);
     return mxq::check_launch("mxq_block_quantize");
   }
   auto aligned = [&](int vec) {
-    return inner % vec == 0 && av % (vec * sizeof(T)) == 0 && ap % (vec * 4) == 0 && ax % (vec * 4) == 0;
+    return inner % vec == 0 && av % (vec * sizeof(T)) == 0 && ap % (vec * OB) == 0 && ax % (vec * OB) == 0;
   };
   const int vec = aligned(4) ? 4 : (aligned(2) ? 2 : 1);
   if (bs == 32) {
@@ -392,38 +536,46 @@ int launch_quant(const T* V, float* P, float* X, int64_t outer, int64_t n, int64
     const int64_t wpr = mxq::ceil_div(inner / vec, 64 / R);
     const int64_t threads = outer * nb * wpr * 64;
     const dim3 grid = mxq::grid_for(threads, 256);
-    if (vec == 4) k_quant_split<T, ELEM, MODE, 4, R><<<grid, 256, 0, st>>>(V, P, X, outer, n, inner, nb, wpr, q);
-    else if (vec == 2) k_quant_split<T, ELEM, MODE, 2, R><<<grid, 256, 0, st>>>(V, P, X, outer, n, inner, nb, wpr, q);
-    else k_quant_split<T, ELEM, MODE, 1, R><<<grid, 256, 0, st>>>(V, P, X, outer, n, inner, nb, wpr, q);
+    if (vec == 4) k_quant_split<T, ELEM, MODE, 4, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
+    else if (vec == 2) k_quant_split<T, ELEM, MODE, 2, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
+    else k_quant_split<T, ELEM, MODE, 1, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
     return mxq::check_launch("mxq_block_quantize");
   }
   const int64_t threads = outer * nb * (inner / vec);
   const dim3 grid = mxq::grid_for(threads, 256);
-  if (vec == 4) k_quant_strided<T, ELEM, MODE, 4><<<grid, 256, 0, st>>>(V, P, X, outer, n, inner, bs, nb, q);
-  else if (vec == 2) k_quant_strided<T, ELEM, MODE, 2><<<grid, 256, 0, st>>>(V, P, X, outer, n, inner, bs, nb, q);
-  else k_quant_strided<T, ELEM, MODE, 1><<<grid, 256, 0, st>>>(V, P, X, outer, n, inner, bs, nb, q);
+  if (vec == 4) k_quant_strided<T, ELEM, MODE, 4, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, bs, nb, q);
+  else if (vec == 2) k_quant_strided<T, ELEM, MODE, 2, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, bs, nb, q);
+  else k_quant_strided<T, ELEM, MODE, 1, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, bs, nb, q);
   return mxq::check_launch("mxq_block_quantize");
 }
 
-template <typename T, int ELEM>
-int launch_mode(const T* V, float* P, float* X, int64_t outer, int64_t n, int64_t inner, int64_t bs,
+template <typename T, int ELEM, typename SINK>
+int launch_mode(const T* V, const SINK& out, int64_t outer, int64_t n, int64_t inner, int64_t bs,
                 const mxq_block_spec& q, hipStream_t st) {
   switch (q.rounding) {
-    case MXQ_RNE: return launch_quant<T, ELEM, MXQ_RNE>(V, P, X, outer, n, inner, bs, q, st);
-    case MXQ_TIES_AWAY: return launch_quant<T, ELEM, MXQ_TIES_AWAY>(V, P, X, outer, n, inner, bs, q, st);
-    default: return launch_quant<T, ELEM, MXQ_TRUNC>(V, P, X, outer, n, inner, bs, q, st);
+    case MXQ_RNE: return launch_quant<T, ELEM, MXQ_RNE>(V, out, outer, n, inner, bs, q, st);
+    case MXQ_TIES_AWAY: return launch_quant<T, ELEM, MXQ_TIES_AWAY>(V, out, outer, n, inner, bs, q, st);
+    default: return launch_quant<T, ELEM, MXQ_TRUNC>(V, out, outer, n, inner, bs, q, st);
   }
 }
 
-template <typename T>
-int dispatch_elem(const T* V, float* P, float* X, int64_t outer, int64_t n, int64_t inner, int64_t bs,
+// Float32 outputs: every element rule.  Bytes: the rules whose grids are the OCP element formats' (mxgemmini's
+// ocp grid, block.ocp's microxcaling step) and mxquant's qtorch grid (whose smallest values some formats lack:
+// those set the error word).
+template <typename T, typename SINK>
+int dispatch_elem(const T* V, const SINK& out, int64_t outer, int64_t n, int64_t inner, int64_t bs,
                   const mxq_block_spec& q, hipStream_t st) {
   switch (q.elem) {
-    case MXQ_ELEM_QTORCH: return launch_quant<T, MXQ_ELEM_QTORCH, -1>(V, P, X, outer, n, inner, bs, q, st);
-    case MXQ_ELEM_IEEE: return launch_quant<T, MXQ_ELEM_IEEE, -1>(V, P, X, outer, n, inner, bs, q, st);
-    case MXQ_ELEM_OCP: return launch_mode<T, MXQ_ELEM_OCP>(V, P, X, outer, n, inner, bs, q, st);
-    case MXQ_ELEM_MICROSOFT: return launch_mode<T, MXQ_ELEM_MICROSOFT>(V, P, X, outer, n, inner, bs, q, st);
-    default: return launch_quant<T, MXQ_ELEM_NONE, -1>(V, P, X, outer, n, inner, bs, q, st);
+    case MXQ_ELEM_QTORCH: return launch_quant<T, MXQ_ELEM_QTORCH, -1>(V, out, outer, n, inner, bs, q, st);
+    case MXQ_ELEM_OCP: return launch_mode<T, MXQ_ELEM_OCP>(V, out, outer, n, inner, bs, q, st);
+    case MXQ_ELEM_MICROSOFT: return launch_mode<T, MXQ_ELEM_MICROSOFT>(V, out, outer, n, inner, bs, q, st);
+    default: break;
+  }
+  if constexpr (SINK::kBytes == 4) {
+    if (q.elem == MXQ_ELEM_IEEE) return launch_quant<T, MXQ_ELEM_IEEE, -1>(V, out, outer, n, inner, bs, q, st);
+    return launch_quant<T, MXQ_ELEM_NONE, -1>(V, out, outer, n, inner, bs, q, st);
+  } else {
+    return mxq::invalid("mxq_block_quantize_packed: the element rule has no byte format");
   }
 }
 

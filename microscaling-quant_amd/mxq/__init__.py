@@ -21,7 +21,7 @@ __version__ = "0.1.0"
 
 import torch  # noqa: F401  (first: libmxq_hip.so binds to the HIP runtime torch loads)
 
-from . import rounding, arith, schedule, scale_factor, element_quant, lut, block, matmul, scheme, nn
+from . import rounding, arith, schedule, scale_factor, element_quant, lut, block, matmul, scheme, nn, packed
 from .block import BLOCK
 from ._fp64_accum import fp64_accum
 from ._mfma_accum import mfma_accum, mfma_tolerance
@@ -29,4 +29,4 @@ from .element_quant.formats import Format
 from .scheme import Scheme
 
 __all__ = ["rounding", "arith", "schedule", "scale_factor", "element_quant", "lut", "block", "matmul", "scheme", "nn",
-           "BLOCK", "Format", "Scheme", "fp64_accum", "mfma_accum", "mfma_tolerance"]
+           "packed", "BLOCK", "Format", "Scheme", "fp64_accum", "mfma_accum", "mfma_tolerance"]

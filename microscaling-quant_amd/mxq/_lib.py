@@ -60,6 +60,13 @@ SIGNATURES = {
     "mxq_block_quantize_t": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, ctypes.POINTER(BlockSpec),
                                      c_ptr]),
     "mxq_block_dequantize": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr]),
+    "mxq_block_quantize_packed": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64,
+                                          ctypes.POINTER(BlockSpec), c_ptr]),
+    "mxq_pack": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_ptr]),
+    "mxq_unpack": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_ptr]),
+    "mxq_dequantize_packed": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i32, c_i32, c_ptr]),
+    "mxq_lut_pick_packed": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr]),
+    "mxq_lut_lookup_packed": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr]),
     "mxq_systolic": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,
                              ctypes.POINTER(ArithSpec), c_ptr, c_i32, c_ptr]),
     "mxq_systolic_batched": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, ctypes.POINTER(SystolicLayout), c_i64,

@@ -129,3 +129,24 @@ class HostNumerics:
         self.lib.h_block_quantize(self._p(V3), self._p(P), self._p(X), ctypes.c_int64(outer), ctypes.c_int64(n),
                                   ctypes.c_int64(inner), ctypes.c_int64(bs), ctypes.byref(spec))
         return P, X
+
+    def mx_encode(self, q, e, m):
+        q = np.ascontiguousarray(q, dtype=F32)
+        codes = np.empty(q.shape, dtype=np.uint8)
+        ok = np.empty(q.shape, dtype=np.uint8)
+        self.lib.h_mx_encode(self._p(q), self._p(codes), self._p(ok), ctypes.c_int64(q.size), e, m)
+        return codes, ok.astype(bool)
+
+    def mx_decode(self, codes, e, m):
+        return self._un("h_mx_decode", codes, e, m, in_dtype=np.uint8)
+
+    def e8m0_encode(self, x, zero):
+        x = np.ascontiguousarray(x, dtype=F32)
+        z = np.ascontiguousarray(np.broadcast_to(zero, x.shape), dtype=np.uint8)
+        b = np.empty(x.shape, dtype=np.uint8)
+        ok = np.empty(x.shape, dtype=np.uint8)
+        self.lib.h_e8m0_encode(self._p(x), self._p(z), self._p(b), self._p(ok), ctypes.c_int64(x.size))
+        return b, ok.astype(bool)
+
+    def e8m0_decode(self, b):
+        return self._un("h_e8m0_decode", b, in_dtype=np.uint8)

@@ -75,4 +75,26 @@ void h_block_quantize(const float* V, float* P, float* X, int64_t outer, int64_t
       }
 }
 
+// Packed byte codes: codes[i] = mx_encode(q[i]) with ok[i] its flag; mx_decode; E8M0 both ways.
+void h_mx_encode(const float* q, uint8_t* codes, uint8_t* ok, int64_t n, int e, int m) {
+  for (int64_t i = 0; i < n; ++i) {
+    bool good = true;
+    codes[i] = (uint8_t)mx_encode(q[i], e, m, &good);
+    ok[i] = good ? 1 : 0;
+  }
+}
+void h_mx_decode(const uint8_t* codes, float* out, int64_t n, int e, int m) {
+  for (int64_t i = 0; i < n; ++i) out[i] = mx_decode(codes[i], e, m);
+}
+void h_e8m0_encode(const float* x, const uint8_t* zero, uint8_t* b, uint8_t* ok, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    bool good = true;
+    b[i] = (uint8_t)e8m0_encode(x[i], zero[i] != 0, &good);
+    ok[i] = good ? 1 : 0;
+  }
+}
+void h_e8m0_decode(const uint8_t* b, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = e8m0_decode(b[i]);
+}
+
 }  // extern "C"

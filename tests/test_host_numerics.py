@@ -210,3 +210,35 @@ def test_block_quantize(H, case):
         hp, hx = H.block_quantize(V3, bs, spec)
         assert_bits_equal(hp.reshape(P.shape), P, f"{name} P axis {axis} bs {bs}")
         assert_bits_equal(hx.reshape(X.shape), X, f"{name} X axis {axis} bs {bs}")
+
+
+@pytest.mark.parametrize("em", OCP_EM)
+def test_mx_encode_decode(H, corpus, em):
+    """mx_encode/mx_decode (the kernels' bit manipulation) against the oracle's table lookup: every code, every
+    code value, neighbouring bit patterns of each value, the corpus and a million random patterns."""
+    from oracle import packed as op
+    e, m = em
+    n = 1 << (1 + e + m)
+    codes = np.arange(n, dtype=np.uint8)
+    assert_bits_equal(H.mx_decode(codes, e, m), op.decode(codes, e, m), f"decode {em}")
+    vals = op.code_table(e, m)
+    u = vals.view(np.uint32)
+    near = np.concatenate([u, u + 1, u - 1, u ^ 0x80000000]).view(np.float32)
+    rng = np.random.default_rng(e * 10 + m)
+    rand = rng.integers(0, 2 ** 32, 1_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    for q in (near, corpus, rand):
+        got_c, got_ok = H.mx_encode(q, e, m)
+        want_c, want_ok = op.encode(q, e, m)
+        assert np.array_equal(got_ok, want_ok), f"encode ok {em}"
+        assert np.array_equal(got_c[want_ok], want_c[want_ok]), f"encode codes {em}"
+
+
+def test_e8m0_encode_decode(H, corpus):
+    from oracle import packed as op
+    b = np.arange(256, dtype=np.uint8)
+    assert_bits_equal(H.e8m0_decode(b), op.e8m0_decode(b), "e8m0 decode")
+    x = np.concatenate([corpus, op.e8m0_decode(b[:255]), np.float32([1e-38, 2.0 ** -127, 2.0 ** -128, 0.0])])
+    for zero in (False, True):
+        got_b, got_ok = H.e8m0_encode(x, zero)
+        want_b, want_ok = op.e8m0_encode(x, zero)
+        assert np.array_equal(got_ok, want_ok) and np.array_equal(got_b[want_ok], want_b[want_ok]), zero
