@@ -264,6 +264,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the systolic line (no quantize, LUT, attend)")
     ap.add_argument("--copy-calibration", action="store_true", help="run only the counter-calibration copy")
+    ap.add_argument("--only", choices=("quantize", "lut", "attend", "mfma", "trees"),
+                    help="run one extra line alone (for profiling) and print it; not the benchmark line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the systolic path "
@@ -278,6 +280,11 @@ def main():
     import mxq  # noqa: F401
     from mxq import block, matmul
     dev = torch.device("cuda", 0)
+    if args.only in ("quantize", "lut", "attend"):
+        fn = {"quantize": lambda: quantize_lines(torch, max(5, args.steps // 2)),
+              "lut": lambda: lut_line(torch, 3), "attend": lambda: attend_line(torch, 3)}[args.only]
+        print(json.dumps({"only": args.only, args.only: fn()}), flush=True)
+        return
     M, N, K = 512, 4096, 4096
     g = torch.Generator().manual_seed(0)
     x = torch.randn(M, K, generator=g)
@@ -285,6 +292,11 @@ def main():
     P_A, X_A = block.mxgemmini.quantize(x.t().contiguous().to(dev), "MXFP8_E4M3", axis=0)
     P_B, X_B = block.mxgemmini.quantize(W.t().contiguous().to(dev), "MXFP8_E4M3", axis=0)
     ar = matmul.MXGEMMINI()
+    if args.only in ("mfma", "trees"):
+        fn = {"mfma": lambda: mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B),
+              "trees": lambda: trees_line(torch, 3, P_A, X_A, P_B, X_B)}[args.only]
+        print(json.dumps({"only": args.only, args.only: fn()}), flush=True)
+        return
     step = lambda: matmul.systolic(P_A, X_A, P_B, X_B, ar, matmul.HW_FINAL)   # noqa: E731
     for _ in range(args.warmup):
         step()
@@ -313,7 +325,7 @@ def main():
                      "note": "VALU-bound emulation (neither HBM nor MFMA): achieved = 2 x 8,589,934,592 emulated "
                              "MACs / the fast kernel's average duration; peak = MI355X vector FP32 157.3 TFLOP/s "
                              "= 78.6 T 32-bit lane-ops/s, / 10 lane-ops per emulated MAC (the datapath's primitive "
-                             "count) x 2 ops per MAC; the kernel executes 7.8 VALU lane-ops per MAC "
+                             "count) x 2 ops per MAC; the kernel executes 8.1 VALU lane-ops per MAC "
                              "(SQ_INSTS_VALU, profiles/systolic_fast_c2_valu.txt)"},
     }
     if not args.no_extra:
