@@ -129,7 +129,7 @@ int mxq_dequantize_packed(const uint8_t* codes, const uint8_t* scales, float* ou
  * (ceil(K/block_size) x M), X_B (ceil(K/block_size) x N), all float32 row-major.  Per block of K the scale map
  * X_A[g] (x) X_B[g]; per reduction of `size` k a fresh sum accumulated lane by lane (lane i has the format
  * (lane_e[i], lane_m[i]), host arrays of `size` entries), rescaled and added into C; K tails as the reference.
- * size must divide block_size and 32.  `workspace` is device memory of mxq_systolic_workspace(M, N, 1) uint32
+ * size must divide block_size and 32.  `workspace` is device memory of mxq_systolic_workspace(K, M, N, 1) uint32
  * (which kernel computes each output tile is decided on the device; the call makes no host synchronisation).
  * force_general = 1 skips the fast kernel.  Replaces mxq/matmul/_systolic.py:23-62 with
  * mxq/matmul/_arithmetic.py:64-134. */
@@ -148,19 +148,37 @@ typedef struct mxq_systolic_layout {
   int64_t ld_c, batch_c;    /* C, M x N (problems may not overlap) */
 } mxq_systolic_layout;
 
+/* Optional hints to mxq_systolic_batched (no counterpart in the reference; they let attention skip the work its
+ * causal mask makes moot).  Either pointer may be NULL; so may the struct.
+ *   skip   per problem z, 32-row group i and 32-column group j of C: skip[(z * ceil(M/32) + i) * ceil(N/32) + j]
+ *          != 0 marks outputs the caller does not need.  A fast tile made only of such groups is written as +0
+ *          and not computed (the general kernel, when it runs alone, computes them); the tiles left to compute
+ *          are dispatched first, spread over the whole chip.
+ *   k_end  per problem z and 64-column group t of A: k_end[z * ceil(M/64) + t] bounds the rows of A where those
+ *          columns hold a nonzero code.  Their reduction stops there (rounded up to 32 rows); the rows left out
+ *          are checked by a pass over them (once per problem, not per tile), and unless A is +-0 there and B
+ *          and the block scales finite, the tile is recomputed by the general kernel: a wrong k_end costs time,
+ *          never bits.  Tiles are dispatched longest reduction first. */
+typedef struct mxq_systolic_hints {
+  const uint8_t* skip;
+  const int32_t* k_end;
+} mxq_systolic_hints;
+
 /* `count` independent systolic problems of one shape in one launch, operands addressed through `layout` (any
  * column slice of a larger matrix, any spacing of the problems).  Each problem's result is bit-identical to
- * mxq_systolic on that problem alone.  workspace: mxq_systolic_workspace(M, N, count) uint32.  The reference
+ * mxq_systolic on that problem alone.  workspace: mxq_systolic_workspace(K, M, N, count) uint32.  The reference
  * calls matmul.systolic once per problem (mxq/nn/_attention.py:108-141, once per head and query chunk);
  * this is that loop as one launch. */
 int mxq_systolic_batched(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C,
                          const mxq_systolic_layout* layout, int64_t count, int64_t K, int64_t M, int64_t N,
                          const int32_t* lane_e, const int32_t* lane_m, int32_t size, int32_t block_size,
-                         const mxq_arith_spec* arith, uint32_t* workspace, int32_t force_general,
+                         const mxq_arith_spec* arith, const mxq_systolic_hints* hints, uint32_t* workspace,
+                         int32_t force_general,
                          mxq_stream_t stream);
 
-/* uint32 elements of workspace mxq_systolic / mxq_systolic_batched need (at least 1). */
-int64_t mxq_systolic_workspace(int64_t M, int64_t N, int64_t count);
+/* uint32 elements of workspace mxq_systolic / mxq_systolic_batched need for `count` problems of K x M codes A
+ * and K x N codes B (at least 1); mxq_adder_tree and mxq_anchor_tree need the same with count 1. */
+int64_t mxq_systolic_workspace(int64_t K, int64_t M, int64_t N, int64_t count);
 
 /* Per contraction row k of codes P (K x cols) with scales X (ceil(K/block_size) x cols), float32 row-major, and
  * per group g of cols/groups adjacent columns: out[k * groups + g] = max over the group of |P[k, c]| *
@@ -191,10 +209,25 @@ int mxq_scores_scale_mask(float* S, int64_t Z, int64_t n, int64_t m, int64_t Tk,
                           int64_t mask_b_stride, int64_t mask_row_stride, int64_t z0, int64_t z_per_b,
                           int32_t round_bf16, mxq_stream_t stream);
 
+/* The batched attention path's hints to its two systolic launches (no counterpart in the reference: they skip
+ * work its computation makes moot, without changing a bit).  mxq_mask_minabs: per mask batch row, 32-row group
+ * of the call's `rows` = n*m score rows (row r reads the mask row of query r % m) and 32-key group, the
+ * smallest |mask| (0 for a NaN) into out[(batch * ceil(rows/32) + group) * ceil(Tk/32) + key group].
+ * mxq_attend_hints: per call z (mask batch row (z0 + z) / z_per_b - z0 / z_per_b when `batched`, else 0), its
+ * masked-key bound b as mxq_attend_windows takes it; skip[(z * ceil(rows/32) + g) * ceil(Tk/32) + j] = 1 when
+ * that group's smallest |mask| c absorbs 2b in float32 (scores there do not matter: the mask absorbs any the
+ * call can produce); k_end[z * ceil(rows/64) + t] = 32 * (1 + the last key group some row of 64-row group t
+ * still sees), 0 when none. */
+int mxq_mask_minabs(const float* mask, int64_t mask_b_stride, int64_t mask_row_stride, int64_t batches, int64_t rows,
+                    int64_t m, int64_t Tk, float* out, mxq_stream_t stream);
+int mxq_attend_hints(const double* amax_a, int64_t lda, const double* amax_k, int64_t ldk, int64_t D, int64_t Z,
+                     double slack_scale, const float* minabs, int64_t z0, int64_t z_per_b, int32_t batched,
+                     int64_t rows, int64_t Tk, uint8_t* skip, int32_t* k_end, mxq_stream_t stream);
+
 /* The adder tree: the operands, Arithmetic, scales and output of mxq_systolic; each reduction of `size` products
  * (zeros past a K tail) summed by log2(size) levels of adjacent-pair acc_adds, level l in (level_e[l],
  * level_m[l]), the root rescaled and tile-added into C.  size: a power of two in [2, 32] dividing block_size.
- * workspace: device memory of mxq_systolic_workspace(M, N, 1) uint32 (the fast kernel's tile flags).
+ * workspace: device memory of mxq_systolic_workspace(K, M, N, 1) uint32.
  * force_general: run the general kernel alone, also where the fast one applies (the two are bit-identical).
  * Replaces mxq/matmul/_adder.py:42-71 (the reduction of :24-32). */
 int mxq_adder_tree(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C, int64_t K,

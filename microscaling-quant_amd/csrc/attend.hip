@@ -7,6 +7,16 @@
 //                        multiply, the rounding r (none, or bf16 RNE for vector precision "bf16"), the float32
 //                        add of the query's mask row, r again -- the reference's two elementwise steps with their
 //                        two roundings, read and written once.
+//   k_mask_minabs        per mask batch row, 32-row group of a call's n*m score rows and 32-key group, the
+//                        smallest |mask| (0 for a NaN)
+//   k_attend_hints       the two batched launches' hints (include/mxq_hip.h mxq_systolic_hints) from those and
+//                        each call's masked-key bound b: a 32 x 32 group of scores is not needed when its
+//                        smallest |mask| c absorbs 2b (c + 2b == c and c - 2b == c in float32), for then every
+//                        mask value there absorbs every score the call can produce, r(r(s * scale) + mask) is
+//                        r(mask) whatever s is, and a +0 score gives the same; k_end of a 64-row group is the
+//                        end of its last key group that some of its rows still see.  Where every key of a row is
+//                        masked softmax is uniform, not zero, and the systolic kernel's check of the rows past
+//                        k_end sends that tile to the general kernel.
 #include "mxq_common.h"
 #include "mxq_numerics.h"
 
@@ -156,6 +166,62 @@ __global__ void __launch_bounds__(256) k_attend_windows(const double* __restrict
   if (threadIdx.x == 0 && (first || last)) atomicOr(flags + z, (first ? 1 : 0) | (last ? 2 : 0));
 }
 
+__global__ void __launch_bounds__(256) k_mask_minabs(const float* __restrict__ mask, int64_t mask_b_stride,
+                                                     int64_t mask_row_stride, int64_t rows, int64_t m, int64_t Tk,
+                                                     int64_t rgroups, int64_t kgroups, float* __restrict__ out) {
+  const int64_t bb = blockIdx.z, rg = blockIdx.y, key = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  float mn = f_inf();                                          // keys past Tk take no part
+  if (key < Tk) {
+    for (int i = 0; i < 32; ++i) {
+      const int64_t r = rg * 32 + i;
+      if (r >= rows) break;
+      const float c = mask[bb * mask_b_stride + (r % m) * mask_row_stride + key];
+      mn = fminf(mn, c != c ? 0.0f : fabsf(c));
+    }
+  }
+  for (int off = 16; off > 0; off >>= 1) mn = fminf(mn, __shfl_xor(mn, off, 32));
+  const int64_t kg = key >> 5;
+  if ((threadIdx.x & 31) == 0 && kg < kgroups) out[(bb * rgroups + rg) * kgroups + kg] = mn;
+}
+
+// Workgroup (t, z): 64-row group t of call z.  The bound as k_attend_windows takes it.
+__global__ void __launch_bounds__(256) k_attend_hints(const double* __restrict__ amax_a, int64_t lda,
+                                                      const double* __restrict__ amax_k, int64_t ldk, int64_t D,
+                                                      double slack_scale, const float* __restrict__ minabs,
+                                                      int64_t z0, int64_t z_per_b, int batched, int64_t rgroups,
+                                                      int64_t kgroups, int64_t tgroups, uint8_t* __restrict__ skip,
+                                                      int32_t* __restrict__ k_end) {
+  __shared__ float b2;
+  __shared__ int last;
+  const int64_t t = blockIdx.x, z = blockIdx.y;
+  if (threadIdx.x == 0) {
+    double sum = 0.0;
+    for (int64_t d = 0; d < D; ++d) sum += amax_a[d * lda + z] * amax_k[d * ldk + z];
+    double bound = slack_scale * sum;
+    if (bound < 1.1754943508222875e-38) bound = 1.1754943508222875e-38;     // NaN stays NaN
+    b2 = (float)(2.0 * bound);
+    last = -1;
+  }
+  __syncthreads();
+  const float b = b2;
+  const bool usable = is_finite_f(b);
+  const int64_t bb = batched ? (z0 + z) / z_per_b - z0 / z_per_b : 0;
+  int mine = -1;
+  for (int64_t rg = 2 * t; rg < 2 * t + 2 && rg < rgroups; ++rg) {
+    const float* mrow = minabs + (bb * rgroups + rg) * kgroups;
+    uint8_t* srow = skip + (z * rgroups + rg) * kgroups;
+    for (int64_t kg = threadIdx.x; kg < kgroups; kg += 256) {
+      const float c = mrow[kg];
+      const bool sk = usable && (c + b) == c && (c - b) == c;
+      srow[kg] = sk ? 1 : 0;
+      if (!sk && kg > mine) mine = (int)kg;
+    }
+  }
+  atomicMax(&last, mine);
+  __syncthreads();
+  if (threadIdx.x == 0) k_end[z * tgroups + t] = (int32_t)((last + 1) * 32);
+}
+
 }  // namespace
 
 extern "C" int mxq_scores_scale_mask(float* S, int64_t Z, int64_t n, int64_t m, int64_t Tk, float scale,
@@ -206,4 +272,35 @@ extern "C" int mxq_attend_windows(const double* amax_a, int64_t lda, const doubl
       amax_a, lda, amax_k, ldk, D, slack_scale, mask, mask_b_stride, mask_row_stride, z0, (int)m, (int)Tk,
       (int)block, (int)chunks, z_per_b, flags);
   return mxq::check_launch("mxq_attend_windows");
+}
+
+extern "C" int mxq_mask_minabs(const float* mask, int64_t mask_b_stride, int64_t mask_row_stride, int64_t batches,
+                               int64_t rows, int64_t m, int64_t Tk, float* out, mxq_stream_t stream) {
+  if (batches < 0 || rows < 0 || m < 1 || Tk < 0 || mask_b_stride < 0 || mask_row_stride < 0)
+    return mxq::invalid("mxq_mask_minabs: bad shape");
+  if (batches == 0 || rows == 0 || Tk == 0) return MXQ_OK;
+  if (!mask || !out) return mxq::invalid("mxq_mask_minabs: NULL pointer");
+  const int64_t rgroups = mxq::ceil_div(rows, 32), kgroups = mxq::ceil_div(Tk, 32);
+  if (rgroups > 65535 || batches > 65535 || mxq::ceil_div(Tk, 256) > INT32_MAX)
+    return mxq::invalid("mxq_mask_minabs: too large");
+  const dim3 grid((unsigned)mxq::ceil_div(Tk, 256), (unsigned)rgroups, (unsigned)batches);
+  k_mask_minabs<<<grid, 256, 0, mxq::as_stream(stream)>>>(mask, mask_b_stride, mask_row_stride, rows, m, Tk, rgroups,
+                                                          kgroups, out);
+  return mxq::check_launch("mxq_mask_minabs");
+}
+
+extern "C" int mxq_attend_hints(const double* amax_a, int64_t lda, const double* amax_k, int64_t ldk, int64_t D,
+                                int64_t Z, double slack_scale, const float* minabs, int64_t z0, int64_t z_per_b,
+                                int32_t batched, int64_t rows, int64_t Tk, uint8_t* skip, int32_t* k_end,
+                                mxq_stream_t stream) {
+  if (D < 0 || Z < 0 || rows < 0 || Tk < 0 || z0 < 0 || z_per_b < 1 || lda < Z || ldk < Z)
+    return mxq::invalid("mxq_attend_hints: bad shape");
+  if (Z == 0 || rows == 0) return MXQ_OK;
+  if (!amax_a || !amax_k || !minabs || !skip || !k_end) return mxq::invalid("mxq_attend_hints: NULL pointer");
+  const int64_t rgroups = mxq::ceil_div(rows, 32), kgroups = mxq::ceil_div(Tk, 32), tgroups = mxq::ceil_div(rows, 64);
+  if (tgroups > INT32_MAX || Z > 65535 || kgroups > INT32_MAX / 32) return mxq::invalid("mxq_attend_hints: too large");
+  k_attend_hints<<<dim3((unsigned)tgroups, (unsigned)Z), 256, 0, mxq::as_stream(stream)>>>(
+      amax_a, lda, amax_k, ldk, D, slack_scale, minabs, z0, z_per_b, batched ? 1 : 0, rgroups, kgroups, tgroups, skip,
+      k_end);
+  return mxq::check_launch("mxq_attend_hints");
 }

@@ -61,6 +61,20 @@ struct SysArgs {
   int8_t lane_e[kMaxLanes];
   int8_t lane_m[kMaxLanes];
   float fast_prod_max;    // the fast kernel's bound on max|a| * max|b| (see fast_prod_bound)
+  // the caller's hints (mxq_systolic_hints), NULL when absent
+  const uint8_t* skip;    // per problem, 32-row group and 32-column group of C: nonzero = not needed
+  int64_t skip_rows, skip_cols;
+  const int32_t* k_end;   // per problem and 64-column group of A: rows at and past it hold only +-0 codes
+  int64_t kend_groups;
+  // dispatch position (blockIdx.x + tiles_x * (blockIdx.y + tiles_y * blockIdx.z)) -> fast tile
+  // (z * tiles_y + ty) * tiles_x + tx, by descending work (k_tile_order); NULL: the grid's own tile, rows last
+  // first
+  const uint32_t* order;
+  // with k_end: per problem, 32-row stage and 32-column group of A (suf_a) and of B (suf_b), nonzero when rows
+  // of that stage may not be skipped (k_suffix_flags)
+  const uint8_t* suf_a;
+  const uint8_t* suf_b;
+  int64_t stages;
 };
 
 // ---------------------------------------------------------------------------------- fast datapath
@@ -149,6 +163,157 @@ struct ScaledRows {
   }
 };
 
+// A thread's TM x TN outputs of problem z into C (inside C only).
+template <int TM, int TN>
+__device__ __forceinline__ void write_tile(const SysArgs& a, int64_t z, int64_t mr, int64_t nc,
+                                           const float (&C)[TM][TN]) {
+  float* Cz = a.C + z * a.batch_c;
+#pragma unroll
+  for (int x = 0; x < TM; ++x) {
+    if (mr + x >= a.M) continue;
+#pragma unroll
+    for (int y = 0; y < TN; ++y)
+      if (nc + y < a.N) Cz[(mr + x) * a.ldc + nc + y] = C[x][y];
+  }
+}
+
+// Whether every 32 x 32 group of the bm x bn tile at (m0, n0) of problem z is marked in the caller's skip map.
+__device__ __forceinline__ bool tile_skipped(const SysArgs& a, int64_t z, int64_t m0, int64_t n0, int bm, int bn) {
+  const uint8_t* sk = a.skip + z * a.skip_rows * a.skip_cols;
+  bool all = true;
+  for (int64_t r = m0 / 32; r < (m0 + bm) / 32 && r < a.skip_rows; ++r)
+    for (int64_t c = n0 / 32; c < (n0 + bn) / 32 && c < a.skip_cols; ++c) all = all && sk[r * a.skip_cols + c];
+  return all;
+}
+
+// Where the reduction of the tile whose rows start at m0 stops under the caller's k_end: at K without one, else
+// k_end rounded up to a whole stage.
+__device__ __forceinline__ int64_t tile_kstop(const SysArgs& a, int64_t z, int64_t m0) {
+  if (!a.k_end) return a.K;
+  const int64_t ke = a.k_end[z * a.kend_groups + m0 / 64];
+  const int64_t ks = ke <= 0 ? 0 : (ke + KT - 1) / KT * KT;
+  return ks > a.K ? a.K : ks;
+}
+
+// Whether the rows of 32-row stage s may be left out of a reduction that ends before them, per 32-column
+// group: of A only where every code is +-0 (0 * b = +-0 adds nothing), and only if every block scale holding
+// those rows is finite; of B where codes and those scales are finite (0 * Inf would have made a NaN).  One wave
+// per (stage, group), 16 loads in flight per lane; a byte per answer, 1 = may not.  A's groups are checked only
+// at stages at or past their kstop (no tile reads the others).
+__global__ void __launch_bounds__(256) k_suffix_flags(const SysArgs a, int64_t ga, int64_t gb, uint8_t* fa,
+                                                      uint8_t* fb) {
+  const int lane = threadIdx.x & 63;
+  const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), s = blockIdx.y, z = blockIdx.z;
+  if (g >= ga + gb) return;
+  const bool is_a = g < ga;
+  const int64_t grp = is_a ? g : g - ga, c0 = grp * 32;
+  if (is_a && KT * s < tile_kstop(a, z, c0)) return;
+  const Operand& op = is_a ? a.A : a.B;
+  const Operand& xo = is_a ? a.XA : a.XB;
+  const int64_t L = is_a ? a.M : a.N, K = a.K;
+  const float* P = op.p + z * op.batch;
+  const float* X = xo.p + z * xo.batch;
+  const int64_t c = c0 + (lane & 31), r0 = KT * s + (lane >> 5);
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t r = r0 + 2 * i;
+    v[i] = (r < K && c < L) ? P[r * op.ld + c] : 0.0f;
+  }
+  uint32_t mx = 0u, mxs = 0u;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) mx = umax(mx, f2u(v[i]) & 0x7FFFFFFFu);
+  const int64_t r_end = (KT * s + KT < K ? KT * s + KT : K) - 1, bs = a.block_size;
+  if (lane < 32 && c < L)
+    for (int64_t gg = KT * s / bs; gg <= r_end / bs; ++gg) mxs = umax(mxs, f2u(X[gg * xo.ld + c]) & 0x7FFFFFFFu);
+  const bool bad = mxs >= 0x7F800000u || (is_a ? mx != 0u : mx >= 0x7F800000u);
+  const bool any = __any(bad);
+  if (lane == 0) (is_a ? fa : fb)[(z * a.stages + s) * (is_a ? ga : gb) + grp] = any ? 1u : 0u;
+}
+
+// The fast kernel's dispatch order under the caller's hints: tiles by descending work (stages to reduce),
+// skipped tiles (+0 writes) last.  Workgroups are handed to the XCDs and their shader engines in turn as their
+// ids rise, and a later one waits for an earlier one's slot.  In the grid's own order a causal triangle gives
+// the engines owning the low tile columns a whole row's work (skipping half the tiles then saves little), and
+// k_end's row-dependent work lands unevenly on them too.  Sorted by work, each run of consecutive ids carries
+// about equal work to every engine, heaviest first.  One workgroup: a counting sort over work buckets of one
+// stage (the last bucket holds everything longer), eight tiles per thread per pass so their hint loads overlap.
+constexpr int kOrderThreads = 1024, kOrderPer = 8, kOrderBuckets = 2048;
+
+__device__ __forceinline__ void order_tile(const SysArgs& a, int64_t p, uint32_t& tile, int& bucket) {
+  const int64_t per_z = a.tiles_x * a.tiles_y;
+  const int64_t z = p / per_z, r = p - z * per_z, by = r / a.tiles_x, tx = r - by * a.tiles_x;
+  const int64_t ty = a.tiles_y - 1 - by;
+  tile = (uint32_t)((z * a.tiles_y + ty) * a.tiles_x + tx);
+  if (a.skip && tile_skipped(a, z, ty * a.fbm, tx * a.fbn, a.fbm, a.fbn)) {
+    bucket = 0;
+    return;
+  }
+  const int64_t st = tile_kstop(a, z, ty * a.fbm) / KT;
+  bucket = 1 + (int)(st < kOrderBuckets - 2 ? st : kOrderBuckets - 2);
+}
+
+__global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, int64_t total, uint32_t* order) {
+  constexpr int PB = kOrderBuckets / kOrderThreads;
+  static_assert(PB * kOrderThreads == kOrderBuckets, "whole buckets per thread");
+  __shared__ uint32_t cur[kOrderBuckets];
+  __shared__ uint32_t wsum[kOrderThreads / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderThreads) cur[b] = 0u;
+  __syncthreads();
+  const int64_t stride = (int64_t)kOrderThreads * kOrderPer;
+  for (int64_t c0 = 0; c0 < total; c0 += stride) {
+    uint32_t tile[kOrderPer];
+    int bucket[kOrderPer];
+#pragma unroll
+    for (int u = 0; u < kOrderPer; ++u) {
+      const int64_t p = c0 + (int64_t)u * kOrderThreads + threadIdx.x;
+      bucket[u] = -1;
+      if (p < total) order_tile(a, p, tile[u], bucket[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kOrderPer; ++u)
+      if (bucket[u] >= 0) atomicAdd(&cur[bucket[u]], 1u);
+  }
+  __syncthreads();
+  // cur[b] <- the first position of bucket b: the count of every bucket above it (heavier work first)
+  uint32_t cnt[PB], sum = 0u;
+#pragma unroll
+  for (int u = 0; u < PB; ++u) {
+    cnt[u] = cur[kOrderBuckets - 1 - (threadIdx.x * PB + u)];
+    sum += cnt[u];
+  }
+  uint32_t incl = sum;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)incl, off, 64);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  uint32_t at = incl - sum;
+  for (int w = 0; w < wave; ++w) at += wsum[w];
+#pragma unroll
+  for (int u = 0; u < PB; ++u) {
+    cur[kOrderBuckets - 1 - (threadIdx.x * PB + u)] = at;
+    at += cnt[u];
+  }
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < total; c0 += stride) {
+    uint32_t tile[kOrderPer];
+    int bucket[kOrderPer];
+#pragma unroll
+    for (int u = 0; u < kOrderPer; ++u) {
+      const int64_t p = c0 + (int64_t)u * kOrderThreads + threadIdx.x;
+      bucket[u] = -1;
+      if (p < total) order_tile(a, p, tile[u], bucket[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kOrderPer; ++u)
+      if (bucket[u] >= 0) order[atomicAdd(&cur[bucket[u]], 1u)] = tile[u];
+  }
+}
+
 // BM x BN outputs per workgroup, (BM / 16) x (BN / 16) per thread.
 // HWF: the lanes are HW_FINAL's (SIZE 16, bf16 last), whose constants are then immediates.
 template <int SIZE, bool BF16_LAST, int BM, int BN, bool HWF>
@@ -159,9 +324,29 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   static_assert((BM / TM) * (BN / TN) == NT, "256 threads");
   __shared__ __align__(16) Smem<BM, BN> sm;
   __shared__ uint32_t red[3][4];
+  __shared__ uint32_t live[2][4];   // per staged buffer and wave: bit 0, A has a nonzero code; bit 1, B has
   const int tn = threadIdx.x % (BN / TN), tm = threadIdx.x / (BN / TN);
-  const int64_t z = blockIdx.z;
-  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  // A stage whose A tile or B tile is all +-0 makes every product +-0, so every sum +-0 and every tile add
+  // C + (+-0) * (finite scale) = C: the workgroup skips its lanes (its scales are still read and checked).
+  auto note_live = [&](int to, uint32_t ma, uint32_t mb) {
+    const uint32_t v = (__any(ma != 0u) ? 1u : 0u) | (__any(mb != 0u) ? 2u : 0u);
+    if ((threadIdx.x & 63) == 0) live[to][threadIdx.x >> 6] = v;
+  };
+  // Row tiles are dispatched last row first.  Where A is zero above a diagonal (attention's P^T under a causal
+  // mask) the late rows carry the most nonzero stages: starting them first keeps them out of the tail.
+  int64_t z, ty, tx;
+  if (args.order) {
+    const uint32_t t = args.order[blockIdx.x + args.tiles_x * (blockIdx.y + args.tiles_y * (int64_t)blockIdx.z)];
+    const uint32_t zy = t / (uint32_t)args.tiles_x;
+    tx = t - zy * (uint32_t)args.tiles_x;
+    z = zy / (uint32_t)args.tiles_y;
+    ty = zy - (uint32_t)z * (uint32_t)args.tiles_y;
+  } else {
+    z = blockIdx.z;
+    ty = args.tiles_y - 1 - blockIdx.y;
+    tx = blockIdx.x;
+  }
+  const int64_t m0 = ty * BM, n0 = tx * BN;
   const float* A = args.A.p + z * args.A.batch;
   const float* B = args.B.p + z * args.B.batch;
   const float* XA = args.XA.p + z * args.XA.batch;
@@ -176,6 +361,19 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 #pragma unroll
     for (int y = 0; y < TN; ++y) C[x][y] = 0.0f;
 
+  // a tile made only of groups the caller does not need is written as +0, uncomputed (the same decision in
+  // every thread)
+  if (args.skip) {
+    if (tile_skipped(args, z, m0, n0, BM, BN)) {
+      if (threadIdx.x == 0) args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = 0u;
+      write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
+      return;
+    }
+  }
+  // the reduction runs to kstop: past the caller's k_end for these columns of A (a multiple of the stage height;
+  // the rows skipped are checked below)
+  const int64_t kstop = tile_kstop(args, z, m0);
+
   uint32_t max_a = 0u, max_b = 0u, max_x = 0u;   // largest |a|, |b| and scale this thread has read
   TileLoader<BM, NT> la;
   TileLoader<BN, NT> lb;
@@ -184,8 +382,12 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   int buf = 0;
   la.load(A, args.A.ld, K, M, 0, m0, va);
   lb.load(B, args.B.ld, K, N, 0, n0, vb);
-  max_a = umax(max_a, la.max_bits());
-  max_b = umax(max_b, lb.max_bits());
+  {
+    const uint32_t ma = la.max_bits(), mb = lb.max_bits();
+    max_a = umax(max_a, ma);
+    max_b = umax(max_b, mb);
+    note_live(0, ma, mb);
+  }
   rows.apply(la.v);
   la.store(sm.a[0], va);
   lb.store(sm.b[0], vb);
@@ -195,13 +397,15 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   bool short_add = false;  // this block's scales make bf16(S * scale) exact (bf16 last lane only)
   int in_block = 0;      // k of the current reduction within its block
   int64_t g = 0;         // its block
-  for (int64_t k0 = 0; k0 < K; k0 += KT) {
-    const bool more = k0 + KT < K;
+  for (int64_t k0 = 0; k0 < kstop; k0 += KT) {
+    const bool more = k0 + KT < kstop;
     if (more) {
       la.load(A, args.A.ld, K, M, k0 + KT, m0, va);
       lb.load(B, args.B.ld, K, N, k0 + KT, n0, vb);
     }
     const int kend = (int)((K - k0 < KT) ? (K - k0) : KT);
+    const uint32_t lv = live[buf][0] | live[buf][1] | live[buf][2] | live[buf][3];
+    const bool zero_stage = lv != 3u;
     // rows past K are zero in LDS: their products are +0 and leave every lane's sum unchanged, so a short
     // last reduction runs as a whole one
     for (int r0 = 0; r0 < kend; r0 += SIZE) {
@@ -231,6 +435,14 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
           for (int y = 0; y < TN; ++y) ex = ex && exact_scale(xb[y], fl.xs_lo, fl.xs_hi);
           short_add = __all(ex) != 0;                            // one decision per wave and block
         }
+      }
+      if (zero_stage) {
+        in_block += SIZE;
+        if (in_block == bs) {
+          in_block = 0;
+          ++g;
+        }
+        continue;
       }
       float S[TM][TN];
 #pragma unroll
@@ -313,14 +525,36 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
       }
     }
     if (more) {
-      max_a = umax(max_a, la.max_bits());
-      max_b = umax(max_b, lb.max_bits());
+      const uint32_t ma = la.max_bits(), mb = lb.max_bits();
+      max_a = umax(max_a, ma);
+      max_b = umax(max_b, mb);
+      note_live(buf ^ 1, ma, mb);
       rows.apply(la.v);
       la.store(sm.a[buf ^ 1], va);
       lb.store(sm.b[buf ^ 1], vb);
     }
     __syncthreads();
     buf ^= 1;
+  }
+
+  // rows past kstop: the results are exact only if A holds +-0 there, B and every remaining block scale are
+  // finite (k_suffix_flags' bytes for this tile's groups and the stages it left out)
+  if (kstop < K) {
+    constexpr int GT = BM / 32 + BN / 32;
+    const int64_t s0 = kstop / KT, ga = (M + 31) / 32, gb = (N + 31) / 32;
+    bool bad = false;
+    for (int64_t i = threadIdx.x; i < (args.stages - s0) * GT; i += 256) {
+      const int64_t st = s0 + i / GT;
+      const int j = (int)(i % GT);
+      if (j < BM / 32) {
+        const int64_t g = m0 / 32 + j;
+        bad = bad || (g < ga && args.suf_a[(z * args.stages + st) * ga + g]);
+      } else {
+        const int64_t g = n0 / 32 + (j - BM / 32);
+        bad = bad || (g < gb && args.suf_b[(z * args.stages + st) * gb + g]);
+      }
+    }
+    max_b = umax(max_b, bad ? 0x7F800000u : 0u);
   }
 
   // the workgroup's verdict: its maxima over everything it read
@@ -342,19 +576,9 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   const bool ok = wa < kFastAMaxBits && wb < 0x7F800000u && wx < 0x7F800000u &&
                   u2f(wa) * u2f(wb) <= args.fast_prod_max;
   if (threadIdx.x == 0)
-    args.flags[(z * args.tiles_y + blockIdx.y) * args.tiles_x + blockIdx.x] = ok ? 0u : 1u;
+    args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = ok ? 0u : 1u;
   if (!ok) return;
-  float* Cz = args.C + z * args.batch_c;
-#pragma unroll
-  for (int x = 0; x < TM; ++x) {
-    const int64_t mm = m0 + tm * TM + x;
-    if (mm >= M) continue;
-#pragma unroll
-    for (int y = 0; y < TN; ++y) {
-      const int64_t nn = n0 + tn * TN + y;
-      if (nn < N) Cz[mm * args.ldc + nn] = C[x][y];
-    }
-  }
+  write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
 }
 
 // ------------------------------------------------------------------------------- general datapath
@@ -601,6 +825,28 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
   const dim3 grid_g((unsigned)mxq::ceil_div(a.N, 32), (unsigned)mxq::ceil_div(a.M, 32), (unsigned)count);
   if (fast_lanes) {
     a.fast_prod_max = fast_prod_bound(lane_e, lane_m, a.size);
+    // workspace: a flag per 32 x 32 tile (W), the dispatch order (W), the suffix bytes of A's and B's groups
+    const int64_t W = mxq::ceil_div(a.M, 32) * mxq::ceil_div(a.N, 32) * count;
+    const int64_t total = a.tiles_x * a.tiles_y * count;
+    if (a.k_end) {
+      const int64_t stages = mxq::ceil_div(a.K, KT), ga = mxq::ceil_div(a.M, 32), gb = mxq::ceil_div(a.N, 32);
+      if (stages <= 65535) {
+        uint8_t* fa = reinterpret_cast<uint8_t*>(a.flags + 2 * W);
+        uint8_t* fb = fa + count * stages * ga;
+        a.stages = stages;
+        k_suffix_flags<<<dim3((unsigned)mxq::ceil_div(ga + gb, 4), (unsigned)stages, (unsigned)count), 256, 0,
+                         st>>>(a, ga, gb, fa, fb);
+        a.suf_a = fa;
+        a.suf_b = fb;
+      } else {
+        a.k_end = nullptr;   // the hint is dropped: every reduction runs to K
+      }
+    }
+    if ((a.skip || a.k_end) && total <= (int64_t)0xFFFFFFFFu) {
+      uint32_t* order = a.flags + W;
+      k_tile_order<<<1, kOrderThreads, 0, st>>>(a, total, order);
+      a.order = order;
+    }
     {
       mxq::KernelTimer timer("systolic_fast", st);
       launch_fast(a.size, lane_e[a.size - 1] == 8, is_hw_final(lane_e, lane_m, a.size), grid_f, st, a,
@@ -649,8 +895,9 @@ extern "C" int mxq_systolic(const float* P_A, const float* X_A, const float* P_B
 extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const float* P_B, const float* X_B,
                                     float* C, const mxq_systolic_layout* layout, int64_t count, int64_t K,
                                     int64_t M, int64_t N, const int32_t* lane_e, const int32_t* lane_m, int32_t size,
-                                    int32_t block_size, const mxq_arith_spec* arith, uint32_t* workspace,
-                                    int32_t force_general, mxq_stream_t stream) {
+                                    int32_t block_size, const mxq_arith_spec* arith,
+                                    const mxq_systolic_hints* hints, uint32_t* workspace, int32_t force_general,
+                                    mxq_stream_t stream) {
   if (int rc = check_common(K, M, N, count, lane_e, lane_m, size, block_size, arith)) return rc;
   if (!layout) return mxq::invalid("mxq_systolic_batched: NULL layout");
   const mxq_systolic_layout& L = *layout;
@@ -667,10 +914,20 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
   a.B = {P_B, L.ld_b, L.batch_b}; a.XB = {X_B, L.ld_xb, L.batch_xb};
   a.C = C; a.ldc = L.ld_c; a.batch_c = L.batch_c; a.flags = workspace;
   a.K = K; a.M = M; a.N = N; a.size = size; a.block_size = block_size; a.ar = *arith;
+  if (hints) {
+    a.skip = hints->skip;
+    a.skip_rows = mxq::ceil_div(M, 32);
+    a.skip_cols = mxq::ceil_div(N, 32);
+    a.k_end = hints->k_end;
+    a.kend_groups = mxq::ceil_div(M, 64);
+  }
   return run_systolic(a, lane_e, lane_m, count, force_general, mxq::as_stream(stream));
 }
 
-extern "C" int64_t mxq_systolic_workspace(int64_t M, int64_t N, int64_t count) {
-  if (M <= 0 || N <= 0 || count <= 0) return 1;
-  return mxq::ceil_div(M, 32) * mxq::ceil_div(N, 32) * count;    // the smallest fast tile
+extern "C" int64_t mxq_systolic_workspace(int64_t K, int64_t M, int64_t N, int64_t count) {
+  if (K < 0 || M <= 0 || N <= 0 || count <= 0) return 1;
+  // a flag per smallest fast tile, room for the dispatch order of the largest number of fast tiles, and a byte
+  // per problem, 32-row stage and 32-column group of A and of B (the rows k_end leaves out)
+  const int64_t suffix = count * mxq::ceil_div(K, KT) * (mxq::ceil_div(M, 32) + mxq::ceil_div(N, 32));
+  return 2 * mxq::ceil_div(M, 32) * mxq::ceil_div(N, 32) * count + mxq::ceil_div(suffix, 4);
 }

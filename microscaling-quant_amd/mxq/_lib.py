@@ -38,6 +38,11 @@ class ArithSpec(ctypes.Structure):
                 ("sat_limit", c_f32), ("sat_value", c_f32)]
 
 
+class SystolicHints(ctypes.Structure):
+    """include/mxq_hip.h mxq_systolic_hints: device pointers (0 for none) to the skip map and the k_end bounds."""
+    _fields_ = [("skip", c_ptr), ("k_end", c_ptr)]
+
+
 class SystolicLayout(ctypes.Structure):
     """mxq_systolic_layout (include/mxq_hip.h): row and problem strides of the five operands, in elements."""
     _fields_ = [(n, c_i64) for n in ("ld_a", "batch_a", "ld_xa", "batch_xa", "ld_b", "batch_b", "ld_xb", "batch_xb",
@@ -71,11 +76,14 @@ SIGNATURES = {
                              ctypes.POINTER(ArithSpec), c_ptr, c_i32, c_ptr]),
     "mxq_systolic_batched": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, ctypes.POINTER(SystolicLayout), c_i64,
                                      c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32, ctypes.POINTER(ArithSpec),
-                                     c_ptr, c_i32, c_ptr]),
-    "mxq_systolic_workspace": (c_i64, [c_i64, c_i64, c_i64]),
+                                     c_ptr, c_ptr, c_i32, c_ptr]),
+    "mxq_systolic_workspace": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
     "mxq_scores_scale_mask": (c_i32, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64, c_i64, c_i64, c_i64,
                                       c_i32, c_ptr]),
     "mxq_group_amax": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
+    "mxq_mask_minabs": (c_i32, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
+    "mxq_attend_hints": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_f64, c_ptr, c_i64, c_i64, c_i32, c_i64,
+                                 c_i64, c_ptr, c_ptr, c_ptr]),
     "mxq_attend_windows": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_f64, c_ptr, c_i64, c_i64, c_i64,
                                    c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
     "mxq_adder_tree": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,

@@ -50,7 +50,7 @@ def adder_tree(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: tor
     import ctypes
     le = (ctypes.c_int32 * levels)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * levels)(*[int(m) for _, m in schedule])
-    work = torch.empty(workspace_elements(M, N, 1), dtype=torch.int32, device=dev)
+    work = torch.empty(workspace_elements(K, M, N, 1), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_adder_tree", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, le, lm, size, block_size,
                  kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))

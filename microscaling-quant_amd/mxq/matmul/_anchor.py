@@ -89,7 +89,7 @@ def anchor_tree(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: to
     tb = (ctypes.c_int32 * (trees * (lg + 1)))(*[int(b) for _, _, ws in per_tree for b in ws])
     spec = _lib.AnchorSpec(width=width, drop=DROPS.index(drop), headroom=head, has_emin=int(emin is not None),
                            emin=0 if emin is None else emin, nbits=lg + 1)
-    work = torch.empty(workspace_elements(M, N, 1), dtype=torch.int32, device=dev)
+    work = torch.empty(workspace_elements(K, M, N, 1), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_anchor_tree", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, te, tm, tb, size, block_size,
                  ctypes.byref(spec), kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))

@@ -10,7 +10,7 @@ With MXGEMMINI or MXQUANT (or compiled(...) of them) the whole call is one HIP l
 loop staged through LDS.  A hand-made Arithmetic, or a size the kernel does not take (it needs size | 32),
 runs the reference's loop with the Arithmetic's own callables.
 """
-from typing import Sequence, Tuple
+from typing import Optional, Sequence, Tuple
 
 import torch
 
@@ -57,25 +57,30 @@ def systolic(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: torch
     import ctypes
     le = (ctypes.c_int32 * size)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
-    work = torch.empty(workspace_elements(M, N, 1), dtype=torch.int32, device=dev)
+    work = torch.empty(workspace_elements(K, M, N, 1), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_systolic", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, le, lm, size, block_size,
                  kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))
     return _lib.back(C, P_A)
 
 
-def workspace_elements(M: int, N: int, count: int) -> int:
-    """int32 elements of device workspace a systolic launch of `count` M x N problems needs."""
-    return int(_lib.load().mxq_systolic_workspace(M, N, count))
+def workspace_elements(K: int, M: int, N: int, count: int) -> int:
+    """int32 elements of device workspace a systolic launch of `count` problems (K x M codes A, K x N codes B)
+    needs."""
+    return int(_lib.load().mxq_systolic_workspace(K, M, N, count))
 
 
 def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: int, N: int, C: torch.Tensor,
                      arith: Arithmetic, schedule: Sequence[Tuple[int, int]], size: int = 16,
-                     block_size: int = BLOCK) -> None:
+                     block_size: int = BLOCK, *, skip: Optional[torch.Tensor] = None,
+                     k_end: Optional[torch.Tensor] = None) -> None:
     """`count` problems of one shape in one launch, written into C (mxq_systolic_batched).  ops: the four
     device tensors the layout's strides address (codes A, scales X_A, codes B, scales X_B), float32 on C's
     device.  Each problem's result equals systolic() on that problem alone.  The Arithmetic must carry a
-    kernel description (MXGEMMINI, MXQUANT, compiled)."""
+    kernel description (MXGEMMINI, MXQUANT, compiled).
+    Hints (include/mxq_hip.h mxq_systolic_hints): `skip`, uint8 count x ceil(M/32) x ceil(N/32), nonzero where
+    the caller does not need C's 32 x 32 group (such tiles come back +0); `k_end`, int32 count x ceil(M/64), a
+    bound on the rows of A holding nonzero codes in each 64-column group (checked: a wrong one costs time)."""
     import ctypes
     kernel = getattr(arith, "kernel", None)
     if kernel is None or size > 64 or 32 % size != 0 or block_size % size != 0:
@@ -90,10 +95,16 @@ def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: 
         raise ValueError("codes, scales and C must be float32 on one device")
     le = (ctypes.c_int32 * size)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
-    work = torch.empty(workspace_elements(M, N, count), dtype=torch.int32, device=dev)
+    for t, dt, shape in ((skip, torch.uint8, (count, -(-M // 32), -(-N // 32))),
+                         (k_end, torch.int32, (count, -(-M // 64)))):
+        if t is not None and (t.dtype != dt or tuple(t.shape) != shape or t.device != dev or not t.is_contiguous()):
+            raise ValueError(f"systolic_batched: a hint must be a contiguous {dt} tensor of shape {shape} on {dev}")
+    hints = _lib.SystolicHints(skip=_lib.ptr(skip), k_end=_lib.ptr(k_end))
+    work = torch.empty(workspace_elements(K, M, N, count), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_systolic_batched", *(_lib.ptr(t) for t in ops), _lib.ptr(C), ctypes.byref(layout), count,
-                 K, M, N, le, lm, size, block_size, kernel.ctype(), _lib.ptr(work), 0, _lib.stream(dev))
+                 K, M, N, le, lm, size, block_size, kernel.ctype(), ctypes.byref(hints), _lib.ptr(work), 0,
+                 _lib.stream(dev))
 
 
 def _reference_loop(P_A, X_A, P_B, X_B, arith, schedule, size, block_size, K, M, N):

@@ -248,6 +248,32 @@ def _windows(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale
     return flags
 
 
+def _hints(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale: float, bias: torch.Tensor,
+           Hkv: int, s0: int, m: int, rows: int, Tk: int):
+    """The two batched launches' hints from the mask rows s0.. of pairs z0..z0+Zc and each call's bound
+    (include/mxq_hip.h mxq_attend_hints): the 32 x 32 score groups whose mask absorbs every score the call can
+    produce, where a +0 score gives the reference's r(r(s * scale) + mask) (skip, for Q K^T), and per 64 rows
+    the end of the keys some row still sees (k_end, for P V; checked by the kernel, so a row whose every key
+    is masked, where softmax is uniform, costs time, not bits)."""
+    from .. import _lib
+    D = a_amax.shape[0]
+    mask, b_stride, r_stride = _mask_rows(bias, z0, Hkv, s0)
+    batched = bias.shape[0] > 1
+    batches = (z0 + Zc - 1) // Hkv - z0 // Hkv + 1 if batched else 1
+    rg, kg, tg = -(-rows // 32), -(-Tk // 32), -(-rows // 64)
+    dev = a_amax.device
+    minabs = torch.empty(batches, rg, kg, dtype=torch.float32, device=dev)
+    skip = torch.empty(Zc, rg, kg, dtype=torch.uint8, device=dev)
+    k_end = torch.empty(Zc, tg, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.run("mxq_mask_minabs", _lib.ptr(mask), b_stride, r_stride, batches, rows, m, Tk, _lib.ptr(minabs),
+                 _lib.stream(dev))
+        _lib.run("mxq_attend_hints", _lib.ptr(a_amax), a_amax.shape[1], _lib.ptr(k_amax[:, z0:]), k_amax.shape[1],
+                 D, Zc, SLACK * abs(scale), _lib.ptr(minabs), z0, Hkv, int(batched), rows, Tk, _lib.ptr(skip),
+                 _lib.ptr(k_end), _lib.stream(dev))
+    return skip, k_end
+
+
 @dataclass
 class _Batched:
     """attend built from the library's own pieces (column-wise block quantizers, matmul.systolic with a kernel
@@ -313,17 +339,18 @@ class _Batched:
         Zc, n, m, Tk, D, Hkv = z1 - z0, dims.group, e0 - s0, dims.Tk, dims.D, dims.Hkv
         cols = n * m                                                              # one call's columns
         A_P, A_X = qk.a(qg[z0:z1, :, s0:e0].to(torch.float32).permute(3, 0, 1, 2).reshape(D, Zc * cols))
-        flags = None
+        flags = skip = k_end = None
         if bias is not None:
-            flags = _windows(_group_amax(A_P, A_X, qk.block_size, Zc), k_amax, z0, Zc, scale, bias, Hkv, s0, m,
-                             pv.block_size)
+            a_amax = _group_amax(A_P, A_X, qk.block_size, Zc)
+            flags = _windows(a_amax, k_amax, z0, Zc, scale, bias, Hkv, s0, m, pv.block_size)
+            skip, k_end = _hints(a_amax, k_amax, z0, Zc, scale, bias, Hkv, s0, m, cols, Tk)
         arith, sched, size = self.qk_red
         S = torch.empty(Zc, cols, Tk, dtype=torch.float32, device=qg.device)
         systolic_batched((A_P, A_X, KT_P[:, z0 * Tk:], KT_X[:, z0 * Tk:]),
                          _lib.SystolicLayout(ld_a=Zc * cols, batch_a=cols, ld_xa=Zc * cols, batch_xa=cols,
                                              ld_b=KT_P.shape[1], batch_b=Tk, ld_xb=KT_X.shape[1], batch_xb=Tk,
                                              ld_c=Tk, batch_c=cols * Tk),
-                         Zc, D, cols, Tk, S, arith, sched, size, qk.block_size)
+                         Zc, D, cols, Tk, S, arith, sched, size, qk.block_size, skip=skip)
         _scale_mask(S, bias, scale, vector, n, m, z0, Hkv, s0)
         P = softmax(S, vector)
         # every call's P^T side by side, quantized from P as it lies (a transposed view: no copy)
@@ -334,7 +361,7 @@ class _Batched:
                          _lib.SystolicLayout(ld_a=Zc * cols, batch_a=cols, ld_xa=Zc * cols, batch_xa=cols,
                                              ld_b=D, batch_b=Tk * D, ld_xb=D, batch_xb=V_X.shape[1] * D,
                                              ld_c=D, batch_c=cols * D),
-                         Zc, Tk, cols, D, O, arith, sched, size, pv.block_size)
+                         Zc, Tk, cols, D, O, arith, sched, size, pv.block_size, k_end=k_end)
         O = O.view(Zc, n, m, D)
         for b in range(z0 // Hkv, (z1 - 1) // Hkv + 1):                          # pairs into B x Tq x H x D
             h0, h1 = max(z0, b * Hkv) - b * Hkv, min(z1, (b + 1) * Hkv) - b * Hkv

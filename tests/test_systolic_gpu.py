@@ -279,3 +279,109 @@ def test_all_fast_tile_shapes(cuda):
             for cols in (slice(0, 8), slice(N - 6, N)):
                 want = osys.systolic(P_A, X_A, P_B[:, cols], X_B[:, cols], nx.MXGEMMINI(), sched)
                 assert_bits_equal(Y[:, cols], want, f"{M}x{N} cols {cols}")
+
+
+def test_zero_stages_skip_exactly(cuda):
+    """Stages (32 K rows) whose A or B tile is all +-0 are skipped by the fast kernel: a zero block for every
+    tile, zero blocks for some row or column tiles only, -0 codes, a zero stage whose block scale is not a power
+    of two, and a would-be-zero stage holding one NaN (which must not be skipped): every output equal to the
+    general kernel's and the oracle's."""
+    from mxq import matmul
+    rng = np.random.default_rng(21)
+    K, M, N = 320, 130, 140
+    P_A, X_A = _codes(rng, K, M)
+    P_B, X_B = _codes(rng, K, N, scale=0.05)
+    P_A[32:96, :] = 0.0
+    P_A[96:128, :] = -0.0
+    P_B[160:192, 70:] = 0.0
+    P_A[224:256, :64] = 0.0
+    X_A[7, :64] = np.float32(0.3)
+    P_B[256:288, :] = 0.0
+    P_B[270, 5] = np.nan
+    ar, orc = _arith("MXGEMMINI")
+    for sched in (HW_FINAL, [(4, 4)] * 15 + [(8, 7)]):
+        got = _run(P_A, X_A, P_B, X_B, ar, sched)
+        gen = _run(P_A, X_A, P_B, X_B, ar, sched, force_general=True)
+        assert_bits_equal(got, gen, "fast vs general")
+        assert_bits_equal(got, osys.systolic(P_A, X_A, P_B, X_B, orc, sched), "fast vs oracle")
+
+
+@pytest.mark.parametrize("count,M,N", [(32, 512, 512), (3, 200, 300)], ids=["tiles64", "tiles32"])
+def test_batched_hints(cuda, count, M, N):
+    """mxq_systolic_batched's hints change no needed bit.  Skip maps (a causal triangle, random 32 x 32 groups,
+    random whole 64 x 64 tiles, everything): each group the map leaves is bit-equal to the hint-free result, each
+    it marks is that result or +0, and a fully marked map gives +0 everywhere.  k_end: the true bound of A's
+    nonzero rows, and a bound too small for some groups (those tiles fall back to the general kernel), both
+    equal to the hint-free result."""
+    from mxq import _lib, matmul
+    from mxq.matmul._systolic import systolic_batched
+    rng = np.random.default_rng(M)
+    K = 160
+    P_A, X_A = _codes(rng, K, count * M)
+    P_B, X_B = _codes(rng, K, count * N, scale=0.1)
+    gm, gn, g64 = -(-M // 32), -(-N // 32), -(-M // 64)
+    ends = rng.integers(0, K // 32 + 1, (count, g64)) * 32 - rng.integers(0, 20, (count, g64))
+    ends = np.clip(ends, 0, K).astype(np.int32)
+    for z in range(count):
+        for t in range(g64):
+            P_A[ends[z, t]:, z * M + 64 * t: min(z * M + 64 * t + 64, (z + 1) * M)] = 0.0
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()          # noqa: E731
+    ops = (t(P_A), t(X_A), t(P_B), t(X_B))
+    lay = _lib.SystolicLayout(ld_a=count * M, batch_a=M, ld_xa=count * M, batch_xa=M,
+                              ld_b=count * N, batch_b=N, ld_xb=count * N, batch_xb=N, ld_c=N, batch_c=M * N)
+    ar = matmul.MXGEMMINI()
+
+    def run(**hints):
+        C = torch.full((count, M, N), float("nan"), device="cuda")
+        systolic_batched(ops, lay, count, K, M, N, C, ar, HW_FINAL, **hints)
+        return C.cpu().numpy()
+
+    want = run()
+    gi, gj = np.arange(gm)[:, None], np.arange(gn)[None, :]
+    tiles = rng.random((count, -(-gm // 2), -(-gn // 2))) < 0.5
+    maps = {"triangle": np.broadcast_to(gj > gi, (count, gm, gn)),
+            "groups": rng.random((count, gm, gn)) < 0.5,
+            "tiles": tiles.repeat(2, 1).repeat(2, 2)[:, :gm, :gn],
+            "all": np.ones((count, gm, gn), dtype=bool)}
+    for name, mp in maps.items():
+        got = run(skip=torch.from_numpy(np.ascontiguousarray(mp).astype(np.uint8)).cuda())
+        full = mp.repeat(32, 1).repeat(32, 2)[:, :M, :N]
+        assert_bits_equal(got[~full], want[~full], f"{name}: groups left")
+        gb, wb = got.view(np.uint32), want.view(np.uint32)
+        assert ((gb == wb) | (gb == 0))[full].all(), f"{name}: marked groups"
+        if name == "all":
+            assert (gb == 0).all()
+    for name, ke in (("exact", ends), ("short", np.maximum(ends - 40, 0))):
+        got = run(k_end=torch.from_numpy(ke.astype(np.int32)).cuda())
+        assert_bits_equal(got, want, f"k_end {name}")
+    got = run(skip=torch.from_numpy(np.ascontiguousarray(maps["triangle"]).astype(np.uint8)).cuda(),
+              k_end=torch.from_numpy(ends).cuda())
+    keep = ~np.broadcast_to(maps["triangle"], (count, gm, gn)).repeat(32, 1).repeat(32, 2)[:, :M, :N]
+    assert_bits_equal(got[keep], want[keep], "skip and k_end together")
+
+
+def test_k_end_nonfinite_past_the_end(cuda):
+    """Rows past k_end where A is +-0 but B holds an Inf, or a scale of A's is NaN, or one of B's is Inf: 0 * Inf
+    makes NaN there, so those tiles must not stop early.  Every output equals the hint-free run (NaN included)."""
+    from mxq import _lib, matmul
+    from mxq.matmul._systolic import systolic_batched
+    rng = np.random.default_rng(5)
+    count, K, M, N = 3, 200, 96, 70
+    P_A, X_A = _codes(rng, K, count * M)
+    P_B, X_B = _codes(rng, K, count * N, scale=0.1)
+    P_A[40:, :] = 0.0
+    P_B[150, 3] = np.inf                                   # problem 0
+    X_A[4, M + 10] = np.nan                                # problem 1, block 4 (rows 128..159)
+    X_B[6, 2 * N + 60] = np.inf                            # problem 2, block 6 (rows 192..199)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()          # noqa: E731
+    ops = (t(P_A), t(X_A), t(P_B), t(X_B))
+    lay = _lib.SystolicLayout(ld_a=count * M, batch_a=M, ld_xa=count * M, batch_xa=M,
+                              ld_b=count * N, batch_b=N, ld_xb=count * N, batch_xb=N, ld_c=N, batch_c=M * N)
+    outs = []
+    for ke in (None, torch.full((count, 2), 40, dtype=torch.int32, device="cuda")):
+        C = torch.full((count, M, N), float("nan"), device="cuda")
+        systolic_batched(ops, lay, count, K, M, N, C, matmul.MXGEMMINI(), HW_FINAL, k_end=ke)
+        outs.append(C.cpu().numpy())
+    want, got = outs
+    assert np.isnan(want[0, :, 3]).all() and np.isnan(want[1, 10, :]).all() and np.isnan(want[2, :, 60]).all()
+    assert_bits_equal(got, want, "k_end with non-finite values past it")
