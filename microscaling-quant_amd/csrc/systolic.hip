@@ -177,13 +177,37 @@ __device__ __forceinline__ void write_tile(const SysArgs& a, int64_t z, int64_t 
   }
 }
 
-// Whether every 32 x 32 group of the bm x bn tile at (m0, n0) of problem z is marked in the caller's skip map.
-__device__ __forceinline__ bool tile_skipped(const SysArgs& a, int64_t z, int64_t m0, int64_t n0, int bm, int bn) {
+// Whether every 32 x 32 group of the bm x bn tile (bm, bn in {32, 64}) at (m0, n0) of problem z is marked in
+// the caller's skip map.  The four candidate bytes are loaded together, unconditionally (indices clamped into
+// the map, the unwanted bytes ignored), rather than one after another.
+__device__ __forceinline__ void skip_bytes(const SysArgs& a, int64_t z, int64_t m0, int64_t n0, uint32_t (&v)[4]) {
   const uint8_t* sk = a.skip + z * a.skip_rows * a.skip_cols;
+  const int64_t r0 = m0 / 32, c0 = n0 / 32;   // inside the map: m0 < M, n0 < N
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t r = r0 + (k >> 1) < a.skip_rows ? r0 + (k >> 1) : a.skip_rows - 1;
+    const int64_t c = c0 + (k & 1) < a.skip_cols ? c0 + (k & 1) : a.skip_cols - 1;
+    v[k] = sk[r * a.skip_cols + c];
+  }
+}
+
+__device__ __forceinline__ bool skip_all(const SysArgs& a, int64_t m0, int64_t n0, int bm, int bn,
+                                         const uint32_t (&v)[4]) {
+  const int64_t r0 = m0 / 32, c0 = n0 / 32;
   bool all = true;
-  for (int64_t r = m0 / 32; r < (m0 + bm) / 32 && r < a.skip_rows; ++r)
-    for (int64_t c = n0 / 32; c < (n0 + bn) / 32 && c < a.skip_cols; ++c) all = all && sk[r * a.skip_cols + c];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const bool in = 32 * (k >> 1) < bm && 32 * (k & 1) < bn && r0 + (k >> 1) < a.skip_rows &&
+                    c0 + (k & 1) < a.skip_cols;
+    all &= !in || v[k] != 0u;
+  }
   return all;
+}
+
+__device__ __forceinline__ bool tile_skipped(const SysArgs& a, int64_t z, int64_t m0, int64_t n0, int bm, int bn) {
+  uint32_t v[4];
+  skip_bytes(a, z, m0, n0, v);
+  return skip_all(a, m0, n0, bm, bn, v);
 }
 
 // Where the reduction of the tile whose rows start at m0 stops under the caller's k_end: at K without one, else
@@ -197,38 +221,66 @@ __device__ __forceinline__ int64_t tile_kstop(const SysArgs& a, int64_t z, int64
 
 // Whether the rows of 32-row stage s may be left out of a reduction that ends before them, per 32-column
 // group: of A only where every code is +-0 (0 * b = +-0 adds nothing), and only if every block scale holding
-// those rows is finite; of B where codes and those scales are finite (0 * Inf would have made a NaN).  One wave
-// per (stage, group), 16 loads in flight per lane; a byte per answer, 1 = may not.  A's groups are checked only
-// at stages at or past their kstop (no tile reads the others).
+// those rows is finite; of B where codes and those scales are finite (0 * Inf would have made a NaN).  A byte
+// per answer, 1 = may not.  A's groups are checked only at stages at or past their kstop (no tile reads the
+// others).  One workgroup per stage and 256 columns (the first x blocks A's, the rest B's): a lane reads 4
+// adjacent columns of 8 rows, so each row is read as one 1 KB piece.
+constexpr int kSufCols = 256;
 __global__ void __launch_bounds__(256) k_suffix_flags(const SysArgs a, int64_t ga, int64_t gb, uint8_t* fa,
                                                       uint8_t* fb) {
-  const int lane = threadIdx.x & 63;
-  const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), s = blockIdx.y, z = blockIdx.z;
-  if (g >= ga + gb) return;
-  const bool is_a = g < ga;
-  const int64_t grp = is_a ? g : g - ga, c0 = grp * 32;
-  if (is_a && KT * s < tile_kstop(a, z, c0)) return;
+  __shared__ uint32_t bad_g[kSufCols / 32];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t s = blockIdx.y, z = blockIdx.z, xa = (a.M + kSufCols - 1) / kSufCols;
+  const bool is_a = (int64_t)blockIdx.x < xa;
+  const int64_t c0 = (is_a ? (int64_t)blockIdx.x : (int64_t)blockIdx.x - xa) * kSufCols;
+  if (threadIdx.x < kSufCols / 32) bad_g[threadIdx.x] = 0u;
   const Operand& op = is_a ? a.A : a.B;
   const Operand& xo = is_a ? a.XA : a.XB;
   const int64_t L = is_a ? a.M : a.N, K = a.K;
   const float* P = op.p + z * op.batch;
   const float* X = xo.p + z * xo.batch;
-  const int64_t c = c0 + (lane & 31), r0 = KT * s + (lane >> 5);
-  float v[16];
+  const int64_t c = c0 + 4 * lane;                  // this lane's 4 columns, inside one 32-column group
+  const bool needed = c < L && (!is_a || KT * s >= tile_kstop(a, z, c));
+  bool bad = false;
+  if (needed) {
+    const bool vec = vec_ok(op, P) && c + 3 < L;
+    float v[8][4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int64_t r = r0 + 2 * i;
-    v[i] = (r < K && c < L) ? P[r * op.ld + c] : 0.0f;
+    for (int i = 0; i < 8; ++i) {
+      const int64_t r = KT * s + wave * 8 + i;
+      const float* q = P + r * op.ld + c;
+      if (r >= K) {
+        v[i][0] = v[i][1] = v[i][2] = v[i][3] = 0.0f;
+      } else if (vec) {
+        const float4 t = *reinterpret_cast<const float4*>(q);
+        v[i][0] = t.x; v[i][1] = t.y; v[i][2] = t.z; v[i][3] = t.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i][e] = c + e < L ? q[e] : 0.0f;
+      }
+    }
+    uint32_t mx = 0u, mxs = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mx = umax(mx, f2u(v[i][e]) & 0x7FFFFFFFu);
+    if (wave == 0) {
+      const int64_t r_end = (KT * s + KT < K ? KT * s + KT : K) - 1, bs = a.block_size;
+      for (int64_t gg = KT * s / bs; gg <= r_end / bs; ++gg)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (c + e < L) mxs = umax(mxs, f2u(X[gg * xo.ld + c + e]) & 0x7FFFFFFFu);
+    }
+    bad = mxs >= 0x7F800000u || (is_a ? mx != 0u : mx >= 0x7F800000u);
   }
-  uint32_t mx = 0u, mxs = 0u;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) mx = umax(mx, f2u(v[i]) & 0x7FFFFFFFu);
-  const int64_t r_end = (KT * s + KT < K ? KT * s + KT : K) - 1, bs = a.block_size;
-  if (lane < 32 && c < L)
-    for (int64_t gg = KT * s / bs; gg <= r_end / bs; ++gg) mxs = umax(mxs, f2u(X[gg * xo.ld + c]) & 0x7FFFFFFFu);
-  const bool bad = mxs >= 0x7F800000u || (is_a ? mx != 0u : mx >= 0x7F800000u);
-  const bool any = __any(bad);
-  if (lane == 0) (is_a ? fa : fb)[(z * a.stages + s) * (is_a ? ga : gb) + grp] = any ? 1u : 0u;
+  const uint64_t m = __ballot(bad);
+  __syncthreads();   // bad_g cleared
+  if (lane < kSufCols / 32 && ((m >> (8 * lane)) & 0xFFu)) atomicOr(&bad_g[lane], 1u);
+  __syncthreads();
+  if (threadIdx.x < kSufCols / 32) {
+    const int64_t g = c0 / 32 + threadIdx.x;
+    if (g < (is_a ? ga : gb)) (is_a ? fa : fb)[(z * a.stages + s) * (is_a ? ga : gb) + g] = bad_g[threadIdx.x] ? 1u : 0u;
+  }
 }
 
 // The fast kernel's dispatch order under the caller's hints: tiles by descending work (stages to reduce),
@@ -238,22 +290,48 @@ __global__ void __launch_bounds__(256) k_suffix_flags(const SysArgs a, int64_t g
 // k_end's row-dependent work lands unevenly on them too.  Sorted by work, each run of consecutive ids carries
 // about equal work to every engine, heaviest first.  One workgroup: a counting sort over work buckets of one
 // stage (the last bucket holds everything longer), eight tiles per thread per pass so their hint loads overlap.
-constexpr int kOrderThreads = 1024, kOrderPer = 8, kOrderBuckets = 2048;
+constexpr int kOrderThreads = 1024, kOrderPer = 4, kOrderBuckets = 2048;
 
-__device__ __forceinline__ void order_tile(const SysArgs& a, int64_t p, uint32_t& tile, int& bucket) {
-  const int64_t per_z = a.tiles_x * a.tiles_y;
-  const int64_t z = p / per_z, r = p - z * per_z, by = r / a.tiles_x, tx = r - by * a.tiles_x;
-  const int64_t ty = a.tiles_y - 1 - by;
-  tile = (uint32_t)((z * a.tiles_y + ty) * a.tiles_x + tx);
-  if (a.skip && tile_skipped(a, z, ty * a.fbm, tx * a.fbn, a.fbm, a.fbn)) {
-    bucket = 0;
-    return;
-  }
-  const int64_t st = tile_kstop(a, z, ty * a.fbm) / KT;
-  bucket = 1 + (int)(st < kOrderBuckets - 2 ? st : kOrderBuckets - 2);
+// Dispatch position p -> its tile in the grid's own order (rows last first); 32-bit: the host launches the
+// order kernel only while every position fits.
+__device__ __forceinline__ uint32_t grid_tile(const SysArgs& a, uint32_t p, uint32_t& z, uint32_t& ty,
+                                              uint32_t& tx) {
+  const uint32_t nx = (uint32_t)a.tiles_x, ny = (uint32_t)a.tiles_y;
+  const uint32_t zy = p / nx;
+  tx = p - zy * nx;
+  z = zy / ny;
+  ty = ny - 1u - (zy - z * ny);
+  return (z * ny + ty) * nx + tx;
 }
 
-__global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, int64_t total, uint32_t* order) {
+
+// atomicAdd(&cur[b], 1) for every active lane; returns the lane's old value.  The buckets of up to two lanes'
+// (the wave's first active lanes') take one atomic each for every lane holding them: under a skip map most of
+// a wave shares one or two buckets, whose returning atomics would otherwise serialize.  The rest (k_end gives
+// a wave many buckets, each held by few lanes) go one lane at a time.
+__device__ __forceinline__ uint32_t wave_bucket_add(uint32_t* cur, int b, bool active) {
+  const int lane = threadIdx.x & 63;
+  uint64_t todo = __ballot(active);
+  uint32_t pos = 0u;
+  for (int round = 0; round < 2 && todo; ++round) {
+    const int leader = __ffsll((unsigned long long)todo) - 1;
+    const int lb = __shfl(b, leader, 64);
+    const bool mine = ((todo >> lane) & 1ull) && b == lb;
+    const uint64_t same = __ballot(mine);
+    uint32_t base = 0u;
+    if (lane == leader) base = atomicAdd(&cur[lb], (uint32_t)__popcll(same));
+    base = (uint32_t)__shfl((int)base, leader, 64);
+    if (mine) pos = base + (uint32_t)__popcll(same & ((1ull << lane) - 1ull));
+    todo &= ~same;
+  }
+  if ((todo >> lane) & 1ull) pos = atomicAdd(&cur[b], 1u);
+  return pos;
+}
+
+// scratch: one uint32 per position (the fast kernel's flag area, which it rewrites afterwards) keeps each
+// position's bucket between the two passes.
+__global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, uint32_t total, uint32_t* scratch,
+                                                              uint32_t* order) {
   constexpr int PB = kOrderBuckets / kOrderThreads;
   static_assert(PB * kOrderThreads == kOrderBuckets, "whole buckets per thread");
   __shared__ uint32_t cur[kOrderBuckets];
@@ -261,19 +339,45 @@ __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, i
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderThreads) cur[b] = 0u;
   __syncthreads();
-  const int64_t stride = (int64_t)kOrderThreads * kOrderPer;
-  for (int64_t c0 = 0; c0 < total; c0 += stride) {
-    uint32_t tile[kOrderPer];
+  const uint32_t stride = (uint32_t)kOrderThreads * kOrderPer;
+  for (uint32_t c0 = 0; c0 < total; c0 += stride) {
+    // straight-line, positions past the end clamped to the last one, so every tile's hint loads are in
+    // flight together
     int bucket[kOrderPer];
+    bool skipped[kOrderPer];
+    int64_t kst[kOrderPer], zz[kOrderPer], m0[kOrderPer], n0[kOrderPer];
 #pragma unroll
     for (int u = 0; u < kOrderPer; ++u) {
-      const int64_t p = c0 + (int64_t)u * kOrderThreads + threadIdx.x;
-      bucket[u] = -1;
-      if (p < total) order_tile(a, p, tile[u], bucket[u]);
+      const uint32_t p = c0 + (uint32_t)u * kOrderThreads + threadIdx.x;
+      uint32_t z, ty, tx;
+      grid_tile(a, p < total ? p : total - 1u, z, ty, tx);
+      zz[u] = z;
+      m0[u] = (int64_t)ty * a.fbm;
+      n0[u] = (int64_t)tx * a.fbn;
+      skipped[u] = false;
+      kst[u] = a.K / KT;
+    }
+    if (a.skip) {
+      uint32_t v[kOrderPer][4];
+#pragma unroll
+      for (int u = 0; u < kOrderPer; ++u) skip_bytes(a, zz[u], m0[u], n0[u], v[u]);
+#pragma unroll
+      for (int u = 0; u < kOrderPer; ++u) skipped[u] = skip_all(a, m0[u], n0[u], a.fbm, a.fbn, v[u]);
+    }
+    if (a.k_end) {
+#pragma unroll
+      for (int u = 0; u < kOrderPer; ++u) kst[u] = tile_kstop(a, zz[u], m0[u]) / KT;
     }
 #pragma unroll
-    for (int u = 0; u < kOrderPer; ++u)
-      if (bucket[u] >= 0) atomicAdd(&cur[bucket[u]], 1u);
+    for (int u = 0; u < kOrderPer; ++u) {
+      const uint32_t p = c0 + (uint32_t)u * kOrderThreads + threadIdx.x;
+      bucket[u] = p >= total ? -1 : skipped[u] ? 0 : 1 + (int)(kst[u] < kOrderBuckets - 2 ? kst[u] : kOrderBuckets - 2);
+    }
+#pragma unroll
+    for (int u = 0; u < kOrderPer; ++u) {
+      wave_bucket_add(cur, bucket[u], bucket[u] >= 0);
+      if (bucket[u] >= 0) scratch[c0 + (uint32_t)u * kOrderThreads + threadIdx.x] = (uint32_t)bucket[u];
+    }
   }
   __syncthreads();
   // cur[b] <- the first position of bucket b: the count of every bucket above it (heavier work first)
@@ -299,18 +403,20 @@ __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, i
     at += cnt[u];
   }
   __syncthreads();
-  for (int64_t c0 = 0; c0 < total; c0 += stride) {
-    uint32_t tile[kOrderPer];
-    int bucket[kOrderPer];
+  for (uint32_t c0 = 0; c0 < total; c0 += stride) {
+    uint32_t b[kOrderPer];
 #pragma unroll
     for (int u = 0; u < kOrderPer; ++u) {
-      const int64_t p = c0 + (int64_t)u * kOrderThreads + threadIdx.x;
-      bucket[u] = -1;
-      if (p < total) order_tile(a, p, tile[u], bucket[u]);
+      const uint32_t p = c0 + (uint32_t)u * kOrderThreads + threadIdx.x;
+      b[u] = p < total ? scratch[p] : 0u;
     }
 #pragma unroll
-    for (int u = 0; u < kOrderPer; ++u)
-      if (bucket[u] >= 0) order[atomicAdd(&cur[bucket[u]], 1u)] = tile[u];
+    for (int u = 0; u < kOrderPer; ++u) {
+      const uint32_t p = c0 + (uint32_t)u * kOrderThreads + threadIdx.x;
+      const uint32_t at = wave_bucket_add(cur, (int)b[u], p < total);
+      uint32_t z, ty, tx;
+      if (p < total) order[at] = grid_tile(a, p, z, ty, tx);
+    }
   }
 }
 
@@ -582,19 +688,12 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 }
 
 // ------------------------------------------------------------------------------- general datapath
-// only_flagged: compute just the outputs whose fast tile has its flag set (the fast kernel ran first).
+// The BM x BN outputs at (m0, n0) of problem z.
 template <int BM, int BN, int TM, int TN>
-__global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const SysArgs args, int only_flagged) {
-  static_assert(32 % BM == 0 && 32 % BN == 0, "a general tile lies inside one fast tile");
+__device__ __forceinline__ void gen_tile_at(const SysArgs& args, int64_t z, int64_t m0, int64_t n0,
+                                            Smem<BM, BN>& sm) {
   constexpr int NT = (BM / TM) * (BN / TN);
-  const int64_t z = blockIdx.z;
-  if (only_flagged) {
-    const int64_t fy = (int64_t)blockIdx.y * BM / args.fbm, fx = (int64_t)blockIdx.x * BN / args.fbn;
-    if (args.flags[(z * args.tiles_y + fy) * args.tiles_x + fx] == 0u) return;
-  }
-  __shared__ Smem<BM, BN> sm;
   const int tn = threadIdx.x % (BN / TN), tm = threadIdx.x / (BN / TN);
-  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
   const float* A = args.A.p + z * args.A.batch;
   const float* B = args.B.p + z * args.B.batch;
   const float* XA = args.XA.p + z * args.XA.batch;
@@ -689,6 +788,27 @@ __global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const Sy
       if (nn < N) Cz[mm * args.ldc + nn] = C[x][y];
     }
   }
+}
+
+// only_flagged: the grid is the fast kernel's tiles (it ran first); a workgroup whose tile has its flag set
+// computes that tile's BM x BN pieces in turn, the others return at once.  Otherwise one piece per workgroup.
+template <int BM, int BN, int TM, int TN>
+__global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const SysArgs args, int only_flagged) {
+  static_assert(32 % BM == 0 && 32 % BN == 0, "a general tile lies inside one fast tile");
+  __shared__ Smem<BM, BN> sm;
+  const int64_t z = blockIdx.z;
+  if (!only_flagged) {
+    gen_tile_at<BM, BN, TM, TN>(args, z, (int64_t)blockIdx.y * BM, (int64_t)blockIdx.x * BN, sm);
+    return;
+  }
+  if (args.flags[(z * args.tiles_y + blockIdx.y) * args.tiles_x + blockIdx.x] == 0u) return;
+  for (int64_t m0 = (int64_t)blockIdx.y * args.fbm; m0 < (int64_t)(blockIdx.y + 1) * args.fbm && m0 < args.M;
+       m0 += BM)
+    for (int64_t n0 = (int64_t)blockIdx.x * args.fbn; n0 < (int64_t)(blockIdx.x + 1) * args.fbn && n0 < args.N;
+         n0 += BN) {
+      gen_tile_at<BM, BN, TM, TN>(args, z, m0, n0, sm);
+      __syncthreads();   // the next piece restages sm
+    }
 }
 
 // ------------------------------------------------------------------------------------------- host side
@@ -823,6 +943,7 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
   const bool fast_lanes = !force_general && a.K > 0 && lanes_fast(lane_e, lane_m, a.size, ar);
   const dim3 grid_f((unsigned)a.tiles_x, (unsigned)a.tiles_y, (unsigned)count);
   const dim3 grid_g((unsigned)mxq::ceil_div(a.N, 32), (unsigned)mxq::ceil_div(a.M, 32), (unsigned)count);
+  const dim3 grid_gf((unsigned)a.tiles_x, (unsigned)a.tiles_y, (unsigned)count);   // after the fast kernel
   if (fast_lanes) {
     a.fast_prod_max = fast_prod_bound(lane_e, lane_m, a.size);
     // workspace: a flag per 32 x 32 tile (W), the dispatch order (W), the suffix bytes of A's and B's groups
@@ -834,8 +955,8 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
         uint8_t* fa = reinterpret_cast<uint8_t*>(a.flags + 2 * W);
         uint8_t* fb = fa + count * stages * ga;
         a.stages = stages;
-        k_suffix_flags<<<dim3((unsigned)mxq::ceil_div(ga + gb, 4), (unsigned)stages, (unsigned)count), 256, 0,
-                         st>>>(a, ga, gb, fa, fb);
+        const int64_t blocks = mxq::ceil_div(a.M, kSufCols) + mxq::ceil_div(a.N, kSufCols);
+        k_suffix_flags<<<dim3((unsigned)blocks, (unsigned)stages, (unsigned)count), 256, 0, st>>>(a, ga, gb, fa, fb);
         a.suf_a = fa;
         a.suf_b = fb;
       } else {
@@ -844,7 +965,7 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
     }
     if ((a.skip || a.k_end) && total <= (int64_t)0xFFFFFFFFu) {
       uint32_t* order = a.flags + W;
-      k_tile_order<<<1, kOrderThreads, 0, st>>>(a, total, order);
+      k_tile_order<<<1, kOrderThreads, 0, st>>>(a, (uint32_t)total, a.flags, order);
       a.order = order;
     }
     {
@@ -854,7 +975,7 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
     }
     if (int rc = mxq::check_launch("mxq_systolic fast")) return rc;
     mxq::KernelTimer timer("systolic_general", st);
-    k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a, 1);
+    k_systolic_gen<32, 32, 2, 2><<<grid_gf, 256, 0, st>>>(a, 1);
   } else {
     mxq::KernelTimer timer("systolic_general", st);
     k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a, 0);

@@ -260,8 +260,9 @@ def test_batched_matches_single(cuda, sched_name):
 def test_all_fast_tile_shapes(cuda):
     """The fast kernel's three tiles: 2048 x 4096 outputs run on 64 x 64 tiles, 1024 x 4096 on 32 x 64 and
     500 x 4000 on 32 x 32 (too few larger tiles to give every CU 8 workgroups), with HW_FINAL's instance and a
-    generic ladder: every output equal to the general kernel's, edge column slices equal to the oracle's
-    (columns are independent chains)."""
+    generic ladder, two columns of A past the fast kernel's bound (their tiles, one a tail, are computed by the
+    general kernel): every output equal to the general kernel's alone, edge column slices equal to the
+    oracle's (columns are independent chains)."""
     from mxq import matmul
     rng = np.random.default_rng(8)
     ladder = [(4, 4)] * 6 + [(4, 5)] * 6 + [(4, 7)] * 3 + [(8, 7)]
@@ -270,6 +271,9 @@ def test_all_fast_tile_shapes(cuda):
         K = 64
         P_A, X_A = _codes(rng, K, M)
         P_B, X_B = _codes(rng, K, N, scale=0.1)
+        for r, c in ((5, 70), (9, M - 3)):                 # products past the fast bound: these tiles, and a
+            P_A[r, c] = 448.0                              # tail tile, go to the general kernel
+            X_A[0, c] = np.float32(2.0 ** 20)
         ops = [t(x) for x in (P_A, X_A, P_B, X_B)]
         for sched in (HW_FINAL, ladder):
             Y = matmul.systolic(*ops, matmul.MXGEMMINI(), sched)
