@@ -4,6 +4,7 @@ matrix-core comparison product, each next to its roofline, and the oracle's CPU 
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
     python bench.py --copy-calibration        # only a 256 MiB device copy, 5 times (counter calibration)
+    python bench.py --only LINE               # one extra line alone: quantize, lut, attend, mfma, trees, llm
 
 A step is one systolic call over the benchmark workload (A = x^T with x 512 x 4096 ~ N(0,1), B = W^T with
 W 4096 x 4096 ~ N(0, 0.02), both block.mxgemmini MXFP8_E4M3 codes along K: M = 512, N = 4096, K = 4096),
@@ -196,6 +197,35 @@ def attend_line(torch, steps):
             "ms": round(ms, 3), "emulated_TOPs": round(2 * macs / ms / 1e9, 3)}
 
 
+def llm_line(torch, steps):
+    """experiments.llm_ppl's loss on a TinyLlama-1.1B-shaped Llama (22 layers, hidden 2048, MLP 5632, 32 heads,
+    4 KV heads, vocab 32000), random-init in bf16, patched with the hw_mxfp8_tapeout rules (every MLP Linear
+    and lm_head through the systolic Scheme), one window of 2048 synthetic tokens.  Opt-in (--only llm)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from experiments import llm_ppl, recipes
+    from mxq.nn import patch
+    dev = torch.device("cuda", 0)
+    s = torch.cuda.current_stream(dev)
+    cfg = LlamaConfig(vocab_size=32000, hidden_size=2048, intermediate_size=5632, num_hidden_layers=22,
+                      num_attention_heads=32, num_key_value_heads=4, max_position_embeddings=2048)
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = LlamaForCausalLM(cfg).to(torch.bfloat16).eval()
+    ids = torch.randint(0, 32000, (2048,), generator=torch.Generator().manual_seed(1))
+    llm_ppl.sample_nll(model, ids)                                            # warm-up (library handles)
+    base_ms = _events_ms(lambda: llm_ppl.sample_nll(model, ids), steps, s)
+    handle = patch(model, recipes.RULES["hw_mxfp8_tapeout"])
+    nll, n = llm_ppl.sample_nll(model, ids)                                   # also caches the weight codes
+    ms = _events_ms(lambda: llm_ppl.sample_nll(model, ids), steps, s)
+    macs = sum(2048 * k * m for _, k, m, _, scheme in handle.table if scheme)
+    return {"workload": "experiments.llm_ppl sample_nll, TinyLlama-1.1B-shaped random bf16 Llama, hw_mxfp8_tapeout "
+                        "(MLP + lm_head), 2048 tokens",
+            "ms": round(ms, 1), "tokens_per_s": round(2048 / ms * 1e3, 1), "bf16_unpatched_ms": round(base_ms, 1),
+            "emulated_macs": macs, "emulated_TOPs_incl_rest": round(2 * macs / ms / 1e9, 3),
+            "nll_per_token": round(nll / n, 4)}
+
+
 def trees_line(torch, steps, P_A, X_A, P_B, X_B):
     """The other two reducers on the benchmark's own codes (M = 512, N = 4096, K = 4096), MXGEMMINI, size 16:
     matmul.adder_tree with bf16 at every level and with the README's ladder [(4, 4), (4, 5), (4, 6), (8, 7)],
@@ -264,7 +294,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the systolic line (no quantize, LUT, attend)")
     ap.add_argument("--copy-calibration", action="store_true", help="run only the counter-calibration copy")
-    ap.add_argument("--only", choices=("quantize", "lut", "attend", "mfma", "trees"),
+    ap.add_argument("--only", choices=("quantize", "lut", "attend", "mfma", "trees", "llm"),
                     help="run one extra line alone (for profiling) and print it; not the benchmark line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -280,9 +310,10 @@ def main():
     import mxq  # noqa: F401
     from mxq import block, matmul
     dev = torch.device("cuda", 0)
-    if args.only in ("quantize", "lut", "attend"):
+    if args.only in ("quantize", "lut", "attend", "llm"):
         fn = {"quantize": lambda: quantize_lines(torch, max(5, args.steps // 2)),
-              "lut": lambda: lut_line(torch, 3), "attend": lambda: attend_line(torch, 3)}[args.only]
+              "lut": lambda: lut_line(torch, 3), "attend": lambda: attend_line(torch, 3),
+              "llm": lambda: llm_line(torch, 2)}[args.only]
         print(json.dumps({"only": args.only, args.only: fn()}), flush=True)
         return
     M, N, K = 512, 4096, 4096
