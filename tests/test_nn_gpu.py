@@ -205,3 +205,38 @@ def test_attend_batched_pairwise_fallback(cuda):
     got = mxq.nn.attend(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), D ** -0.5, hw, hw).cpu().numpy()
     want = oatt.attend(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), D ** -0.5, hwo, hwo, _gpu_softmax)
     assert_bits_equal(got, want, "pairwise fallback")
+
+
+@pytest.mark.parametrize("kind", ["causal_min", "causal_weak", "window"])
+def test_attend_skip_hints(cuda, monkeypatch, kind):
+    """The batched path's skip hints (32 x 32 score groups whose mask absorbs every score the call can make):
+    every output bit for bit against the oracle; the absorbing causal mask (finfo.min) and a sliding window of
+    96 keys mark groups, a causal mask of -30 (which scores can outweigh) marks none."""
+    import mxq
+    from mxq.nn import _attention as at
+    B, H, Hkv, T, D = 1, 2, 2, 256, 64
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(B, h, T, D, generator=g) for h in (H, Hkv, Hkv))
+    i, j = torch.arange(T)[:, None], torch.arange(T)[None, :]
+    low = torch.finfo(torch.float32).min
+    if kind == "causal_min":
+        mask = _causal(B, T, T)
+    elif kind == "causal_weak":
+        mask = torch.where(j > i, -30.0, 0.0)[None, None]
+    else:
+        mask = torch.where((j > i) | (j < i - 96), low, 0.0)[None, None]
+    marked = []
+    orig = at._hints
+
+    def spy(*a, **kw):
+        skip, k_end = orig(*a, **kw)
+        marked.append(0 if skip is None else int(skip.sum()))
+        return skip, k_end
+
+    monkeypatch.setattr(at, "_hints", spy)
+    hw, hwo = _hw(mxq), _hw_oracle()
+    got = mxq.nn.attend(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), D ** -0.5, hw, hw).cpu().numpy()
+    want = oatt.attend(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), D ** -0.5, hwo, hwo, _gpu_softmax)
+    assert_bits_equal(got, want, f"attend with {kind} mask")
+    assert marked, "the batched path ran"
+    assert (sum(marked) == 0) if kind == "causal_weak" else (sum(marked) > 0), marked
