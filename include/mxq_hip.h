@@ -164,16 +164,31 @@ typedef struct mxq_systolic_hints {
   const int32_t* k_end;
 } mxq_systolic_hints;
 
+/* An elementwise step mxq_systolic_batched applies to every output as it is stored (no counterpart in the
+ * reference as a fused step: it is attention's score step, mxq/nn/_attention.py:128-135, done where the scores
+ * are written instead of in a pass of its own).  Output (r, c) of problem z becomes R(R(C * scale) + mask value)
+ * in float32, R the identity (bf16 == 0) or bf16 RNE (bf16 != 0); without a mask, R(C * scale).  The mask value
+ * is mask[b * mask_b_stride + (r % m) * mask_row_stride + c] with b = (z0 + z) / z_per_b - z0 / z_per_b.  Tiles
+ * the skip hint marks take C = +0.  The same step as mxq_scores_scale_mask, bit for bit. */
+typedef struct mxq_systolic_epilogue {
+  float scale;
+  int32_t bf16;
+  const float* mask;
+  int64_t mask_b_stride, mask_row_stride;
+  int64_t z0, z_per_b, m;
+} mxq_systolic_epilogue;
+
 /* `count` independent systolic problems of one shape in one launch, operands addressed through `layout` (any
  * column slice of a larger matrix, any spacing of the problems).  Each problem's result is bit-identical to
- * mxq_systolic on that problem alone.  workspace: mxq_systolic_workspace(K, M, N, count) uint32.  The reference
+ * mxq_systolic on that problem alone (then `epilogue`, when not NULL).  workspace: mxq_systolic_workspace(K, M,
+ * N, count) uint32.  The reference
  * calls matmul.systolic once per problem (mxq/nn/_attention.py:108-141, once per head and query chunk);
  * this is that loop as one launch. */
 int mxq_systolic_batched(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C,
                          const mxq_systolic_layout* layout, int64_t count, int64_t K, int64_t M, int64_t N,
                          const int32_t* lane_e, const int32_t* lane_m, int32_t size, int32_t block_size,
-                         const mxq_arith_spec* arith, const mxq_systolic_hints* hints, uint32_t* workspace,
-                         int32_t force_general,
+                         const mxq_arith_spec* arith, const mxq_systolic_hints* hints,
+                         const mxq_systolic_epilogue* epilogue, uint32_t* workspace, int32_t force_general,
                          mxq_stream_t stream);
 
 /* uint32 elements of workspace mxq_systolic / mxq_systolic_batched need for `count` problems of K x M codes A

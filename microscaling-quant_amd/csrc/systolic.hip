@@ -75,7 +75,23 @@ struct SysArgs {
   const uint8_t* suf_a;
   const uint8_t* suf_b;
   int64_t stages;
+  int epi_on;                 // apply `epi` to every output as it is stored
+  mxq_systolic_epilogue epi;
 };
+
+// The caller's epilogue on output (r, c) of problem z: R(R(v * scale) + mask value), R = bf16 RNE or identity.
+__device__ __forceinline__ float epilogue(const SysArgs& a, int64_t z, int64_t r, int64_t c, float v) {
+  if (!a.epi_on) return v;
+  const mxq_systolic_epilogue& e = a.epi;
+  v = v * e.scale;
+  if (e.bf16) v = bf16_rne(v);
+  if (e.mask) {
+    const int64_t b = (e.z0 + z) / e.z_per_b - e.z0 / e.z_per_b;
+    v = v + e.mask[b * e.mask_b_stride + (r % e.m) * e.mask_row_stride + c];
+    if (e.bf16) v = bf16_rne(v);
+  }
+  return v;
+}
 
 // ---------------------------------------------------------------------------------- fast datapath
 // Per-lane constants of the fast kernel, built on the host from the schedule (see make_fast_lanes).
@@ -173,7 +189,7 @@ __device__ __forceinline__ void write_tile(const SysArgs& a, int64_t z, int64_t 
     if (mr + x >= a.M) continue;
 #pragma unroll
     for (int y = 0; y < TN; ++y)
-      if (nc + y < a.N) Cz[(mr + x) * a.ldc + nc + y] = C[x][y];
+      if (nc + y < a.N) Cz[(mr + x) * a.ldc + nc + y] = epilogue(a, z, mr + x, nc + y, C[x][y]);
   }
 }
 
@@ -785,7 +801,7 @@ __device__ __forceinline__ void gen_tile_at(const SysArgs& args, int64_t z, int6
 #pragma unroll
     for (int y = 0; y < TN; ++y) {
       const int64_t nn = n0 + tn * TN + y;
-      if (nn < N) Cz[mm * args.ldc + nn] = C[x][y];
+      if (nn < N) Cz[mm * args.ldc + nn] = epilogue(args, z, mm, nn, C[x][y]);
     }
   }
 }
@@ -1017,8 +1033,8 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
                                     float* C, const mxq_systolic_layout* layout, int64_t count, int64_t K,
                                     int64_t M, int64_t N, const int32_t* lane_e, const int32_t* lane_m, int32_t size,
                                     int32_t block_size, const mxq_arith_spec* arith,
-                                    const mxq_systolic_hints* hints, uint32_t* workspace, int32_t force_general,
-                                    mxq_stream_t stream) {
+                                    const mxq_systolic_hints* hints, const mxq_systolic_epilogue* epilogue,
+                                    uint32_t* workspace, int32_t force_general, mxq_stream_t stream) {
   if (int rc = check_common(K, M, N, count, lane_e, lane_m, size, block_size, arith)) return rc;
   if (!layout) return mxq::invalid("mxq_systolic_batched: NULL layout");
   const mxq_systolic_layout& L = *layout;
@@ -1028,6 +1044,8 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
     return mxq::invalid("mxq_systolic_batched: negative batch stride");
   if (count > 1 && M > 0 && N > 0 && L.batch_c < (M - 1) * L.ld_c + N)
     return mxq::invalid("mxq_systolic_batched: outputs of two problems overlap");
+  if (epilogue && (epilogue->m < 1 || epilogue->z_per_b < 1 || epilogue->z0 < 0))
+    return mxq::invalid("mxq_systolic_batched: epilogue needs m >= 1, z_per_b >= 1, z0 >= 0");
   if (M == 0 || N == 0 || count == 0) return MXQ_OK;
   if (!P_A || !X_A || !P_B || !X_B || !C || !workspace) return mxq::invalid("mxq_systolic_batched: NULL pointer");
   SysArgs a{};
@@ -1041,6 +1059,10 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
     a.skip_cols = mxq::ceil_div(N, 32);
     a.k_end = hints->k_end;
     a.kend_groups = mxq::ceil_div(M, 64);
+  }
+  if (epilogue) {
+    a.epi_on = 1;
+    a.epi = *epilogue;
   }
   return run_systolic(a, lane_e, lane_m, count, force_general, mxq::as_stream(stream));
 }

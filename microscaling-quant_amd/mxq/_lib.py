@@ -43,6 +43,13 @@ class SystolicHints(ctypes.Structure):
     _fields_ = [("skip", c_ptr), ("k_end", c_ptr)]
 
 
+class SystolicEpilogue(ctypes.Structure):
+    """include/mxq_hip.h mxq_systolic_epilogue: R(R(C * scale) + mask value) on every stored output."""
+    _fields_ = [("scale", ctypes.c_float), ("bf16", ctypes.c_int32), ("mask", c_ptr),
+                ("mask_b_stride", ctypes.c_int64), ("mask_row_stride", ctypes.c_int64), ("z0", ctypes.c_int64),
+                ("z_per_b", ctypes.c_int64), ("m", ctypes.c_int64)]
+
+
 class SystolicLayout(ctypes.Structure):
     """mxq_systolic_layout (include/mxq_hip.h): row and problem strides of the five operands, in elements."""
     _fields_ = [(n, c_i64) for n in ("ld_a", "batch_a", "ld_xa", "batch_xa", "ld_b", "batch_b", "ld_xb", "batch_xb",
@@ -76,7 +83,7 @@ SIGNATURES = {
                              ctypes.POINTER(ArithSpec), c_ptr, c_i32, c_ptr]),
     "mxq_systolic_batched": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, ctypes.POINTER(SystolicLayout), c_i64,
                                      c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32, ctypes.POINTER(ArithSpec),
-                                     c_ptr, c_ptr, c_i32, c_ptr]),
+                                     c_ptr, c_ptr, c_ptr, c_i32, c_ptr]),
     "mxq_systolic_workspace": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
     "mxq_scores_scale_mask": (c_i32, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64, c_i64, c_i64, c_i64,
                                       c_i32, c_ptr]),

@@ -73,14 +73,15 @@ def workspace_elements(K: int, M: int, N: int, count: int) -> int:
 def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: int, N: int, C: torch.Tensor,
                      arith: Arithmetic, schedule: Sequence[Tuple[int, int]], size: int = 16,
                      block_size: int = BLOCK, *, skip: Optional[torch.Tensor] = None,
-                     k_end: Optional[torch.Tensor] = None) -> None:
+                     k_end: Optional[torch.Tensor] = None, epilogue: Optional["_lib.SystolicEpilogue"] = None) -> None:
     """`count` problems of one shape in one launch, written into C (mxq_systolic_batched).  ops: the four
     device tensors the layout's strides address (codes A, scales X_A, codes B, scales X_B), float32 on C's
     device.  Each problem's result equals systolic() on that problem alone.  The Arithmetic must carry a
     kernel description (MXGEMMINI, MXQUANT, compiled).
     Hints (include/mxq_hip.h mxq_systolic_hints): `skip`, uint8 count x ceil(M/32) x ceil(N/32), nonzero where
     the caller does not need C's 32 x 32 group (such tiles come back +0); `k_end`, int32 count x ceil(M/64), a
-    bound on the rows of A holding nonzero codes in each 64-column group (checked: a wrong one costs time)."""
+    bound on the rows of A holding nonzero codes in each 64-column group (checked: a wrong one costs time).
+    `epilogue` (mxq_systolic_epilogue): R(R(C * scale) + mask value) applied to every output as it is stored."""
     import ctypes
     kernel = getattr(arith, "kernel", None)
     if kernel is None or size > 64 or 32 % size != 0 or block_size % size != 0:
@@ -103,8 +104,8 @@ def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: 
     work = torch.empty(workspace_elements(K, M, N, count), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_systolic_batched", *(_lib.ptr(t) for t in ops), _lib.ptr(C), ctypes.byref(layout), count,
-                 K, M, N, le, lm, size, block_size, kernel.ctype(), ctypes.byref(hints), _lib.ptr(work), 0,
-                 _lib.stream(dev))
+                 K, M, N, le, lm, size, block_size, kernel.ctype(), ctypes.byref(hints),
+                 None if epilogue is None else ctypes.byref(epilogue), _lib.ptr(work), 0, _lib.stream(dev))
 
 
 def _reference_loop(P_A, X_A, P_B, X_B, arith, schedule, size, block_size, K, M, N):

@@ -346,12 +346,15 @@ class _Batched:
             skip, k_end = _hints(a_amax, k_amax, z0, Zc, scale, bias, Hkv, s0, m, cols, Tk)
         arith, sched, size = self.qk_red
         S = torch.empty(Zc, cols, Tk, dtype=torch.float32, device=qg.device)
+        # the score step r(r(S * scale) + mask row) is applied as the scores are stored (_scale_mask's step)
+        mask, b_stride, r_stride = (None, 0, 0) if bias is None else _mask_rows(bias, z0, Hkv, s0)
+        epi = _lib.SystolicEpilogue(scale=float(scale), bf16=int(vector == "bf16"), mask=_lib.ptr(mask),
+                                    mask_b_stride=b_stride, mask_row_stride=r_stride, z0=z0, z_per_b=Hkv, m=m)
         systolic_batched((A_P, A_X, KT_P[:, z0 * Tk:], KT_X[:, z0 * Tk:]),
                          _lib.SystolicLayout(ld_a=Zc * cols, batch_a=cols, ld_xa=Zc * cols, batch_xa=cols,
                                              ld_b=KT_P.shape[1], batch_b=Tk, ld_xb=KT_X.shape[1], batch_xb=Tk,
                                              ld_c=Tk, batch_c=cols * Tk),
-                         Zc, D, cols, Tk, S, arith, sched, size, qk.block_size, skip=skip)
-        _scale_mask(S, bias, scale, vector, n, m, z0, Hkv, s0)
+                         Zc, D, cols, Tk, S, arith, sched, size, qk.block_size, skip=skip, epilogue=epi)
         P = softmax(S, vector)
         # every call's P^T side by side, quantized from P as it lies (a transposed view: no copy)
         PT_P, PT_X = pv.a(P.contiguous().view(Zc * cols, Tk).t())

@@ -389,3 +389,42 @@ def test_k_end_nonfinite_past_the_end(cuda):
     want, got = outs
     assert np.isnan(want[0, :, 3]).all() and np.isnan(want[1, 10, :]).all() and np.isnan(want[2, :, 60]).all()
     assert_bits_equal(got, want, "k_end with non-finite values past it")
+
+
+@pytest.mark.parametrize("bf16", [0, 1])
+@pytest.mark.parametrize("masked", [True, False])
+def test_batched_epilogue(cuda, bf16, masked):
+    """The score step fused into the stores (mxq_systolic_epilogue) equals the batched run followed by the
+    step's own kernel (mxq_scores_scale_mask) bit for bit: six problems, two per mask batch row from the second
+    on, rows s0.. of the mask, a problem whose tiles go to the general kernel, and a skip map."""
+    from mxq import _lib, matmul
+    from mxq.matmul._systolic import systolic_batched
+    from mxq.nn._attention import _mask_rows, _scale_mask
+    rng = np.random.default_rng(17 + bf16)
+    count, K, n, m, N, z0, Hkv, s0 = 6, 64, 2, 48, 200, 2, 2, 5
+    M = n * m
+    P_A, X_A = _codes(rng, K, count * M, scale=2.0)
+    P_B, X_B = _codes(rng, K, count * N)
+    P_A[3, 4 * M + 7] = 448.0                                        # problem 4: the general kernel's tiles
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()    # noqa: E731
+    ops = (t(P_A), t(X_A), t(P_B), t(X_B))
+    lay = _lib.SystolicLayout(ld_a=count * M, batch_a=M, ld_xa=count * M, batch_xa=M,
+                              ld_b=count * N, batch_b=N, ld_xb=count * N, batch_xb=N, ld_c=N, batch_c=M * N)
+    bias = None
+    if masked:
+        bias = torch.from_numpy(rng.standard_normal((4, s0 + m, N)).astype(np.float32) * 3)
+        bias[:, :, N // 2:] = torch.finfo(torch.float32).min
+        bias = bias.cuda()
+    skip = torch.zeros((count, -(-M // 32), -(-N // 32)), dtype=torch.uint8, device="cuda")
+    skip[:, :, 4:] = 1
+    scale = 0.088388
+    ar = matmul.MXGEMMINI()
+    want = torch.empty((count, M, N), device="cuda")
+    systolic_batched(ops, lay, count, K, M, N, want, ar, HW_FINAL, skip=skip)
+    _scale_mask(want, bias, scale, "bf16" if bf16 else None, n, m, z0, Hkv, s0)
+    mask, bs_, rs_ = (None, 0, 0) if bias is None else _mask_rows(bias, z0, Hkv, s0)
+    epi = _lib.SystolicEpilogue(scale=scale, bf16=bf16, mask=_lib.ptr(mask), mask_b_stride=bs_,
+                                mask_row_stride=rs_, z0=z0, z_per_b=Hkv, m=m)
+    got = torch.full((count, M, N), float("nan"), device="cuda")
+    systolic_batched(ops, lay, count, K, M, N, got, ar, HW_FINAL, skip=skip, epilogue=epi)
+    assert_bits_equal(got.cpu().numpy(), want.cpu().numpy(), f"epilogue bf16={bf16} masked={masked}")
