@@ -119,7 +119,7 @@ def test_transposed_view_layout(cuda, dtype):
                   (block.mxquant.quantize, lambda V, f: ob.mxquant_quantize(V, f, 0, 32), {}),
                   (block.ocp.quantize, lambda V, f: ob.ocp_quantize(V, f, 0, 32, "nearest", 8, "top"),
                    dict(rounding_mode="nearest"))]
-    for n, inner in [(2048, 256), (100, 70), (33, 130), (64, 3), (7, 65)]:
+    for n, inner in [(2048, 256), (192, 128), (100, 70), (33, 130), (64, 3), (7, 65)]:
         M = torch.from_numpy(_edge_matrix(rng, inner, n, scale=float(np.exp2(rng.integers(-10, 10))))).to(dtype)
         V32 = M.to(torch.float32).numpy().T.copy()
         Md = M.cuda()
