@@ -55,3 +55,29 @@ def test_structs_match_header():
         ctypes_of = {"int32_t": ctypes.c_int32, "float": ctypes.c_float, "double": ctypes.c_double,
                      "int64_t": ctypes.c_int64}
         assert [(n, ctypes_of[t]) for t, n in fields] == [(n, t) for n, t in py._fields_], struct
+
+
+def test_struct_offsets_match_header(tmp_path):
+    """Field offsets and sizes of every struct the host side passes, ctypes against the header compiled by gcc
+    (pointer fields included)."""
+    import subprocess
+
+    from mxq import _lib
+    structs = {"mxq_block_spec": _lib.BlockSpec, "mxq_arith_spec": _lib.ArithSpec,
+               "mxq_systolic_layout": _lib.SystolicLayout, "mxq_systolic_hints": _lib.SystolicHints,
+               "mxq_systolic_epilogue": _lib.SystolicEpilogue}
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "mxq_hip.h"', "int main(void) {"]
+    for name, py in structs.items():
+        lines.append(f'  printf("{name} size %zu\\n", sizeof({name}));')
+        for f, _ in py._fields_:
+            lines.append(f'  printf("{name} {f} %zu\\n", offsetof({name}, {f}));')
+    lines.append("  return 0;\n}")
+    src, exe = tmp_path / "offsets.c", tmp_path / "offsets"
+    src.write_text("\n".join(lines))
+    subprocess.run(["gcc", "-I", os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                                 check=True).stdout.splitlines())
+    for name, py in structs.items():
+        assert int(got[f"{name} size"]) == ctypes.sizeof(py), name
+        for f, _ in py._fields_:
+            assert int(got[f"{name} {f}"]) == getattr(py, f).offset, f"{name}.{f}"

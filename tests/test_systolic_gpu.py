@@ -428,3 +428,27 @@ def test_batched_epilogue(cuda, bf16, masked):
     got = torch.full((count, M, N), float("nan"), device="cuda")
     systolic_batched(ops, lay, count, K, M, N, got, ar, HW_FINAL, skip=skip, epilogue=epi)
     assert_bits_equal(got.cpu().numpy(), want.cpu().numpy(), f"epilogue bf16={bf16} masked={masked}")
+
+
+def test_batched_hint_and_epilogue_errors(cuda):
+    """A hint of the wrong shape or type, and an epilogue with m < 1, are refused before any launch."""
+    from mxq import _lib, matmul
+    from mxq.matmul._systolic import systolic_batched
+    rng = np.random.default_rng(1)
+    P_A, X_A = _codes(rng, 64, 2 * 40)
+    P_B, X_B = _codes(rng, 64, 2 * 50)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()    # noqa: E731
+    ops = (t(P_A), t(X_A), t(P_B), t(X_B))
+    lay = _lib.SystolicLayout(ld_a=80, batch_a=40, ld_xa=80, batch_xa=40, ld_b=100, batch_b=50, ld_xb=100,
+                              batch_xb=50, ld_c=50, batch_c=2000)
+    C = torch.empty((2, 40, 50), device="cuda")
+    ar = matmul.MXGEMMINI()
+    with pytest.raises(ValueError, match="hint must be a contiguous"):
+        systolic_batched(ops, lay, 2, 64, 40, 50, C, ar, HW_FINAL,
+                         skip=torch.zeros((2, 2, 1), dtype=torch.uint8, device="cuda"))
+    with pytest.raises(ValueError, match="hint must be a contiguous"):
+        systolic_batched(ops, lay, 2, 64, 40, 50, C, ar, HW_FINAL,
+                         k_end=torch.zeros((2, 1), dtype=torch.int64, device="cuda"))
+    with pytest.raises(Exception, match="epilogue needs m >= 1"):
+        systolic_batched(ops, lay, 2, 64, 40, 50, C, ar, HW_FINAL,
+                         epilogue=_lib.SystolicEpilogue(scale=1.0, m=0, z_per_b=1))
