@@ -127,6 +127,28 @@ __global__ void __launch_bounds__(256) k_group_amax(const float* __restrict__ P,
 // Tk <= block sets both.  The mask row of query j of call z as in k_scores_scale_mask.
 constexpr int WROWS = 64;
 
+// Thread 0 gets the masked-key bound of call z: slack_scale * the float64 sum over d, in d order, of
+// amax_a[d * lda + z] * amax_k[d * ldk + z], at least the smallest normal float32 (a NaN stays NaN).  The whole
+// workgroup loads and multiplies 256 terms at a time into `terms`; thread 0 adds them in order.  Every thread
+// of the workgroup must call it.
+__device__ double call_bound(const double* __restrict__ amax_a, int64_t lda, const double* __restrict__ amax_k,
+                             int64_t ldk, int64_t D, int64_t z, double slack_scale, double* terms) {
+  double sum = 0.0;
+  for (int64_t d0 = 0; d0 < D; d0 += 256) {
+    const int64_t d = d0 + threadIdx.x;
+    if (d < D) terms[threadIdx.x] = amax_a[d * lda + z] * amax_k[d * ldk + z];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int64_t n = D - d0 < 256 ? D - d0 : 256;
+      for (int64_t e = 0; e < n; ++e) sum += terms[e];
+    }
+    __syncthreads();
+  }
+  double bound = slack_scale * sum;
+  if (bound < 1.1754943508222875e-38) bound = 1.1754943508222875e-38;
+  return bound;
+}
+
 __global__ void __launch_bounds__(256) k_attend_windows(const double* __restrict__ amax_a, int64_t lda,
                                                         const double* __restrict__ amax_k, int64_t ldk, int64_t D,
                                                         double slack_scale, const float* __restrict__ mask,
@@ -139,13 +161,9 @@ __global__ void __launch_bounds__(256) k_attend_windows(const double* __restrict
     if (threadIdx.x == 0 && chunk == 0) atomicOr(flags + z, 3);
     return;
   }
-  if (threadIdx.x == 0) {
-    double sum = 0.0;
-    for (int64_t d = 0; d < D; ++d) sum += amax_a[d * lda + z] * amax_k[d * ldk + z];
-    double bound = slack_scale * sum;
-    if (bound < 1.1754943508222875e-38) bound = 1.1754943508222875e-38;     // NaN stays NaN
-    b32 = (float)bound;
-  }
+  __shared__ double terms[256];
+  const double bound = call_bound(amax_a, lda, amax_k, ldk, D, z, slack_scale, terms);
+  if (threadIdx.x == 0) b32 = (float)bound;
   __syncthreads();
   const float bnd = b32;
   const float* rows = mask + ((z0 + z) / z_per_b - z0 / z_per_b) * mask_b_stride;
@@ -194,11 +212,9 @@ __global__ void __launch_bounds__(256) k_attend_hints(const double* __restrict__
   __shared__ float b2;
   __shared__ int last;
   const int64_t t = blockIdx.x, z = blockIdx.y;
+  __shared__ double terms[256];
+  const double bound = call_bound(amax_a, lda, amax_k, ldk, D, z, slack_scale, terms);
   if (threadIdx.x == 0) {
-    double sum = 0.0;
-    for (int64_t d = 0; d < D; ++d) sum += amax_a[d * lda + z] * amax_k[d * ldk + z];
-    double bound = slack_scale * sum;
-    if (bound < 1.1754943508222875e-38) bound = 1.1754943508222875e-38;     // NaN stays NaN
     b2 = (float)(2.0 * bound);
     last = -1;
   }
