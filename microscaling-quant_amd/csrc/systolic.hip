@@ -79,15 +79,21 @@ struct SysArgs {
   mxq_systolic_epilogue epi;
 };
 
-// The caller's epilogue on output (r, c) of problem z: R(R(v * scale) + mask value), R = bf16 RNE or identity.
-__device__ __forceinline__ float epilogue(const SysArgs& a, int64_t z, int64_t r, int64_t c, float v) {
-  if (!a.epi_on) return v;
+// The caller's epilogue, per output row: the mask row of output row r of problem z (NULL without a mask), then
+// R(R(v * scale) + row[c]) per output, R = bf16 RNE or identity.  Rows and m fit 32 bits (M / 32 <= 65535).
+__device__ __forceinline__ const float* epi_row(const SysArgs& a, int64_t z, int64_t r) {
+  const mxq_systolic_epilogue& e = a.epi;
+  if (!e.mask) return nullptr;
+  const int64_t b = (e.z0 + z) / e.z_per_b - e.z0 / e.z_per_b;
+  return e.mask + b * e.mask_b_stride + (int64_t)((uint32_t)r % (uint32_t)e.m) * e.mask_row_stride;
+}
+
+__device__ __forceinline__ float epi_apply(const SysArgs& a, const float* row, int64_t c, float v) {
   const mxq_systolic_epilogue& e = a.epi;
   v = v * e.scale;
   if (e.bf16) v = bf16_rne(v);
-  if (e.mask) {
-    const int64_t b = (e.z0 + z) / e.z_per_b - e.z0 / e.z_per_b;
-    v = v + e.mask[b * e.mask_b_stride + (r % e.m) * e.mask_row_stride + c];
+  if (row) {
+    v = v + row[c];
     if (e.bf16) v = bf16_rne(v);
   }
   return v;
@@ -187,9 +193,16 @@ __device__ __forceinline__ void write_tile(const SysArgs& a, int64_t z, int64_t 
 #pragma unroll
   for (int x = 0; x < TM; ++x) {
     if (mr + x >= a.M) continue;
+    if (a.epi_on) {
+      const float* row = epi_row(a, z, mr + x);
 #pragma unroll
-    for (int y = 0; y < TN; ++y)
-      if (nc + y < a.N) Cz[(mr + x) * a.ldc + nc + y] = epilogue(a, z, mr + x, nc + y, C[x][y]);
+      for (int y = 0; y < TN; ++y)
+        if (nc + y < a.N) Cz[(mr + x) * a.ldc + nc + y] = epi_apply(a, row, nc + y, C[x][y]);
+    } else {
+#pragma unroll
+      for (int y = 0; y < TN; ++y)
+        if (nc + y < a.N) Cz[(mr + x) * a.ldc + nc + y] = C[x][y];
+    }
   }
 }
 
@@ -304,9 +317,9 @@ __global__ void __launch_bounds__(256) k_suffix_flags(const SysArgs a, int64_t g
 // ids rise, and a later one waits for an earlier one's slot.  In the grid's own order a causal triangle gives
 // the engines owning the low tile columns a whole row's work (skipping half the tiles then saves little), and
 // k_end's row-dependent work lands unevenly on them too.  Sorted by work, each run of consecutive ids carries
-// about equal work to every engine, heaviest first.  One workgroup: a counting sort over work buckets of one
-// stage (the last bucket holds everything longer), eight tiles per thread per pass so their hint loads overlap.
-constexpr int kOrderThreads = 1024, kOrderPer = 4, kOrderBuckets = 2048;
+// about equal work to every engine, heaviest first.  Two launches: k_tile_bucket gives every position its work
+// bucket (one stage wide) over the whole grid, then k_tile_order, one workgroup, counting-sorts the positions.
+constexpr int kOrderThreads = 1024, kOrderBuckets = 2048;
 
 // Dispatch position p -> its tile in the grid's own order (rows last first); 32-bit: the host launches the
 // order kernel only while every position fits.
@@ -344,10 +357,27 @@ __device__ __forceinline__ uint32_t wave_bucket_add(uint32_t* cur, int b, bool a
   return pos;
 }
 
-// scratch: one uint32 per position (the fast kernel's flag area, which it rewrites afterwards) keeps each
-// position's bucket between the two passes.
-__global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, uint32_t total, uint32_t* scratch,
-                                                              uint32_t* order) {
+// Each dispatch position's work bucket (0: skipped; else 1 + stages to reduce, the last bucket holding
+// everything longer) into `bucket`, one thread per position over the whole grid.
+__global__ void __launch_bounds__(256) k_tile_bucket(const SysArgs a, uint32_t total, uint16_t* bucket) {
+  const uint32_t p = blockIdx.x * 256u + threadIdx.x;
+  if (p >= total) return;
+  uint32_t z, ty, tx;
+  grid_tile(a, p, z, ty, tx);
+  const int64_t m0 = (int64_t)ty * a.fbm, n0 = (int64_t)tx * a.fbn;
+  if (a.skip && tile_skipped(a, z, m0, n0, a.fbm, a.fbn)) {
+    bucket[p] = 0;
+    return;
+  }
+  const int64_t st = tile_kstop(a, z, m0) / KT;
+  bucket[p] = (uint16_t)(1 + (st < kOrderBuckets - 2 ? st : kOrderBuckets - 2));
+}
+
+// The counting sort of the positions by bucket, heaviest first, in one workgroup: sixteen adjacent positions'
+// buckets per thread per pass (two 16-byte loads), counted, then placed.
+constexpr int kOrderRun = 16;
+__global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, uint32_t total,
+                                                              const uint16_t* __restrict__ bucket, uint32_t* order) {
   constexpr int PB = kOrderBuckets / kOrderThreads;
   static_assert(PB * kOrderThreads == kOrderBuckets, "whole buckets per thread");
   __shared__ uint32_t cur[kOrderBuckets];
@@ -355,45 +385,28 @@ __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, u
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderThreads) cur[b] = 0u;
   __syncthreads();
-  const uint32_t stride = (uint32_t)kOrderThreads * kOrderPer;
+  const uint32_t stride = (uint32_t)kOrderThreads * kOrderRun;
+  auto load_run = [&](uint32_t p0, uint16_t (&b)[kOrderRun]) {
+    if (p0 + kOrderRun <= total) {
+      const uint4* q = reinterpret_cast<const uint4*>(bucket + p0);   // p0 is a multiple of 16: 32-byte aligned
+      const uint4 lo = q[0], hi = q[1];
+      const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        b[2 * u] = (uint16_t)(w[u] & 0xFFFFu);
+        b[2 * u + 1] = (uint16_t)(w[u] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kOrderRun; ++u) b[u] = p0 + u < total ? bucket[p0 + u] : 0;
+    }
+  };
   for (uint32_t c0 = 0; c0 < total; c0 += stride) {
-    // straight-line, positions past the end clamped to the last one, so every tile's hint loads are in
-    // flight together
-    int bucket[kOrderPer];
-    bool skipped[kOrderPer];
-    int64_t kst[kOrderPer], zz[kOrderPer], m0[kOrderPer], n0[kOrderPer];
+    const uint32_t p0 = c0 + (uint32_t)threadIdx.x * kOrderRun;
+    uint16_t b[kOrderRun];
+    load_run(p0, b);
 #pragma unroll
-    for (int u = 0; u < kOrderPer; ++u) {
-      const uint32_t p = c0 + (uint32_t)u * kOrderThreads + threadIdx.x;
-      uint32_t z, ty, tx;
-      grid_tile(a, p < total ? p : total - 1u, z, ty, tx);
-      zz[u] = z;
-      m0[u] = (int64_t)ty * a.fbm;
-      n0[u] = (int64_t)tx * a.fbn;
-      skipped[u] = false;
-      kst[u] = a.K / KT;
-    }
-    if (a.skip) {
-      uint32_t v[kOrderPer][4];
-#pragma unroll
-      for (int u = 0; u < kOrderPer; ++u) skip_bytes(a, zz[u], m0[u], n0[u], v[u]);
-#pragma unroll
-      for (int u = 0; u < kOrderPer; ++u) skipped[u] = skip_all(a, m0[u], n0[u], a.fbm, a.fbn, v[u]);
-    }
-    if (a.k_end) {
-#pragma unroll
-      for (int u = 0; u < kOrderPer; ++u) kst[u] = tile_kstop(a, zz[u], m0[u]) / KT;
-    }
-#pragma unroll
-    for (int u = 0; u < kOrderPer; ++u) {
-      const uint32_t p = c0 + (uint32_t)u * kOrderThreads + threadIdx.x;
-      bucket[u] = p >= total ? -1 : skipped[u] ? 0 : 1 + (int)(kst[u] < kOrderBuckets - 2 ? kst[u] : kOrderBuckets - 2);
-    }
-#pragma unroll
-    for (int u = 0; u < kOrderPer; ++u) {
-      wave_bucket_add(cur, bucket[u], bucket[u] >= 0);
-      if (bucket[u] >= 0) scratch[c0 + (uint32_t)u * kOrderThreads + threadIdx.x] = (uint32_t)bucket[u];
-    }
+    for (int u = 0; u < kOrderRun; ++u) wave_bucket_add(cur, b[u], p0 + u < total);
   }
   __syncthreads();
   // cur[b] <- the first position of bucket b: the count of every bucket above it (heavier work first)
@@ -420,18 +433,14 @@ __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, u
   }
   __syncthreads();
   for (uint32_t c0 = 0; c0 < total; c0 += stride) {
-    uint32_t b[kOrderPer];
+    const uint32_t p0 = c0 + (uint32_t)threadIdx.x * kOrderRun;
+    uint16_t b[kOrderRun];
+    load_run(p0, b);
 #pragma unroll
-    for (int u = 0; u < kOrderPer; ++u) {
-      const uint32_t p = c0 + (uint32_t)u * kOrderThreads + threadIdx.x;
-      b[u] = p < total ? scratch[p] : 0u;
-    }
-#pragma unroll
-    for (int u = 0; u < kOrderPer; ++u) {
-      const uint32_t p = c0 + (uint32_t)u * kOrderThreads + threadIdx.x;
-      const uint32_t at = wave_bucket_add(cur, (int)b[u], p < total);
+    for (int u = 0; u < kOrderRun; ++u) {
+      const uint32_t pos = wave_bucket_add(cur, b[u], p0 + u < total);
       uint32_t z, ty, tx;
-      if (p < total) order[at] = grid_tile(a, p, z, ty, tx);
+      if (p0 + u < total) order[pos] = grid_tile(a, p0 + u, z, ty, tx);
     }
   }
 }
@@ -798,10 +807,11 @@ __device__ __forceinline__ void gen_tile_at(const SysArgs& args, int64_t z, int6
   for (int x = 0; x < TM; ++x) {
     const int64_t mm = m0 + tm * TM + x;
     if (mm >= M) continue;
+    const float* row = args.epi_on ? epi_row(args, z, mm) : nullptr;
 #pragma unroll
     for (int y = 0; y < TN; ++y) {
       const int64_t nn = n0 + tn * TN + y;
-      if (nn < N) Cz[mm * args.ldc + nn] = epilogue(args, z, mm, nn, C[x][y]);
+      if (nn < N) Cz[mm * args.ldc + nn] = args.epi_on ? epi_apply(args, row, nn, C[x][y]) : C[x][y];
     }
   }
 }
@@ -980,8 +990,11 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
       }
     }
     if ((a.skip || a.k_end) && total <= (int64_t)0xFFFFFFFFu) {
+      // the buckets live in the flag area until the fast kernel rewrites it
       uint32_t* order = a.flags + W;
-      k_tile_order<<<1, kOrderThreads, 0, st>>>(a, (uint32_t)total, a.flags, order);
+      uint16_t* bucket = reinterpret_cast<uint16_t*>(a.flags);
+      k_tile_bucket<<<(unsigned)mxq::ceil_div(total, 256), 256, 0, st>>>(a, (uint32_t)total, bucket);
+      k_tile_order<<<1, kOrderThreads, 0, st>>>(a, (uint32_t)total, bucket, order);
       a.order = order;
     }
     {
@@ -1044,8 +1057,8 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
     return mxq::invalid("mxq_systolic_batched: negative batch stride");
   if (count > 1 && M > 0 && N > 0 && L.batch_c < (M - 1) * L.ld_c + N)
     return mxq::invalid("mxq_systolic_batched: outputs of two problems overlap");
-  if (epilogue && (epilogue->m < 1 || epilogue->z_per_b < 1 || epilogue->z0 < 0))
-    return mxq::invalid("mxq_systolic_batched: epilogue needs m >= 1, z_per_b >= 1, z0 >= 0");
+  if (epilogue && (epilogue->m < 1 || epilogue->m > 0x7FFFFFFF || epilogue->z_per_b < 1 || epilogue->z0 < 0))
+    return mxq::invalid("mxq_systolic_batched: epilogue needs m >= 1 (below 2^31), z_per_b >= 1, z0 >= 0");
   if (M == 0 || N == 0 || count == 0) return MXQ_OK;
   if (!P_A || !X_A || !P_B || !X_B || !C || !workspace) return mxq::invalid("mxq_systolic_batched: NULL pointer");
   SysArgs a{};
