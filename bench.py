@@ -268,7 +268,7 @@ def mfma_line(torch, steps, P_A, X_A, P_B, X_B):
     flops = 2 * P_A.shape[0] * P_A.shape[1] * P_B.shape[1]
     k_tf = flops / (kms / 1e3) / 1e12 if kms else None
     return {"workload": "mfma_accum on the same MXFP8_E4M3 codes (M = 512, N = 4096, K = 4096)",
-            "ms": round(ms, 4), "kernel": "k_mx_mfma<0, 0>", "kernel_ms": round(kms, 4) if kms else None,
+            "ms": round(ms, 4), "kernel": "k_mx_mfma<0, 0, 1>", "kernel_ms": round(kms, 4) if kms else None,
             "kernel_TFLOPs": round(k_tf, 2) if k_tf else None, "peak_TFLOPs": FP8_PEAK_TFLOPS,
             "frac": round(k_tf / FP8_PEAK_TFLOPS, 4) if k_tf else None}
 

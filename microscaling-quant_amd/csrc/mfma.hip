@@ -120,13 +120,16 @@ __global__ void __launch_bounds__(256) k_mx_pack(const float* __restrict__ P, co
   if (bad) atomicOr(err, 1);
 }
 
-// One wave per 64 x 64 block of C (2 x 2 instructions per K step, so each operand load feeds two of them);
-// four waves per workgroup in a 2 x 2 arrangement (128 x 128).  Tiles past the packed operand (M or N not
-// reaching this wave's second tile) re-read the last tile: valid bytes whose results are never stored.
-// Operands are loaded kDepth K steps ahead of the instructions that use them.
+// One wave per (32 TA) x 64 block of C (TA x 2 instructions per K step, so each B load feeds TA of them and
+// each A load two); four waves per workgroup in a 2 x 2 arrangement ((64 TA) x 128).  TA = 2 where that still
+// gives the chip 1024 waves, else TA = 1: on C2's 512 x 4096 the 64 x 64 blocks leave half the SIMDs idle.
+// Tiles past the packed operand (M or N not reaching this wave's last tile) re-read the last tile: valid
+// bytes whose results are never stored.  Operands are loaded kDepth K steps ahead of the instructions that
+// use them.  A block's K order is the same for either TA, so the results are too.
+template <int TA>
 struct MxStep {
-  v8i a[2], b[2];
-  int sa[2], sb[2];
+  v8i a[TA], b[2];
+  int sa[TA], sb[2];
 };
 
 constexpr int kDepth = 4;
@@ -138,37 +141,40 @@ __device__ __forceinline__ v8i load_codes(const uint8_t* codes, int64_t chunk, i
   return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-__device__ __forceinline__ void load_step(MxStep& st, const uint8_t* A, const uint8_t* SA, const uint8_t* B,
-                                          const uint8_t* SB, const int64_t ta[2], const int64_t tb[2], int64_t nk,
-                                          int64_t s, int lane) {
+template <int TA>
+__device__ __forceinline__ void load_step(MxStep<TA>& st, const uint8_t* A, const uint8_t* SA, const uint8_t* B,
+                                          const uint8_t* SB, const int64_t (&ta)[TA], const int64_t (&tb)[2],
+                                          int64_t nk, int64_t s, int lane) {
+#pragma unroll
+  for (int t = 0; t < TA; ++t) {
+    st.a[t] = load_codes(A, ta[t] * nk + s, lane);
+    st.sa[t] = SA[(ta[t] * nk + s) * 64 + lane];
+  }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    st.a[t] = load_codes(A, ta[t] * nk + s, lane);
     st.b[t] = load_codes(B, tb[t] * nk + s, lane);
-    st.sa[t] = SA[(ta[t] * nk + s) * 64 + lane];
     st.sb[t] = SB[(tb[t] * nk + s) * 64 + lane];
   }
 }
 
-template <int KA, int KB>
+template <int KA, int KB, int TA>
 __global__ void __launch_bounds__(256) k_mx_mfma(const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA,
                                                  const uint8_t* __restrict__ B, const uint8_t* __restrict__ SB,
                                                  float* __restrict__ C, int64_t K64, int64_t M, int64_t N) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = lane & 31, h = lane >> 5;
-  const int64_t m0 = (int64_t)blockIdx.y * 128 + (wave >> 1) * 64;
+  const int64_t m0 = (int64_t)blockIdx.y * (64 * TA) + (wave >> 1) * (32 * TA);
   const int64_t n0 = (int64_t)blockIdx.x * 128 + (wave & 1) * 64;
   const int64_t nk = K64 / 64, tiles_m = (M + 31) / 32, tiles_n = (N + 31) / 32;
-  int64_t ta[2], tb[2];
+  int64_t ta[TA], tb[2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    ta[t] = min(m0 / 32 + t, tiles_m - 1);
-    tb[t] = min(n0 / 32 + t, tiles_n - 1);
-  }
-  v16f acc[2][2] = {};
+  for (int t = 0; t < TA; ++t) ta[t] = min(m0 / 32 + t, tiles_m - 1);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) tb[t] = min(n0 / 32 + t, tiles_n - 1);
+  v16f acc[TA][2] = {};
   // kDepth K steps in flight: step s of each round issues its instructions, then refills its slot with the
   // step kDepth ahead (past the end it re-reads the last step, whose values are never used).
-  MxStep slot[kDepth];
+  MxStep<TA> slot[kDepth];
 #pragma unroll
   for (int s = 0; s < kDepth; ++s) load_step(slot[s], A, SA, B, SB, ta, tb, nk, min((int64_t)s, nk - 1), lane);
   for (int64_t k = 0; k < nk; k += kDepth) {
@@ -176,7 +182,7 @@ __global__ void __launch_bounds__(256) k_mx_mfma(const uint8_t* __restrict__ A, 
     for (int s = 0; s < kDepth; ++s) {
       if (k + s < nk) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TA; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(slot[s].a[i], slot[s].b[j], acc[i][j], KA, KB,
@@ -190,13 +196,22 @@ __global__ void __launch_bounds__(256) k_mx_mfma(const uint8_t* __restrict__ A, 
     const int64_t n = n0 + 32 * j + r;
     if (n >= N) continue;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TA; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t m = m0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
         if (m < M) C[m * N + n] = acc[i][j][e];
       }
   }
+}
+
+template <int TA>
+void launch_mfma(int a_kind, int b_kind, dim3 grid, hipStream_t st, const uint8_t* A, const uint8_t* SA,
+                 const uint8_t* B, const uint8_t* SB, float* C, int64_t K64, int64_t M, int64_t N) {
+  if (a_kind == kE4M3 && b_kind == kE4M3) k_mx_mfma<kE4M3, kE4M3, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
+  else if (a_kind == kE4M3) k_mx_mfma<kE4M3, kE5M2, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
+  else if (b_kind == kE4M3) k_mx_mfma<kE5M2, kE4M3, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
+  else k_mx_mfma<kE5M2, kE5M2, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
 }
 
 }  // namespace
@@ -224,13 +239,13 @@ extern "C" int mxq_mx_mfma(const uint8_t* A, const uint8_t* SA, int32_t a_kind, 
   if (!A || !SA || !B || !SB || !C) return mxq::invalid("mxq_mx_mfma: NULL pointer");
   if (reinterpret_cast<uintptr_t>(A) % 16 || reinterpret_cast<uintptr_t>(B) % 16)
     return mxq::invalid("mxq_mx_mfma: codes must be 16-byte aligned");
-  if (mxq::ceil_div(M, 128) > 65535) return mxq::invalid("mxq_mx_mfma: M too large");
-  const dim3 grid((unsigned)mxq::ceil_div(N, 128), (unsigned)mxq::ceil_div(M, 128));
+  // 64 x 64 blocks per wave while they give at least 1024 waves, else 32 x 64
+  const bool two = mxq::ceil_div(N, 128) * mxq::ceil_div(M, 128) * 4 >= 1024;
+  if (mxq::ceil_div(M, two ? 128 : 64) > 65535) return mxq::invalid("mxq_mx_mfma: M too large");
+  const dim3 grid((unsigned)mxq::ceil_div(N, 128), (unsigned)mxq::ceil_div(M, two ? 128 : 64));
   hipStream_t st = mxq::as_stream(stream);
   mxq::KernelTimer timer("mx_mfma", st);
-  if (a_kind == kE4M3 && b_kind == kE4M3) k_mx_mfma<kE4M3, kE4M3><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
-  else if (a_kind == kE4M3) k_mx_mfma<kE4M3, kE5M2><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
-  else if (b_kind == kE4M3) k_mx_mfma<kE5M2, kE4M3><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
-  else k_mx_mfma<kE5M2, kE5M2><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
+  if (two) launch_mfma<2>(a_kind, b_kind, grid, st, A, SA, B, SB, C, K64, M, N);
+  else launch_mfma<1>(a_kind, b_kind, grid, st, A, SA, B, SB, C, K64, M, N);
   return mxq::check_launch("mxq_mx_mfma");
 }

@@ -240,3 +240,18 @@ def test_rejects(cuda):
                        block_size=16)
     with pytest.raises(ValueError, match="element format"):
         mxq.mfma_accum(ones, X, ones, X, "FP32")
+
+
+def test_wave_block_shapes_agree(cuda):
+    """2048 x 2048 outputs run on 64 x 64 blocks per wave, 128-column slices of them on 32 x 64 blocks (too few
+    larger ones to fill the chip): every output identical, each keeping its K order."""
+    from mxq import _mfma_accum as mfa
+    rng = np.random.default_rng(12)
+    K, M, N = 128, 2048, 2048
+    PA, XA = ob.mxgemmini_quantize(rng.standard_normal((K, M)).astype(np.float32), "MXFP8_E4M3", 0)
+    PB, XB = ob.mxgemmini_quantize(rng.standard_normal((K, N)).astype(np.float32), "MXFP8_E4M3", 0)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()          # noqa: E731
+    whole = mfa.mfma_accum(t(PA), t(XA), t(PB), t(XB), "MXFP8_E4M3").cpu().numpy()
+    for c in (0, 1024, 1920):
+        part = mfa.mfma_accum(t(PA), t(XA), t(PB[:, c:c + 128]), t(XB[:, c:c + 128]), "MXFP8_E4M3").cpu().numpy()
+        assert np.array_equal(part.view(np.uint32), whole[:, c:c + 128].view(np.uint32)), c
