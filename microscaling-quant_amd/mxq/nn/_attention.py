@@ -398,7 +398,8 @@ def _scale_mask(S: torch.Tensor, bias: Optional[torch.Tensor], scale: float, vec
     """S (Zc x n*m x Tk scores of pairs z0.., queries s0..) <- r(r(S * scale) + mask rows) in place, one pass:
     the reference's `r(S * scale)` and `r(S + mask)` (mxq/nn/_attention.py:128-135), float32 multiply and add
     with the scale as float32, r the vector rounding.  Pair z's mask is bias[z // Hkv] (bias[0] when the mask has
-    one batch row), rows s0.., keys contiguous."""
+    one batch row), rows s0.., keys contiguous.  The batched path applies the same step inside the systolic
+    launch's stores (mxq_systolic_epilogue); this is its standalone form, against which that one is tested."""
     from .. import _lib
     Zc, _, Tk = S.shape
     mask, b_stride, r_stride = (None, 0, 0) if bias is None else _mask_rows(bias, z0, Hkv, s0)
