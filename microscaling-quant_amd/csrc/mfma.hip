@@ -232,7 +232,8 @@ extern "C" int mxq_mx_pack(const float* P, const float* X, int64_t K, int64_t n,
 
 extern "C" int mxq_mx_mfma(const uint8_t* A, const uint8_t* SA, int32_t a_kind, const uint8_t* B, const uint8_t* SB,
                            int32_t b_kind, float* C, int64_t K64, int64_t M, int64_t N, mxq_stream_t stream) {
-  if (K64 < 0 || K64 % 64 || M < 0 || N < 0) return mxq::invalid("mxq_mx_mfma: bad shape");
+  // K64 == 0 is refused: the kernel's prologue reads its first K step before the loop tests the count
+  if (K64 <= 0 || K64 % 64 || M < 0 || N < 0) return mxq::invalid("mxq_mx_mfma: bad shape (K64 must be a positive multiple of 64)");
   if ((a_kind != kE4M3 && a_kind != kE5M2) || (b_kind != kE4M3 && b_kind != kE5M2))
     return mxq::invalid("mxq_mx_mfma: bad operand kind");
   if (M == 0 || N == 0) return MXQ_OK;

@@ -96,6 +96,22 @@ def _live_span(mask_rows: torch.Tensor, bound: float, block: int) -> Tuple[int, 
     return first - first % block, min(Tk, -(-(last + 1) // block) * block)
 
 
+def _bias(mask: Optional[torch.Tensor], dims: _Dims) -> Optional[torch.Tensor]:
+    """The mask as Bm x Tq x Tk float32: mask[:, 0, :, :Tk], its query and key dimensions broadcast where they
+    are 1 (batch row b reads mask row b, or row 0 when Bm == 1).  Extents that cannot serve B x 1 x Tq x Tk are
+    refused here, before a kernel reads Tk values from each mask row."""
+    if mask is None:
+        return None
+    if mask.dim() != 4:
+        raise ValueError(f"attend: mask must be B x 1 x Tq x Tk, got {tuple(mask.shape)}")
+    bias = mask[:, 0, :, :dims.Tk].to(torch.float32)
+    Bm, Tq_m, Tk_m = bias.shape
+    if (Bm != 1 and Bm < dims.B) or Tq_m not in (1, dims.Tq) or Tk_m not in (1, dims.Tk):
+        raise ValueError(f"attend: mask {tuple(mask.shape)} does not broadcast to "
+                         f"{dims.B} x 1 x {dims.Tq} x {dims.Tk}")
+    return bias.expand(Bm, dims.Tq, dims.Tk)
+
+
 @torch.no_grad()
 def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor], scale: float,
            qk: Scheme, pv: Scheme, chunk: Optional[int] = None, vector: Optional[str] = None) -> torch.Tensor:
@@ -110,10 +126,7 @@ def attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[tor
     step = chunk or max(rows, ELEMENTS_PER_STEP // (dims.group * dims.Tk) // rows * rows)
     rnd = rounder(vector)
     out = q.new_empty(dims.B, dims.Tq, dims.H, dims.D)
-    bias = None                                                                   # Bm x Tq x Tk, Bm = 1 or B
-    if mask is not None:
-        bias = mask[:, 0, :, :dims.Tk].to(torch.float32)
-        bias = bias.expand(bias.shape[0], dims.Tq, dims.Tk) if bias.shape[1] == 1 else bias
+    bias = _bias(mask, dims)                                                      # Bm x Tq x Tk, Bm = 1 or B
     batch = _Batched.of(qk, pv, q)
     if batch is not None:
         batch.run(q, k, v, bias, scale, step, vector, rnd, dims, out)

@@ -81,3 +81,19 @@ def test_struct_offsets_match_header(tmp_path):
         assert int(got[f"{name} size"]) == ctypes.sizeof(py), name
         for f, _ in py._fields_:
             assert int(got[f"{name} {f}"]) == getattr(py, f).offset, f"{name}.{f}"
+
+
+def test_mfma_refuses_empty_contraction():
+    """mxq_mx_mfma with K64 == 0 (or not a multiple of 64) returns MXQ_EINVAL before any HIP call: its kernel's
+    prologue would read a K step that does not exist."""
+    from mxq import _lib
+    lib = _lib.load()
+    lib.mxq_last_error.restype = ctypes.c_char_p
+    buf = (ctypes.c_uint8 * 64)()
+    out = (ctypes.c_float * 4)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    for K64 in (0, 32, -64):
+        rc = lib.mxq_mx_mfma(p, p, 0, p, p, 0, ctypes.cast(out, ctypes.c_void_p), ctypes.c_int64(K64),
+                             ctypes.c_int64(2), ctypes.c_int64(2), ctypes.c_void_p(0))
+        assert rc == 1, K64
+        assert b"K64" in lib.mxq_last_error()

@@ -71,6 +71,30 @@ def test_c4_shape(cuda):
     assert_bits_equal(P.cpu().numpy(), wP, "P_lut")
 
 
+def test_c4_systolic_on_lut_operands(cuda):
+    """The LUT benchmark's product: matmul.systolic MXGEMMINI HW_FINAL on two block.lut MXFP6_E3M2 operands of
+    4096 x 4096 (seeds 0 and 1; K = M = N = 4096).  The second operand's codes and scales bit for bit against the
+    oracle's quantizer (the first one's are test_c4_shape's), then the full GPU product against the oracle's
+    reducer on the last 32 columns and on two rows over all 4096 columns (every output is its own chain)."""
+    import _pool
+    from mxq import block, matmul
+    q = lambda V: block.lut.quantize(V, "MXFP6_E3M2", 0, 32, rounding_mode="rne", scale_floor=2.0 ** -23,  # noqa
+                                     group=1, max_iters=50)
+    A = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0))
+    B = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(1))
+    PA, XA = q(A.cuda())
+    PB, XB = q(B.cuda())
+    Y = matmul.systolic(PA, XA, PB, XB, matmul.MXGEMMINI(), matmul.HW_FINAL).cpu().numpy()
+    pa, xa, pb, xb = (t.cpu().numpy() for t in (PA, XA, PB, XB))
+    wP, wX = ol.lut_quantize(B.numpy(), "MXFP6_E3M2", 0, 32, "rne", 2.0 ** -23, 1, 50)
+    assert_bits_equal(xb, wX, "X_B")
+    assert_bits_equal(pb, wP, "P_B")
+    cols = slice(4064, 4096)
+    assert_bits_equal(Y[:, cols], _pool.systolic(pa, xa, pb[:, cols], xb[:, cols]), "C4 last 32 columns")
+    rows = [0, 2731]
+    assert_bits_equal(Y[rows], _pool.systolic(pa[:, rows], xa[:, rows], pb, xb), "C4 two rows")
+
+
 def test_lut_errors(cuda):
     from mxq import lut
     P = torch.tensor([[0.5, 0.3]], device="cuda")

@@ -240,3 +240,50 @@ def test_attend_skip_hints(cuda, monkeypatch, kind):
     assert_bits_equal(got, want, f"attend with {kind} mask")
     assert marked, "the batched path ran"
     assert (sum(marked) == 0) if kind == "causal_weak" else (sum(marked) > 0), marked
+
+
+def _c5_inputs(Hkv=32):
+    """The attention benchmark's inputs: q, k, v of 1 x heads x 2048 x 128 ~ N(0, 1) from seeds 0, 1, 2, and the
+    HF eager causal mask (finfo(float32).min above the diagonal)."""
+    q = torch.randn(1, 32, 2048, 128, generator=torch.Generator().manual_seed(0))
+    k, v = (torch.randn(1, Hkv, 2048, 128, generator=torch.Generator().manual_seed(i)) for i in (1, 2))
+    return q, k, v, _causal(1, 2048, 2048)
+
+
+def test_c5_full_shape_heads_against_oracle(cuda):
+    """The attention benchmark's own call (1 x 32 heads x 2048 x 128, causal, one query chunk, the batched path
+    with its causal skip), heads 0 and 31 bit for bit against the oracle run on those two heads alone (each head
+    is its own KV head, so heads do not interact), with the GPU's softmax.  The oracle's reducer runs over the
+    host cores (tests/_pool.py)."""
+    import _pool
+    import mxq
+    from mxq.nn import _attention as at
+    q, k, v, mask = _c5_inputs()
+    hw = _hw(mxq)
+    assert at._Batched.of(hw, hw, q.cuda()) is not None, "the benchmark's Scheme takes the batched path"
+    got = mxq.nn.attend(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), 128 ** -0.5, hw, hw).cpu().numpy()
+    heads = [0, 31]
+    qz = lambda V: ob.mxgemmini_quantize(V, "MXFP8_E4M3", 0)                       # noqa: E731
+    side = oatt.Side(qz, qz, _pool.reducer())
+    want = oatt.attend(q[:, heads].numpy(), k[:, heads].numpy(), v[:, heads].numpy(), mask.numpy(), 128 ** -0.5,
+                       side, side, _gpu_softmax)
+    assert_bits_equal(got[:, :, heads], want, "attend 1x32x2048x128 causal, heads 0 and 31")
+
+
+@pytest.mark.parametrize("Hkv", [32, 8], ids=["mha", "gqa8"])
+def test_c5_full_shape_batched_against_per_pair(cuda, Hkv):
+    """Every head of the attention benchmark's call (and of its GQA variant with 8 KV heads) from the batched
+    path, bit for bit against the reference's per-pair loop on the same library kernels (a Scheme of plain
+    callables, which the batched path does not take)."""
+    import mxq
+    from mxq import Scheme, block, matmul
+    from mxq.nn import _attention as at
+    q, k, v, mask = (t.cuda() for t in _c5_inputs(Hkv))
+    hw = _hw(mxq)
+    loose = Scheme("hw", a=lambda V: block.mxgemmini.quantize(V, "MXFP8_E4M3", axis=0),
+                   b=lambda V: block.mxgemmini.quantize(V, "MXFP8_E4M3", axis=0),
+                   reduce=lambda *ops: matmul.systolic(*ops, matmul.MXGEMMINI(), matmul.HW_FINAL))
+    assert at._Batched.of(loose, loose, q) is None
+    got = mxq.nn.attend(q, k, v, mask, 128 ** -0.5, hw, hw)
+    want = mxq.nn.attend(q, k, v, mask, 128 ** -0.5, loose, loose)
+    assert_bits_equal(got.cpu().numpy(), want.cpu().numpy(), f"attend C5 batched vs per pair, {Hkv} KV heads")

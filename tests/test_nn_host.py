@@ -134,6 +134,32 @@ def test_attend_rejects():
         attend(torch.zeros(1, 2, 8, 64), torch.zeros(1, 1, 8, 64), torch.zeros(1, 1, 8, 64), None, 1.0, bad, bad)
 
 
+def test_attend_mask_extents():
+    """A mask whose key (or query) dimension is 1 broadcasts: the same result as the mask expanded to Tq x Tk.
+    A key dimension that is neither 1 nor Tk (after the :Tk cut), a query dimension that is neither 1 nor Tq,
+    and 1 < mask batch < B cannot broadcast and are refused before any call."""
+    t, n = _schemes(1)
+    g = torch.Generator().manual_seed(3)
+    B, H, T, D = 2, 2, 40, 32
+    q, k, v = (torch.randn(B, H, T, D, generator=g) for _ in range(3))
+    row = torch.where(torch.arange(T) % 3 == 0, torch.finfo(torch.float32).min, 0.0)
+    key1 = row[None, None, :, None].repeat(B, 1, 1, 1)                     # B x 1 x Tq x 1
+    got = attend(q, k, v, key1, D ** -0.5, t, t)
+    want = attend(q, k, v, key1.expand(B, 1, T, T).contiguous(), D ** -0.5, t, t)
+    assert_bits_equal(got.numpy(), want.numpy(), "key-broadcast mask")
+    wo = oatt.attend(q.numpy(), k.numpy(), v.numpy(), key1.expand(B, 1, T, T).numpy(), D ** -0.5, n, n, _cpu_softmax)
+    assert_bits_equal(got.numpy(), wo, "key-broadcast mask vs oracle")
+    longer = _causal(B, T, T + 8)                                            # extra keys are cut off, as HF's
+    assert_bits_equal(attend(q, k, v, longer, D ** -0.5, t, t).numpy(),
+                      attend(q, k, v, longer[..., :T].contiguous(), D ** -0.5, t, t).numpy(), "long mask")
+    for bad in (_causal(B, T, T)[..., :T - 5], _causal(B, T, T)[:, :, :T - 1], torch.zeros(T, T)):
+        with pytest.raises(ValueError, match="mask"):
+            attend(q, k, v, bad, D ** -0.5, t, t)
+    q3, k3, v3 = (torch.randn(3, H, T, D, generator=g) for _ in range(3))
+    with pytest.raises(ValueError, match="mask"):
+        attend(q3, k3, v3, _causal(2, T, T), D ** -0.5, t, t)
+
+
 def test_default_step():
     assert attention_mod.ELEMENTS_PER_STEP == 1 << 26 and attention_mod.SLACK == 2.0 ** 16
 

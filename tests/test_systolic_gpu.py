@@ -222,11 +222,13 @@ def test_c2_shape_column_slice(cuda):
     P_A, X_A = block.mxgemmini.quantize(x.t().contiguous().cuda(), "MXFP8_E4M3", axis=0)
     P_B, X_B = block.mxgemmini.quantize(W.t().contiguous().cuda(), "MXFP8_E4M3", axis=0)
     Y = matmul.systolic(P_A, X_A, P_B, X_B, matmul.MXGEMMINI(), matmul.HW_FINAL).cpu().numpy()
+    import _pool
     cols = slice(1000, 1032)
     pa, xa = P_A.cpu().numpy(), X_A.cpu().numpy()
-    pb, xb = P_B.cpu().numpy()[:, cols], X_B.cpu().numpy()[:, cols]
-    want = osys.systolic(pa, xa, pb, xb, nx.MXGEMMINI(), HW_FINAL)
-    assert_bits_equal(Y[:, cols], want, "C2 column slice")
+    pb, xb = P_B.cpu().numpy(), X_B.cpu().numpy()
+    assert_bits_equal(Y[:, cols], _pool.systolic(pa, xa, pb[:, cols], xb[:, cols]), "C2 column slice")
+    rows = [7, 511]
+    assert_bits_equal(Y[rows], _pool.systolic(pa[:, rows], xa[:, rows], pb, xb), "C2 two rows")
 
 
 @pytest.mark.parametrize("sched_name", ["hw", "general"])
