@@ -191,6 +191,18 @@ int mxq_systolic_batched(const float* P_A, const float* X_A, const float* P_B, c
                          const mxq_systolic_epilogue* epilogue, uint32_t* workspace, int32_t force_general,
                          mxq_stream_t stream);
 
+/* mxq_systolic without the workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * fast kernel's per-tile flags live in a 1 MiB array the library holds on each GPU (kept until the process
+ * ends), so ceil(M/32) * ceil(N/32) may be at most 262144 (M * N up to 2^28 outputs); larger shapes return
+ * MXQ_EINVAL.  The call allocates nothing and makes no host synchronisation; the current device must be the
+ * stream's.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams or
+ * threads) race and must be serialised by the caller.  Results are bit-identical to mxq_systolic's. */
+int mxq_systolic_noalloc(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C,
+                         int64_t K, int64_t M, int64_t N, const int32_t* lane_e, const int32_t* lane_m, int32_t size,
+                         int32_t block_size, const mxq_arith_spec* arith, int32_t force_general,
+                         mxq_stream_t stream);
+
 /* uint32 elements of workspace mxq_systolic / mxq_systolic_batched need for `count` problems of K x M codes A
  * and K x N codes B (at least 1); mxq_adder_tree and mxq_anchor_tree need the same with count 1. */
 int64_t mxq_systolic_workspace(int64_t K, int64_t M, int64_t N, int64_t count);

@@ -31,6 +31,7 @@
 //                   flag is 1; alone (no fast case, or forced) it computes everything.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "mxq_common.h"
 #include "mxq_numerics.h"
@@ -1078,6 +1079,76 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
     a.epi = *epilogue;
   }
   return run_systolic(a, lane_e, lane_m, count, force_general, mxq::as_stream(stream));
+}
+
+// ------------------------------------------------------------------------ the allocation-free entry point
+// mxq_systolic_noalloc keeps the fast kernel's per-tile flags (its only scratch when no hints are given) in this
+// array instead of a caller's workspace.  Each GPU holds its own copy for the life of the process.  In host code
+// the name `scratch` is a stand-in, not a device address: the kernels get the address hipGetSymbolAddress gives
+// on each device, looked up once per device on that device's first call and kept in g_scratch.
+constexpr int64_t kScratchWords = int64_t(1) << 18;                 // 1 MiB: ceil(M/32) * ceil(N/32) flags
+static __device__ __align__(256) uint32_t scratch[kScratchWords];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint32_t* g_scratch[kMaxDevices] = {};
+
+// the scratch array's address on the current device (which must be the stream's device)
+int scratch_on_device(hipStream_t st, uint32_t** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    mxq::set_error(std::string("mxq_systolic_noalloc: hipGetDevice: ") + hipGetErrorString(err));
+    return MXQ_EHIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return mxq::invalid("mxq_systolic_noalloc: device index out of range");
+  if (st) {
+    int sdev = -1;
+    err = hipStreamGetDevice(st, &sdev);
+    if (err != hipSuccess) {
+      mxq::set_error(std::string("mxq_systolic_noalloc: hipStreamGetDevice: ") + hipGetErrorString(err));
+      return MXQ_EHIP;
+    }
+    if (sdev != dev) return mxq::invalid("mxq_systolic_noalloc: the stream belongs to another device than the current one");
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p) {
+      mxq::set_error(std::string("mxq_systolic_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(err));
+      return MXQ_EHIP;
+    }
+    g_scratch[dev] = static_cast<uint32_t*>(p);
+  }
+  *out = g_scratch[dev];
+  return MXQ_OK;
+}
+
+}  // namespace
+
+extern "C" int mxq_systolic_noalloc(const float* P_A, const float* X_A, const float* P_B, const float* X_B,
+                                    float* C, int64_t K, int64_t M, int64_t N, const int32_t* lane_e,
+                                    const int32_t* lane_m, int32_t size, int32_t block_size,
+                                    const mxq_arith_spec* arith, int32_t force_general, mxq_stream_t stream) {
+  if (int rc = check_common(K, M, N, 1, lane_e, lane_m, size, block_size, arith)) return rc;
+  if (M == 0 || N == 0) return MXQ_OK;
+  if (!P_A || !X_A || !P_B || !X_B || !C) return mxq::invalid("mxq_systolic_noalloc: NULL pointer");
+  if (mxq::ceil_div(M, 32) * mxq::ceil_div(N, 32) > kScratchWords)
+    return mxq::invalid("mxq_systolic_noalloc: ceil(M/32) * ceil(N/32) exceeds its 262144 tile flags "
+                        "(use mxq_systolic with a workspace)");
+  hipStream_t st = mxq::as_stream(stream);
+  uint32_t* flags = nullptr;
+  if (int rc = scratch_on_device(st, &flags)) return rc;
+  // every flag the general kernel reads is written by the fast kernel of the same call first: nothing in the
+  // array has to start at zero
+  SysArgs a{};
+  a.A = {P_A, M, 0}; a.XA = {X_A, M, 0}; a.B = {P_B, N, 0}; a.XB = {X_B, N, 0};
+  a.C = C; a.ldc = N; a.batch_c = 0; a.flags = flags;
+  a.K = K; a.M = M; a.N = N; a.size = size; a.block_size = block_size; a.ar = *arith;
+  return run_systolic(a, lane_e, lane_m, 1, force_general, st);
 }
 
 extern "C" int64_t mxq_systolic_workspace(int64_t K, int64_t M, int64_t N, int64_t count) {

@@ -84,6 +84,8 @@ SIGNATURES = {
     "mxq_systolic_batched": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, ctypes.POINTER(SystolicLayout), c_i64,
                                      c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32, ctypes.POINTER(ArithSpec),
                                      c_ptr, c_ptr, c_ptr, c_i32, c_ptr]),
+    "mxq_systolic_noalloc": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32,
+                                     c_i32, ctypes.POINTER(ArithSpec), c_i32, c_ptr]),
     "mxq_systolic_workspace": (c_i64, [c_i64, c_i64, c_i64, c_i64]),
     "mxq_scores_scale_mask": (c_i32, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64, c_i64, c_i64, c_i64,
                                       c_i32, c_ptr]),
