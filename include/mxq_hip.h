@@ -34,7 +34,7 @@ enum { MXQ_DT_F32 = 0, MXQ_DT_BF16 = 1, MXQ_DT_F16 = 2 };
 
 /* Step 1 (scale factor) rules: mxq/scale_factor.py:40-81. */
 enum { MXQ_SCALE_NONE = 0, MXQ_SCALE_MXQUANT = 1, MXQ_SCALE_OCP = 2, MXQ_SCALE_OCP_NO_CLIP = 3 };
-/* Step 2 (element) rules: float_em grids (mxq/element_quant/float_em.py:64-134) and microxcaling's
+/* Step 2 (element) rules: float_em grids (mxq/element_quant/float_em.py:53-123) and microxcaling's
  * _quantize_elemwise (mxq/element_quant/microsoft.py:18-23). */
 enum { MXQ_ELEM_NONE = 0, MXQ_ELEM_QTORCH = 1, MXQ_ELEM_IEEE = 2, MXQ_ELEM_OCP = 3, MXQ_ELEM_MICROSOFT = 4 };
 
@@ -357,7 +357,7 @@ int mxq_round_int(const void* k, int32_t dtype, void* out, int64_t n, int32_t mo
 int mxq_bf16(const float* x, float* out, int64_t n, mxq_stream_t stream);
 
 /* float_em.quantize on a float32 (dtype 0) or float64 (dtype 3) input, float32 out; max_norm for grid ocp.
- * Replaces mxq/element_quant/float_em.py:50-61. */
+ * Replaces mxq/element_quant/float_em.py:39-50. */
 int mxq_float_em(const void* z, int32_t dtype, float* out, int64_t n, int32_t e, int32_t m, int32_t mode,
                  int32_t grid, float max_norm, mxq_stream_t stream);
 

@@ -178,7 +178,7 @@ MXQ_HD float compose_grid64(uint64_t k, int q, int emax) {
 }
 
 // ------------------------------------------------------------------------------------- float_em grids
-// mxq/element_quant/float_em.py:64-84 `_qtorch`: round the float32 bits at m, then clip the exponent to
+// mxq/element_quant/float_em.py:53-73 `_qtorch`: round the float32 bits at m, then clip the exponent to
 // [127 - L, 127 + L]; above saturates to +-max, below goes to +-2^-L when above 2^(-L-1), else +0.
 MXQ_HD float qtorch_round(float z, int e, int m, int mode) {
   const uint32_t bits = f2u(z);
@@ -194,7 +194,7 @@ MXQ_HD float qtorch_round(float z, int e, int m, int mode) {
   return u2f(q);
 }
 
-// mxq/element_quant/float_em.py:87-110 `_ieee` on a float32 input: step 2^(max(E, emin) - m), k = round(|x|/step),
+// mxq/element_quant/float_em.py:76-99 `_ieee` on a float32 input: step 2^(max(E, emin) - m), k = round(|x|/step),
 // overflow at 2^(emax+1) -> Inf, NaN/Inf/+-0 pass, underflow -> +0 (e < 8) or signed zero (e = 8, float64 path).
 MXQ_HD float ieee_round32(float x, int e, int m, int mode) {
   const uint32_t u = f2u(x), a = u & 0x7FFFFFFFu;
@@ -230,7 +230,7 @@ MXQ_HD float ieee_round64(double x, int e, int m, int mode) {
   return copysign_f(val, sx);
 }
 
-// mxq/element_quant/float_em.py:113-134 `_ocp` on a float32 input: ieee's step, clamp at max_norm, exact +-0 -> +0,
+// mxq/element_quant/float_em.py:102-123 `_ocp` on a float32 input: ieee's step, clamp at max_norm, exact +-0 -> +0,
 // a negative value that rounds to zero -> -0, Inf/NaN pass.
 MXQ_HD float ocp_round32(float x, int e, int m, int mode, float max_norm) {
   const uint32_t u = f2u(x), a = u & 0x7FFFFFFFu;
@@ -259,7 +259,7 @@ MXQ_HD float ocp_round64(double x, int e, int m, int mode, float max_norm) {
   return copysign_f(val, (u >> 63) ? -1.0f : 1.0f);
 }
 
-// mxq/element_quant/float_em.py:50-61 `quantize` for a float32 input with validated (e, m, mode, grid).
+// mxq/element_quant/float_em.py:39-50 `quantize` for a float32 input with validated (e, m, mode, grid).
 MXQ_HD float float_em_quantize32(float z, int e, int m, int mode, int grid, float max_norm) {
   if (e == 8 && m == 23) return z;
   if (grid == MXQ_GRID_QTORCH) return qtorch_round(z, e, m, mode);
@@ -516,7 +516,7 @@ MXQ_HD Div make_div(float X) {
 }
 MXQ_HD float apply_div(float v, const Div& d) { return d.inv != 0.0f ? v * d.inv : v / d.X; }
 
-// The OCP element grid (float_em.py:113-134) for e <= 5, m <= 3 on a float32 z, both paths computed and one
+// The OCP element grid (float_em.py:102-123) for e <= 5, m <= 3 on a float32 z, both paths computed and one
 // selected.  At or above the format's min normal: the significand rounded at m fraction bits on the bit
 // pattern (the carry runs into the exponent).  Below it: k = round(|z| / step) evaluated in float32 exactly as
 // round_int does (ties_away adds 0.5 in float32), times the step.  Then the max_norm clamp and the sign;

@@ -1,4 +1,5 @@
-"""Block quantization driver (mxq/block/_driver.py:1-72): `compose` and `dequantize`.
+"""Block quantization driver (mxq/block/_driver.py:1-72): `compose`, `dequantize` and the block layout helpers
+`Blocks`, `to_blocks`, `codes_from_blocks`, `scales_from_blocks`.
 
 Layout contract (MXQuant's mx_block32_quantize):
     quantize(V, axis) -> (P, X)   P: V's shape, the codes (float32)
@@ -11,10 +12,9 @@ transpose, padding or reassembly copy is made.  `compose` with arbitrary Python 
 reference's generic composition: the layout steps are torch views and copies on the tensor's device, the
 callables run as given.
 """
-from typing import Callable, Optional, Tuple
+from typing import Callable, NamedTuple, Optional, Tuple
 
 import torch
-import torch.nn.functional as F
 
 from .. import _lib
 
@@ -34,6 +34,41 @@ def _check_block(block_size: int) -> None:
         raise ZeroDivisionError("integer division or modulo by zero")
     if block_size < 0:
         raise ValueError(f"block_size must be positive, got {block_size}")
+
+
+class Blocks(NamedTuple):
+    """A tensor cut into blocks along one axis (mxq/block/_driver.py:17-20).  `data` is (..., nblocks,
+    block_size): the axis moved last and cut into rows of block_size, the last one zero-padded.  `axis`
+    (non-negative) and `n` (the axis' length) are what undoing the cut needs."""
+    data: torch.Tensor
+    axis: int
+    n: int
+
+
+def to_blocks(V: torch.Tensor, axis: int, block_size: int) -> Blocks:
+    """V's blocks along `axis` (mxq/block/_driver.py:23-32), in V's dtype and on its device.  IndexError for an
+    axis out of range."""
+    axis = _axis(V, axis)
+    _check_block(block_size)
+    last = V.movedim(axis, -1)
+    n = last.shape[-1]
+    nb = -(-n // block_size)
+    data = last.new_zeros(*last.shape[:-1], nb * block_size)
+    data[..., :n] = last
+    return Blocks(data.view(*last.shape[:-1], nb, block_size), axis, n)
+
+
+def codes_from_blocks(P: torch.Tensor, b: Blocks) -> torch.Tensor:
+    """Codes in block form (..., nblocks, block_size) back in the layout of the tensor `b` was cut from, the
+    padding dropped, contiguous (mxq/block/_driver.py:35-37)."""
+    rows = P.flatten(-2)
+    return rows.narrow(-1, 0, b.n).movedim(-1, b.axis).contiguous()
+
+
+def scales_from_blocks(X: torch.Tensor, b: Blocks) -> torch.Tensor:
+    """Scales in block form (..., nblocks, 1) in the layout of that tensor with its axis nblocks long,
+    contiguous (mxq/block/_driver.py:40-42)."""
+    return X.squeeze(-1).movedim(-1, b.axis).contiguous()
 
 
 def _view3(shape, axis: int):
@@ -94,24 +129,15 @@ def compose(V: torch.Tensor, *, scale: Optional[Callable[[torch.Tensor], torch.T
     if scale is None and elem is None:
         return quantize_fused(V, axis, block_size, _lib.BlockSpec())
     V = V.to(torch.float32)
-    axis = _axis(V, axis)
-    _check_block(block_size)
-    Vt = V.movedim(axis, -1)
-    n = Vt.shape[-1]
-    pad = (-n) % block_size
-    if pad:
-        Vt = F.pad(Vt, (0, pad))
-    data = Vt.reshape(*Vt.shape[:-1], -1, block_size)
+    b = to_blocks(V, axis, block_size)
     if scale is None:
-        X = torch.ones(data.shape[:-1] + (1,), dtype=torch.float32, device=V.device)
-        z = data
+        X = torch.ones(b.data.shape[:-1] + (1,), dtype=torch.float32, device=V.device)
+        z = b.data
     else:
-        X = scale(data.abs().amax(dim=-1, keepdim=True))
-        z = data / X
+        X = scale(b.data.abs().amax(dim=-1, keepdim=True))
+        z = b.data / X
     P = z.clone() if elem is None else elem(z)
-    P = P.reshape(*P.shape[:-2], -1)[..., :n].movedim(-1, axis).contiguous()
-    X = X.squeeze(-1).movedim(-1, axis).contiguous()
-    return P, X
+    return codes_from_blocks(P, b), scales_from_blocks(X, b)
 
 
 def dequantize(P: torch.Tensor, X: torch.Tensor, axis: int = 0, block_size: int = BLOCK) -> torch.Tensor:

@@ -1,4 +1,4 @@
-"""Element quantization to float(e, m) on one of three grids (mxq/element_quant/float_em.py:1-134), on the GPU.
+"""Element quantization to float(e, m) on one of three grids (mxq/element_quant/float_em.py:1-123), on the GPU.
 
     grid="qtorch"   qtorch 0.2.0 float_quantize: round the float32 bits at m, clip the biased exponent to
                     [127-L, 127+L] (L = 2^(e-1)-1): top exponent reserved, one binade of fake subnormals at

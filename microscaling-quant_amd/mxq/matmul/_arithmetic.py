@@ -153,9 +153,10 @@ def MXGEMMINI(prod_e: int = 4, prod_m: int = 3, prod_floor: Optional[int] = PROD
                       kernel=KernelArith(_lib.ARITH_MXGEMMINI, prod_e, prod_m, prod_floor, st.limit, st.value))
 
 
-def compiled(arith_: Arithmetic) -> Arithmetic:
-    """The same Arithmetic under the name "compiled(...)".  The systolic kernel already runs a whole call as one
-    fused GPU kernel, bit-identical to the step-by-step rule, so no torch.compile graph is built."""
-    return Arithmetic(name=f"compiled({arith_.name})", product=arith_.product, acc_add=arith_.acc_add,
-                      tile_add=arith_.tile_add, fused_reduction=arith_.fused_reduction,
-                      fused_block=arith_.fused_block, fuse=arith_.fuse, kernel=arith_.kernel)
+def compiled(arith: Arithmetic) -> Arithmetic:
+    """The same Arithmetic under the name "compiled(...)" (mxq/matmul/_arithmetic.py:154-211).  The systolic kernel
+    already runs a whole call as one fused GPU kernel, bit-identical to the step-by-step rule, so no torch.compile
+    graph is built."""
+    return Arithmetic(name=f"compiled({arith.name})", product=arith.product, acc_add=arith.acc_add,
+                      tile_add=arith.tile_add, fused_reduction=arith.fused_reduction,
+                      fused_block=arith.fused_block, fuse=arith.fuse, kernel=arith.kernel)

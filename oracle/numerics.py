@@ -124,7 +124,7 @@ def bias(e):
 
 
 def float_em(z, e, m, rounding_mode="ties_away", grid="qtorch"):
-    """mxq/element_quant/float_em.py:50-61."""
+    """mxq/element_quant/float_em.py:39-50."""
     z = np.asarray(z)
     if (e, m) == (8, 23):
         if z.dtype == F64:
@@ -134,7 +134,7 @@ def float_em(z, e, m, rounding_mode="ties_away", grid="qtorch"):
 
 
 def _qtorch(z, e, m, rounding_mode):
-    """mxq/element_quant/float_em.py:64-84."""
+    """mxq/element_quant/float_em.py:53-73."""
     z32 = f32(z)
     bits = bits_of(z32)
     q = round_bits(bits, m, rounding_mode)
@@ -154,7 +154,7 @@ def _qtorch(z, e, m, rounding_mode):
 
 
 def _ieee(z, e, m, rounding_mode):
-    """mxq/element_quant/float_em.py:87-110."""
+    """mxq/element_quant/float_em.py:76-99."""
     x = np.asarray(z)
     x = x if x.dtype == F64 else x.astype(F64 if e == 8 else F32)
     dt = x.dtype.type
@@ -176,7 +176,7 @@ def _ieee(z, e, m, rounding_mode):
 
 
 def _ocp(z, e, m, rounding_mode):
-    """mxq/element_quant/float_em.py:113-134."""
+    """mxq/element_quant/float_em.py:102-123."""
     f = next((v for v in FORMATS.values() if (v[0], v[1]) == (e, m)), None)
     if f is None:
         raise ValueError(f"grid='ocp' is defined only for the OCP element formats, not (e={e}, m={m})")

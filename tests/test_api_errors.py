@@ -150,6 +150,7 @@ def test_arithmetic_names():
     assert matmul.MXGEMMINI().name == "mxgemmini(prod=e4m3)"
     assert matmul.MXQUANT(4, 3).name == "mxquant(prod=e4m3)"
     assert matmul.compiled(matmul.MXGEMMINI()).name.startswith("compiled(")
+    assert matmul.compiled(arith=matmul.MXQUANT(4, 3)).name == "compiled(mxquant(prod=e4m3))"   # the reference's keyword
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the behaviour without a GPU")

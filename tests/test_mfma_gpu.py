@@ -255,3 +255,29 @@ def test_wave_block_shapes_agree(cuda):
     for c in (0, 1024, 1920):
         part = mfa.mfma_accum(t(PA), t(XA), t(PB[:, c:c + 128]), t(XB[:, c:c + 128]), "MXFP8_E4M3").cpu().numpy()
         assert np.array_equal(part.view(np.uint32), whole[:, c:c + 128].view(np.uint32)), c
+
+
+@pytest.mark.parametrize("K, M, N", [(4096, 96, 160), (1000, 33, 70)])
+def test_fp64_accum_against_oracle(cuda, K, M, N):
+    """mxq.fp64_accum (dequantize kernel, float64 GEMM on the device) against the oracle's fp64_accum (numpy's
+    float64 product): each output within its stated 1 float32 ulp (the two float64 sums run in different orders;
+    they round to different float32 values only where the float64 sum lies next to a float32 rounding
+    boundary), most of them equal; integer-valued operands, whose float64 sums are exact, bit for bit."""
+    import mxq
+    from oracle import systolic as osys
+    rng = np.random.default_rng(K + M)
+    pa, xa = ob.mxgemmini_quantize(rng.standard_normal((K, M)).astype(np.float32), "MXFP8_E4M3", 0)
+    pb, xb = ob.mxgemmini_quantize((rng.standard_normal((K, N)) * 0.02).astype(np.float32), "MXFP8_E4M3", 0)
+    t = [torch.from_numpy(x).cuda() for x in (pa, xa, pb, xb)]
+    got = mxq.fp64_accum(*t).cpu().numpy()
+    want = osys.fp64_accum(pa, xa, pb, xb)
+    gi, wi = got.view(np.int32).astype(np.int64), want.view(np.int32).astype(np.int64)
+    assert np.all((np.sign(got) == np.sign(want)) | (got == 0) | (want == 0))
+    assert np.abs(gi - wi).max() <= 1, "more than 1 float32 ulp apart"
+    assert (gi == wi).mean() >= 0.99
+    ia = rng.integers(-8, 9, (K, M)).astype(np.float32)
+    ib = rng.integers(-8, 9, (K, N)).astype(np.float32)
+    ones_a = np.ones((-(-K // 32), M), np.float32)
+    ones_b = np.ones((-(-K // 32), N), np.float32)
+    got = mxq.fp64_accum(*(torch.from_numpy(x).cuda() for x in (ia, ones_a, ib, ones_b))).cpu().numpy()
+    assert np.array_equal(got, osys.fp64_accum(ia, ones_a, ib, ones_b))

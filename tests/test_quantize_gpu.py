@@ -240,3 +240,32 @@ def test_c3_full_size_column_slices(cuda):
             D = block.mxgemmini.dequantize(P[:, c].contiguous(), X[:, c].contiguous(), axis=0).cpu().numpy()
             assert_bits_equal(D, ob.dequantize(wP, wX, 0), f"C3 dequantize {fmt} {c}")
         del P, X
+
+
+def test_compose_with_callables(cuda):
+    """block.compose with callables the fused kernel does not take (the reference's generic composition on the
+    device): the library's own scale and element functions passed as callables, a user's torch pair, and each
+    step left out, on 2-D and 3-D inputs with padded last blocks and negative axes, against the oracle's compose
+    with the numpy twins."""
+    from functools import partial
+
+    from mxq import block, element_quant, scale_factor
+    rng = np.random.default_rng(12)
+    pairs = [
+        (lambda a: scale_factor.mxquant(a), partial(element_quant.float_em.quantize, e=4, m=3, rounding_mode="rne",
+                                                    grid="ocp"),
+         lambda a: nx.scale_mxquant(a), lambda z: nx.float_em(z, 4, 3, "rne", "ocp")),
+        (lambda a: torch.where(a > 0, a, torch.ones_like(a)), lambda z: torch.round(z * 16) / 16,
+         lambda a: np.where(a > 0, a, np.float32(1)).astype(np.float32),
+         lambda z: (np.round(z * np.float32(16)) / np.float32(16)).astype(np.float32)),
+        (None, lambda z: torch.round(z * 4) / 4, None, lambda z: (np.round(z * np.float32(4)) / 4).astype(np.float32)),
+        (lambda a: scale_factor.mxquant(a), None, lambda a: nx.scale_mxquant(a), None),
+    ]
+    for shape, axis, bs in [((100, 40), 0, 32), ((3, 70, 5), -2, 32), ((48, 33), -1, 16)]:
+        V = (rng.standard_normal(shape) * 3).astype(np.float32)
+        for ts, te, ns, ne in pairs:
+            P, X = block.compose(torch.from_numpy(V).cuda(), scale=ts, elem=te, axis=axis, block_size=bs)
+            assert P.device.type == "cuda" and P.is_contiguous() and X.is_contiguous()
+            wP, wX = ob.compose(V, ns, ne, axis, bs)
+            assert_bits_equal(P.cpu().numpy(), wP, f"compose P {shape} axis {axis}")
+            assert_bits_equal(X.cpu().numpy(), wX, f"compose X {shape} axis {axis}")
