@@ -30,13 +30,9 @@ SIZE = 16
 FORMATS = ("MXFP6_E3M2", "MXFP6_E2M3", "MXFP8_E5M2", "MXFP8_E4M3")
 
 
-def _split(code: int, e: int, m: int):
-    return (code >> (e + m)) & 1, (code >> m) & ((1 << e) - 1), code & ((1 << m) - 1)
-
-
 def _fixed(code: int, e: int, m: int) -> int:
     """The finder's signed fixed point of an element code."""
-    sign, ex, man = _split(code, e, m)
+    sign, ex, man = (code >> (e + m)) & 1, (code >> m) & ((1 << e) - 1), code & ((1 << m) - 1)
     if (e, m) == (2, 3):                              # E2M3: value * 8 exactly, no mask
         mag = man if ex == 0 else ((8 + man) << (ex - 1))
         return -mag if sign else mag
@@ -66,34 +62,57 @@ def _format(fmt: Union[str, Format]) -> Format:
     return f
 
 
+def _code_fields(e: int, m: int) -> torch.Tensor:
+    """Every code of a (1 + e + m)-bit element format as rows (sign, exponent field, mantissa field), int64."""
+    codes = torch.arange(1 << (1 + e + m), dtype=torch.int64)
+    return torch.stack([codes >> (e + m), (codes >> m) & ((1 << e) - 1), codes & ((1 << m) - 1)])
+
+
+def _code_values(e: int, m: int) -> torch.Tensor:
+    """The value of every code, float32: significand (the mantissa, plus 2^m unless subnormal) times 2 to the
+    power (max(exponent field, 1) - bias - m), signed.  E5M2 alone reserves its top exponent for Inf and NaN;
+    the other formats' top codes are ordinary values (E4M3's S.1111.111 is 480 on MX-Gemmini)."""
+    sign, ex, man = _code_fields(e, m)
+    bias = (1 << (e - 1)) - 1
+    sig = torch.where(ex == 0, man, man + (1 << m)).to(torch.float64)
+    mag = torch.ldexp(sig, (ex.clamp(min=1) - bias - m).to(torch.float64))
+    if (e, m) == (5, 2):
+        top = ex == (1 << e) - 1
+        mag = torch.where(top & (man == 0), torch.tensor(float("inf"), dtype=torch.float64), mag)
+        mag = torch.where(top & (man != 0), torch.tensor(float("nan"), dtype=torch.float64), mag)
+    return torch.where(sign == 1, -mag, mag).to(torch.float32)
+
+
+def _safe_values(vals: torch.Tensor, fx: torch.Tensor) -> torch.Tensor:
+    """Of the finite codes sharing one fixed point, the value of smallest magnitude (the earliest code when
+    magnitudes tie, so +0 over -0); those values once each, ascending."""
+    finite = torch.isfinite(vals).nonzero().flatten()
+    by_mag = finite[torch.sort(vals[finite].abs(), stable=True).indices]     # finite codes, smallest |v| first
+    _, point = torch.unique(fx[by_mag], return_inverse=True)                 # each code's fixed-point class
+    head = torch.full((int(point.max()) + 1,), by_mag.numel(), dtype=torch.int64)
+    head.scatter_reduce_(0, point, torch.arange(by_mag.numel()), reduce="amin")   # each class's first code
+    chosen = vals[by_mag[head]]
+    return torch.unique(torch.where(chosen == 0, torch.zeros_like(chosen), chosen))   # one +0, ascending
+
+
 @lru_cache(maxsize=None)
 def _tables(name: str):
-    """(all code values float32, all code fixed points int64, finder-safe values float32 ascending), on the CPU."""
+    """(every code's value float32, every code's fixed point int64, finder-safe values float32 ascending), on
+    the CPU."""
     f = _format(name)
-    e, m = f.e, f.m
-    n = 1 << (1 + e + m)
-    b = (1 << (e - 1)) - 1
-    vals = []
-    for c in range(n):
-        s, ex, man = _split(c, e, m)
-        if (e, m) == (5, 2) and ex == 0x1F:           # E5M2 alone keeps IEEE Inf / NaN codes
-            v = float("nan") if man else float("inf")
-        elif ex == 0:
-            v = man * 2.0 ** (1 - b - m)
-        else:
-            v = (1.0 + man / (1 << m)) * 2.0 ** (ex - b)
-        vals.append(-v if s else v)
-    fx = [_fixed(c, e, m) for c in range(n)]
-    keep = {}                                         # fixed point -> value of smallest magnitude
-    for c in range(n):
-        v = vals[c]
-        if v != v or v in (float("inf"), float("-inf")):
-            continue
-        if fx[c] not in keep or abs(v) < abs(keep[fx[c]]):
-            keep[fx[c]] = v
-    safe = sorted(set(keep.values()))                 # one zero (-0.0 == 0.0)
-    return (torch.tensor(vals, dtype=torch.float32), torch.tensor(fx, dtype=torch.int64),
-            torch.tensor(safe, dtype=torch.float32))
+    vals = _code_values(f.e, f.m)
+    fx = torch.tensor([_fixed(c, f.e, f.m) for c in range(vals.numel())], dtype=torch.int64)
+    return vals, fx, _safe_values(vals, fx)
+
+
+@lru_cache(maxsize=None)
+def _encoder(name: str):
+    """(distinct value bit patterns ascending, the lowest code holding each), int64 on the CPU."""
+    bits = _tables(name)[0].view(torch.int32).to(torch.int64)
+    keys, where = torch.unique(bits, return_inverse=True)
+    lowest = torch.full((keys.numel(),), bits.numel(), dtype=torch.int64)
+    lowest.scatter_reduce_(0, where, torch.arange(bits.numel()), reduce="amin")
+    return keys, lowest
 
 
 @lru_cache(maxsize=None)
@@ -106,9 +125,8 @@ def _grid(name: str):
 
 
 def decode(codes: torch.Tensor, fmt: Union[str, Format]) -> torch.Tensor:
-    """Element codes (integers) -> their float32 values."""
-    table = _tables(_format(fmt).name)[0].to(codes.device)
-    return table[codes.long()]
+    """Element codes (integers) -> their float32 values (a gather from the format's code table)."""
+    return _tables(_format(fmt).name)[0].to(codes.device)[codes.long()]
 
 
 def values(fmt: Union[str, Format]) -> torch.Tensor:
@@ -117,18 +135,17 @@ def values(fmt: Union[str, Format]) -> torch.Tensor:
 
 
 def encode(T: torch.Tensor, fmt: Union[str, Format]) -> torch.Tensor:
-    """Exact values -> element codes (the lowest code of each value).  Raises on a value the format lacks."""
+    """Exact values -> element codes (the lowest code of each value's bit pattern).  Raises ValueError on a value
+    the format lacks."""
     f = _format(fmt)
-    table = _tables(f.name)[0]
-    lookup = {}
-    for c, bits in enumerate(table.view(torch.int32).tolist()):
-        lookup.setdefault(bits, c)
-    flat = T.detach().to("cpu", torch.float32).reshape(-1).view(torch.int32).tolist()
-    missing = [b for b in flat if b not in lookup]
-    if missing:
-        bad = torch.tensor(missing[:1], dtype=torch.int32).view(torch.float32).item()
+    keys, lowest = _encoder(f.name)
+    bits = T.detach().to("cpu", torch.float32).reshape(-1).view(torch.int32).to(torch.int64)
+    at = torch.searchsorted(keys, bits).clamp(max=keys.numel() - 1)
+    found = keys[at] == bits
+    if not bool(found.all()):
+        bad = bits[~found][:1].to(torch.int32).view(torch.float32).item()
         raise ValueError(f"mxq.lut: {bad!r} is not an exact {f.name} value, so it cannot be a table entry")
-    return torch.tensor([lookup[b] for b in flat], dtype=torch.int64, device=T.device).reshape(T.shape)
+    return lowest[at].reshape(T.shape).to(T.device)
 
 
 def finder(codes: torch.Tensor, T: torch.Tensor, fmt: Union[str, Format], *, group: int) -> torch.Tensor:

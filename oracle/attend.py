@@ -2,18 +2,20 @@
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 
-`attend` follows mxq/nn/_attention.py:70-143: per batch row and KV head, K^T and V quantized once; queries
-taken `step` at a time, the query heads of one KV head side by side (head-major columns) up to a multiple of
-`rows` and the rest head by head; S = fl(reduce * scale), + mask, softmax, P^T quantized, O = reduce over the
-key blocks some query still sees (mxq/nn/_attention.py:108-141, the SLACK bound of :60-62 and _amax of :65-67).
+`attend` follows mxq/nn/_attention.py:70-143 (vector None or "bf16"): per batch row and KV head, K^T and V
+quantized once; queries taken `step` at a time, the query heads of one KV head side by side (head-major columns)
+up to a multiple of `rows` and the rest head by head; S = fl(reduce * scale), + mask, softmax, P^T quantized,
+O = reduce over the key blocks some query still sees (mxq/nn/_attention.py:108-141, the SLACK bound of :60-62
+and _amax of :65-67).
 
 The quantizers, reducers and softmax are callables on numpy float32 arrays, so the same loop runs with the
 oracle's block quantizers and systolic reducer, and with whichever softmax produced the probabilities under
 test (torch.softmax on a given device): S and O are then pinned bit for bit, the softmax itself is torch's.
 
 Pins: the reference's own outputs on four shapes (tests/golden/attend.npz: chunking, GQA, padding-free and
-causal masks, the key-block skip) with torch's CPU softmax; with no mask and one chunk it reduces to
-softmax(A^T B * scale) V over the oracle reducers, which the tests check directly.
+causal masks, the key-block skip) with torch's CPU softmax, and on three with vector="bf16"
+(tests/golden/vector.npz) with oracle/vector.py's rounded softmax over torch's CPU exp and sum; with no mask
+and one chunk it reduces to softmax(A^T B * scale) V over the oracle reducers, which the tests check directly.
 """
 import math
 
@@ -40,8 +42,12 @@ def amax_rows(P, X, block_size):
         return (np.abs(P) * Xr).astype(F32).max(axis=1).astype(F64)
 
 
-def attend(q, k, v, mask, scale, qk, pv, softmax, chunk=None):
-    """mxq/nn/_attention.py:70-143 with vector=None.  q: B x H x Tq x D, k, v: B x Hkv x Tk x D."""
+def attend(q, k, v, mask, scale, qk, pv, softmax, chunk=None, vector=None):
+    """mxq/nn/_attention.py:70-143.  q: B x H x Tq x D, k, v: B x Hkv x Tk x D.  vector=None or "bf16": with
+    "bf16" the score steps S * scale and + mask are rounded to bf16 (oracle/vector.py's rounder), and `softmax`
+    is expected to be the rounded one (oracle.vector.softmax_bf16 with the device's exp and row sum)."""
+    from .vector import rounder
+    r = rounder(vector)
     q, k, v = (np.asarray(t, F32) for t in (q, k, v))
     B, H, Tq, D = q.shape
     Hkv, Tk = k.shape[1], k.shape[2]
@@ -87,13 +93,13 @@ def attend(q, k, v, mask, scale, qk, pv, softmax, chunk=None):
                         else:
                             hi = min(Tk, bv)
                     with np.errstate(all="ignore"):
-                        live = (qk.reduce(AP, AX, KP[:, lo:hi], KX[:, lo:hi]) * sc).astype(F32)
+                        live = r((qk.reduce(AP, AX, KP[:, lo:hi], KX[:, lo:hi]) * sc).astype(F32))
                         if mb is not None:
-                            live = (live.reshape(n, m, hi - lo) + mb[s0:e0, lo:hi]).astype(F32).reshape(n * m, -1)
+                            live = r((live.reshape(n, m, hi - lo) + mb[s0:e0, lo:hi]).astype(F32)).reshape(n * m, -1)
                     if lo == 0 and hi == Tk:
                         S = live
                     else:
-                        S = np.tile(np.asarray(mb[s0:e0], F32), (n, 1))
+                        S = np.tile(r(np.asarray(mb[s0:e0], F32)), (n, 1))
                         S.reshape(n, m, Tk)[:, :, lo:hi] = live.reshape(n, m, hi - lo)
                     P = np.asarray(softmax(S), F32)
                     if (lo or hi < Tk) and (P[:, :lo].any() or P[:, hi:].any()):

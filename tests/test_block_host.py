@@ -35,3 +35,26 @@ def test_to_blocks_keeps_dtype_and_rejects_bad_axis():
     assert torch.equal(b.data[0, 1, 8:], torch.zeros(24, dtype=torch.bfloat16))
     with pytest.raises(IndexError, match="axis"):
         _driver.to_blocks(V, 2, 32)
+
+
+def test_lut_host_tables_against_reference_fixtures():
+    """mxq.lut's host-side tables (no kernel): values, decode, and encode back to codes, against the reference's
+    own outputs (tests/golden/lut_*.npz) for the four LUT formats."""
+    import os
+
+    from mxq import lut
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    for fmt in lut.FORMATS:
+        z = np.load(os.path.join(golden, f"lut_{fmt}.npz"), allow_pickle=False)
+        assert_bits_equal(lut.values(fmt).numpy(), z["values"], f"values {fmt}")
+        dec = lut.decode(torch.from_numpy(z["decode_codes"]), fmt).numpy()
+        assert_bits_equal(dec, z["decode"], f"decode {fmt}")
+        finite = np.isfinite(dec)
+        codes = lut.encode(torch.from_numpy(dec[finite]), fmt).numpy()
+        assert_bits_equal(lut.decode(torch.from_numpy(codes), fmt).numpy(), dec[finite], f"encode {fmt}")
+        first = {}
+        for c, b in enumerate(dec.view(np.uint32)):
+            first.setdefault(int(b), c)
+        assert [first[int(b)] for b in dec[finite].view(np.uint32)] == codes.tolist(), "lowest code of each value"
+        with pytest.raises(ValueError, match="not an exact"):
+            lut.encode(torch.tensor([0.3]), fmt)

@@ -99,19 +99,83 @@ def test_attend_against_oracle(cuda, case):
     assert_bits_equal(got, want, f"attend {case}")
 
 
+def _gpu_fn(fn):
+    """A numpy -> numpy callable running the torch call fn on the GPU (the device under test's library op)."""
+    return lambda x: fn(torch.from_numpy(np.ascontiguousarray(x)).cuda()).cpu().numpy()
+
+
+GPU_EXP = _gpu_fn(torch.exp)
+GPU_ROWSUM = _gpu_fn(lambda t: t.sum(-1, keepdim=True))
+GPU_MEAN = _gpu_fn(lambda t: t.mean(-1, keepdim=True))
+GPU_RSQRT = _gpu_fn(torch.rsqrt)
+
+
+def _bf16_steps_apart(a, b):
+    """How many bf16 steps two bf16-valued float32 arrays are apart, elementwise (as integers)."""
+    return np.abs((a.view(np.int32) >> 16).astype(np.int64) - (b.view(np.int32) >> 16).astype(np.int64))
+
+
+def test_vector_bf16_softmax_and_rmsnorm(cuda):
+    """vector="bf16" softmax and RMSNorm on the GPU: bit for bit against oracle/vector.py given the GPU's exp,
+    sum, mean and rsqrt (every step around those library calls, and every bf16 rounding, pinned); against the
+    reference's own CPU outputs (tests/golden/vector.npz) they differ only where those library calls do: at most
+    1 bf16 step, on at most 2 % of the outputs."""
+    from mxq.nn import _vector
+    from oracle import vector as ov
+    z = np.load(os.path.join(GOLDEN, "vector.npz"), allow_pickle=False)
+    S = z["softmax_S"]
+    got = _vector.softmax(torch.from_numpy(S).cuda(), "bf16").cpu().numpy()
+    assert_bits_equal(got, ov.softmax_bf16(S, GPU_EXP, GPU_ROWSUM), "softmax bf16 vs oracle")
+    d = _bf16_steps_apart(got, z["softmax_bf16"])
+    assert d.max() <= 1 and (d > 0).mean() <= 0.02, (d.max(), (d > 0).mean())
+    dt = {"torch.bfloat16": torch.bfloat16, "torch.float32": torch.float32}
+    for i in range(3):
+        xd, wd = (dt[str(v)] for v in z[f"rms{i}_dtypes"])
+        x = torch.from_numpy(z[f"rms{i}_x"]).to(xd).cuda()
+        w = torch.from_numpy(z[f"rms{i}_w"]).to(wd).cuda()
+        for prec in (None, "bf16"):
+            got = _vector.rmsnorm(x, w, 1e-6, prec).float().cpu().numpy()
+            want = ov.rmsnorm(z[f"rms{i}_x"], z[f"rms{i}_w"], 1e-6, prec, GPU_MEAN, GPU_RSQRT,
+                              xd == torch.bfloat16, wd == torch.bfloat16)
+            assert_bits_equal(got, want, f"rmsnorm {xd} x {wd} {prec} vs oracle")
+            ref = z[f"rms{i}_{prec}"]
+            if prec == "bf16" or (xd == torch.bfloat16 and wd == torch.bfloat16):
+                d = _bf16_steps_apart(got, ref)
+                assert d.max() <= 1 and (d > 0).mean() <= 0.02, (xd, wd, prec, d.max())
+            else:
+                np.testing.assert_allclose(got, ref, rtol=2.0 ** -20, atol=0)
+
+
 def test_attend_vector_bf16(cuda):
-    """vector="bf16": every softmax step rounded; the bf16 rounding is the library's kernel."""
+    """attend with vector="bf16" (score steps and softmax rounded) on the reference's three fixture shapes and on
+    a batched causal shape: bit for bit against oracle/attend.py with oracle/vector.py's softmax over the GPU's
+    exp and row sum; against the reference's CPU outputs the only difference allowed is what those library calls
+    leave (at most 2 % of outputs, none by more than 2^-4 of the largest |output|)."""
     import mxq
-    from mxq.nn._vector import softmax
-    g = torch.Generator().manual_seed(5)
-    S = (torch.randn(64, 96, generator=g) * 4).cuda()
-    P = softmax(S, "bf16")
-    r = lambda x: x.to(torch.bfloat16).float()                                         # noqa: E731
-    e = r(torch.exp(r(S - S.amax(-1, keepdim=True))))
-    assert torch.equal(P, r(e / r(e.sum(-1, keepdim=True))))
-    q, k, v = (torch.randn(1, 2, 64, 32, generator=g).cuda() for _ in range(3))
-    o = mxq.nn.attend(q, k, v, _causal(1, 64, 64).cuda(), 32 ** -0.5, _hw(mxq), _hw(mxq), vector="bf16")
-    assert torch.isfinite(o).all()
+    from functools import partial
+
+    from oracle import vector as ov
+    z = np.load(os.path.join(GOLDEN, "vector.npz"), allow_pickle=False)
+    sm = partial(ov.softmax_bf16, exp=GPU_EXP, rowsum=GPU_ROWSUM)
+    hwo = _hw_oracle()
+    t = lambda a: None if a is None else torch.from_numpy(a).cuda()                   # noqa: E731
+    for i in range(3):
+        B, H, Hkv, T, D, masked, chunk = (int(x) for x in z[f"c{i}_meta"])
+        q, k, v = z[f"c{i}_q"], z[f"c{i}_k"], z[f"c{i}_v"]
+        mask = z[f"c{i}_mask"] if masked else None
+        chunk = None if chunk < 0 else chunk
+        got = mxq.nn.attend(t(q), t(k), t(v), t(mask), D ** -0.5, _hw(mxq), _hw(mxq), chunk=chunk,
+                            vector="bf16").cpu().numpy()
+        want = oatt.attend(q, k, v, mask, D ** -0.5, hwo, hwo, sm, chunk=chunk, vector="bf16")
+        assert_bits_equal(got, want, f"attend vector bf16 c{i} vs oracle")
+        o_ref = z[f"c{i}_o"]
+        assert (got != o_ref).mean() <= 0.02 and np.abs(got - o_ref).max() <= np.abs(o_ref).max() * 2.0 ** -4
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(1, h, 256, 64, generator=g) for h in (4, 2, 2))
+    mask = _causal(1, 256, 256)
+    got = mxq.nn.attend(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), 0.125, _hw(mxq), _hw(mxq), vector="bf16")
+    want = oatt.attend(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), 0.125, hwo, hwo, sm, vector="bf16")
+    assert_bits_equal(got.cpu().numpy(), want, "attend vector bf16 batched 1x4x256x64 GQA 2:1")
 
 
 def test_mxlinear_against_oracle(cuda):

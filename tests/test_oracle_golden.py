@@ -1,6 +1,7 @@
 """The oracle against the fixtures the reference itself wrote (tests/golden/make_golden.py): the functions only
 an import of the reference pins -- LUT tables, safe sets and finder, ocp_no_clip, microxcaling "even", the
 composed systolic datapaths."""
+import json
 import os
 
 import numpy as np
@@ -112,3 +113,81 @@ def test_attend(case):
     side = _hw_side()
     got = oatt.attend(q, k, v, mask, scale, side, side, _torch_cpu_softmax, chunk=chunk)
     assert_bits_equal(got, o, f"attend c{i}")
+
+
+def _tree_cases():
+    z = _load("trees.npz")
+    return [tuple(c) for c in json.loads(str(z["cases"]))]
+
+
+@pytest.mark.parametrize("case", _tree_cases(), ids=lambda c: c[0])
+def test_trees(case):
+    """oracle/trees.py against the reference's anchor_tree and adder_tree on the cases tests/golden/make_golden.py
+    lists: widths 1-16, sizes 2-32, falling level widths, both drops, emin, headroom, MXGEMMINI and MXQUANT,
+    four code formats, K tails, zero rows, columns and blocks."""
+    from oracle import trees as otr
+    name, tree, (aname, aargs), fmt, K, M, N, kw = case
+    z = _load("trees.npz")
+    ops = [z[f"{name}_{k}"] for k in ("PA", "XA", "PB", "XB")]
+    ar = getattr(nx, aname)(*aargs)
+    kw = dict(kw)
+    if "schedule" in kw:
+        kw["schedule"] = [tuple(x) for x in kw["schedule"]]
+    if tree == "anchor":
+        Y = otr.anchor_tree(*ops, ar, **kw)
+    else:
+        Y = otr.adder_tree(*ops, ar, kw.pop("schedule"), **kw)
+    assert_bits_equal(Y, z[f"{name}_Y"], f"{tree} tree {name}")
+
+
+def _cpu_exp(x):
+    import torch
+    return torch.exp(torch.from_numpy(np.ascontiguousarray(x))).numpy()
+
+
+def _cpu_rowsum(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).sum(-1, keepdim=True).numpy()
+
+
+def _cpu_mean(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).mean(-1, keepdim=True).numpy()
+
+
+def _cpu_rsqrt(x):
+    import torch
+    return torch.rsqrt(torch.from_numpy(np.ascontiguousarray(x))).numpy()
+
+
+def test_vector_bf16_softmax_and_rmsnorm():
+    """oracle/vector.py against the reference's vector="bf16" softmax (with -inf and finfo.min scores) and its
+    RMSNorm, rounded and not, on bf16 and float32 activations and weights, with torch's CPU exp, sum, mean and
+    rsqrt as the reference calls them."""
+    from oracle import vector as ov
+    z = _load("vector.npz")
+    assert_bits_equal(ov.softmax_bf16(z["softmax_S"], _cpu_exp, _cpu_rowsum), z["softmax_bf16"], "softmax bf16")
+    for i in range(3):
+        xd, wd = (str(d) for d in z[f"rms{i}_dtypes"])
+        for prec in (None, "bf16"):
+            y = ov.rmsnorm(z[f"rms{i}_x"], z[f"rms{i}_w"], 1e-6, prec, _cpu_mean, _cpu_rsqrt,
+                           xd == "torch.bfloat16", wd == "torch.bfloat16")
+            assert_bits_equal(y, z[f"rms{i}_{prec}"], f"rmsnorm {xd} x {wd} {prec}")
+
+
+def test_vector_bf16_attend():
+    """oracle/attend.py with vector="bf16" against the reference's attend on three shapes (GQA 2:1 causal, chunks
+    of 16, batch 2 with no mask)."""
+    from functools import partial
+
+    from oracle import attend as oatt
+    from oracle import vector as ov
+    z = _load("vector.npz")
+    q = lambda V: ob.mxgemmini_quantize(V, "MXFP8_E4M3", 0)                           # noqa: E731
+    hw = oatt.Side(q, q, lambda *ops: osys.systolic(*ops, nx.MXGEMMINI(), osys.HW_FINAL))
+    sm = partial(ov.softmax_bf16, exp=_cpu_exp, rowsum=_cpu_rowsum)
+    for i in range(3):
+        B, H, Hkv, T, D, masked, chunk = (int(x) for x in z[f"c{i}_meta"])
+        o = oatt.attend(z[f"c{i}_q"], z[f"c{i}_k"], z[f"c{i}_v"], z[f"c{i}_mask"] if masked else None, D ** -0.5,
+                        hw, hw, sm, chunk=None if chunk < 0 else chunk, vector="bf16")
+        assert_bits_equal(o, z[f"c{i}_o"], f"attend vector bf16 c{i}")
