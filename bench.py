@@ -1,6 +1,7 @@
 """Benchmark: emulated MX GEMM throughput of matmul.systolic (bit-exact MXGEMMINI, HW_FINAL ladder) on one GPU,
 plus block-quantize HBM throughput, the LUT pipeline, the attention core, the adder and anchor trees and the
-matrix-core comparison product, each next to its roofline, and the oracle's CPU rate.
+matrix-core comparison product, each next to its roofline, the oracle's CPU rate on the same work, and a
+parity check of what was timed against the oracle.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
     python bench.py --copy-calibration        # only a 256 MiB device copy, 5 times (counter calibration)
@@ -11,8 +12,14 @@ W 4096 x 4096 ~ N(0, 0.02), both block.mxgemmini MXFP8_E4M3 codes along K: M = 5
 operands and scales resident in HBM.  `value` is emulated GEMM ops per second (2 per MAC) over the timed
 steps.  `roofline.achieved` uses the fast systolic kernel's own average duration, timed with HIP events the
 library records around each of its launches on the launch's stream.  One JSON line is printed.
+
+CPU baselines: the oracle (a numpy restatement of the reference's algorithms) on the host cores, in a process
+pool forked before anything touches the GPU, on the same seeded inputs: C2 on a column slice, C1 and C3 at full
+size, C4's LUT quantize at full size and its product on a column slice, C5 on two of its 32 heads.  The oracle's
+results are then compared with the timed GPU outputs (`parity` in each line).
 """
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -27,14 +34,199 @@ METRIC = "emulated MX GEMM GOP/s (systolic, bit-exact) + quantize GB/s vs HBM ro
 HBM_PEAK_GBS = 8000.0
 # MI355X's published vector FP32 peak, 157.3 TFLOP/s, is 78.6 T FMA lane-operations per second: the rate at which
 # its 1024 SIMDs retire 32-bit VALU lanes (256 CUs x 128 lanes/clk x 2.4 GHz).  The fast systolic kernel is
-# measured above the single-issue 64 lanes/clk/CU figure (SQ_INSTS_VALU x 64 / duration = 45.5 T lane-ops/s),
+# measured above the single-issue 64 lanes/clk/CU figure (SQ_INSTS_VALU x 64 / duration = 48.7 T lane-ops/s),
 # so the 128-lane rate is the ceiling it is held against.
 VALU_LANE_OPS = 157.3e12 / 2
-OPS_PER_MAC_MODEL = 10                      # canonical datapath primitives per emulated MAC
+VALU_SINGLE_ISSUE = 256 * 64 * 2.4e9        # one wave64 VALU instruction per SIMD per 4 clocks
+OPS_PER_MAC_MODEL = 10                      # the datapath's primitives per emulated MAC (a model, not a count)
 VALU_ROOF_TOPS = VALU_LANE_OPS / OPS_PER_MAC_MODEL * 2 / 1e12   # 15.73 TOP/s emulated
 FP8_PEAK_TFLOPS = 5000.0                    # MI355X dense FP8 matrix-core peak
+MAX_POOL = 16                               # host processes for the CPU baselines (one GPU's CPU share)
+
+C3_FORMATS = ("MXFP8_E4M3", "MXFP8_E5M2", "MXFP6_E3M2", "MXFP6_E2M3", "MXFP4")
+C5_HEADS = (0, 31)
 
 
+# ------------------------------------------------------------------------------------------------ inputs
+def make_inputs(torch):
+    """Every line's seeded synthetic input, on the CPU (the GPU lines copy them over)."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(512, 4096, generator=g)
+    W = torch.randn(4096, 4096, generator=g) * 0.02
+    c1 = torch.randn(4096, 512, generator=torch.Generator().manual_seed(10))
+    # C3: Student-t (df 3) x 0.5, 0.1 % of the entries (seeded positions) x 100, bfloat16
+    torch.manual_seed(2)
+    t = torch.distributions.StudentT(torch.tensor(3.0)).sample((8192, 8192)) * 0.5
+    idx = torch.randperm(8192 * 8192, generator=torch.Generator().manual_seed(2))[:67109]
+    t.view(-1)[idx] *= 100
+    c3 = t.to(torch.bfloat16)
+    del t
+    c4a = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0))
+    c4b = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(1))
+    q, k, v = (torch.randn(1, 32, 2048, 128, generator=torch.Generator().manual_seed(i)) for i in range(3))
+    mask = torch.triu(torch.full((2048, 2048), torch.finfo(torch.float32).min), 1)[None, None]
+    return {"x": x, "W": W, "c1": c1, "c3": c3, "c4a": c4a, "c4b": c4b, "q": q, "k": k, "v": v, "mask": mask}
+
+
+def _digest(a):
+    import numpy as np
+    return hashlib.blake2b(np.ascontiguousarray(a).tobytes(), digest_size=16).hexdigest()
+
+
+# -------------------------------------------------------------------------------- CPU baselines (oracle)
+_DATA = {}                                   # numpy operands the forked workers read (copy on write)
+
+
+def _task_systolic(ops):
+    from oracle import numerics as nx
+    from oracle import systolic as osys
+    t0 = time.perf_counter()
+    Y = osys.systolic(*ops, nx.MXGEMMINI(), osys.HW_FINAL)
+    return time.perf_counter() - t0, Y
+
+
+def _task_quant(job):
+    from oracle import block as ob
+    key, fmt, c0, c1 = job
+    V = _DATA[key][:, c0:c1]
+    t0 = time.perf_counter()
+    if key == "c1":
+        P, X = ob.ocp_quantize(V, fmt, 0)
+    else:
+        P, X = ob.mxgemmini_quantize(V, fmt, 0, 32, "rne")
+    return time.perf_counter() - t0, _digest(P), _digest(X)
+
+
+def _task_lut(job):
+    from oracle import lut as ol
+    key, c0, c1 = job
+    t0 = time.perf_counter()
+    P, X = ol.lut_quantize(_DATA[key][:, c0:c1], "MXFP6_E3M2", 0, 32, "rne", 2.0 ** -23, 1, 50)
+    return time.perf_counter() - t0, P, X
+
+
+def _pool_map(pool, fn, jobs):
+    t0 = time.perf_counter()
+    out = pool.map(fn, jobs, chunksize=1)
+    return time.perf_counter() - t0, out
+
+
+def _tiles(pa, xa, pb, xb, rows, cols):
+    """Oracle systolic jobs over tiles of rows x cols outputs."""
+    M, N = pa.shape[1], pb.shape[1]
+    return [((r, c), (pa[:, r:r + rows], xa[:, r:r + rows], pb[:, c:c + cols], xb[:, c:c + cols]))
+            for r in range(0, M, rows) for c in range(0, N, cols)]
+
+
+def _assemble(M, N, where, parts):
+    import numpy as np
+    Y = np.zeros((M, N), np.float32)
+    for (r, c), (_, y) in zip(where, parts):
+        Y[r:r + y.shape[0], c:c + y.shape[1]] = y
+    return Y
+
+
+def cpu_baselines(inp, cores):
+    """The oracle on every line's work, timed on `cores` host processes (forked here, before any GPU use).
+    Returns {line: {"cpu_baseline": {...}, "oracle": what the parity check compares}}."""
+    import multiprocessing as mp
+
+    import numpy as np
+    import torch
+
+    from oracle import attend as oatt
+    from oracle import block as ob
+    host = f"{platform.processor() or platform.machine()}, numpy {np.__version__}"
+    _DATA.update(c1=inp["c1"].numpy(), c3=inp["c3"].float().numpy(), c4a=inp["c4a"].numpy(),
+                 c4b=inp["c4b"].numpy())
+    out = {}
+    with mp.get_context("fork").Pool(cores) as pool:
+        # C2: the oracle systolic on the first 32 x cores columns of the benchmark's codes
+        pa, xa = ob.mxgemmini_quantize(inp["x"].t().contiguous().numpy(), "MXFP8_E4M3", 0)
+        ncol = 32 * cores
+        pb, xb = ob.mxgemmini_quantize(inp["W"][:ncol].t().contiguous().numpy(), "MXFP8_E4M3", 0)
+        jobs = _tiles(pa, xa, pb, xb, pa.shape[1], 32)
+        dt, parts = _pool_map(pool, _task_systolic, [j for _, j in jobs])
+        macs = pa.shape[0] * pa.shape[1] * ncol
+        per_core = 2 * pa.shape[0] * pa.shape[1] * 32 / (sum(p[0] for p in parts) / len(parts)) / 1e9
+        out["c2"] = {"cpu_baseline": {
+            "value": round(2 * macs / dt / 1e9, 4), "unit": "GOP/s", "cores": cores, "kind": "port",
+            "single_core_GOPs": round(per_core, 4),
+            "sample": f"oracle systolic MXGEMMINI HW_FINAL on the benchmark's codes, M=512 x N={ncol} (columns "
+                      f"0..{ncol - 1}, 32 per process) x K=4096: {macs / 1e6:.0f} M MAC, {dt:.1f} s wall, "
+                      f"{sum(p[0] for p in parts):.1f} s of CPU work ({host})"},
+            "oracle": _assemble(512, ncol, [w for w, _ in jobs], parts), "cols": ncol}
+        # C1: block.ocp quantize of 4096 x 512 fp32, full size, 32 columns per job
+        jobs = [("c1", "MXFP8_E4M3", c, c + 32) for c in range(0, 512, 32)]
+        dt, parts = _pool_map(pool, _task_quant, jobs)
+        nbytes = 4096 * 512 * 8 + 128 * 512 * 4
+        out["c1"] = {"cpu_baseline": {
+            "value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"oracle block.ocp MXFP8_E4M3 quantize of the whole 4096 x 512 input, 16 column slices "
+                      f"({dt:.2f} s wall, {sum(p[0] for p in parts):.2f} s of CPU work)"},
+            "oracle": [(j, p[1], p[2]) for j, p in zip(jobs, parts)]}
+        # C3: block.mxgemmini quantize of bf16 8192 x 8192, five formats, full size, 512 columns per job
+        per_fmt, c3 = {}, {}
+        for fmt in C3_FORMATS:
+            jobs = [("c3", fmt, c, c + 512) for c in range(0, 8192, 512)]
+            dt, parts = _pool_map(pool, _task_quant, jobs)
+            per_fmt[fmt] = round((8192 * 8192 * 6 + 256 * 8192 * 4) / dt / 1e9, 3)
+            c3[fmt] = [(j, p[1], p[2]) for j, p in zip(jobs, parts)]
+        out["c3"] = {"cpu_baseline": {
+            "value": per_fmt, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": "oracle block.mxgemmini (rne) quantize of the whole bf16 8192 x 8192 input per format, 16 "
+                      "column slices; bytes as the GPU line counts them (bf16 in, float32 P and X out)"},
+            "oracle": c3}
+        # C4: block.lut of both 4096 x 4096 operands at full size (256 columns per job, whole column groups),
+        # then the LUT x LUT product on its last 32 columns (all 4096 rows, 256 per job)
+        lut = {}
+        for key in ("c4a", "c4b"):
+            jobs = [(key, c, c + 256) for c in range(0, 4096, 256)]
+            dt, parts = _pool_map(pool, _task_lut, jobs)
+            lut[key] = (dt, np.concatenate([p[1] for p in parts], axis=1), np.concatenate([p[2] for p in parts], axis=1))
+        pa, xa = lut["c4a"][1], lut["c4a"][2]
+        pb, xb = lut["c4b"][1][:, 4064:], lut["c4b"][2][:, 4064:]
+        jobs = _tiles(pa, xa, pb, xb, 256, 32)
+        dt_mm, parts = _pool_map(pool, _task_systolic, [j for _, j in jobs])
+        mm_macs = 4096 * 4096 * 32
+        out["c4"] = {"cpu_baseline": {
+            "value": {"lut_quantize_ms": round(lut["c4a"][0] * 1e3, 1),
+                      "systolic_GOPs": round(2 * mm_macs / dt_mm / 1e9, 4)},
+            "unit": "ms (block.lut of one operand), GOP/s (systolic)", "cores": cores, "kind": "port",
+            "sample": f"oracle block.lut MXFP6_E3M2 of a whole 4096 x 4096 operand (16 column slices); the oracle "
+                      f"systolic on columns 4064..4095 of the 4096^3 LUT x LUT product ({mm_macs / 1e6:.0f} M MAC, "
+                      f"{dt_mm:.1f} s wall)"},
+            "oracle": {"PA": lut["c4a"][1], "XA": lut["c4a"][2], "PB": lut["c4b"][1], "XB": lut["c4b"][2],
+                       "Y_cols": _assemble(4096, 32, [w for w, _ in jobs], parts)}}
+        # C5: the oracle attend on heads 0 and 31 (each its own KV head), torch's CPU softmax, reduces in the pool
+
+        def reduce(pa, xa, pb, xb):
+            rows = max(1, min(pa.shape[1], (1 << 14) // max(1, min(pb.shape[1], 64))))
+            jobs = _tiles(pa, xa, pb, xb, rows, min(pb.shape[1], 64))
+            parts = pool.map(_task_systolic, [j for _, j in jobs], chunksize=1)
+            return _assemble(pa.shape[1], pb.shape[1], [w for w, _ in jobs], parts)
+
+        qz = lambda V: ob.mxgemmini_quantize(V, "MXFP8_E4M3", 0)                  # noqa: E731
+        side = oatt.Side(qz, qz, reduce)
+        sm = lambda S: torch.softmax(torch.from_numpy(np.ascontiguousarray(S)), dim=-1).numpy()   # noqa: E731
+        hs = list(C5_HEADS)
+        t0 = time.perf_counter()
+        o = oatt.attend(inp["q"][:, hs].numpy(), inp["k"][:, hs].numpy(), inp["v"][:, hs].numpy(),
+                        inp["mask"].numpy(), 128 ** -0.5, side, side, sm)
+        dt = time.perf_counter() - t0
+        macs = 2 * len(hs) * 2048 * 2048 * 128
+        out["c5"] = {"cpu_baseline": {
+            "value": round(2 * macs / dt / 1e9, 4), "unit": "emulated GOP/s", "cores": cores, "kind": "port",
+            "ms_whole_call_estimate": round(dt * 32 / len(hs) * 1e3, 0),
+            "sample": f"oracle attend (quantizers, systolic reducer, torch CPU softmax) on heads 0 and 31 of the "
+                      f"32 (a 1/16 slice: each head is its own KV head), every key computed as the reference "
+                      f"does; {macs / 1e9:.2f} G MAC in {dt:.1f} s wall; the whole call's time is x16"},
+            "oracle": o}
+    _DATA.clear()
+    return out
+
+
+# -------------------------------------------------------------------------------------------- GPU timing
 def _events_ms(fn, steps, stream):
     import torch
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -64,73 +256,32 @@ def _kernel_ms(fn, steps, kernel):
     return total / n if n else None, n
 
 
-def _traffic(name):
-    """HBM bytes per launch for `name` from profiles/<name>_traffic.txt ("bytes_per_launch: N"), else None."""
-    path = os.path.join(REPO, "profiles", f"{name}_traffic.txt")
+def _profile_value(name, key):
+    """`key: N` from profiles/<name>.txt, else None."""
+    path = os.path.join(REPO, "profiles", f"{name}.txt")
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("bytes_per_launch:"):
-                    return float(line.split(":", 1)[1])
-    except OSError:
+                if line.startswith(f"{key}:"):
+                    return float(line.split(":", 1)[1].split()[0])
+    except (OSError, ValueError):
         pass
     return None
 
 
-def _oracle_columns(ops):
-    """One worker's share of the CPU baseline: the oracle systolic on a column slice; returns its seconds."""
-    from oracle import numerics as nx
-    from oracle import systolic as osys
-    t0 = time.perf_counter()
-    osys.systolic(*ops, nx.MXGEMMINI(), osys.HW_FINAL)
-    return time.perf_counter() - t0
-
-
-def cpu_baseline_systolic(x, W, cols_per_core=32):
-    """The oracle (numpy port of the reference's reducer) on the benchmark's operands, over a column slice of
-    B: one slice of cols_per_core columns per host core, in a process pool.  Output columns are independent
-    chains, so the slice is a fair sample of the whole.  It runs before anything touches the GPU (the pool
-    forks), on codes the oracle's own quantizer makes from the same x and W (the GPU's codes equal them bit for
-    bit: tests/test_quantize_gpu.py).  cores = the CPUs this process may use, at most 16 (the box's share)."""
-    import multiprocessing as mp
-
-    from oracle import block as ob
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
-    cols = cols_per_core * cores
-    pa, xa = ob.mxgemmini_quantize(x.t().contiguous().numpy(), "MXFP8_E4M3", 0)
-    pb, xb = ob.mxgemmini_quantize(W[:cols].t().contiguous().numpy(), "MXFP8_E4M3", 0)
-    K, M = pa.shape
-    parts = [(pa, xa, pb[:, c:c + cols_per_core], xb[:, c:c + cols_per_core]) for c in range(0, cols, cols_per_core)]
-    t0 = time.perf_counter()
-    with mp.get_context("fork").Pool(cores) as pool:
-        each = pool.map(_oracle_columns, parts)
-    dt = time.perf_counter() - t0
-    macs = K * M * cols
-    one = 2 * K * M * cols_per_core / (sum(each) / len(each)) / 1e9
-    return {"value": round(2 * macs / dt / 1e9, 4), "unit": "GOP/s", "cores": cores, "kind": "port",
-            "single_core_GOPs": round(one, 4),
-            "sample": f"oracle systolic MXGEMMINI HW_FINAL on the benchmark's codes, M={M} x N={cols} columns "
-                      f"({cols_per_core} per core) x K={K} ({macs / 1e6:.1f} M MAC, {dt:.1f} s wall, "
-                      f"{sum(each):.1f} s of CPU work, numpy, {cores} processes, "
-                      f"{platform.processor() or platform.machine()})"}
-
-
-def quantize_lines(torch, steps):
+def quantize_lines(torch, steps, inp):
     """block.mxgemmini on bf16 8192 x 8192 (5 formats, rne) and block.ocp quantize + dequantize on 4096 x 512
-    fp32 with rotating buffers past the 256 MB last-level cache: GB/s of algorithmic bytes."""
+    fp32 with rotating buffers past the 256 MB last-level cache: GB/s of algorithmic bytes.  Returns the line
+    and the outputs the parity check compares."""
     from mxq import block
     dev = torch.device("cuda", 0)
-    g = torch.Generator(device="cpu").manual_seed(2)
-    t = torch.distributions.StudentT(torch.tensor(3.0)).sample((8192, 8192)) * 0.5
-    idx = torch.randperm(8192 * 8192, generator=g)[:67109]
-    t.view(-1)[idx] *= 100
-    V = t.to(torch.bfloat16).to(dev)
+    V = inp["c3"].to(dev)
     s = torch.cuda.current_stream(dev)
-    out, kern = {}, {}
+    out, kern, outputs = {}, {}, {}
     bytes_c3 = 8192 * 8192 * 2 + 8192 * 8192 * 4 + 256 * 8192 * 4
-    for fmt in ("MXFP8_E4M3", "MXFP8_E5M2", "MXFP6_E3M2", "MXFP6_E2M3", "MXFP4"):
+    for fmt in C3_FORMATS:
         fn = lambda: block.mxgemmini.quantize(V, fmt, axis=0, rounding_mode="rne")   # noqa: E731
-        fn()
+        outputs[fmt] = _slice_digests(*(t.cpu().numpy() for t in fn()), 512)
         ms = _events_ms(fn, steps, s)
         out[fmt] = round(bytes_c3 / ms / 1e6, 1)
         kms, _ = _kernel_ms(fn, steps, "block_quantize")
@@ -139,7 +290,7 @@ def quantize_lines(torch, steps):
     import mxq
     bytes_pk = 8192 * 8192 * 2 + 8192 * 8192 + 256 * 8192
     pk, pk_kern = {}, {}
-    for fmt in ("MXFP8_E4M3", "MXFP8_E5M2", "MXFP6_E3M2", "MXFP6_E2M3", "MXFP4"):
+    for fmt in C3_FORMATS:
         fn = lambda: mxq.packed.quantize(V, fmt, rounding_mode="rne", check=False)            # noqa: E731
         fn()
         ms = _events_ms(fn, steps, s)
@@ -147,8 +298,10 @@ def quantize_lines(torch, steps):
         kms, _ = _kernel_ms(fn, steps, "block_quantize")
         pk_kern[fmt] = round(bytes_pk / kms / 1e6, 1) if kms else None
     del V
-    # 17 MB per call: rotate over 64 inputs (1.1 GB with outputs) so HBM, not the cache, serves them
-    rot = [torch.randn(4096, 512, device=dev) for _ in range(64)]
+    # 17 MB per call: rotate over 64 inputs (1.1 GB with outputs) so HBM, not the cache, serves them; the first
+    # is the seeded input the parity check and the CPU baseline use
+    g = torch.Generator(device=dev).manual_seed(11)
+    rot = [inp["c1"].to(dev)] + [torch.randn(4096, 512, device=dev, generator=g) for _ in range(63)]
     bytes_c1 = 4096 * 512 * 4 * 2 + 128 * 512 * 4
     i = [0]
 
@@ -159,6 +312,7 @@ def quantize_lines(torch, steps):
     ms1 = _events_ms(q1, 64, s)
     kms1, _ = _kernel_ms(q1, 64, "block_quantize")
     P, X = block.ocp.quantize(rot[0], "MXFP8_E4M3", axis=0)
+    outputs["c1"] = _slice_digests(P.cpu().numpy(), X.cpu().numpy(), 32)
     ms1d = _events_ms(lambda: block.ocp.dequantize(P, X, axis=0), 64, s)
     return {"mxgemmini_bf16_8192x8192_rne_GBs": out, "mxgemmini_bf16_8192x8192_rne_kernel_GBs": kern,
             "mxgemmini_bytes_per_call": bytes_c3,
@@ -167,36 +321,48 @@ def quantize_lines(torch, steps):
             "ocp_e4m3_4096x512_quantize_GBs": round(bytes_c1 / ms1 / 1e6, 1),
             "ocp_e4m3_4096x512_quantize_kernel_GBs": round(bytes_c1 / kms1 / 1e6, 1) if kms1 else None,
             "ocp_e4m3_4096x512_dequantize_GBs_cache_resident": round(bytes_c1 / ms1d / 1e6, 1),
-            "peak_GBs": HBM_PEAK_GBS}
+            "peak_GBs": HBM_PEAK_GBS}, outputs
 
 
-def lut_line(torch, steps):
+def lut_line(torch, steps, inp):
     """block.lut MXFP6_E3M2 (rne, 2^-23, group 1, 50 iterations) on two fp32 4096 x 4096 operands, then the
     systolic MXGEMMINI HW_FINAL product of the two LUT operands (K = M = N = 4096)."""
     from mxq import block, matmul
     dev = torch.device("cuda", 0)
     s = torch.cuda.current_stream(dev)
-    A = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(0)).to(dev)
-    B = torch.randn(4096, 4096, generator=torch.Generator().manual_seed(1)).to(dev)
+    A, B = inp["c4a"].to(dev), inp["c4b"].to(dev)
     q = lambda V: block.lut.quantize(V, "MXFP6_E3M2", 0, 32, rounding_mode="rne", scale_floor=2.0 ** -23,  # noqa
                                      group=1, max_iters=50)
     PA, XA = q(A)
     PB, XB = q(B)
     ms_q = _events_ms(lambda: q(A), steps, s)
     mm = lambda: matmul.systolic(PA, XA, PB, XB, matmul.MXGEMMINI(), matmul.HW_FINAL)        # noqa: E731
-    mm()
+    Y = mm()
     ms_mm = _events_ms(mm, steps, s)
     kms, _ = _kernel_ms(mm, steps, "systolic_fast")
     macs = 4096 ** 3
-    return {"workload": "block.lut MXFP6_E3M2 4096x4096 (tables, pick, lookup) + systolic 4096^3",
+    line = {"workload": "block.lut MXFP6_E3M2 4096x4096 (tables, pick, lookup) + systolic 4096^3",
             "lut_quantize_ms": round(ms_q, 3), "systolic_ms": round(ms_mm, 3),
             "systolic_TOPs": round(2 * macs / ms_mm / 1e9, 3),
-            "systolic_kernel_TOPs": round(2 * macs / kms / 1e9, 3) if kms else None}
+            "systolic_kernel_TOPs": round(2 * macs / kms / 1e9, 3) if kms else None,
+            "systolic_kernel_frac": round(2 * macs / kms / 1e9 / VALU_ROOF_TOPS, 4) if kms else None}
+    outputs = {k: t.cpu().numpy() for k, t in (("PA", PA), ("XA", XA), ("PB", PB), ("XB", XB))}
+    outputs["Y_cols"] = Y[:, 4064:].cpu().numpy()
+    return line, outputs
 
 
-def attend_line(torch, steps):
+def causal_computed_fraction(T=2048, tile=64):
+    """The share of attend C5's MACs its kernels compute: on the causal mask the batched launches run on
+    64 x 64 output tiles (32 problems of 2048 x 2048 scores, 32 x 32 tiles each, at least 8 per CU), Q K^T skips
+    the tiles wholly above the diagonal and P V stops each 64-query tile's reduction at its last key: both
+    compute n (n + 1) / 2 of n^2 tile-units, n = T / tile."""
+    n = T // tile
+    return n * (n + 1) / 2 / (n * n)
+
+
+def attend_line(torch, steps, inp):
     """mxq.nn.attend, Llama-3-8B-shaped: 1 x 32 heads x 2048 x 128, causal HF eager mask, Q K^T and P V through
-    the MXGEMMINI MXFP8_E4M3 Scheme, softmax in fp32."""
+    the MXGEMMINI MXFP8_E4M3 Scheme, softmax in fp32; and its GQA variant with 8 KV heads."""
     from functools import partial
 
     import mxq
@@ -205,14 +371,28 @@ def attend_line(torch, steps):
     s = torch.cuda.current_stream(dev)
     qz = partial(block.mxgemmini.quantize, fmt="MXFP8_E4M3", axis=0)
     hw = Scheme("hw", a=qz, b=qz, reduce=partial(matmul.systolic, arith=matmul.MXGEMMINI(), schedule=matmul.HW_FINAL))
-    q, k, v = (torch.randn(1, 32, 2048, 128, generator=torch.Generator().manual_seed(i)).to(dev) for i in range(3))
-    mask = torch.triu(torch.full((2048, 2048), torch.finfo(torch.float32).min), 1)[None, None].to(dev)
+    q, k, v, mask = (inp[n].to(dev) for n in ("q", "k", "v", "mask"))
     fn = lambda: mxq.nn.attend(q, k, v, mask, 128 ** -0.5, hw, hw)                      # noqa: E731
-    fn()
+    o = fn()
     ms = _events_ms(fn, steps, s)
+    kq, _ = _kernel_ms(fn, steps, "systolic_fast")
+    k8, v8 = k[:, :8].contiguous(), v[:, :8].contiguous()
+    fn8 = lambda: mxq.nn.attend(q, k8, v8, mask, 128 ** -0.5, hw, hw)                   # noqa: E731
+    fn8()
+    ms8 = _events_ms(fn8, steps, s)
     macs = 2 * 32 * 2048 * 2048 * 128
-    return {"workload": "nn.attend 1x32x2048x128 causal, MXGEMMINI MXFP8_E4M3 Scheme for QK^T and PV",
-            "ms": round(ms, 3), "emulated_TOPs": round(2 * macs / ms / 1e9, 3)}
+    done = macs * causal_computed_fraction()
+    line = {"workload": "nn.attend 1x32x2048x128 causal, MXGEMMINI MXFP8_E4M3 Scheme for QK^T and PV",
+            "ms": round(ms, 3), "emulated_TOPs": round(2 * macs / ms / 1e9, 3),
+            "computed_macs": int(done),
+            "computed_TOPs": round(2 * done / ms / 1e9, 3),
+            "computed_frac_whole_call": round(2 * done / ms / 1e9 / VALU_ROOF_TOPS, 4),
+            "systolic_fast_kernels_ms": round(2 * kq, 3) if kq else None,
+            "computed_frac_kernels": round(2 * done / (2 * kq) / 1e9 / VALU_ROOF_TOPS, 4) if kq else None,
+            "gqa8_ms": round(ms8, 3),
+            "note": "emulated_TOPs counts every MAC of the call (the reference computes them all); computed_* count "
+                    "the MACs the kernels run after the exact causal skip"}
+    return line, o[:, :, list(C5_HEADS)].cpu().numpy()
 
 
 def llm_line(torch, steps):
@@ -286,7 +466,7 @@ def mfma_line(torch, steps, P_A, X_A, P_B, X_B):
     flops = 2 * P_A.shape[0] * P_A.shape[1] * P_B.shape[1]
     k_tf = flops / (kms / 1e3) / 1e12 if kms else None
     return {"workload": "mfma_accum on the same MXFP8_E4M3 codes (M = 512, N = 4096, K = 4096)",
-            "ms": round(ms, 4), "kernel": "k_mx_mfma<0, 0, 1>", "kernel_ms": round(kms, 4) if kms else None,
+            "ms": round(ms, 4), "kernel": "k_mx_mfma", "kernel_ms": round(kms, 4) if kms else None,
             "kernel_TFLOPs": round(k_tf, 2) if k_tf else None, "peak_TFLOPs": FP8_PEAK_TFLOPS,
             "frac": round(k_tf / FP8_PEAK_TFLOPS, 4) if k_tf else None}
 
@@ -304,12 +484,40 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_per_launch": x.numel() * 4, "launches": 5}), flush=True)
 
 
+# -------------------------------------------------------------------------------------------- parity
+def _slice_digests(P, X, width):
+    """Digests of P's and X's column slices of `width` columns, as the CPU baseline's jobs cut them."""
+    return [(c, c + width, _digest(P[:, c:c + width]), _digest(X[:, c:c + width])) for c in range(0, P.shape[1], width)]
+
+
+def _slices_equal(gpu, oracle):
+    """The GPU's P and X against the oracle's, slice by slice, by digest."""
+    return len(gpu) == len(oracle) and all(
+        (c0, c1, dp, dx) == (j[2], j[3], op, ox) for (c0, c1, dp, dx), (j, op, ox) in zip(gpu, oracle))
+
+
+def _bits_equal(a, b):
+    import numpy as np
+    a, b = np.ascontiguousarray(a, np.float32), np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))
+
+
+def _softmax_tolerance(got, want):
+    """attend against the oracle run with torch's CPU softmax: the GPU's softmax may differ in the last bits;
+    at most 2 % of outputs may differ, none by more than 2^-4 of the largest |output|."""
+    import numpy as np
+    differ = float((got != want).mean())
+    worst = float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+    return {"equal_frac": round(1 - differ, 5), "max_rel_to_largest": worst,
+            "within_tolerance": differ <= 0.02 and worst <= 2.0 ** -4}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines and the parity checks")
     ap.add_argument("--no-extra", action="store_true", help="only the systolic line (no quantize, LUT, attend)")
     ap.add_argument("--copy-calibration", action="store_true", help="run only the counter-calibration copy")
     ap.add_argument("--only", choices=("quantize", "lut", "attend", "mfma", "trees", "llm"),
@@ -325,31 +533,34 @@ def main():
 
     import torch
 
-    M, N, K = 512, 4096, 4096
-    g = torch.Generator().manual_seed(0)
-    x = torch.randn(M, K, generator=g)
-    W = torch.randn(N, K, generator=g) * 0.02
-    # the CPU baseline forks its worker pool, so it runs before anything touches the GPU
-    cpu = cpu_baseline_systolic(x, W) if not args.no_cpu and args.only is None else None
+    inp = make_inputs(torch)
+    cores = max(1, min(MAX_POOL, len(os.sched_getaffinity(0))))
+    # the CPU baselines fork their worker pool, so they run before anything touches the GPU
+    cpu = cpu_baselines(inp, cores) if not args.no_cpu and args.only is None else None
+    print(f"bench: inputs ready{', CPU baselines done' if cpu else ''}", file=sys.stderr, flush=True)
 
     import mxq  # noqa: F401
     from mxq import block, matmul
     dev = torch.device("cuda", 0)
     if args.only in ("quantize", "lut", "attend", "llm"):
-        fn = {"quantize": lambda: quantize_lines(torch, max(5, args.steps // 2)),
-              "lut": lambda: lut_line(torch, 3), "attend": lambda: attend_line(torch, 3),
+        fn = {"quantize": lambda: quantize_lines(torch, max(5, args.steps // 2), inp)[0],
+              "lut": lambda: lut_line(torch, 3, inp)[0], "attend": lambda: attend_line(torch, 3, inp)[0],
               "llm": lambda: llm_line(torch, 2)}[args.only]
         print(json.dumps({"only": args.only, args.only: fn()}), flush=True)
         return
-    P_A, X_A = block.mxgemmini.quantize(x.t().contiguous().to(dev), "MXFP8_E4M3", axis=0)
-    P_B, X_B = block.mxgemmini.quantize(W.t().contiguous().to(dev), "MXFP8_E4M3", axis=0)
+    M, N, K = 512, 4096, 4096
+    P_A, X_A = block.mxgemmini.quantize(inp["x"].t().contiguous().to(dev), "MXFP8_E4M3", axis=0)
+    P_B, X_B = block.mxgemmini.quantize(inp["W"].t().contiguous().to(dev), "MXFP8_E4M3", axis=0)
     ar = matmul.MXGEMMINI()
     if args.only in ("mfma", "trees"):
         fn = {"mfma": lambda: mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B),
               "trees": lambda: trees_line(torch, 3, P_A, X_A, P_B, X_B)}[args.only]
         print(json.dumps({"only": args.only, args.only: fn()}), flush=True)
         return
-    step = lambda: matmul.systolic(P_A, X_A, P_B, X_B, ar, matmul.HW_FINAL)   # noqa: E731
+    Y = [None]
+
+    def step():
+        Y[0] = matmul.systolic(P_A, X_A, P_B, X_B, ar, matmul.HW_FINAL)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -361,6 +572,7 @@ def main():
     macs = M * N * K
     gops = 2 * macs / (ms / 1e3) / 1e9
     k_tops = 2 * macs / (kms / 1e3) / 1e12 if kms else None
+    ops_per_mac = _profile_value("systolic_fast_c2_valu", "valu_lane_ops_per_mac")
     line = {
         "metric": METRIC, "value": round(gops, 2), "unit": "GOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -371,23 +583,53 @@ def main():
         "roofline": {"bound": "valu", "achieved": round(k_tops, 4) if k_tops else None,
                      "peak": round(VALU_ROOF_TOPS, 3), "unit": "TOP/s",
                      "frac": round(k_tops / VALU_ROOF_TOPS, 4) if k_tops else None,
-                     "traffic": _traffic("systolic_fast_c2"),
-                     "kernel": "k_systolic_fast<16, true>", "kernel_ms": round(kms, 4) if kms else None,
+                     "traffic": _profile_value("systolic_fast_c2_traffic", "bytes_per_launch"),
+                     "kernel": "k_systolic_fast<16, true, 32, 32, HW_FINAL>", "kernel_ms": round(kms, 4) if kms else None,
                      "kernel_launches_timed": launches,
+                     "executed": None if not (ops_per_mac and k_tops) else {
+                         "valu_lane_ops_per_mac": ops_per_mac,
+                         "valu_lane_ops_per_s_T": round(k_tops / 2 * ops_per_mac, 2),
+                         "frac_of_78.6T_lane_rate": round(k_tops * 1e12 / 2 * ops_per_mac / VALU_LANE_OPS, 4),
+                         "frac_of_39.3T_single_issue": round(k_tops * 1e12 / 2 * ops_per_mac / VALU_SINGLE_ISSUE, 4),
+                         "source": "SQ_INSTS_VALU x 64 / emulated MACs, profiles/systolic_fast_c2_valu.txt"},
                      "note": "VALU-bound emulation (neither HBM nor MFMA): achieved = 2 x 8,589,934,592 emulated "
-                             "MACs / the fast kernel's average duration; peak = MI355X vector FP32 157.3 TFLOP/s "
-                             "= 78.6 T 32-bit lane-ops/s, / 10 lane-ops per emulated MAC (the datapath's primitive "
-                             "count) x 2 ops per MAC; the kernel executes 8.1 VALU lane-ops per MAC "
-                             "(SQ_INSTS_VALU, profiles/systolic_fast_c2_valu.txt)"},
+                             "MACs / the fast kernel's average duration; peak is a datapath MODEL: MI355X vector FP32 "
+                             "157.3 TFLOP/s = 78.6 T 32-bit lane-ops/s, / 10 lane-ops per emulated MAC (the "
+                             "datapath's primitive count, not the kernel's instruction count) x 2 ops per MAC; "
+                             "`executed` holds the counted instructions against the lane rates"},
     }
+    extra = {}
     if not args.no_extra:
-        line["quantize"] = quantize_lines(torch, max(5, args.steps // 2))
-        line["lut_c4"] = lut_line(torch, 3)
-        line["attend_c5"] = attend_line(torch, 3)
+        line["quantize"], extra["quantize"] = quantize_lines(torch, max(5, args.steps // 2), inp)
+        line["lut_c4"], extra["lut"] = lut_line(torch, 3, inp)
+        line["attend_c5"], extra["attend"] = attend_line(torch, 3, inp)
         line["mfma_c2"] = mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B)
         line["trees_c2"] = trees_line(torch, 3, P_A, X_A, P_B, X_B)
     if cpu is not None:
-        line["cpu_baseline"] = cpu
+        line["cpu_baseline"] = cpu["c2"]["cpu_baseline"]
+        ncol = cpu["c2"]["cols"]
+        line["parity"] = {"checked": f"the timed output's columns 0..{ncol - 1} (all 512 rows) against the oracle",
+                          "bit_exact": _bits_equal(Y[0][:, :ncol].cpu().numpy(), cpu["c2"]["oracle"])}
+        if "quantize" in extra:
+            q = extra["quantize"]
+            line["quantize"]["cpu_baseline"] = {"c1_ocp_4096x512": cpu["c1"]["cpu_baseline"],
+                                                "c3_mxgemmini_bf16_8192x8192": cpu["c3"]["cpu_baseline"]}
+            line["quantize"]["parity"] = {
+                "checked": "P and X of C1 and of C3 (every format), whole tensors, against the oracle's",
+                "c1_bit_exact": _slices_equal(q["c1"], cpu["c1"]["oracle"]),
+                "c3_bit_exact": {f: _slices_equal(q[f], cpu["c3"]["oracle"][f]) for f in C3_FORMATS}}
+        if "lut" in extra:
+            o, w = extra["lut"], cpu["c4"]["oracle"]
+            line["lut_c4"]["cpu_baseline"] = cpu["c4"]["cpu_baseline"]
+            line["lut_c4"]["parity"] = {
+                "checked": "both LUT operands (P, X) whole, and the product's last 32 columns, against the oracle",
+                "lut_operands_bit_exact": all(_bits_equal(o[k], w[k]) for k in ("PA", "XA", "PB", "XB")),
+                "systolic_columns_bit_exact": _bits_equal(o["Y_cols"], w["Y_cols"])}
+        if "attend" in extra:
+            line["attend_c5"]["cpu_baseline"] = cpu["c5"]["cpu_baseline"]
+            line["attend_c5"]["parity"] = {"checked": "heads 0 and 31 against the oracle with torch's CPU softmax "
+                                                      "(bit for bit with the GPU's softmax: tests/test_nn_gpu.py)",
+                                           **_softmax_tolerance(extra["attend"], cpu["c5"]["oracle"])}
     print(json.dumps(line), flush=True)
 
 

@@ -271,3 +271,28 @@ def test_trees_fast_kernel_falls_back(cuda, which):
     assert n == 1
     assert_bits_equal(got.cpu().numpy(), fn(True).cpu().numpy(), f"{which} fallback vs general")
     assert_bits_equal(got.cpu().numpy(), want, f"{which} fallback vs oracle")
+
+
+def _golden_tree_cases():
+    import json
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "trees.npz"), allow_pickle=False)
+    return z, [tuple(c) for c in json.loads(str(z["cases"]))]
+
+
+@pytest.mark.parametrize("case", _golden_tree_cases()[1], ids=lambda c: c[0])
+def test_trees_against_reference_fixtures(cuda, case):
+    """Both reducers on the GPU against the reference's own outputs (tests/golden/trees.npz), bit for bit."""
+    from mxq import matmul
+    z, _ = _golden_tree_cases()
+    name, tree, (aname, aargs), fmt, K, M, N, kw = case
+    ops = _t(*(z[f"{name}_{k}"] for k in ("PA", "XA", "PB", "XB")))
+    ar = getattr(matmul, aname)(*aargs)
+    kw = dict(kw)
+    if "schedule" in kw:
+        kw["schedule"] = [tuple(x) for x in kw["schedule"]]
+    if tree == "anchor":
+        Y = matmul.anchor_tree(*ops, ar, **kw)
+    else:
+        Y = matmul.adder_tree(*ops, ar, kw.pop("schedule"), **kw)
+    assert_bits_equal(Y.cpu().numpy(), z[f"{name}_Y"], f"{tree} tree {name}")
