@@ -336,13 +336,25 @@ def lut_line(torch, steps, inp):
     PA, XA = q(A)
     PB, XB = q(B)
     ms_q = _events_ms(lambda: q(A), steps, s)
+    # the one-call path's kernels: quantize (fp32 in, code bytes, float32 scales and per-split counts out),
+    # k-means, and the pick (code bytes in, float32 entries out)
+    kl = {name: _kernel_ms(lambda: q(A), steps, name)[0] for name in ("lut_quant", "lut_kmeans", "lut_pick_codes")}
+    elems = 4096 * 4096
+    quant_bytes = elems * 4 + elems + elems // 32 * 4                 # V read; codes and scales written
+    pick_bytes = elems + elems * 4                                    # codes read, entries written
     mm = lambda: matmul.systolic(PA, XA, PB, XB, matmul.MXGEMMINI(), matmul.HW_FINAL)        # noqa: E731
     Y = mm()
     ms_mm = _events_ms(mm, steps, s)
     kms, _ = _kernel_ms(mm, steps, "systolic_fast")
     macs = 4096 ** 3
-    line = {"workload": "block.lut MXFP6_E3M2 4096x4096 (tables, pick, lookup) + systolic 4096^3",
-            "lut_quantize_ms": round(ms_q, 3), "systolic_ms": round(ms_mm, 3),
+    line = {"workload": "block.lut MXFP6_E3M2 4096x4096 (quantize and count, k-means, pick) + systolic 4096^3",
+            "lut_quantize_ms": round(ms_q, 3),
+            "lut_kernels_us": {k: round(v * 1e3, 2) if v else None for k, v in kl.items()},
+            "lut_quant_kernel_GBs": round(quant_bytes / kl["lut_quant"] / 1e6, 1) if kl["lut_quant"] else None,
+            "lut_pick_kernel_GBs": round(pick_bytes / kl["lut_pick_codes"] / 1e6, 1) if kl["lut_pick_codes"] else None,
+            "lut_pick_kernel_frac": (round(pick_bytes / kl["lut_pick_codes"] / 1e6 / HBM_PEAK_GBS, 3)
+                                     if kl["lut_pick_codes"] else None),
+            "systolic_ms": round(ms_mm, 3),
             "systolic_TOPs": round(2 * macs / ms_mm / 1e9, 3),
             "systolic_kernel_TOPs": round(2 * macs / kms / 1e9, 3) if kms else None,
             "systolic_kernel_frac": round(2 * macs / kms / 1e9 / VALU_ROOF_TOPS, 4) if kms else None}

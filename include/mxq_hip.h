@@ -309,12 +309,14 @@ int mxq_mx_mfma(const uint8_t* A, const uint8_t* SA, int32_t a_kind, const uint8
  * (quantile seeds, Lloyd passes until numpy.allclose or max_iters), snap to the finder-safe values, pad with
  * unused safe values smallest magnitude first (safe_order: indices of `safe` sorted by |value|, negative
  * first), sort.  grid: the format's nv distinct finite values ascending; safe: its ns finder-safe values
- * ascending.  T: ceil(n / 2^group) x 16 float32.  workspace: int32 of ceil(n/2^group) * nv + 1 elements; its
- * last element is set nonzero when P holds a value that is not a code (the caller reports it).
+ * ascending.  (fmt_e, fmt_m): the element format whose codes P holds (a code's grid bin is then read off its
+ * bits; 0, 0 or a grid the format does not give: a binary search of the grid instead).  T: ceil(n / 2^group)
+ * x 16 float32.  workspace: int32 of ceil(n/2^group) * nv + 1 elements; its last element is set nonzero when P
+ * holds a value that is not a code (the caller reports it).
  * Replaces mxq/lut/kmeans.py:46-122. */
 int mxq_lut_tables(const float* P, int64_t K, int64_t n, int32_t group, int32_t max_iters, const float* grid,
-                   int32_t nv, const float* safe, int32_t ns, const int32_t* safe_order, float* T,
-                   int32_t* workspace, mxq_stream_t stream);
+                   int32_t nv, const float* safe, int32_t ns, const int32_t* safe_order, int32_t fmt_e,
+                   int32_t fmt_m, float* T, int32_t* workspace, mxq_stream_t stream);
 
 /* lut.pick: each code's nearest entry of its group's ascending table of `width` entries, ties to the lower
  * index; writes int64 indices to I, or (I NULL) the entries themselves to P_lut (pick then lookup, fused).
@@ -336,6 +338,27 @@ int mxq_lut_pick_packed(const float* P, int64_t K, int64_t n, int32_t group, con
 /* mxq_lut_lookup of 4-bit indices in mxq_lut_pick_packed's layout. */
 int mxq_lut_lookup_packed(const uint8_t* I4, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,
                           float* out, mxq_stream_t stream);
+
+/* block.lut along axis 0 in one call: V (K x n, row-major, float32 / bf16 / f16 by v_dtype) block-quantized
+ * in blocks of 32 rows by spec (mxgemmini's: the OCP element grid of a LUT format, no via), the element codes
+ * kept as bytes in the workspace while their grid bins are counted per column group, the tables fitted as
+ * mxq_lut_tables fits them (T: ceil(n / 2^group) x 16), and every code replaced by its nearest entry: P_lut
+ * (K x n float32) and X (ceil(K / 32) x n float32 scales) are what block.lut returns.  grid, nv, safe, ns,
+ * safe_order: as mxq_lut_tables, for spec's format.  K >= 1, n % 16 == 0, V, P_lut and X 16-byte aligned.
+ * workspace: device memory of mxq_block_lut_workspace bytes, 256-byte aligned.  *err (device) gets bit 0 set
+ * when V yields a value that is not a code of the format (a non-finite V), which block.lut reports as
+ * lut.tables does; the caller clears it first.
+ * Replaces mxq/block/lut.py:23-34 (axis 0: the quantize, mxq/lut/kmeans.py:46-122 and :125-146). */
+int mxq_block_lut(const void* V, int32_t v_dtype, int64_t K, int64_t n, const mxq_block_spec* spec, int32_t group,
+                  int32_t max_iters, const float* grid, int32_t nv, const float* safe, int32_t ns,
+                  const int32_t* safe_order, float* P_lut, float* X, float* T, void* workspace,
+                  int64_t workspace_bytes, int32_t* err, mxq_stream_t stream);
+
+/* The bytes of workspace mxq_block_lut needs for a K x n tensor of the element format (fmt_e, fmt_m) whose grid
+ * has nv values, at `group` (0 when K or n is 0).  MXQ_EINVAL for what mxq_block_lut refuses (n % 16, a
+ * format with no LUT). */
+int mxq_block_lut_workspace(int64_t K, int64_t n, int32_t group, int32_t fmt_e, int32_t fmt_m, int32_t nv,
+                            int64_t* bytes);
 
 /* lut.finder: fx_all[c] is element code c's fixed point (ncodes entries), lut_fx the fixed points of each
  * group's 16 entries (ceil(n/2^group) x 16); out = argmin over entries of |fx - lut_fx| & mask (mask 0: none),

@@ -1,8 +1,9 @@
 // MX-Gemmini look-up tables on gfx950 (mxq/lut/kmeans.py:27-152, mxq/lut/formats.py:140-159).
 //
 //   k_lut_hist    counts of each distinct code value per column group: the group's columns of a K-row stripe
-//                 are binned into an LDS histogram (binary search in the sorted value grid, exact-match check),
-//                 then added into the global counts with one atomic per nonzero bin
+//                 are binned into an LDS histogram (the grid bin read off a code's bits, or a binary search of
+//                 the sorted grid with an exact-match check), then added into the global counts with one atomic
+//                 per nonzero bin
 //   k_lut_kmeans  one wavefront per group: quantile seeds (or the present values when 16 or fewer), weighted
 //                 Lloyd passes in float64 until two passes agree (numpy.allclose's tolerances) or max_iters,
 //                 snap to the nearest finder-safe value, pad with unused safe values smallest magnitude first,
@@ -13,13 +14,16 @@
 //                 up through a shuffle)
 //   k_lut_lookup  the entries named by int64 indices; k_lut_lookup4 by 4-bit ones
 //   k_lut_finder  the chip's finder: nearest in fixed point with the format's |difference| mask, first index
-#include "mxq_common.h"
-#include "mxq_numerics.h"
+#include <cmath>
+
+#include "lut_impl.h"
+
+using mxq_lut::kMaxGrid;
+using mxq_lut::kSize;
+using mxq_lut::stream_rows;
+using mxq_lut::stripe_rows;
 
 namespace {
-
-constexpr int kSize = 16;            // entries per table
-constexpr int kMaxGrid = 256;        // distinct finite values of the largest LUT format (E5M2: 247)
 
 // lower_bound in a sorted float array: the first index with a[i] >= v (NaN compares false: count of a[i] < v)
 __device__ __forceinline__ int lower_bound_f(const float* a, int n, float v) {
@@ -32,92 +36,132 @@ __device__ __forceinline__ int lower_bound_f(const float* a, int n, float v) {
   return lo;
 }
 
-// Grid values of the LUT formats have at most 4 significand bits past the leading one, so a value's top
-// 9 + kGridKeyBits bits (sign, exponent, first mantissa bits) name its grid index; the low bits must be zero.
-constexpr int kGridKeyBits = 4;
-constexpr int kGridKeys = 1 << (9 + kGridKeyBits);
+// The nearest entry of an ascending row of `width` values to v (mxq/lut/kmeans.py:125-138): the insertion point
+// `hi` of v (the count of entries below it) clamped to [1, width - 1], then lo = hi - 1 unless v is strictly
+// nearer row[hi]; ties to the lower index.
+__device__ __forceinline__ int nearest_entry(const float* row, int width, float v) {
+  int hi = lower_bound_f(row, width, v);
+  hi = hi < 1 ? 1 : (hi > width - 1 ? width - 1 : hi);
+  const int lo = hi - 1;
+  return (fabsf(v - row[lo]) <= fabsf(row[hi] - v)) ? lo : hi;
+}
+
+// nearest_entry for a row of kSize = 16: the count of entries below v in four fixed probes (8, 4, 2, 1 ahead
+// of the count so far), no loop.
+__device__ __forceinline__ int nearest16(const float* row, float v) {
+  int below = 0;
+#pragma unroll
+  for (int step = kSize / 2; step >= 1; step >>= 1)
+    if (row[below + step - 1] < v) below += step;
+  const int hi = below < 1 ? 1 : (below > kSize - 1 ? kSize - 1 : below);
+  return (fabsf(v - row[hi - 1]) <= fabsf(row[hi] - v)) ? hi - 1 : hi;
+}
+
+// Where a float32 value that is a code of a LUT format sits in the format's value grid (mxq_lut::CodeGrid's
+// order): the code's bits read off the value (normal values by their exponent and mantissa fields, subnormal
+// ones as multiples of the smallest step).  A value that is no code of the format gets -1.  ok == 0: the grid
+// is not a LUT format's (the callers search it instead).  Built on the host by grid_index_of.
+struct GridIndex {
+  int ok;
+  int m, nneg;
+  uint32_t nmin, nsub, lowmask, maxbits;
+  float sub_mul;
+};
+
+__device__ __forceinline__ int grid_index(float v, const GridIndex& g) {
+  const uint32_t u = f2u(v), a = u & 0x7FFFFFFFu;
+  int c;
+  bool good;
+  if (a >= g.nmin) {
+    c = (int)((a >> (23 - g.m)) - g.nsub);
+    good = (a & g.lowmask) == 0u && a <= g.maxbits;
+  } else {
+    const float t = u2f(a) * g.sub_mul;
+    c = (int)t;
+    good = (float)c == t;
+  }
+  return good ? g.nneg + ((u >> 31) ? -c : c) : -1;
+}
+
+// A group's slot in a block's per-group LDS arrays: the even groups first, then the odd ones, so the two groups
+// of a lane's four columns (group 1) land half an array apart and a wave's 64 lanes spread over the banks.
+__device__ __forceinline__ int group_slot(int gl, int half) { return (gl & 1) * half + (gl >> 1); }
 
 // blockDim = 256; CB columns per block, 256 / CB row lanes per column; rows [k0, k0 + rows_per_block).
-// Each code is placed by its key in an LDS table built from the grid (one load), when every grid value has at
-// most kGridKeyBits fraction bits; otherwise by binary search.  A value is counted only when it equals a grid
-// value (-0 counts as the 0 bin, as == says); anything else sets the error flag.
+// INDEXED: a code's bin is read off its bits (grid_index); otherwise found by binary search in the grid.  A
+// value is counted only when it equals a grid value (-0 counts as the 0 bin, as == says); anything else sets
+// the error flag.
+template <int VEC, bool INDEXED>
 __global__ void __launch_bounds__(256) k_lut_hist(const float* __restrict__ P, int64_t K, int64_t n, int group,
-                                                  const float* __restrict__ grid, int nv, int CB,
+                                                  const float* __restrict__ grid, int nv, GridIndex gi, int CB,
                                                   int64_t rows_per_block, int* __restrict__ counts,
                                                   int* __restrict__ err) {
-  extern __shared__ int hist[];                      // (CB >> group, at least 1) x nv, then the key table
+  extern __shared__ int hist[];                      // per group slot nv counts (2 * half slots)
   __shared__ float g_s[kMaxGrid];
-  __shared__ int frac_bits;
   const int64_t c0 = (int64_t)blockIdx.x * CB;
   const int64_t k0 = (int64_t)blockIdx.y * rows_per_block;
   const int gpb = (CB >> group) > 0 ? (CB >> group) : 1;
-  short* key = reinterpret_cast<short*>(hist + gpb * nv);
-  if (threadIdx.x == 0) frac_bits = 0;
-  for (int i = threadIdx.x; i < gpb * nv; i += blockDim.x) hist[i] = 0;
-  // the key table is 16-byte aligned when gpb * nv is a multiple of 4; clear it 8 entries per store then
-  if ((gpb * nv) % 4 == 0) {
-    int4* k4 = reinterpret_cast<int4*>(key);
-    for (int i = threadIdx.x; i < kGridKeys / 8; i += blockDim.x) k4[i] = make_int4(-1, -1, -1, -1);
-  } else {
-    for (int i = threadIdx.x; i < kGridKeys; i += blockDim.x) key[i] = -1;
-  }
+  const int half = (gpb + 1) / 2;
+  for (int i = threadIdx.x; i < 2 * half * nv; i += blockDim.x) hist[i] = 0;
+  if constexpr (!INDEXED)
+    for (int i = threadIdx.x; i < nv; i += blockDim.x) g_s[i] = grid[i];
   __syncthreads();
-  for (int i = threadIdx.x; i < nv; i += blockDim.x) {
-    const float gv = grid[i];
-    g_s[i] = gv;
-    const uint32_t mant = f2u(gv) & 0x007FFFFFu;
-    atomicMax(&frac_bits, mant ? 23 - __builtin_ctz(mant) : 0);
-  }
-  __syncthreads();
-  const bool keyed = frac_bits <= kGridKeyBits;
-  constexpr int sh = 23 - kGridKeyBits;
-  if (keyed) {
-    for (int i = threadIdx.x; i < nv; i += blockDim.x) {
-      key[f2u(g_s[i]) >> sh] = (short)i;
-      if (g_s[i] == 0.0f) {                            // the grid's zero (either sign) takes +0 and -0
-        key[0u] = (short)i;
-        key[0x80000000u >> sh] = (short)i;
-      }
-    }
-  }
-  __syncthreads();
-  const int col = threadIdx.x % CB, rl = threadIdx.x / CB, nrl = blockDim.x / CB;
+  // a lane bins VEC adjacent columns (one VEC-wide load per row); CB / VEC lanes span the block's columns and
+  // the 256 / (CB / VEC) row lanes split its rows
+  const int lanes_x = CB / VEC;
+  const int col = (threadIdx.x % lanes_x) * VEC, rl = threadIdx.x / lanes_x, nrl = blockDim.x / lanes_x;
   const int64_t j = c0 + col;
   const int64_t g0 = c0 >> group;
-  int* h = hist + (int)((j >> group) - g0) * nv;
   bool bad = false;
   if (j < n) {
+    int* h[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) h[e] = hist + group_slot((int)(((j + e < n ? j + e : j) >> group) - g0), half) * nv;
     const int64_t kend = (k0 + rows_per_block < K) ? k0 + rows_per_block : K;
-    constexpr int U = 16;                              // loads in flight per thread before binning them
-    for (int64_t kb = k0 + rl; kb < kend; kb += (int64_t)U * nrl) {
-      float v[U];
+    const int64_t kfirst = k0 + rl;                    // this lane's rows: kfirst, kfirst + nrl, ... < kend
+    const int64_t rows = kfirst < kend ? (kend - kfirst + nrl - 1) / nrl : 0;
+    const float* src = P + kfirst * n + j;
+    const int64_t rstep = (int64_t)nrl * n;
+    constexpr int U = VEC == 4 ? 8 : 16;               // rows per batch
+    using Buf = float[U][VEC];
+    auto load = [&](Buf& v, int64_t batch, int count) {
+      const float* p = src + batch * U * rstep;
 #pragma unroll
       for (int t = 0; t < U; ++t) {
-        const int64_t k = kb + (int64_t)t * nrl;
-        v[t] = k < kend ? P[k * n + j] : 0.0f;
-      }
-#pragma unroll
-      for (int t = 0; t < U; ++t) {
-        if (kb + (int64_t)t * nrl >= kend) break;
-        int b;
-        if (keyed) {
-          const uint32_t u = f2u(v[t]);
-          b = key[u >> sh];
-          if (b < 0 || (u & ((1u << sh) - 1u))) b = -1;
+        if constexpr (VEC == 4) {
+          float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (t < count) q = *reinterpret_cast<const float4*>(p + t * rstep);
+          v[t][0] = q.x; v[t][1] = q.y; v[t][2] = q.z; v[t][3] = q.w;
         } else {
-          b = lower_bound_f(g_s, nv, v[t]);
-          if (b >= nv || !(g_s[b] == v[t])) b = -1;
+          v[t][0] = t < count ? p[t * rstep] : 0.0f;
         }
-        if (b < 0) bad = true;
-        else atomicAdd(&h[b], 1);
       }
-    }
+    };
+    auto bin = [&](const Buf& v, int64_t, int count) {
+#pragma unroll
+      for (int t = 0; t < U; ++t) {
+        if (t >= count) break;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          int b;
+          if constexpr (INDEXED) {
+            b = grid_index(v[t][e], gi);
+          } else {
+            b = lower_bound_f(g_s, nv, v[t][e]);
+            if (b >= nv || !(g_s[b] == v[t][e])) b = -1;
+          }
+          if (b < 0) bad = true;
+          else atomicAdd(&h[e][b], 1);
+        }
+      }
+    };
+    stream_rows<U, Buf>(rows, load, bin);
   }
   if (bad) atomicOr(err, 1);
   __syncthreads();
   const int64_t ng = (n + (1 << group) - 1) >> group;
   for (int i = threadIdx.x; i < gpb * nv; i += blockDim.x) {
-    const int c = hist[i];
+    const int c = hist[group_slot(i / nv, half) * nv + i % nv];
     const int64_t g = g0 + i / nv;
     if (c && g < ng) atomicAdd(&counts[g * nv + (i % nv)], c);
   }
@@ -176,10 +220,14 @@ __device__ __forceinline__ double wave_scan(double v, int lane) {
 //   snap    lane c < 16: the nearest safe value to centre c (first minimum); the distinct ones are the table's
 //           members; the unused safe values in safe_order order fill it to 16 (ranks by ballot); the members
 //           are written in ascending order, +Inf past them
-__global__ void __launch_bounds__(64) k_lut_kmeans(const int* __restrict__ counts, int nv, const float* __restrict__ grid,
+//   code map (when not NULL) per element code c of the format: the bits of the table entry pick chooses for
+//           the code's value (NaN for a code with no grid bin), at code_map[g * ncodes + c]
+// The counts of group g are summed from src (mxq_lut::CountSource): every split's units of the group.
+__global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int nv, const float* __restrict__ grid,
                                                    const float* __restrict__ safe, int ns,
                                                    const int* __restrict__ safe_order, int max_iters,
-                                                   float* __restrict__ T) {
+                                                   float* __restrict__ T, uint32_t* __restrict__ code_map,
+                                                   mxq_lut::CodeGrid cg) {
   constexpr int kRounds = kMaxGrid / 64;
   __shared__ double x_s[kMaxGrid];
   __shared__ double w_s[kMaxGrid];
@@ -188,10 +236,18 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(const int* __restrict__ count
   __shared__ float safe_s[kMaxGrid];
   __shared__ int order_s[kMaxGrid];
   __shared__ unsigned char member[kMaxGrid];
+  __shared__ float T_s[kSize];
   const int g = blockIdx.x, lane = threadIdx.x;
+  const int64_t u0 = (int64_t)g << src.shift;
+  const int64_t u1 = ((int64_t)(g + 1) << src.shift) < src.nunits ? ((int64_t)(g + 1) << src.shift) : src.nunits;
   for (int i = lane; i < nv; i += 64) {
     x_s[i] = (double)grid[i];
-    w_s[i] = (double)counts[(int64_t)g * nv + i];
+    int64_t c = 0;
+    for (int s = 0; s < src.nsplit; ++s) {
+      const int* p = src.p + s * src.split_stride + i;
+      for (int64_t u = u0; u < u1; ++u) c += p[u * nv];
+    }
+    w_s[i] = (double)c;
   }
   for (int i = lane; i < ns; i += 64) {
     safe_s[i] = safe[i];
@@ -341,54 +397,124 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(const int* __restrict__ count
     const int i = r * 64 + lane;
     const bool mem = i < ns && member[i];
     const int rank = base + lanes_below(mem, lane);
-    if (mem && rank < kSize) T[(int64_t)g * kSize + rank] = safe_s[i];
+    if (mem && rank < kSize) {
+      T[(int64_t)g * kSize + rank] = safe_s[i];
+      T_s[rank] = safe_s[i];
+    }
     base += __popcll(__ballot(mem));
   }
-  if (lane >= base && lane < kSize) T[(int64_t)g * kSize + lane] = f_inf();
+  if (lane >= base && lane < kSize) {
+    T[(int64_t)g * kSize + lane] = f_inf();
+    T_s[lane] = f_inf();
+  }
+  if (!code_map) return;
+  __syncthreads();
+  const int ncodes = 2 << cg.sign_at;
+  for (int c = lane; c < ncodes; c += 64) {
+    const int b = mxq_lut::code_bin((uint32_t)c, cg);
+    code_map[(int64_t)g * ncodes + c] = b >= 0 ? f2u(T_s[nearest16(T_s, (float)x_s[b])]) : 0x7FC00000u;
+  }
 }
 
-// Nearest entry of each code's group table (ascending; ties to the lower index).  mode 0: int64 index to I;
-// mode 1: the entry's value to Pout.  One thread per column walks a stripe of rows; the block's tables in LDS.
-// Exactly one of I, Pout, I4 is set.  I4: row k's byte j / 2 holds column j's index in its low nibble (j even)
-// and column j + 1's in its high one (0 past n).
+// Nearest entry of each code's group table (ascending; ties to the lower index): int64 index to I, the entry's
+// value to Pout, or I4: row k's byte j / 2 holds column j's index in its low nibble (j even) and column
+// j + 1's in its high one (0 past n).  Exactly one of I, Pout, I4 is set.  W16: tables of kSize entries
+// (nearest16); otherwise `width` entries, searched.
+template <int VEC, bool W16>
 __global__ void __launch_bounds__(256) k_lut_pick(const float* __restrict__ P, int64_t K, int64_t n, int group,
                                                   const float* __restrict__ T, int width, int64_t rows_per_block,
                                                   int64_t* __restrict__ I, float* __restrict__ Pout,
                                                   uint8_t* __restrict__ I4) {
-  extern __shared__ float rows_s[];                 // (256 >> group, at least 1) x width
+  // (256 >> group, at least 1) rows of the block's tables, each `width` values and one float of padding (rows
+  // an odd number of words apart: the lanes' searches in different rows fall in different LDS banks)
+  extern __shared__ float rows_s[];
+  const int stride = width + 1;
   const int64_t c0 = (int64_t)blockIdx.x * 256;
   const int64_t g0 = c0 >> group;
   const int64_t ng = (n + (1 << group) - 1) >> group;
   const int gpb = (256 >> group) > 0 ? (256 >> group) : 1;
-  for (int i = threadIdx.x; i < gpb * width; i += blockDim.x) {
-    const int64_t g = g0 + i / width;
-    rows_s[i] = g < ng ? T[g * width + (i % width)] : 0.0f;
+  // the block's tables are T[g0 * width, + gpb * width): eight loads in flight per thread before their stores
+  {
+    const int total = gpb * width;
+    const int64_t avail = (ng - g0) * width;
+    for (int base = 0; base < total; base += 256 * 8) {
+      float w[8];
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        const int i = base + f * 256 + (int)threadIdx.x;
+        w[f] = (i < total && i < avail) ? T[g0 * width + i] : 0.0f;
+      }
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        const int i = base + f * 256 + (int)threadIdx.x;
+        if (i < total) rows_s[(i / width) * stride + i % width] = w[f];
+      }
+    }
   }
   __syncthreads();
+  auto nearest = [&](const float* row, float v) { return W16 ? nearest16(row, v) : nearest_entry(row, width, v); };
+  const int64_t k0 = (int64_t)blockIdx.y * rows_per_block;
+  const int64_t kend = (k0 + rows_per_block < K) ? k0 + rows_per_block : K;
+  if constexpr (VEC == 4) {
+    // four adjacent columns per lane (16-byte loads and stores), 64 lanes across the block's 256 columns, four
+    // row lanes; n % 4 == 0, so a lane's columns are all inside the tensor or all past it
+    const int64_t j = c0 + (threadIdx.x & 63) * 4;
+    if (j >= n) return;
+    const int rl = threadIdx.x >> 6;
+    const float* row[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) row[e] = rows_s + (int)(((j + e) >> group) - g0) * stride;
+    // this wave's rows: kfirst, kfirst + 4, ... < kend
+    const int64_t kfirst = k0 + rl;
+    const int64_t rows = kfirst < kend ? (kend - kfirst + 3) / 4 : 0;
+    const int64_t rstep = 4 * n;
+    const int64_t at0 = kfirst * n + j;
+    constexpr int U = 4;
+    using Buf = float4[U];
+    auto load = [&](Buf& v, int64_t batch, int count) {
+      const float* p = P + at0 + batch * U * rstep;
+#pragma unroll
+      for (int t = 0; t < U; ++t)
+        v[t] = t < count ? *reinterpret_cast<const float4*>(p + t * rstep) : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto use = [&](const Buf& v, int64_t batch, int count) {
+#pragma unroll
+      for (int t = 0; t < U; ++t) {
+        if (t >= count) break;
+        const int64_t at = at0 + (batch * U + t) * rstep;
+        const int p0 = nearest(row[0], v[t].x), p1 = nearest(row[1], v[t].y), p2 = nearest(row[2], v[t].z),
+                  p3 = nearest(row[3], v[t].w);
+        if (I) {
+          *reinterpret_cast<longlong2*>(I + at) = make_longlong2(p0, p1);
+          *reinterpret_cast<longlong2*>(I + at + 2) = make_longlong2(p2, p3);
+        } else {
+          *reinterpret_cast<float4*>(Pout + at) = make_float4(row[0][p0], row[1][p1], row[2][p2], row[3][p3]);
+        }
+      }
+    };
+    stream_rows<U, Buf>(rows, load, use);
+    return;
+  }
   const int64_t j = c0 + threadIdx.x;
   const bool live = j < n;
   if (!live && !I4) return;                          // the nibble output keeps every lane for its shuffle
   const int64_t jj = live ? j : n - 1;               // a column of this block (c0 < n)
-  const float* row = rows_s + (int)((jj >> group) - g0) * width;
+  const float* row = rows_s + (int)((jj >> group) - g0) * stride;
   const int64_t nbytes = (n + 1) >> 1;
-  const int64_t k0 = (int64_t)blockIdx.y * rows_per_block;
-  const int64_t kend = (k0 + rows_per_block < K) ? k0 + rows_per_block : K;
-  constexpr int U = 8;                                 // loads in flight per thread
-  for (int64_t kb = k0; kb < kend; kb += U) {
-    float v[U];
+  constexpr int U = 8;
+  using Buf = float[U];
+  auto load = [&](Buf& v, int64_t batch, int count) {
+    const float* p = P + (k0 + batch * U) * n + jj;
 #pragma unroll
-    for (int t = 0; t < U; ++t) v[t] = kb + t < kend ? P[(kb + t) * n + jj] : 0.0f;
+    for (int t = 0; t < U; ++t) v[t] = t < count ? p[t * n] : 0.0f;
+  };
+  auto use = [&](const Buf& v, int64_t batch, int count) {
 #pragma unroll
     for (int t = 0; t < U; ++t) {
-      const int64_t k = kb + t;
-      if (k >= kend) break;
-      int hi = lower_bound_f(row, width, v[t]);
-      hi = hi < 1 ? 1 : (hi > width - 1 ? width - 1 : hi);
-      const int lo = hi - 1;
-      const float d_lo = fabsf(v[t] - row[lo]);
-      const float d_hi = fabsf(row[hi] - v[t]);
-      const int pick = (d_lo <= d_hi) ? lo : hi;
-      if (I4) {                                       // k < kend holds for the whole block: all lanes shuffle
+      if (t >= count) break;
+      const int64_t k = k0 + batch * U + t;
+      const int pick = nearest(row, v[t]);
+      if (I4) {                                       // count is the block's: all lanes shuffle
         const int next = __shfl_xor(pick, 1, 64);
         if (live && (j & 1) == 0) I4[k * nbytes + (j >> 1)] = (uint8_t)(pick | ((j + 1 < n ? next : 0) << 4));
       } else if (I) {
@@ -397,7 +523,8 @@ __global__ void __launch_bounds__(256) k_lut_pick(const float* __restrict__ P, i
         Pout[k * n + j] = row[pick];
       }
     }
-  }
+  };
+  stream_rows<U, Buf>(kend - k0, load, use);
 }
 
 __global__ void __launch_bounds__(256) k_lut_lookup(const int64_t* __restrict__ I, int64_t K, int64_t n, int group,
@@ -450,14 +577,62 @@ __global__ void k_fill_i32(int* p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0;
 }
 
+// The grid index of a LUT format (e, m) whose grid has nv values: ok == 0 unless nv is what the format gives.
+GridIndex grid_index_of(int e, int m, int nv) {
+  GridIndex g{};
+  const mxq_lut::CodeGrid cg = mxq_lut::code_grid_of(e, m, nv);
+  if (!cg.ok) return g;
+  const int bias = (1 << (e - 1)) - 1, emin = 1 - bias;
+  const int ex = cg.cmax >> m, man = cg.cmax & ((1 << m) - 1);
+  g.maxbits = ((uint32_t)(ex - bias + 127) << 23) | ((uint32_t)man << (23 - m));
+  g.nmin = (uint32_t)(emin + 127) << 23;
+  g.nsub = (uint32_t)(127 - bias) << m;
+  g.lowmask = (1u << (23 - m)) - 1u;
+  g.sub_mul = std::ldexp(1.0f, m - emin);
+  g.m = m;
+  g.nneg = cg.cmax;
+  g.ok = 1;
+  return g;
+}
+
+int launch_pick(const float* P, int64_t K, int64_t n, int group, const float* T, int width, int64_t* I,
+                float* P_lut, uint8_t* I4, bool vec4, hipStream_t st) {
+  const int gpb = (256 >> group) > 0 ? (256 >> group) : 1;
+  const size_t lds = (size_t)gpb * (width + 1) * sizeof(float);
+  if (lds > 65536) return mxq::invalid("mxq_lut_pick: tables too wide");
+  const int64_t col_blocks = mxq::ceil_div(n, 256);
+  const int64_t rpb = stripe_rows(K, col_blocks, 1024);           // about four blocks per CU
+  const dim3 grid((unsigned)col_blocks, (unsigned)mxq::ceil_div(K, rpb));
+  const bool w16 = width == kSize;
+  if (vec4 && w16) k_lut_pick<4, true><<<grid, 256, lds, st>>>(P, K, n, group, T, width, rpb, I, P_lut, I4);
+  else if (vec4) k_lut_pick<4, false><<<grid, 256, lds, st>>>(P, K, n, group, T, width, rpb, I, P_lut, I4);
+  else if (w16) k_lut_pick<1, true><<<grid, 256, lds, st>>>(P, K, n, group, T, width, rpb, I, P_lut, I4);
+  else k_lut_pick<1, false><<<grid, 256, lds, st>>>(P, K, n, group, T, width, rpb, I, P_lut, I4);
+  return MXQ_OK;
+}
+
 }  // namespace
+
+namespace mxq_lut {
+
+int launch_kmeans(const CountSource& src, int64_t ng, int nv, const float* grid, const float* safe, int ns,
+                  const int* safe_order, int max_iters, float* T, uint32_t* code_map, const CodeGrid& cg,
+                  hipStream_t st) {
+  if (code_map && !cg.ok) return mxq::invalid("k-means: a code map needs the format's code grid");
+  mxq::KernelTimer timer("lut_kmeans", st);
+  k_lut_kmeans<<<dim3((unsigned)ng), 64, 0, st>>>(src, nv, grid, safe, ns, safe_order, max_iters, T, code_map, cg);
+  return mxq::check_launch("mxq_lut k-means");
+}
+
+}  // namespace mxq_lut
 
 extern "C" int mxq_lut_tables(const float* P, int64_t K, int64_t n, int32_t group, int32_t max_iters,
                               const float* grid, int32_t nv, const float* safe, int32_t ns, const int32_t* safe_order,
-                              float* T, int32_t* workspace, mxq_stream_t stream) {
+                              int32_t fmt_e, int32_t fmt_m, float* T, int32_t* workspace, mxq_stream_t stream) {
   if (K < 0 || n < 0 || group < 0 || group > 30 || max_iters < 0) return mxq::invalid("mxq_lut_tables: bad arguments");
   if (nv < 1 || nv > kMaxGrid || ns < 1 || ns > kMaxGrid) return mxq::invalid("mxq_lut_tables: bad grid sizes");
   if (n == 0) return MXQ_OK;
+  const GridIndex gi = grid_index_of(fmt_e, fmt_m, nv);
   const int64_t ng = (n + (int64_t(1) << group) - 1) >> group;
   hipStream_t st = mxq::as_stream(stream);
   int* counts = workspace;                              // ng * nv, then one error flag
@@ -467,28 +642,27 @@ extern "C" int mxq_lut_tables(const float* P, int64_t K, int64_t n, int32_t grou
     k_fill_i32<<<dim3((unsigned)(blocks < 4096 ? blocks : 4096)), 256, 0, st>>>(workspace, nz);
   }
   if (K > 0) {
-    // columns per block: the LDS histogram (groups x nv ints) within 64 KiB
+    // columns per block: the LDS histogram (group slots x nv ints) within 64 KiB
+    auto slots = [&](int cb) { const int gpb = (cb >> group) > 0 ? (cb >> group) : 1; return (int64_t)(gpb + 1) / 2 * 2; };
     int CB = 256;
-    while (CB > 1 && (int64_t)(((CB >> group) > 0 ? (CB >> group) : 1)) * nv * 4 + kGridKeys * 2 > 65536) CB >>= 1;
+    while (CB > 1 && slots(CB) * nv * 4 > 65536) CB >>= 1;
     const int64_t col_blocks = mxq::ceil_div(n, CB);
-    // about two blocks per CU: every block adds its histogram into the global counts with one atomic per
-    // nonzero bin, so fewer, taller blocks (each thread bins a long stripe, 16 loads in flight) do best
-    int64_t row_blocks = mxq::ceil_div(512, col_blocks);
-    if (row_blocks > K) row_blocks = K;
-    if (row_blocks < 1) row_blocks = 1;
-    if (row_blocks > 65535) row_blocks = 65535;
-    const int64_t rpb = mxq::ceil_div(K, row_blocks);
-    row_blocks = mxq::ceil_div(K, rpb);
-    const size_t lds = (size_t)((CB >> group) > 0 ? (CB >> group) : 1) * nv * sizeof(int) + kGridKeys * sizeof(short);
-    k_lut_hist<<<dim3((unsigned)col_blocks, (unsigned)row_blocks), 256, lds, st>>>(P, K, n, group, grid, nv, CB, rpb,
-                                                                                     counts, err);
+    // about three blocks per CU (as many as their LDS lets a CU hold), each thread binning a long stripe with
+    // many loads in flight; every block then adds its histogram into the global counts, one atomic per
+    // nonzero bin
+    const int64_t rpb = stripe_rows(K, col_blocks, 768);
+    const dim3 hgrid((unsigned)col_blocks, (unsigned)mxq::ceil_div(K, rpb));
+    const size_t lds = (size_t)(slots(CB) * nv * sizeof(int));
+    // four adjacent columns per lane (16-byte loads) when rows are 16-byte aligned and the block spans 4 lanes
+    const bool vec4 = n % 4 == 0 && reinterpret_cast<uintptr_t>(P) % 16 == 0 && CB >= 4 && 256 % (CB / 4) == 0;
+    if (vec4 && gi.ok) k_lut_hist<4, true><<<hgrid, 256, lds, st>>>(P, K, n, group, grid, nv, gi, CB, rpb, counts, err);
+    else if (vec4) k_lut_hist<4, false><<<hgrid, 256, lds, st>>>(P, K, n, group, grid, nv, gi, CB, rpb, counts, err);
+    else if (gi.ok) k_lut_hist<1, true><<<hgrid, 256, lds, st>>>(P, K, n, group, grid, nv, gi, CB, rpb, counts, err);
+    else k_lut_hist<1, false><<<hgrid, 256, lds, st>>>(P, K, n, group, grid, nv, gi, CB, rpb, counts, err);
     if (int rc = mxq::check_launch("mxq_lut_tables histogram")) return rc;
   }
-  {
-    mxq::KernelTimer timer("lut_kmeans", st);
-    k_lut_kmeans<<<dim3((unsigned)ng), 64, 0, st>>>(counts, nv, grid, safe, ns, safe_order, max_iters, T);
-  }
-  return mxq::check_launch("mxq_lut_tables k-means");
+  const mxq_lut::CountSource src{counts, 1, 0, ng, 0};
+  return mxq_lut::launch_kmeans(src, ng, nv, grid, safe, ns, safe_order, max_iters, T, nullptr, mxq_lut::CodeGrid{}, st);
 }
 
 extern "C" int mxq_lut_pick(const float* P, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,
@@ -496,16 +670,9 @@ extern "C" int mxq_lut_pick(const float* P, int64_t K, int64_t n, int32_t group,
   if (K < 0 || n < 0 || group < 0 || group > 30 || width < 2 || width > 4096) return mxq::invalid("mxq_lut_pick: bad arguments");
   if ((I == nullptr) == (P_lut == nullptr)) return mxq::invalid("mxq_lut_pick: exactly one of I and P_lut");
   if (K == 0 || n == 0) return MXQ_OK;
-  const size_t lds = (size_t)((256 >> group) > 0 ? (256 >> group) : 1) * width * sizeof(float);
-  if (lds > 65536) return mxq::invalid("mxq_lut_pick: tables too wide");
-  const int64_t col_blocks = mxq::ceil_div(n, 256);
-  int64_t row_blocks = mxq::ceil_div(1024, col_blocks);             // about four blocks per CU, long stripes
-  if (row_blocks > K) row_blocks = K;
-  if (row_blocks > 65535) row_blocks = 65535;
-  const int64_t rpb = mxq::ceil_div(K, row_blocks);
-  row_blocks = mxq::ceil_div(K, rpb);
-  k_lut_pick<<<dim3((unsigned)col_blocks, (unsigned)row_blocks), 256, lds, mxq::as_stream(stream)>>>(
-      P, K, n, group, T, width, rpb, I, P_lut, nullptr);
+  const uintptr_t out_addr = I ? reinterpret_cast<uintptr_t>(I) : reinterpret_cast<uintptr_t>(P_lut);
+  const bool vec4 = n % 4 == 0 && (reinterpret_cast<uintptr_t>(P) | out_addr) % 16 == 0;
+  if (int rc = launch_pick(P, K, n, group, T, width, I, P_lut, nullptr, vec4, mxq::as_stream(stream))) return rc;
   return mxq::check_launch("mxq_lut_pick");
 }
 
@@ -515,15 +682,7 @@ extern "C" int mxq_lut_pick_packed(const float* P, int64_t K, int64_t n, int32_t
     return mxq::invalid("mxq_lut_pick_packed: bad arguments");
   if (K == 0 || n == 0) return MXQ_OK;
   if (!P || !T || !I4) return mxq::invalid("mxq_lut_pick_packed: NULL pointer");
-  const size_t lds = (size_t)((256 >> group) > 0 ? (256 >> group) : 1) * width * sizeof(float);
-  const int64_t col_blocks = mxq::ceil_div(n, 256);
-  int64_t row_blocks = mxq::ceil_div(1024, col_blocks);
-  if (row_blocks > K) row_blocks = K;
-  if (row_blocks > 65535) row_blocks = 65535;
-  const int64_t rpb = mxq::ceil_div(K, row_blocks);
-  row_blocks = mxq::ceil_div(K, rpb);
-  k_lut_pick<<<dim3((unsigned)col_blocks, (unsigned)row_blocks), 256, lds, mxq::as_stream(stream)>>>(
-      P, K, n, group, T, width, rpb, nullptr, nullptr, I4);
+  if (int rc = launch_pick(P, K, n, group, T, width, nullptr, nullptr, I4, false, mxq::as_stream(stream))) return rc;
   return mxq::check_launch("mxq_lut_pick_packed");
 }
 

@@ -59,14 +59,18 @@ extern "C" int mxq_block_dequantize(const float* P, const float* X, float* out, 
                   ao = reinterpret_cast<uintptr_t>(out);
   auto aligned = [&](int vec) { return inner % vec == 0 && (ap | ax | ao) % (vec * 4) == 0; };
   const int vec = aligned(4) ? 4 : (aligned(2) ? 2 : 1);
-  const int64_t threads = outer * nb * (inner / vec);
+  const int64_t count = outer * n * (inner / vec), xcount = outer * nb * inner;
   hipStream_t st = mxq::as_stream(stream);
-  if (vec == 4)
-    mxq_quant::k_dequant_strided<4><<<mxq::grid_for(threads, 256), 256, 0, st>>>(P, X, out, outer, n, inner, block_size, nb);
-  else if (vec == 2)
-    mxq_quant::k_dequant_strided<2><<<mxq::grid_for(threads, 256), 256, 0, st>>>(P, X, out, outer, n, inner, block_size, nb);
-  else
-    mxq_quant::k_dequant_strided<1><<<mxq::grid_for(threads, 256), 256, 0, st>>>(P, X, out, outer, n, inner, block_size, nb);
+  auto go = [&](auto vec_const, auto idx) {
+    constexpr int VEC = decltype(vec_const)::value;
+    using I = decltype(idx);
+    mxq_quant::k_dequant_flat<VEC, I><<<mxq::grid_for(count, 256), 256, 0, st>>>(
+        P, X, out, (I)count, (I)(inner / VEC), (I)n, (I)block_size, (I)nb);
+  };
+  const bool narrow = count * vec < ((int64_t)1 << 31) && xcount < ((int64_t)1 << 31);   // no wrap near the end
+  if (vec == 4) narrow ? go(std::integral_constant<int, 4>{}, uint32_t{}) : go(std::integral_constant<int, 4>{}, int64_t{});
+  else if (vec == 2) narrow ? go(std::integral_constant<int, 2>{}, uint32_t{}) : go(std::integral_constant<int, 2>{}, int64_t{});
+  else narrow ? go(std::integral_constant<int, 1>{}, uint32_t{}) : go(std::integral_constant<int, 1>{}, int64_t{});
   return mxq::check_launch("mxq_block_dequantize");
 }
 

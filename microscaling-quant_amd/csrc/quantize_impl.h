@@ -16,6 +16,7 @@
 #include "mxq_numerics.h"
 
 #include <stdlib.h>
+#include <type_traits>
 
 namespace mxq_quant {
 
@@ -144,6 +145,11 @@ struct ByteSink {
   // that the format lacks, take mx_encode.
   template <int ELEM, int MODE, int VEC>
   __device__ __forceinline__ void elems(int64_t at, const float (&z)[VEC], const mxq_block_spec& s) const {
+    store_bytes<VEC>(P + at, word<ELEM, MODE, VEC>(z, s));
+  }
+  // The codes of VEC (at most 4) scaled values, code j in byte j.
+  template <int ELEM, int MODE, int VEC>
+  __device__ __forceinline__ uint32_t word(const float (&z)[VEC], const mxq_block_spec& s) const {
     uint32_t w = 0u;
     bool all_good = true;
     if constexpr (ELEM == MXQ_ELEM_OCP && MODE >= 0) {
@@ -154,9 +160,7 @@ struct ByteSink {
           w |= ocp_code_t<MODE>(z[j], e, m, maxcode, &good) << (8 * j);
           all_good = all_good && good;
         }
-        if (!all_good) w = general_codes<ELEM, MODE, VEC>(z, s);
-        store_bytes<VEC>(P + at, w);
-        return;
+        return all_good ? w : general_codes<ELEM, MODE, VEC>(z, s);
       }
     }
 #pragma unroll
@@ -165,8 +169,7 @@ struct ByteSink {
       w |= short_encode(elem_qm<ELEM, MODE>(z[j], s), k, good) << (8 * j);
       all_good = all_good && good;
     }
-    if (!all_good) w = general_codes<ELEM, MODE, VEC>(z, s);
-    store_bytes<VEC>(P + at, w);
+    return all_good ? w : general_codes<ELEM, MODE, VEC>(z, s);
   }
   template <int ELEM, int MODE, int VEC>
   __device__ __forceinline__ uint32_t general_codes(const float (&z)[VEC], const mxq_block_spec& s) const {
@@ -457,31 +460,23 @@ int launch_quant_t(const T* M, float* P, float* X, int64_t n, int64_t inner, con
   return mxq::check_launch("mxq_block_quantize_t");
 }
 
-template <int VEC>
-__global__ void __launch_bounds__(256) k_dequant_strided(const float* __restrict__ P, const float* __restrict__ X,
-                                                         float* __restrict__ out, int64_t outer, int64_t n,
-                                                         int64_t inner, int64_t bs, int64_t nb) {
-  const int64_t groups = inner / VEC;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= outer * nb * groups) return;
-  int64_t o, b, g;
-  split_index(t, groups, nb, o, b, g);
-  const int64_t k0 = b * bs;
-  const int64_t rows = (n - k0 < bs) ? n - k0 : bs;
-  const int64_t off = (o * n + k0) * inner + g * VEC;
-  float xs[VEC];
-  {
-    VecT<float, VEC> r = *reinterpret_cast<const VecT<float, VEC>*>(X + (o * nb + b) * inner + g * VEC);
+// out = P * expand(X) as one flat pass over the (outer, n, inner) view: a thread takes VEC adjacent elements of a
+// row (one block, so one VEC-wide load of X), and every thread has work, whatever the block size and shape.
+// I is uint32_t while the element count fits it (cheap index arithmetic), else int64_t.
+template <int VEC, typename I>
+__global__ void __launch_bounds__(256) k_dequant_flat(const float* __restrict__ P, const float* __restrict__ X,
+                                                      float* __restrict__ out, I count, I inner_v, I n, I bs, I nb) {
+  const I t = (I)blockIdx.x * 256u + (I)threadIdx.x;
+  if (t >= count) return;
+  const I row = t / inner_v;                      // (o, k) flattened
+  const I iv = t - row * inner_v;
+  const I o = row / n, k = row - o * n;
+  float v[VEC], xs[VEC];
+  load_vec<float, VEC>(P + (int64_t)t * VEC, v);
+  load_vec<float, VEC>(X + ((int64_t)(o * nb + k / bs) * inner_v + iv) * VEC, xs);
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) xs[j] = r.v[j];
-  }
-  for (int64_t r = 0; r < rows; ++r) {
-    float v[VEC];
-    load_vec<float, VEC>(P + off + r * inner, v);
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) v[j] = v[j] * xs[j];
-    store_vec_nt<VEC>(out + off + r * inner, v);
-  }
+  for (int j = 0; j < VEC; ++j) v[j] = v[j] * xs[j];
+  store_vec_nt<VEC>(out + (int64_t)t * VEC, v);
 }
 
 // ------------------------------------------------------------------------------------------ host side
@@ -532,13 +527,20 @@ int launch_quant(const T* V, const SINK& out, int64_t outer, int64_t n, int64_t 
   };
   const int vec = aligned(4) ? 4 : (aligned(2) ? 2 : 1);
   if (bs == 32) {
-    constexpr int R = 8;
-    const int64_t wpr = mxq::ceil_div(inner / vec, 64 / R);
-    const int64_t threads = outer * nb * wpr * 64;
-    const dim3 grid = mxq::grid_for(threads, 256);
-    if (vec == 4) k_quant_split<T, ELEM, MODE, 4, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
-    else if (vec == 2) k_quant_split<T, ELEM, MODE, 2, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
-    else k_quant_split<T, ELEM, MODE, 1, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
+    // R = 8 lanes per block column (4 rows each) while that gives the chip at least 8 waves per SIMD; smaller
+    // tensors take R = 32 (one row per lane, four times the waves), which keeps more loads in flight (MI355X,
+    // block.ocp on 4096 x 512 float32: 12.2 us at R = 8, 9.7 us at R = 32; bf16 8192 x 8192: R = 8 fastest)
+    const int64_t waves8 = outer * nb * mxq::ceil_div(inner / vec, 64 / 8);
+    auto go = [&](auto r_const) {
+      constexpr int R = decltype(r_const)::value;
+      const int64_t wpr = mxq::ceil_div(inner / vec, 64 / R);
+      const dim3 grid = mxq::grid_for(outer * nb * wpr * 64, 256);
+      if (vec == 4) k_quant_split<T, ELEM, MODE, 4, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
+      else if (vec == 2) k_quant_split<T, ELEM, MODE, 2, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
+      else k_quant_split<T, ELEM, MODE, 1, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
+    };
+    if (waves8 >= 8 * 1024) go(std::integral_constant<int, 8>{});
+    else go(std::integral_constant<int, 32>{});
     return mxq::check_launch("mxq_block_quantize");
   }
   const int64_t threads = outer * nb * (inner / vec);

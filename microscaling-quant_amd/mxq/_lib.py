@@ -101,9 +101,12 @@ SIGNATURES = {
                                 c_i32, ctypes.POINTER(AnchorSpec), ctypes.POINTER(ArithSpec), c_ptr, c_i32, c_ptr]),
     "mxq_mx_pack": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_ptr, c_ptr]),
     "mxq_mx_mfma": (c_i32, [c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr]),
-    "mxq_lut_tables": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr,
-                               c_ptr]),
+    "mxq_lut_tables": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_i32, c_i32,
+                               c_ptr, c_ptr, c_ptr]),
     "mxq_lut_pick": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr]),
+    "mxq_block_lut": (c_i32, [c_ptr, c_i32, c_i64, c_i64, ctypes.POINTER(BlockSpec), c_i32, c_i32, c_ptr, c_i32,
+                              c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr]),
+    "mxq_block_lut_workspace": (c_i32, [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, ctypes.POINTER(c_i64)]),
     "mxq_lut_lookup": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr]),
     "mxq_lut_finder": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_i64, c_ptr, c_ptr]),
     "mxq_round_bits": (c_i32, [c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i32, c_ptr]),

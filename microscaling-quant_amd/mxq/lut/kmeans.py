@@ -33,26 +33,50 @@ def _check_tables(T: torch.Tensor, ng: int, n: int, group: int, who: str) -> Non
                          f"got {tuple(T.shape)}")
 
 
-def tables(P: torch.Tensor, fmt, *, group: int, max_iters: int) -> torch.Tensor:
-    """One SIZE-entry table per 2^group columns of P (K x n block codes, each a value of fmt)."""
+_DEVICE_GRIDS = {}
+
+
+def _device_grid(name: str, dev: torch.device):
+    """(value grid, safe values, safe order) of a format on `dev`, copied there once per process."""
+    key = (name, dev)
+    if key not in _DEVICE_GRIDS:
+        grid, order = _grid(name)
+        _DEVICE_GRIDS[key] = (grid.to(dev), _tables(name)[2].to(dev), order.to(dev))
+    return _DEVICE_GRIDS[key]
+
+
+def _not_a_code(fmt_name: str) -> ValueError:
+    return ValueError(f"mxq.lut: P holds a value that is not a {fmt_name} code; quantize it first")
+
+
+def fit(P: torch.Tensor, fmt, group: int, max_iters: int):
+    """(T, err): the tables of `tables` and, on P's compute device, the int32 word the kernels set when P holds
+    a value that is not a code of fmt (read it to raise as `tables` does).  No host synchronisation."""
     f = _format(fmt)
     ng = _check(P, group)
     if not isinstance(max_iters, int) or isinstance(max_iters, bool) or max_iters < 0:
         raise ValueError(f"mxq.lut: max_iters {max_iters!r} must be a non-negative integer")
     dev = _lib.compute_device(P)
     Pd = _lib.to_device(P.detach(), dev).to(torch.float32).contiguous()
-    grid, order = _grid(f.name)
-    safe = _tables(f.name)[2]
+    g_d, s_d, o_d = _device_grid(f.name, dev)
     K, n = Pd.shape
-    nv = grid.numel()
-    g_d, s_d, o_d = grid.to(dev), safe.to(dev), order.to(dev)
+    nv = g_d.numel()
     T = torch.empty((ng, SIZE), dtype=torch.float32, device=dev)
     work = torch.empty(ng * nv + 1, dtype=torch.int32, device=dev)
+    if n == 0:
+        work.zero_()
     with torch.cuda.device(dev):
         _lib.run("mxq_lut_tables", _lib.ptr(Pd), K, n, group, max_iters, _lib.ptr(g_d), nv, _lib.ptr(s_d),
-                 safe.numel(), _lib.ptr(o_d), _lib.ptr(T), _lib.ptr(work), _lib.stream(dev))
-    if n and K and int(work[-1].item()):
-        raise ValueError(f"mxq.lut: P holds a value that is not a {f.name} code; quantize it first")
+                 s_d.numel(), _lib.ptr(o_d), f.e, f.m, _lib.ptr(T), _lib.ptr(work), _lib.stream(dev))
+    return T, work[-1:]
+
+
+def tables(P: torch.Tensor, fmt, *, group: int, max_iters: int) -> torch.Tensor:
+    """One SIZE-entry table per 2^group columns of P (K x n block codes, each a value of fmt)."""
+    f = _format(fmt)
+    T, err = fit(P, fmt, group, max_iters)
+    if int(err.item()):
+        raise _not_a_code(f.name)
     return _lib.back(T, P)
 
 

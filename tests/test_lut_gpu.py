@@ -112,3 +112,127 @@ def test_lut_errors(cuda):
     with pytest.raises(ValueError, match="need"):
         lut.finder(torch.zeros(4, 3, dtype=torch.int64, device="cuda"), torch.zeros(1, 16, device="cuda"), "MXFP6_E3M2",
                    group=1)
+
+
+@pytest.mark.parametrize("fmt", ol.FORMATS)
+def test_grid_index_matches_search(cuda, fmt):
+    """The tables' histogram placing each code by its bits (grid index) against the same kernel searching the
+    grid (the format passed as unknown): identical tables, and both the oracle's, on every code of the format
+    (both zeros, subnormals, the largest, E4M3's 480) at group 0, 1 and 2.  The pick on values that are no code
+    (and on every code) against the oracle, as entries and as int64 indices."""
+    from mxq import _lib, lut
+    from mxq.lut import formats as lf
+    from mxq.lut import kmeans
+    rng = np.random.default_rng(ol.FORMATS.index(fmt) + 40)
+    vals = lf._tables(fmt)[0].numpy()
+    codes = vals[np.isfinite(vals)]
+    for G in (0, 1, 2):
+        P = rng.choice(codes, size=(257, 64)).astype(np.float32)
+        P[:, 5] = -0.0
+        Pd = torch.from_numpy(P).cuda()
+        T, err = kmeans.fit(Pd, fmt, G, 50)
+        assert int(err.item()) == 0
+        f = lf._format(fmt)
+        g_d, s_d, o_d = kmeans._device_grid(f.name, Pd.device)
+        ng, nv = T.shape[0], g_d.numel()
+        T2 = torch.empty_like(T)
+        work = torch.empty(ng * nv + 1, dtype=torch.int32, device="cuda")
+        _lib.run("mxq_lut_tables", _lib.ptr(Pd), 257, 64, G, 50, _lib.ptr(g_d), nv, _lib.ptr(s_d), s_d.numel(),
+                 _lib.ptr(o_d), 0, 0, _lib.ptr(T2), _lib.ptr(work), _lib.stream(Pd.device))
+        assert_bits_equal(T2.cpu().numpy(), T.cpu().numpy(), f"tables by grid search {fmt} G{G}")
+        assert_bits_equal(T.cpu().numpy(), ol.tables(P, fmt, G, 50), f"tables vs oracle {fmt} G{G}")
+        Q = P.copy()
+        Q[3, :7] = [0.3, -1e-30, 1e30, 0.0, -0.0, 2.0 ** -140, -7.7]
+        Qd = torch.from_numpy(Q).cuda()
+        Tn = T.cpu().numpy()
+        want_i = ol.pick(Q, Tn, G)
+        assert_bits_equal(kmeans.pick_values(Qd, T, group=G).cpu().numpy(), ol.lookup(want_i, Tn, G), "values")
+        assert np.array_equal(lut.pick(Qd, T, group=G).cpu().numpy(), want_i), f"pick indices {fmt} G{G}"
+
+
+def _steps(V, fmt, G, iters, mode, floor):
+    """block.lut along axis 0 step by step: the float32 quantize kernel, the histogram and k-means kernels,
+    the pick kernel (the path for shapes the one-call path does not take)."""
+    from mxq import block
+    from mxq.lut import kmeans
+    P, X = block.mxgemmini.quantize(V, fmt, axis=0, rounding_mode=mode, scale_floor=floor)
+    T, err = kmeans.fit(P, fmt, G, iters)
+    assert int(err.item()) == 0
+    return kmeans.pick_values(P, T, group=G), X
+
+
+_FUSED_CASES = [  # (shape, group, input dtype, rounding, scale floor)
+    ((100, 48), 0, torch.float32, "rne", 2.0 ** -23),
+    ((4100, 144), 1, torch.float32, "rne", 2.0 ** -23),      # a tail block, a tile of 16 live columns
+    ((1285, 16), 3, torch.bfloat16, "ties_away", 2.0 ** -23),  # two splits, the second shorter
+    ((2048, 256), 1, torch.float16, "truncate", None),      # four splits of 16 blocks, two tiles
+    ((1, 16), 1, torch.float32, "rne", None),
+    ((96, 2048), 8, torch.float32, "ties_away", 2.0 ** -23),  # groups of two tiles
+    ((33, 160), 5, torch.bfloat16, "rne", 2.0 ** -23),
+    ((70, 4096), 12, torch.float32, "rne", 2.0 ** -23),      # one group over 32 tiles
+]
+
+
+@pytest.mark.parametrize("fmt", ol.FORMATS)
+@pytest.mark.parametrize("case", range(len(_FUSED_CASES)))
+def test_block_lut_one_call_against_steps(cuda, fmt, case):
+    """block.lut's one-call path (mxq_block_lut: byte codes, fused counts, code-map pick) bit for bit against the
+    step-by-step kernels on the same input: P (table entries) and X.  Shapes with tails, one and several splits,
+    groups inside a tile and wider than one, all three input types and rounding modes; the FP8 formats at
+    groups 0 and 1 take 32-column tiles."""
+    from mxq import block
+    from mxq.scale_factor import MXQUANT_FLOOR
+    shape, G, dt, mode, floor = _FUSED_CASES[case]
+    floor = MXQUANT_FLOOR if floor is None else floor
+    g = torch.Generator().manual_seed(case * 10 + ol.FORMATS.index(fmt))
+    V = (torch.randn(shape, generator=g) * torch.exp2(torch.randint(-6, 6, (1, shape[1]), generator=g).float()))
+    V = V.to(dt).cuda()
+    V[0, 0] = 0.0
+    if shape[0] > 40:
+        V[32:64, 1] = 0.0                                    # an all-zero block
+        V[5, 2] = -0.0
+    P, X = block.lut.quantize(V, fmt, 0, 32, rounding_mode=mode, scale_floor=floor, group=G, max_iters=50)
+    wP, wX = _steps(V, fmt, G, 50, mode, floor)
+    assert_bits_equal(X.cpu().numpy(), wX.cpu().numpy(), f"X {fmt} {shape} G{G}")
+    assert_bits_equal(P.cpu().numpy(), wP.cpu().numpy(), f"P {fmt} {shape} G{G}")
+
+
+@pytest.mark.parametrize("fmt", ol.FORMATS)
+def test_block_lut_one_call_against_oracle(cuda, fmt):
+    """The one-call path against the oracle's block.lut on a Student-t input with per-column scale spread
+    (600 x 96, group 1, and 64 x 32, group 0, 7 iterations)."""
+    from mxq import block
+    rng = np.random.default_rng(70 + ol.FORMATS.index(fmt))
+    for shape, G, iters in [((600, 96), 1, 50), ((64, 32), 0, 7)]:
+        V = (rng.standard_t(4, shape) * np.exp2(rng.integers(-8, 8, (1, shape[1])))).astype(np.float32)
+        P, X = block.lut.quantize(torch.from_numpy(V).cuda(), fmt, 0, 32, rounding_mode="rne",
+                                  scale_floor=2.0 ** -23, group=G, max_iters=iters)
+        wP, wX = ol.lut_quantize(V, fmt, 0, 32, "rne", 2.0 ** -23, G, iters)
+        assert_bits_equal(X.cpu().numpy(), wX, f"X {fmt} {shape}")
+        assert_bits_equal(P.cpu().numpy(), wP, f"P {fmt} {shape}")
+
+
+def test_block_lut_one_call_errors(cuda):
+    """A non-finite V gives codes that are not values of the format: the one-call path raises what the tables
+    raise (E3M2 has no NaN or Inf code: the encoder flags it; E5M2 has them: the count flags it), and the
+    argument checks come in the step-by-step path's order."""
+    from mxq import block
+    V = torch.randn(64, 32, device="cuda")
+    V[7, 3] = float("nan")
+    for fmt in ("MXFP6_E3M2", "MXFP8_E5M2"):
+        with pytest.raises(ValueError, match=f"not a {fmt} code"):
+            block.lut.quantize(V, fmt, 0, 32, rounding_mode="rne", scale_floor=2.0 ** -23, group=1, max_iters=5)
+    W = torch.randn(64, 32, device="cuda")
+    W[9, 30] = float("inf")
+    with pytest.raises(ValueError, match="not a MXFP8_E5M2 code"):
+        block.lut.quantize(W, "MXFP8_E5M2", 0, 32, rounding_mode="rne", scale_floor=2.0 ** -23, group=1, max_iters=5)
+    ok = torch.randn(64, 32, device="cuda")
+    with pytest.raises(ValueError, match="group"):
+        block.lut.quantize(ok, "MXFP6_E3M2", 0, 32, rounding_mode="rne", scale_floor=2.0 ** -23, group=-1,
+                           max_iters=5)
+    with pytest.raises(ValueError, match="max_iters"):
+        block.lut.quantize(ok, "MXFP6_E3M2", 0, 32, rounding_mode="rne", scale_floor=2.0 ** -23, group=0,
+                           max_iters=-1)
+    with pytest.raises(ValueError):
+        block.lut.quantize(ok, "MXFP6_E3M2", 0, 32, rounding_mode="nearest", scale_floor=2.0 ** -23, group=0,
+                           max_iters=5)

@@ -152,6 +152,12 @@ def test_dequantize(cuda):
     P2, X2 = block.mxgemmini.quantize(torch.from_numpy(V).cuda(), "MXFP8_E5M2", axis=1, block_size=5)
     got2 = block.mxgemmini.dequantize(P2, X2, axis=1, block_size=5).cpu().numpy()
     assert_bits_equal(got2, ob.dequantize(P2.cpu().numpy(), X2.cpu().numpy(), 1, 5), "dequantize axis 1")
+    # every vector width of the flat kernel (inner a multiple of 4, of 2 only, odd), 3-D views, tails
+    for shape, axis, bs in [((4096, 512), 0, 32), ((3, 70, 6), 1, 32), ((5, 33, 7), 1, 16), ((2, 9, 40), -1, 32)]:
+        W = _edge_matrix(rng, shape[0], int(np.prod(shape[1:]))).reshape(shape)
+        P3, X3 = block.mxquant.quantize(torch.from_numpy(W).cuda(), "MXFP8_E4M3", axis=axis, block_size=bs)
+        got3 = block.dequantize(P3, X3, axis=axis, block_size=bs).cpu().numpy()
+        assert_bits_equal(got3, ob.dequantize(P3.cpu().numpy(), X3.cpu().numpy(), axis, bs), f"dequantize {shape}")
 
 
 # ------------------------------------------------------------------------------------------ elementwise
