@@ -164,8 +164,9 @@ extern "C" int mxq_block_lut(const void* V, int32_t v_dtype, int64_t K, int64_t 
                              int64_t workspace_bytes, int32_t* err, mxq_stream_t stream) {
   if (!spec) return mxq::invalid("mxq_block_lut: spec is NULL");
   if (int rc = mxq_quant::validate(*spec)) return rc;
-  if (spec->elem != MXQ_ELEM_OCP || spec->via_e != 0)
-    return mxq::invalid("mxq_block_lut: the spec must be MX-Gemmini's (the OCP element grid, no via)");
+  if (spec->scale_rule != MXQ_SCALE_MXQUANT || spec->elem != MXQ_ELEM_OCP || spec->via_e != 0 ||
+      !mxq_ocp_hw::has_hw(spec->e, spec->m))
+    return mxq::invalid("mxq_block_lut: the spec must be MX-Gemmini's (its scale, the OCP element grid, no via)");
   CodeGrid cg;
   if (int rc = check_args(K, n, group, spec->e, spec->m, nv, &cg, "mxq_block_lut")) return rc;
   if (max_iters < 0 || ns < 1 || ns > mxq_lut::kMaxGrid) return mxq::invalid("mxq_block_lut: bad max_iters or ns");

@@ -26,7 +26,7 @@ struct LutQuantArgs {
   CodeGrid cg;
   int64_t blocks_per_split;
   int64_t split_stride;      // words between two splits' slices of `partial`
-  mxq_quant::ByteSink sink;  // the element codes (its X is unused)
+  mxq_quant::ByteSink sink;  // the element codes off nearest even (its X is unused)
 };
 
 template <typename T, int MODE, int VEC, int CW>
@@ -98,7 +98,8 @@ __global__ void __launch_bounds__(1024) k_lut_quant(const T* __restrict__ V, Lut
       for (int q = 0; q < VEC / 4; ++q)
         *reinterpret_cast<float4*>(xd + 4 * q) = make_float4(xs[4 * q], xs[4 * q + 1], xs[4 * q + 2], xs[4 * q + 3]);
     }
-    if (s.scale_rule && !__all(p2)) {
+    const bool div = s.scale_rule && !__all(p2);
+    if (div) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -111,16 +112,17 @@ __global__ void __launch_bounds__(1024) k_lut_quant(const T* __restrict__ V, Lut
         for (int i = 0; i < 4; ++i) v[i][j] = v[i][j] * inv;
       }
     }
+    // nearest even: the hardware conversions give the codes (ocp_hw.h).  Under MX-Gemmini's scale every
+    // finite V scales to |z| < 2, inside their range; a non-finite one (whose codes block.lut refuses) sets
+    // the flag instead.
+    if constexpr (MODE == MXQ_RNE) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) bad |= !(am[j] < 0x7F800000u);
+    }
     if (!live) continue;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (rows != 32 && r * 4 + i >= rows) continue;
-      uint32_t wd[VEC / 4];
-#pragma unroll
-      for (int q = 0; q < VEC / 4; ++q) {
-        const float z[4] = {v[i][4 * q], v[i][4 * q + 1], v[i][4 * q + 2], v[i][4 * q + 3]};
-        wd[q] = a.sink.template word<MXQ_ELEM_OCP, MODE, 4>(z, s);
-      }
+    // row i's VEC codes: stored, and each counted in its column's unit (a code with no bin, from a non-finite
+    // V, sets the flag and is counted in bin 0: the call then raises, and no branch per code is needed)
+    auto emit = [&](int i, const uint32_t (&wd)[VEC / 4]) {
       uint8_t* dst = a.codes + (k0 + r * 4 + i) * n + j0;
       if constexpr (VEC == 8) *reinterpret_cast<uint2*>(dst) = make_uint2(wd[0], wd[1]);
       else *reinterpret_cast<uint32_t*>(dst) = wd[0];
@@ -128,12 +130,39 @@ __global__ void __launch_bounds__(1024) k_lut_quant(const T* __restrict__ V, Lut
       for (int q = 0; q < VEC / 4; ++q)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          // a code with no bin (from a non-finite V) sets the flag and is counted in bin 0: the call then
-          // raises, and no branch per code is needed
           const int bin = code_bin((wd[q] >> (8 * t)) & 0xFFu, a.cg);
           bad |= bin < 0;
           atomicAdd(&hist[((jt + 4 * q + t) >> a.group) * a.nv + (bin < 0 ? 0 : bin)], 1);
         }
+    };
+    if constexpr (MODE == MXQ_RNE) {
+      float z[4 * VEC];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) z[i * VEC + j] = v[i][j];
+      uint32_t c[VEC];                                 // row i in words i * VEC / 4 ..
+      mxq_ocp_hw::codes<4 * VEC>(z, s.e, s.m, c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (rows != 32 && r * 4 + i >= rows) continue;
+        uint32_t wd[VEC / 4];
+#pragma unroll
+        for (int q = 0; q < VEC / 4; ++q) wd[q] = c[i * (VEC / 4) + q];
+        emit(i, wd);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (rows != 32 && r * 4 + i >= rows) continue;
+        uint32_t wd[VEC / 4];
+#pragma unroll
+        for (int q = 0; q < VEC / 4; ++q) {
+          const float z[4] = {v[i][4 * q], v[i][4 * q + 1], v[i][4 * q + 2], v[i][4 * q + 3]};
+          wd[q] = a.sink.template word<MXQ_ELEM_OCP, MODE, 4>(z, s);
+        }
+        emit(i, wd);
+      }
     }
   }
   if (bad) atomicOr(a.err, 1);

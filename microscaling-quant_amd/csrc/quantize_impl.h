@@ -14,6 +14,7 @@
 #pragma once
 #include "mxq_common.h"
 #include "mxq_numerics.h"
+#include "ocp_hw.h"
 
 #include <stdlib.h>
 #include <type_traits>
@@ -79,6 +80,28 @@ struct FloatSink {
   __device__ __forceinline__ void scales(int64_t at, const float (&xs)[VEC], const bool (&)[VEC]) const {
     store_vec<VEC>(X + at, xs);
   }
+  // The OCP grid rounded to nearest even by the hardware conversions (ocp_hw.h; the caller has checked the
+  // range): the rows of a lane's strip of VEC (4 or 8) columns, rows [0, live) stored.
+  template <int ROWS, int VEC>
+  __device__ __forceinline__ void hw_rows(int64_t at, int64_t stride, const float (&v)[ROWS][VEC], int live,
+                                          const mxq_block_spec& s) const {
+    float z[ROWS * VEC];
+#pragma unroll
+    for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) z[VEC * i + j] = v[i][j];
+    mxq_ocp_hw::values<ROWS * VEC>(z, s.e, s.m);
+#pragma unroll
+    for (int i = 0; i < ROWS; ++i) {
+      if (i >= live) break;
+#pragma unroll
+      for (int q = 0; q < VEC / 4; ++q) {
+        const float o[4] = {z[VEC * i + 4 * q], z[VEC * i + 4 * q + 1], z[VEC * i + 4 * q + 2], z[VEC * i + 4 * q + 3]};
+        store_vec_nt<4>(P + at + (int64_t)i * stride + 4 * q, o);
+      }
+    }
+  }
+  __device__ __forceinline__ bool hw_format(const mxq_block_spec&) const { return true; }
   __device__ __forceinline__ uintptr_t p_addr() const { return reinterpret_cast<uintptr_t>(P); }
   __device__ __forceinline__ uintptr_t x_addr() const { return reinterpret_cast<uintptr_t>(X); }
 };
@@ -88,6 +111,23 @@ __device__ __forceinline__ void store_bytes(uint8_t* p, uint32_t w) {
   if constexpr (VEC == 4) __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(p));
   else if constexpr (VEC == 2) *reinterpret_cast<uint16_t*>(p) = (uint16_t)w;
   else *p = (uint8_t)w;
+}
+
+// W words of code bytes (1, 2 or 4: 4, 8 or 16 bytes, aligned), one streaming store.
+template <int W>
+__device__ __forceinline__ void store_words(uint8_t* p, const uint32_t (&w)[W]) {
+  if constexpr (W == 1) {
+    __builtin_nontemporal_store(w[0], reinterpret_cast<uint32_t*>(p));
+  } else if constexpr (W == 4) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = {w[0], w[1], w[2], w[3]};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+  } else {
+    static_assert(W == 2, "4, 8 or 16 bytes");
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = {w[0], w[1]};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
+  }
 }
 
 // The element format's constants for the byte sink's short encoder.
@@ -145,7 +185,17 @@ struct ByteSink {
   // that the format lacks, take mx_encode.
   template <int ELEM, int MODE, int VEC>
   __device__ __forceinline__ void elems(int64_t at, const float (&z)[VEC], const mxq_block_spec& s) const {
-    store_bytes<VEC>(P + at, word<ELEM, MODE, VEC>(z, s));
+    if constexpr (VEC == 8 || VEC == 16) {
+      uint32_t w[VEC / 4];
+#pragma unroll
+      for (int q = 0; q < VEC / 4; ++q) {
+        const float z4[4] = {z[4 * q], z[4 * q + 1], z[4 * q + 2], z[4 * q + 3]};
+        w[q] = word<ELEM, MODE, 4>(z4, s);
+      }
+      store_words<VEC / 4>(P + at, w);
+    } else {
+      store_bytes<VEC>(P + at, word<ELEM, MODE, VEC>(z, s));
+    }
   }
   // The codes of VEC (at most 4) scaled values, code j in byte j.
   template <int ELEM, int MODE, int VEC>
@@ -180,13 +230,47 @@ struct ByteSink {
     if (!ok) atomicOr(err, 1);
     return w;
   }
+  // hw_rows of FloatSink with the codes themselves (the byte format is the element format: e, m == s.e, s.m).
+  template <int ROWS, int VEC>
+  __device__ __forceinline__ void hw_rows(int64_t at, int64_t stride, const float (&v)[ROWS][VEC], int live,
+                                          const mxq_block_spec& s) const {
+    float z[ROWS * VEC];
+#pragma unroll
+    for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) z[VEC * i + j] = v[i][j];
+    // the conversions take at most 32 values: in chunks of rows
+    constexpr int CH = ROWS * VEC <= 32 ? ROWS * VEC : 32;
+    uint32_t w[ROWS * VEC / 4];
+#pragma unroll
+    for (int c0 = 0; c0 < ROWS * VEC; c0 += CH) {
+      float zc[CH];
+      uint32_t wc[CH / 4];
+#pragma unroll
+      for (int k = 0; k < CH; ++k) zc[k] = z[c0 + k];
+      mxq_ocp_hw::codes<CH>(zc, s.e, s.m, wc);
+#pragma unroll
+      for (int k = 0; k < CH / 4; ++k) w[c0 / 4 + k] = wc[k];
+    }
+#pragma unroll
+    for (int i = 0; i < ROWS; ++i) {
+      if (i >= live) break;
+      uint32_t row[VEC / 4];
+#pragma unroll
+      for (int q = 0; q < VEC / 4; ++q) row[q] = w[i * (VEC / 4) + q];
+      store_words<VEC / 4>(P + at + (int64_t)i * stride, row);
+    }
+  }
+  // the codes the conversions give are the byte format's when it is the grid's
+  __device__ __forceinline__ bool hw_format(const mxq_block_spec& s) const { return e == s.e && m == s.m; }
   template <int VEC>
   __device__ __forceinline__ void scales(int64_t at, const float (&xs)[VEC], const bool (&zero)[VEC]) const {
     bool ok = true;
-    uint32_t w = 0u;
+    uint32_t w[(VEC + 3) / 4] = {};
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) w |= e8m0_encode(xs[j], zero[j], &ok) << (8 * j);
-    store_bytes<VEC>(X + at, w);
+    for (int j = 0; j < VEC; ++j) w[j / 4] |= e8m0_encode(xs[j], zero[j], &ok) << (8 * (j % 4));
+    if constexpr (VEC >= 8) store_words<VEC / 4>(X + at, w);
+    else store_bytes<VEC>(X + at, w[0]);
     if (!ok) atomicOr(err, 2);
   }
   __device__ __forceinline__ uintptr_t p_addr() const { return reinterpret_cast<uintptr_t>(P); }
@@ -273,15 +357,16 @@ __global__ void __launch_bounds__(256) k_quant_strided(const T* __restrict__ V, 
 //     column group 0 (valid memory) and store nothing.
 //   * The block maximum is the largest |v| bit pattern (non-negative floats order like their patterns, and
 //     every NaN pattern lies above +Inf, so a NaN wins as torch.amax's does).
-//   * The R lanes of a column group hold the same maxima after the exchanges; lane r < VEC computes the scale
-//     of column r alone and the others read it (one scale rule evaluation per lane instead of VEC).
+//   * The R lanes of a column group hold the same maxima after the exchanges; lane r computes the scales of
+//     columns r, r + R, ... alone and the others read them (ceil(VEC / R) scale rule evaluations per lane
+//     instead of VEC).
 template <typename T, int ELEM, int MODE, int VEC, int R, typename SINK>
 __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, const SINK out, int64_t outer,
                                                      int64_t n, int64_t inner, int64_t nb, int64_t waves_per_row,
                                                      mxq_block_spec s) {
   constexpr int CPW = 64 / R;          // column groups per wave
   constexpr int ROWS = 32 / R;         // rows per lane
-  static_assert(VEC <= R, "one scale-computing lane per column");
+  constexpr int PER = (VEC + R - 1) / R;  // scales each lane evaluates
   const int64_t groups = inner / VEC;
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * (256 / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -321,19 +406,26 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, co
   for (int step = CPW; step < 64; step <<= 1)
 #pragma unroll
     for (int j = 0; j < VEC; ++j) am[j] = max(am[j], (uint32_t)__shfl_xor((int)am[j], step, 64));
-  // lane r < VEC: the scale of column r of its group; every lane then reads column j's from lane c + j * CPW
-  uint32_t mine = am[0];
+  // lane r evaluates the scales of columns r, r + R, ... of its group (those below VEC); every lane then reads
+  // column j's from lane c + (j % R) * CPW
+  float own[PER];
 #pragma unroll
-  for (int j = 1; j < VEC; ++j) mine = (r == j) ? am[j] : mine;
-  const float own = block_scale(u2f(mine), s);
+  for (int q = 0; q < PER; ++q) {
+    uint32_t mine = am[q * R];
+#pragma unroll
+    for (int jj = 1; jj < R; ++jj)
+      if (q * R + jj < VEC) mine = (r == jj) ? am[q * R + jj] : mine;
+    own[q] = block_scale(u2f(mine), s);
+  }
   float xs[VEC];
   Div d[VEC];
 #pragma unroll
   for (int j = 0; j < VEC; ++j) {
-    xs[j] = __shfl(own, c + j * CPW, 64);
+    xs[j] = __shfl(own[j / R], c + (j % R) * CPW, 64);
     d[j] = make_div(xs[j]);
   }
-  if (s.scale_rule && wave_needs_div<VEC>(d)) {
+  const bool div = s.scale_rule && wave_needs_div<VEC>(d);
+  if (div) {
 #pragma unroll
     for (int i = 0; i < ROWS; ++i)
 #pragma unroll
@@ -344,11 +436,32 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, co
 #pragma unroll
       for (int j = 0; j < VEC; ++j) v[i][j] = v[i][j] * d[j].inv;
   }
+  // the OCP grid at nearest even by the hardware conversions when every scaled value of the wave is finite
+  // and within their range (a column's largest |z| is its maximum scaled, the division being monotone)
+  bool hw = false;
+  if constexpr (ELEM == MXQ_ELEM_OCP && MODE == MXQ_RNE && VEC >= 4) {
+    if (s.via_e == 0 && mxq_ocp_hw::has_hw(s.e, s.m) && out.hw_format(s)) {
+      const float lim = mxq_ocp_hw::hw_limit(s.e, s.m);
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float a = u2f(am[j]);
+        const float zm = !s.scale_rule ? a : (div ? apply_div(a, d[j]) : a * d[j].inv);
+        ok = ok && am[j] < 0x7F800000u && zm < lim;
+      }
+      hw = __all(ok);
+    }
+  }
   if (!live) return;
   const int64_t dst = (o * n + k0 + r * ROWS) * inner + cg * VEC;
+  if constexpr (ELEM == MXQ_ELEM_OCP && MODE == MXQ_RNE && VEC >= 4) {
+    if (hw) out.template hw_rows<ROWS, VEC>(dst, inner, v, rows == 32 ? ROWS : rows - r * ROWS, s);
+  }
+  if (!hw) {
 #pragma unroll
-  for (int i = 0; i < ROWS; ++i) {
-    if (rows == 32 || r * ROWS + i < rows) out.template elems<ELEM, MODE, VEC>(dst + (int64_t)i * inner, v[i], s);
+    for (int i = 0; i < ROWS; ++i) {
+      if (rows == 32 || r * ROWS + i < rows) out.template elems<ELEM, MODE, VEC>(dst + (int64_t)i * inner, v[i], s);
+    }
   }
   if (r == 0) {
     bool zero[VEC];
@@ -527,14 +640,25 @@ int launch_quant(const T* V, const SINK& out, int64_t outer, int64_t n, int64_t 
   };
   const int vec = aligned(4) ? 4 : (aligned(2) ? 2 : 1);
   if (bs == 32) {
+    // code bytes: eight columns a lane when they align (8-byte stores: a wave's eight lanes write 64 contiguous
+    // bytes of a row, the next wave the other half of the line; sixteen would keep 64 values a lane, which
+    // this layout's registers do not hold)
+    const int bvec = SINK::kBytes == 1 && aligned(8) ? 8 : 0;
+    const int kvec = bvec ? bvec : vec;
     // R = 8 lanes per block column (4 rows each) while that gives the chip at least 8 waves per SIMD; smaller
     // tensors take R = 32 (one row per lane, four times the waves), which keeps more loads in flight (MI355X,
     // block.ocp on 4096 x 512 float32: 12.2 us at R = 8, 9.7 us at R = 32; bf16 8192 x 8192: R = 8 fastest)
-    const int64_t waves8 = outer * nb * mxq::ceil_div(inner / vec, 64 / 8);
+    const int64_t waves8 = outer * nb * mxq::ceil_div(inner / kvec, 64 / 8);
     auto go = [&](auto r_const) {
       constexpr int R = decltype(r_const)::value;
-      const int64_t wpr = mxq::ceil_div(inner / vec, 64 / R);
+      const int64_t wpr = mxq::ceil_div(inner / kvec, 64 / R);
       const dim3 grid = mxq::grid_for(outer * nb * wpr * 64, 256);
+      if constexpr (SINK::kBytes == 1) {
+        if (bvec == 8) {
+          k_quant_split<T, ELEM, MODE, 8, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
+          return;
+        }
+      }
       if (vec == 4) k_quant_split<T, ELEM, MODE, 4, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
       else if (vec == 2) k_quant_split<T, ELEM, MODE, 2, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
       else k_quant_split<T, ELEM, MODE, 1, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);

@@ -275,3 +275,54 @@ def test_compose_with_callables(cuda):
             wP, wX = ob.compose(V, ns, ne, axis, bs)
             assert_bits_equal(P.cpu().numpy(), wP, f"compose P {shape} axis {axis}")
             assert_bits_equal(X.cpu().numpy(), wX, f"compose X {shape} axis {axis}")
+
+
+def _grid_edge_input(fmt, seed):
+    """K = 96 rows (three blocks) by 256 columns: every block's first row is 1.999 (the scale is 1, so the
+    element grid sees the values as they are), the rest cycle through the format's grid values below 2, their
+    midpoints (the ties), the float32 neighbours of those, both zeros and values that round to zero, with random
+    signs.  Column 5 holds a NaN and column 9 an Inf in the first block, beside finite columns of the same waves."""
+    from oracle import packed as op
+    e, m = op.FORMATS[fmt]
+    bias = (1 << (e - 1)) - 1
+    grid = sorted({(mf / (1 << m)) * 2.0 ** (1 - bias) if ef == 0 else (1 + mf / (1 << m)) * 2.0 ** (ef - bias)
+                   for ef in range(1 << e) for mf in range(1 << m)})
+    grid = np.array([g for g in grid if g < 2.0], dtype=np.float64)
+    mids = ((grid[:-1] + grid[1:]) / 2).astype(np.float32)
+    pts = np.concatenate([grid.astype(np.float32), mids, np.nextafter(mids, np.float32(0)),
+                          np.nextafter(mids, np.float32(4)), np.float32([0.0, -0.0, 1e-30, -1e-30, 2.0 ** -126])])
+    rng = np.random.default_rng(seed)
+    V = rng.choice(pts, size=(96, 256)).astype(np.float32)
+    V *= np.where(rng.random(V.shape) < 0.5, np.float32(-1), np.float32(1))
+    V[::32, :] = np.float32(1.999)
+    V[7, 5] = np.nan
+    V[3, 9] = np.inf
+    return V
+
+
+@pytest.mark.parametrize("fmt", ["MXFP8_E4M3", "MXFP8_E5M2", "MXFP6_E3M2", "MXFP6_E2M3", "MXFP4"])
+def test_mxgemmini_rne_grid_edges(cuda, fmt):
+    """mxgemmini at nearest even, which runs on the hardware conversions when a wave's values are finite and
+    in range, on every tie, signed zero and subnormal step of the format: float32 codes against the oracle,
+    and the one-pass code bytes against the oracle's encoding of them; the NaN and Inf blocks take the general
+    path in the same launches."""
+    import mxq
+    from mxq import block
+    from oracle import packed as op
+    V = _grid_edge_input(fmt, 5)
+    for dt in (torch.float32, torch.bfloat16):
+        Vt = torch.from_numpy(V).to(dt)
+        V32 = Vt.float().numpy()
+        P, X = block.mxgemmini.quantize(Vt.cuda(), fmt, axis=0, rounding_mode="rne", scale_floor=2.0 ** -23)
+        wP, wX = ob.mxgemmini_quantize(V32, fmt, 0, 32, "rne", 2.0 ** -23)
+        assert_bits_equal(X.cpu().numpy(), wX, f"X {fmt} {dt}")
+        assert_bits_equal(P.cpu().numpy(), wP, f"P {fmt} {dt}")
+        finite = np.isfinite(V32).all(axis=0)
+        Vf = torch.from_numpy(V32[:, finite]).to(dt).contiguous()
+        codes, scales = mxq.packed.quantize(Vf.cuda(), fmt, "mxgemmini", 0, 32, rounding_mode="rne",
+                                            scale_floor=2.0 ** -23)
+        fP, fX = ob.mxgemmini_quantize(Vf.float().numpy(), fmt, 0, 32, "rne", 2.0 ** -23)
+        want_c, want_s, err = op.pack(fP, fX, fmt, 0, 32)
+        assert not err
+        assert np.array_equal(codes.cpu().numpy(), want_c), f"codes {fmt} {dt}"
+        assert np.array_equal(scales.cpu().numpy(), want_s), f"scales {fmt} {dt}"
