@@ -233,26 +233,59 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
   __shared__ double w_s[kMaxGrid];
   __shared__ double C[kSize];
   __shared__ double sums[kSize], wsum[kSize];
+  __shared__ double pw[kMaxGrid], pwx[kMaxGrid];     // inclusive prefix sums of the counts and counts x values
+  __shared__ int lo_s[kSize], hi_s[kSize];           // a pass's cluster ranges of bins (lo -1: empty)
   __shared__ float safe_s[kMaxGrid];
   __shared__ int order_s[kMaxGrid];
   __shared__ unsigned char member[kMaxGrid];
   __shared__ float T_s[kSize];
   const int g = blockIdx.x, lane = threadIdx.x;
+  // rounds of 64 lanes over the grid's bins and over the safe values (a loop over them stops at these)
+  const int nr = (nv + 63) >> 6, nsr = (ns + 63) >> 6;
   const int64_t u0 = (int64_t)g << src.shift;
   const int64_t u1 = ((int64_t)(g + 1) << src.shift) < src.nunits ? ((int64_t)(g + 1) << src.shift) : src.nunits;
-  for (int i = lane; i < nv; i += 64) {
-    x_s[i] = (double)grid[i];
-    int64_t c = 0;
-    for (int s = 0; s < src.nsplit; ++s) {
-      const int* p = src.p + s * src.split_stride + i;
-      for (int64_t u = u0; u < u1; ++u) c += p[u * nv];
-    }
-    w_s[i] = (double)c;
+  // every load in flight before the stores into LDS: grid, safe values and order, and each bin's count, the
+  // sum over every split and owned unit, eight loads at a time
+  float gv[kRounds], sv[kRounds];
+  int ov[kRounds];
+  int64_t cv[kRounds];
+  const int64_t nu = u1 - u0, terms = (int64_t)src.nsplit * nu;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int i = r * 64 + lane;
+    gv[r] = i < nv ? grid[i] : 0.0f;
+    sv[r] = i < ns ? safe[i] : 0.0f;
+    ov[r] = i < ns ? safe_order[i] : 0;
   }
-  for (int i = lane; i < ns; i += 64) {
-    safe_s[i] = safe[i];
-    order_s[i] = safe_order[i];
-    member[i] = 0;
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int i = r * 64 + lane;
+    cv[r] = 0;
+    if (r >= nr) break;
+    for (int64_t t0 = 0; t0 < terms; t0 += 8) {
+      int v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int64_t t = t0 + k;
+        const int64_t sp = t / nu, u = u0 + (t - sp * nu);
+        v[k] = (t < terms && i < nv) ? src.p[sp * src.split_stride + u * nv + i] : 0;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cv[r] += v[k];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int i = r * 64 + lane;
+    if (i < nv) {
+      x_s[i] = (double)gv[r];
+      w_s[i] = (double)cv[r];
+    }
+    if (i < ns) {
+      safe_s[i] = sv[r];
+      order_s[i] = ov[r];
+      member[i] = 0;
+    }
   }
   __syncthreads();
 
@@ -260,6 +293,7 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
   int npres = 0;
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
+    if (r >= nr) break;
     const int i = r * 64 + lane;
     npres += __popcll(__ballot(i < nv && w_s[i] > 0.0));
   }
@@ -269,6 +303,7 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
     int base = 0;
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
+      if (r >= nr) break;
       const int i = r * 64 + lane;
       const bool pres = i < nv && w_s[i] > 0.0;
       const int rank = base + lanes_below(pres, lane);
@@ -284,62 +319,155 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
     double carry = 0.0;
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) {
+      if (r >= nr) break;
       const int i = r * 64 + lane;
       const double incl = wave_scan(i < nv ? w_s[i] : 0.0, lane) + carry;
       cum[r] = incl;
       carry = __shfl(incl, 63, 64);
     }
     const double total = carry;
+    double carry_x = 0.0;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      if (r >= nr) break;
+      const int i = r * 64 + lane;
+      const double incl = wave_scan(i < nv ? w_s[i] * x_s[i] : 0.0, lane) + carry_x;
+      if (i < nv) {
+        pw[i] = cum[r];
+        pwx[i] = incl;
+      }
+      carry_x = __shfl(incl, 63, 64);
+    }
     double cdf[kRounds];
 #pragma unroll
-    for (int r = 0; r < kRounds; ++r) cdf[r] = cum[r] / total;
-    for (int q = 0; q < kSize; ++q) {
-      const double probe = ((double)q + 0.5) / (double)kSize;
-      int first = nv;                                  // no bin reaches the probe: the last bin
+    for (int r = 0; r < kRounds; ++r) cdf[r] = r < nr ? cum[r] / total : 0.0;
+    // seed q is the first bin whose cdf reaches (q + 0.5) / 16.  The cdf never decreases along the bins, so
+    // with k = the number of probes a bin's cdf reaches, seed q's bin is the number of bins with k <= q (nv:
+    // none reaches it, the last bin then).  The seeds come out ascending, so the reference's sort is the
+    // identity and its dedupe-and-sort keeps the distinct ones in order, +Inf after them.
+    int kreach[kRounds];
 #pragma unroll
-      for (int r = kRounds - 1; r >= 0; --r) {
-        const int i = r * 64 + lane;
-        const unsigned long long m = __ballot(i < nv && cdf[r] >= probe);
-        if (m) first = r * 64 + __ffsll((long long)m) - 1;
-      }
-      if (lane == q) cen = x_s[first < nv ? first : nv - 1];
+    for (int r = 0; r < kRounds; ++r) {
+      kreach[r] = 0;
+#pragma unroll
+      for (int q = 0; q < kSize; ++q) kreach[r] += cdf[r] >= (double)(2 * q + 1) * 0.03125 ? 1 : 0;  // (q+.5)/16
     }
-    cen = sort16_lanes(cen, lane);
+    int seed_bin = nv;                                 // lane q < 16: seed q's bin
+#pragma unroll
+    for (int q = 0; q < kSize; ++q) {
+      int below_q = 0;
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+        if (r >= nr) break;
+        below_q += __popcll(__ballot(r * 64 + lane < nv && kreach[r] <= q));
+      }
+      if (lane == q) seed_bin = below_q;
+    }
+    cen = d_inf();
+    if (lane < kSize) cen = x_s[seed_bin < nv ? seed_bin : nv - 1];
     const double below = __shfl_up(cen, 1, 64);
-    if (lane > 0 && lane < kSize && cen == below) cen = d_inf();
-    cen = sort16_lanes(cen, lane);
-    if (lane < kSize) C[lane] = cen;
+    const bool keep = lane < kSize && (lane == 0 || cen != below);
+    const int rank = lanes_below(keep, lane);
+    if (lane < kSize) C[lane] = d_inf();
+    __syncthreads();
+    if (keep) C[rank] = cen;
     stop = max_iters <= 0;
   }
   __syncthreads();
 
   // ---- Lloyd passes
+  // A pass assigns each bin its nearest centre (first minimum).  The centres are ascending and the bins too, so
+  // the assignment is non-decreasing along the bins and every cluster is a run of bins: its sums are then
+  // differences of the prefix sums (exact, as every sum here is).  A pass whose assignment is not monotone
+  // (rounding at a near-tie could make one) adds its bins into the sums by LDS atomics instead.  The new
+  // centres are sorted and deduplicated only when they need it (a stable sort of ascending, distinct values
+  // is the identity).
   for (int it = 0; it < max_iters && !stop; ++it) {
-    if (lane < kSize) { sums[lane] = 0.0; wsum[lane] = 0.0; }
-    __syncthreads();
-    for (int i = lane; i < nv; i += 64) {
-      const double xv = x_s[i];
-      int best = 0;
-      double bd = fabs(xv - C[0]);
-      for (int c = 1; c < kSize; ++c) {
-        const double d = fabs(xv - C[c]);
-        if (d < bd) { bd = d; best = c; }                        // first minimum (NaN never wins)
+    double cen_r[kSize];
+#pragma unroll
+    for (int c = 0; c < kSize; ++c) cen_r[c] = C[c];
+    int best[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) best[r] = kSize;  // past the bins: above every cluster
+    bool mono = true;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      if (r >= nr) break;
+      const int i = r * 64 + lane;
+      if (i < nv) {
+        // the first minimum of the 16 distances as a tree: the later of a pair wins only when strictly
+        // nearer, which is the linear scan's choice (distances are never NaN: the values are finite)
+        const double xv = x_s[i];
+        double d[kSize];
+        int bi[kSize];
+#pragma unroll
+        for (int c = 0; c < kSize; ++c) {
+          d[c] = fabs(xv - cen_r[c]);
+          bi[c] = c;
+        }
+#pragma unroll
+        for (int step = 1; step < kSize; step <<= 1)
+#pragma unroll
+          for (int c = 0; c < kSize; c += 2 * step)
+            if (d[c + step] < d[c]) {
+              d[c] = d[c + step];
+              bi[c] = bi[c + step];
+            }
+        best[r] = bi[0];
       }
-      if (!(bd == bd)) best = 0;                                   // every centre infinite: argmin of NaNs -> 0
-      const double wv = w_s[i];
-      if (wv != 0.0) {
-        atomicAdd(&sums[best], wv * xv);
-        atomicAdd(&wsum[best], wv);
+      // every lane takes part in each exchange (a lane a shuffle reads from must be active)
+      const int up = __shfl_up(best[r], 1, 64);
+      const int last = r > 0 ? __shfl(best[r > 0 ? r - 1 : 0], 63, 64) : -1;
+      const int prev = lane > 0 ? up : last;
+      mono = mono && best[r] >= prev;
+    }
+    if (lane < kSize) { lo_s[lane] = -1; hi_s[lane] = -1; sums[lane] = 0.0; wsum[lane] = 0.0; }
+    __syncthreads();
+    const bool runs = __all(mono);
+    if (runs) {
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+        if (r >= nr) break;
+        const int i = r * 64 + lane;
+        const int up = __shfl_up(best[r], 1, 64), dn = __shfl_down(best[r], 1, 64);
+        const int last = r > 0 ? __shfl(best[r > 0 ? r - 1 : 0], 63, 64) : -1;
+        const int first = r + 1 < nr ? __shfl(best[r + 1 < kRounds ? r + 1 : r], 0, 64) : kSize;
+        const int prev = lane > 0 ? up : last;
+        const int next = lane < 63 ? dn : first;
+        if (i < nv && best[r] != prev) lo_s[best[r]] = i;
+        if (i < nv && best[r] != next) hi_s[best[r]] = i;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+        if (r >= nr) break;
+        const int i = r * 64 + lane;
+        if (i < nv && w_s[i] != 0.0) {
+          atomicAdd(&sums[best[r]], w_s[i] * x_s[i]);
+          atomicAdd(&wsum[best[r]], w_s[i]);
+        }
       }
     }
     __syncthreads();
     // lane c < 16: the new centre c (the old one when its cluster is empty), the dedupe, allclose by vote
     double cn = d_inf();
-    if (lane < kSize) cn = (wsum[lane] > 0.0) ? sums[lane] / wsum[lane] : C[lane];
-    cn = sort16_lanes(cn, lane);
-    const double below = __shfl_up(cn, 1, 64);
-    if (lane > 0 && lane < kSize && cn == below) cn = d_inf();
-    cn = sort16_lanes(cn, lane);
+    if (lane < kSize) {
+      double sw = wsum[lane], swx = sums[lane];
+      if (runs) {
+        const int lo = lo_s[lane], hi = hi_s[lane];
+        sw = lo < 0 ? 0.0 : pw[hi] - (lo > 0 ? pw[lo - 1] : 0.0);
+        swx = lo < 0 ? 0.0 : pwx[hi] - (lo > 0 ? pwx[lo - 1] : 0.0);
+      }
+      cn = (sw > 0.0) ? swx / sw : C[lane];
+    }
+    const double below0 = __shfl_up(cn, 1, 64);
+    const bool in_order = lane == 0 || lane >= kSize || below0 < cn || (below0 == cn && cn == d_inf());
+    if (!__all(in_order)) {
+      cn = sort16_lanes(cn, lane);
+      const double below = __shfl_up(cn, 1, 64);
+      if (lane > 0 && lane < kSize && cn == below) cn = d_inf();
+      cn = sort16_lanes(cn, lane);
+    }
     bool same = true;
     if (lane < kSize) {
       const double old_c = C[lane];
@@ -357,12 +485,17 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
   if (lane < kSize) {
     const double c = C[lane];
     if (is_finite_d(c)) {
-      int best = 0;
-      double bd = fabs(c - (double)safe_s[0]);
-      for (int i = 1; i < ns; ++i) {
-        const double d = fabs(c - (double)safe_s[i]);
-        if (d < bd) { bd = d; best = i; }
+      // the first nearest safe value: a neighbour of c's insertion point, the lower on a tie (the safe values
+      // lie at least a grid step apart, far above the distances' rounding, so no farther value ties)
+      int lo = 0, hi = ns;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if ((double)safe_s[mid] < c) lo = mid + 1;
+        else hi = mid;
       }
+      int best = lo;
+      if (lo == ns) best = ns - 1;
+      else if (lo > 0 && !(fabs(c - (double)safe_s[lo]) < fabs(c - (double)safe_s[lo - 1]))) best = lo - 1;
       member[best] = 1;
     }
   }
@@ -370,6 +503,7 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
   int cnt = 0;
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
+    if (r >= nsr) break;
     const int i = r * 64 + lane;
     cnt += __popcll(__ballot(i < ns && member[i]));
   }
@@ -379,6 +513,8 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
   int base = 0;
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
+    take[r] = false;
+    if (r >= nsr) continue;
     const int q = r * 64 + lane;
     const bool unused = q < ns && !member[order_s[q]];
     take[r] = unused && base + lanes_below(unused, lane) < need;
@@ -394,6 +530,7 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
   base = 0;
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
+    if (r >= nsr) break;
     const int i = r * 64 + lane;
     const bool mem = i < ns && member[i];
     const int rank = base + lanes_below(mem, lane);
