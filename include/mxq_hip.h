@@ -226,6 +226,15 @@ int mxq_attend_windows(const double* amax_a, int64_t lda, const double* amax_k, 
                        int64_t z0, int64_t z_per_b, int64_t m, int64_t Tk, int64_t block, int32_t* flags,
                        mxq_stream_t stream);
 
+/* The batched attention's softmax and P^T quantize in one pass over the scores: for each row of S (R x T
+ * float32, 32 < T <= 2048), softmax computed exactly as torch's persistent softmax computes it on this GPU (its
+ * element-to-lane order, reduction trees, expf and IEEE division), then P^T (T x R) block-quantized along T in
+ * blocks of 32 by spec (MX-Gemmini's: the mxquant scale and the OCP element grid): PT_P (T x R float32 codes),
+ * PT_X (ceil(T/32) x R float32 scales), as block.mxgemmini.quantize(softmax(S).t(), axis=0) gives them.
+ * Replaces mxq/nn/_attention.py:136-139 (softmax, then pv.a(P.t())) for the batched path. */
+int mxq_softmax_quantize_t(const float* S, int64_t R, int64_t T, float* PT_P, float* PT_X,
+                           const mxq_block_spec* spec, mxq_stream_t stream);
+
 /* attend's two elementwise steps on the scores, in place: S (Z problems x n heads x m queries x Tk keys, float32,
  * contiguous) becomes r(r(S * scale) + mask_row), r the identity or (round_bf16 = 1) rounding.bf16; the add and its
  * rounding are skipped when mask is NULL.  Query j of problem z reads the Tk contiguous floats at

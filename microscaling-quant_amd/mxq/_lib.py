@@ -106,6 +106,7 @@ SIGNATURES = {
     "mxq_lut_pick": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr]),
     "mxq_block_lut": (c_i32, [c_ptr, c_i32, c_i64, c_i64, ctypes.POINTER(BlockSpec), c_i32, c_i32, c_ptr, c_i32,
                               c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr]),
+    "mxq_softmax_quantize_t": (c_i32, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, ctypes.POINTER(BlockSpec), c_ptr]),
     "mxq_block_lut_workspace": (c_i32, [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, ctypes.POINTER(c_i64)]),
     "mxq_lut_lookup": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr]),
     "mxq_lut_finder": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_i64, c_ptr, c_ptr]),

@@ -368,9 +368,13 @@ class _Batched:
                                              ld_b=KT_P.shape[1], batch_b=Tk, ld_xb=KT_X.shape[1], batch_xb=Tk,
                                              ld_c=Tk, batch_c=cols * Tk),
                          Zc, D, cols, Tk, S, arith, sched, size, qk.block_size, skip=skip, epilogue=epi)
-        P = softmax(S, vector)
-        # every call's P^T side by side, quantized from P as it lies (a transposed view: no copy)
-        PT_P, PT_X = pv.a(P.contiguous().view(Zc * cols, Tk).t())
+        # every call's P^T side by side: softmax and the quantizer in one kernel where they are torch's persistent
+        # softmax and an MX-Gemmini quantizer; else P, quantized as it lies (a transposed view: no copy)
+        PT = _softmax_pt(S, pv.a, pv.block_size, vector)
+        if PT is None:
+            P = softmax(S, vector)
+            PT = pv.a(P.contiguous().view(Zc * cols, Tk).t())
+        PT_P, PT_X = PT
         arith, sched, size = self.pv_red
         O = torch.empty(Zc, cols, D, dtype=torch.float32, device=qg.device)
         systolic_batched((PT_P, PT_X, V_P[z0:], V_X[z0:]),
@@ -395,6 +399,35 @@ class _Batched:
             bias_b = None if bias is None else bias[b if bias.shape[0] > 1 else 0]
             _one_call(q[b], ops, bias_b, scale, self.qk, self.pv, vector, rnd, dims, range(h * n, (h + 1) * n),
                       s0, e0, out[b])
+
+
+def _softmax_pt(S: torch.Tensor, quantizer, block_size: int, vector: Optional[str]):
+    """(P^T codes, scales) of softmax(S) over its last dim through `quantizer` (mxq/nn/_attention.py:136-139),
+    as one kernel (mxq_softmax_quantize_t): for float32 rows of 32 < T <= 2048 keys, where torch.softmax runs its
+    persistent softmax, which the kernel reproduces bit for bit, and an MX-Gemmini quantizer of blocks of 32 along
+    the keys.  None where that does not hold."""
+    from .. import _lib
+    from ..block import mxgemmini
+    from ..element_quant.formats import get
+    from ..scale_factor import MXQUANT_FLOOR
+    T = S.shape[-1]
+    if vector is not None or S.dtype != torch.float32 or not 32 < T <= 2048 or block_size != 32:
+        return None
+    if quantizer.func is not mxgemmini.quantize or quantizer.keywords.get("block_size", 32) != 32:
+        return None
+    kw = quantizer.keywords
+    f = get(kw["fmt"])
+    if f is None:
+        return None
+    spec = mxgemmini.spec(f, kw.get("rounding_mode", "ties_away"), kw.get("scale_floor", MXQUANT_FLOOR), kw.get("via"))
+    Sc = S.contiguous()
+    R = Sc.numel() // T
+    PT_P = torch.empty((T, R), dtype=torch.float32, device=S.device)
+    PT_X = torch.empty((-(-T // 32), R), dtype=torch.float32, device=S.device)
+    with torch.cuda.device(S.device):
+        _lib.run("mxq_softmax_quantize_t", _lib.ptr(Sc), R, T, _lib.ptr(PT_P), _lib.ptr(PT_X), spec,
+                 _lib.stream(S.device))
+    return PT_P, PT_X
 
 
 def _launch_ranges(B: int, Hkv: int, per_launch: int):

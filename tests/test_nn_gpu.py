@@ -351,3 +351,31 @@ def test_c5_full_shape_batched_against_per_pair(cuda, Hkv):
     got = mxq.nn.attend(q, k, v, mask, 128 ** -0.5, hw, hw)
     want = mxq.nn.attend(q, k, v, mask, 128 ** -0.5, loose, loose)
     assert_bits_equal(got.cpu().numpy(), want.cpu().numpy(), f"attend C5 batched vs per pair, {Hkv} KV heads")
+
+
+@pytest.mark.parametrize("T", [33, 64, 100, 512, 1000, 2048])
+def test_softmax_quantize_t_against_torch(cuda, T):
+    """The batched path's softmax and P^T quantize in one kernel against torch.softmax followed by
+    block.mxgemmini.quantize of the transpose, as the path otherwise calls them: codes and scales bit for bit,
+    on scores with a large spread, HF-style masked tails (finfo.min added), a fully masked row (softmax
+    uniform), for three formats and both the reference's rounding modes."""
+    from functools import partial
+
+    from mxq import block
+    from mxq.nn import _attention
+    g = torch.Generator(device="cuda").manual_seed(T)
+    R = 300
+    S = torch.randn(R, T, device="cuda", generator=g) * torch.exp2(torch.randint(-4, 6, (R, 1), device="cuda",
+                                                                                 generator=g).float())
+    lo = torch.finfo(torch.float32).min
+    keep = torch.arange(T, device="cuda")[None, :] <= torch.arange(R, device="cuda")[:, None] % T
+    S = torch.where(keep, S, S + lo)
+    S[7] = lo
+    for fmt, mode in [("MXFP8_E4M3", "ties_away"), ("MXFP8_E4M3", "rne"), ("MXFP6_E2M3", "ties_away"),
+                      ("MXFP4", "rne")]:
+        q = partial(block.mxgemmini.quantize, fmt=fmt, axis=0, rounding_mode=mode)
+        got = _attention._softmax_pt(S, q, 32, None)
+        assert got is not None
+        want = q(torch.softmax(S, dim=-1).contiguous().t())
+        assert_bits_equal(got[1].cpu().numpy(), want[1].cpu().numpy(), f"scales T={T} {fmt} {mode}")
+        assert_bits_equal(got[0].cpu().numpy(), want[0].cpu().numpy(), f"codes T={T} {fmt} {mode}")
