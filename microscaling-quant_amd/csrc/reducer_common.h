@@ -56,6 +56,20 @@ struct TileLoader {
       }
     }
   }
+  // The same rows when all of them and all W columns lie inside the matrix, 16-byte aligned: `row0` points at
+  // (k0, c0), an address uniform over the workgroup, and each lane adds its own 32-bit element offset
+  // r * ld + c (loop-invariant; the caller keeps 32 * ld below 2^31), so no bounds or 64-bit address math per
+  // load.
+  __device__ __forceinline__ void load_inner(const float* __restrict__ row0, uint32_t ld) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < PER / 4; ++j) {
+      const int e = (t + j * NT) * 4;
+      const uint32_t r = (uint32_t)(e / W), c = (uint32_t)(e % W);
+      const float4 q = *reinterpret_cast<const float4*>(row0 + (r * ld + c));
+      v[j * 4 + 0] = q.x; v[j * 4 + 1] = q.y; v[j * 4 + 2] = q.z; v[j * 4 + 3] = q.w;
+    }
+  }
   __device__ __forceinline__ void store(float (*dst)[W], bool vec_ok) const {
     const int t = threadIdx.x;
     if (vec_ok) {

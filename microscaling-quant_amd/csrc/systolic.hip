@@ -17,12 +17,14 @@
 //                      p = rint(trunc(a' * b))      float32 multiply, mask the dropped significand bits,
 //                                                   round to an integer = lane(p) (the flush below
 //                                                   2^prod_floor is under half a step, so it is subsumed)
-//                      S = rne_m(S + p)             the sum is an exact integer below 2^24; bit RNE at m
-//                                                   fraction bits is the lane rounding (identity below 2^m)
-//                   7 VALU operations per emulated MAC; the sum is rescaled by 2 when m steps up.  The bf16
-//                   lane and the tile add are one float32 add of two values of at most 8 significant bits
-//                   followed by bit RNE to bf16, which equals the reference's exact add with one rounding
-//                   (double rounding through 24 bits is harmless for 8-bit operands: 24 >= 2*8 + 1).
+//                      S = rne_m(S + p)             the sum is an exact integer below 2^24; RNE at m fraction
+//                                                   bits (Veltkamp's split, split_rne) is the lane rounding
+//                                                   (identity below 2^(m+1))
+//                   7 VALU operations per emulated MAC, all but the rint full-rate on gfx950; the sum is
+//                   rescaled by 2 when m steps up.  The bf16 lane and the tile add are one float32 add of two
+//                   values of at most 8 significant bits followed by RNE to bf16, which equals the reference's
+//                   exact add with one rounding (double rounding through 24 bits is harmless for 8-bit
+//                   operands: 24 >= 2*8 + 1).
 //                   While it computes, each workgroup keeps the largest |a|, |b| and scale it has read.  Its
 //                   results are exact when those are finite, max|a| < 2^100 and max|a| * max|b| stays under
 //                   the ladder's overflow bound; then it writes its tile and a 0 flag, otherwise only a 1 flag.
@@ -43,10 +45,12 @@ using namespace mxq_red;
 
 constexpr int kMaxLanes = 64;
 constexpr uint32_t kFastAMaxBits = 0x71800000u;   // 2^100: A's rows are staged times up to 2^15
+constexpr int64_t kInnerLd = int64_t(1) << 26;     // row strides below this keep 32 * ld in a 32-bit offset
 // The fast kernel's tiles: 64 x 64, 32 x 64 or 32 x 32 outputs, the largest that still gives the chip at least
-// 8 workgroups per CU.  More waves per SIMD issue the VALU chains faster than more outputs per thread: on C2's
-// 512 x 4096 outputs, 32 x 32 tiles (2 x 2 per thread, 2048 workgroups) beat 32 x 64 (1024) by 3 %.  (Holding
-// the 32 x 32 instance to 64 VGPRs for 8 waves per SIMD made it spill and lose 3 %.)
+// 4 workgroups per CU (4 waves per SIMD, as many as the 32 x 64 and 64 x 64 instances' registers allow).  With
+// the full-rate lane rounding a wave's chains keep the VALU busy at that occupancy, and a larger tile does less
+// staging per MAC: on 512 x 4096 outputs (K = 4096) 32 x 64 tiles take 1.16 ms against 1.23 ms for 32 x 32
+// (2048 workgroups); on 4096 x 4096, 64 x 64 tiles.
 
 
 struct SysArgs {
@@ -105,14 +109,25 @@ __device__ __forceinline__ float epi_apply(const SysArgs& a, const float* row, i
 struct FastLanes {
   int32_t a_exp[32];     // A's rows of lane i are staged times 2^a_exp[i]: 6 + m_i (e4 lanes), 0 (bf16 lane)
   float rescale[32];     // before e4 lane i the scaled sum is multiplied by 2^(m_i - m_{i-1}) (1: unchanged)
-  uint32_t half_m1[32];  // bit RNE at m_i fraction bits: add half - 1 + lsb, then mask
-  uint32_t lmask[32];
-  uint32_t dsh[32];      // 23 - m_i: position of the kept lsb
+  float split[32];       // 2^(23 - m_i) + 1: split_rne's constant for RNE at m_i fraction bits
   float out_scale;       // scaled sum -> sum after the last e4 lane: 2^-(6 + m_last)
   uint32_t pmask;        // product truncation to prod_m fraction bits
   float flush_thr;       // bf16 lane: |product| below this becomes zero
   uint32_t xs_lo, xs_hi; // scale magnitudes (bit patterns) for which the tile add needs no inner rounding
 };
+
+// RNE of y at m fraction bits by Veltkamp's split with C = 2^(23 - m) + 1: c = y * C, then c - (c - y).  Three
+// full-rate float operations; the bit form, (u + 2^(22-m) - 1 + lsb) & mask, needs a bit-field extract and a
+// three-way add, which gfx950 issues at half rate.  Equal to the bit form for every integer |y| < 2^24 at
+// m = 1..9 (an exhaustive check), hence, the split commuting with powers of two, for every finite y whose
+// y * C stays finite and normal: the e4 sums (integers in lane units, below 2^(15 + m)) and the bf16 lane's
+// sums (below 2^10 in magnitude, or the workgroup's results are discarded).  Not contracted: an fma of
+// y * C - y would leave c unrounded.
+__device__ __forceinline__ float split_rne(float y, float C) {
+#pragma clang fp contract(off)
+  const float c = y * C;
+  return c - (c - y);
+}
 
 // RNE of a float32 bit pattern at 7 fraction bits (bf16).  Finite values, infinities and the quiet NaNs the
 // ALU makes (0x7FC00000, 0xFFC00000) map as bf16_rne does; a NaN whose low 16 bits would carry is never
@@ -131,17 +146,9 @@ constexpr int hw_final_m(int i) { return i < 8 ? 4 : (i < 10 ? 5 : 6); }
 template <bool HWF>
 struct LaneConsts {
   const FastLanes& fl;
-  __device__ __forceinline__ uint32_t half(int i) const {
-    if constexpr (HWF) return (1u << (22 - hw_final_m(i))) - 1u;
-    else return fl.half_m1[i];
-  }
-  __device__ __forceinline__ uint32_t mask(int i) const {
-    if constexpr (HWF) return ~((1u << (23 - hw_final_m(i))) - 1u);
-    else return fl.lmask[i];
-  }
-  __device__ __forceinline__ uint32_t dsh(int i) const {
-    if constexpr (HWF) return (uint32_t)(23 - hw_final_m(i));
-    else return fl.dsh[i];
+  __device__ __forceinline__ float split(int i) const {
+    if constexpr (HWF) return (float)((1u << (23 - hw_final_m(i))) + 1u);
+    else return fl.split[i];
   }
   // before lane i the scaled sum is multiplied by rescale(i) when the lane's m steps up
   __device__ __forceinline__ bool steps_up(int i) const {
@@ -456,12 +463,14 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   static_assert((BM / TM) * (BN / TN) == NT, "256 threads");
   __shared__ __align__(16) Smem<BM, BN> sm;
   __shared__ uint32_t red[3][4];
-  __shared__ uint32_t live[2][4];   // per staged buffer and wave: bit 0, A has a nonzero code; bit 1, B has
+  __shared__ uint32_t live[2][4];   // per staged buffer and wave: bit 0, A has a nonzero code; bit 1, B has;
+                                    // bit 2, a staged block scale does not allow the short tile add
+  __shared__ float xs_a[2][BM], xs_b[2][BN];   // the stage's block scales (block size 32)
   const int tn = threadIdx.x % (BN / TN), tm = threadIdx.x / (BN / TN);
   // A stage whose A tile or B tile is all +-0 makes every product +-0, so every sum +-0 and every tile add
   // C + (+-0) * (finite scale) = C: the workgroup skips its lanes (its scales are still read and checked).
-  auto note_live = [&](int to, uint32_t ma, uint32_t mb) {
-    const uint32_t v = (__any(ma != 0u) ? 1u : 0u) | (__any(mb != 0u) ? 2u : 0u);
+  auto note_live = [&](int to, uint32_t ma, uint32_t mb, bool inexact) {
+    const uint32_t v = (__any(ma != 0u) ? 1u : 0u) | (__any(mb != 0u) ? 2u : 0u) | (__any(inexact) ? 4u : 0u);
     if ((threadIdx.x & 63) == 0) live[to][threadIdx.x >> 6] = v;
   };
   // Row tiles are dispatched last row first.  Where A is zero above a diagonal (attention's P^T under a causal
@@ -511,18 +520,56 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   TileLoader<BN, NT> lb;
   ScaledRows<BM, NT, SIZE> rows;
   rows.init(fl, va);
-  int buf = 0;
-  la.load(A, args.A.ld, K, M, 0, m0, va);
-  lb.load(B, args.B.ld, K, N, 0, n0, vb);
-  {
+  // STAGED (32-row tiles; the 64 x 64 instance would lose a wave per SIMD to the registers these take): an
+  // interior tile loads whole stages without bounds checks (TileLoader::load_inner), and with block size 32,
+  // where a stage is one block, the block scales are staged with it: thread t < BM reads XA's for the tile's
+  // column t, BM <= t < BM + BN XB's for column t - BM, each checked once (its magnitude into max_x, whether it
+  // allows the short tile add into the stage's live bits).  Otherwise each thread reads the scales of its
+  // rows and columns as the reductions reach a new block.
+  constexpr bool STAGED = BM == 32;
+  const bool inner = STAGED && va && vb && m0 + BM <= M && n0 + BN <= N && args.A.ld < kInnerLd &&
+                     args.B.ld < kInnerLd;
+  const bool xs_staged = STAGED && bs == KT;
+  float xv = 0.0f;
+  auto load_stage = [&](int64_t k) {
+    if (inner && k + KT <= K) {
+      la.load_inner(A + k * args.A.ld + m0, (uint32_t)args.A.ld);
+      lb.load_inner(B + k * args.B.ld + n0, (uint32_t)args.B.ld);
+    } else {
+      la.load(A, args.A.ld, K, M, k, m0, va);
+      lb.load(B, args.B.ld, K, N, k, n0, vb);
+    }
+    if (xs_staged) {
+      const int t = threadIdx.x;
+      const int64_t g = k / KT;
+      xv = 0.0f;
+      if (t < BM) {
+        if (m0 + t < M) xv = XA[g * args.XA.ld + m0 + t];
+      } else if (t < BM + BN) {
+        if (n0 + t - BM < N) xv = XB[g * args.XB.ld + n0 + t - BM];
+      }
+    }
+  };
+  auto store_stage = [&](int to) {
     const uint32_t ma = la.max_bits(), mb = lb.max_bits();
     max_a = umax(max_a, ma);
     max_b = umax(max_b, mb);
-    note_live(0, ma, mb);
-  }
-  rows.apply(la.v);
-  la.store(sm.a[0], va);
-  lb.store(sm.b[0], vb);
+    bool inexact = false;
+    if (xs_staged) {
+      const int t = threadIdx.x;
+      max_x = umax(max_x, f2u(xv) & 0x7FFFFFFFu);
+      if constexpr (BF16_LAST) inexact = !exact_scale(xv, fl.xs_lo, fl.xs_hi);
+      if (t < BM) xs_a[to][t] = xv;
+      else if (t < BM + BN) xs_b[to][t - BM] = xv;
+    }
+    note_live(to, ma, mb, inexact);
+    rows.apply(la.v);
+    la.store(sm.a[to], va);
+    lb.store(sm.b[to], vb);
+  };
+  int buf = 0;
+  load_stage(0);
+  store_stage(0);
   __syncthreads();
 
   float scale[TM][TN];
@@ -531,17 +578,25 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   int64_t g = 0;         // its block
   for (int64_t k0 = 0; k0 < kstop; k0 += KT) {
     const bool more = k0 + KT < kstop;
-    if (more) {
-      la.load(A, args.A.ld, K, M, k0 + KT, m0, va);
-      lb.load(B, args.B.ld, K, N, k0 + KT, n0, vb);
-    }
+    if (more) load_stage(k0 + KT);
     const int kend = (int)((K - k0 < KT) ? (K - k0) : KT);
     const uint32_t lv = live[buf][0] | live[buf][1] | live[buf][2] | live[buf][3];
-    const bool zero_stage = lv != 3u;
+    const bool zero_stage = (lv & 3u) != 3u;
     // rows past K are zero in LDS: their products are +0 and leave every lane's sum unchanged, so a short
     // last reduction runs as a whole one
     for (int r0 = 0; r0 < kend; r0 += SIZE) {
-      if (in_block == 0) {
+      if (in_block == 0 && xs_staged) {
+        float xa[TM], xb[TN];
+#pragma unroll
+        for (int x = 0; x < TM; ++x) xa[x] = xs_a[buf][tm * TM + x];
+#pragma unroll
+        for (int y = 0; y < TN; ++y) xb[y] = xs_b[buf][tn * TN + y];
+#pragma unroll
+        for (int x = 0; x < TM; ++x)
+#pragma unroll
+          for (int y = 0; y < TN; ++y) scale[x][y] = xa[x] * xb[y];
+        short_add = (lv & 4u) == 0u;                             // one decision per workgroup and block
+      } else if (in_block == 0) {
         float xa[TM], xb[TN];
 #pragma unroll
         for (int x = 0; x < TM; ++x) {
@@ -604,7 +659,7 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
             for (int y = 0; y < TN; ++y) {
               float t = u2f(f2u(a[x] * b[y]) & fl.pmask);
               t = fabsf(t) < fl.flush_thr ? 0.0f : t;
-              S[x][y] = bf16_bits(S[x][y] * lc.out_scale() + t);
+              S[x][y] = split_rne(S[x][y] * lc.out_scale() + t, 65537.0f);
             }
         } else if (i == 0) {
           // the first lane: S = lane(p).  p has at most prod_m + 1 <= m + 1 significant bits (an integer at or
@@ -621,14 +676,13 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
               for (int y = 0; y < TN; ++y) S[x][y] *= lc.rescale(i);
           }
           // e4 lane in units of the lane's subnormal step 2^-(6+m)
-          const uint32_t half = lc.half(i), mask = lc.mask(i), d = lc.dsh(i);
+          const float sc = lc.split(i);
 #pragma unroll
           for (int x = 0; x < TM; ++x)
 #pragma unroll
             for (int y = 0; y < TN; ++y) {
               const float p = __builtin_rintf(u2f(f2u(a[x] * b[y]) & fl.pmask));
-              const uint32_t u = f2u(S[x][y] + p);
-              S[x][y] = u2f((u + half + ((u >> d) & 1u)) & mask);
+              S[x][y] = split_rne(S[x][y] + p, sc);
             }
         }
       }
@@ -656,15 +710,7 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
         ++g;
       }
     }
-    if (more) {
-      const uint32_t ma = la.max_bits(), mb = lb.max_bits();
-      max_a = umax(max_a, ma);
-      max_b = umax(max_b, mb);
-      note_live(buf ^ 1, ma, mb);
-      rows.apply(la.v);
-      la.store(sm.a[buf ^ 1], va);
-      lb.store(sm.b[buf ^ 1], vb);
-    }
+    if (more) store_stage(buf ^ 1);
     __syncthreads();
     buf ^= 1;
   }
@@ -887,9 +933,7 @@ FastLanes make_fast_lanes(const int32_t* e, const int32_t* m, int size, const mx
     const int mi = m[i];
     fl.a_exp[i] = 6 + mi;
     if (prev >= 0) fl.rescale[i] = pow2f(mi - prev);
-    fl.half_m1[i] = (1u << (22 - mi)) - 1u;
-    fl.lmask[i] = ~((1u << (23 - mi)) - 1u);
-    fl.dsh[i] = (uint32_t)(23 - mi);
+    fl.split[i] = (float)((1u << (23 - mi)) + 1u);
     prev = mi;
   }
   fl.out_scale = pow2f(-(6 + prev));
@@ -959,8 +1003,8 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
   const mxq_arith_spec& ar = base.ar;
   SysArgs a = base;
   for (int i = 0; i < a.size; ++i) { a.lane_e[i] = (int8_t)lane_e[i]; a.lane_m[i] = (int8_t)lane_m[i]; }
-  // the largest fast tile that gives every CU at least 8 workgroups (else the smallest)
-  const int64_t want = 8 * 256;
+  // the largest fast tile that gives every CU at least 4 workgroups (else the smallest)
+  const int64_t want = 4 * 256;
   if (mxq::ceil_div(a.M, 64) * mxq::ceil_div(a.N, 64) * count >= want) { a.fbm = 64; a.fbn = 64; }
   else if (mxq::ceil_div(a.M, 32) * mxq::ceil_div(a.N, 64) * count >= want) { a.fbm = 32; a.fbn = 64; }
   else { a.fbm = 32; a.fbn = 32; }

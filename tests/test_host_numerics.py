@@ -242,3 +242,42 @@ def test_e8m0_encode_decode(H, corpus):
         got_b, got_ok = H.e8m0_encode(x, zero)
         want_b, want_ok = op.e8m0_encode(x, zero)
         assert np.array_equal(got_ok, want_ok) and np.array_equal(got_b[want_ok], want_b[want_ok]), zero
+
+
+def _bit_rne(y, m):
+    """RNE of float32 values at m fraction bits on the bit pattern (the form the fast kernels' rounding replaces)."""
+    u = y.view(np.uint32)
+    d = np.uint32(23 - m)
+    half = np.uint32((1 << (22 - m)) - 1)
+    mask = np.uint32(~((1 << (23 - m)) - 1) & 0xFFFFFFFF)
+    return ((u + half + ((u >> d) & np.uint32(1))) & mask).view(np.float32)
+
+
+def _split_rne(y, m):
+    """Veltkamp's split as the fast systolic kernel computes it: c = y * (2^(23-m) + 1), then c - (c - y)."""
+    C = np.float32((1 << (23 - m)) + 1)
+    c = y * C
+    return c - (c - y)
+
+
+@pytest.mark.parametrize("m", range(1, 10))
+def test_split_rne_equals_bit_rne_on_lane_sums(m):
+    """The e4 lanes' rounding: for every integer |y| < 2^24 (a lane sum in units of its subnormal step) and
+    -0, Veltkamp's split rounds exactly as bit RNE at m fraction bits (csrc/systolic.hip split_rne)."""
+    y = np.arange(-(1 << 24) + 1, 1 << 24, dtype=np.int64).astype(np.float32)
+    y = np.concatenate([y, np.array([-0.0], np.float32)])
+    assert_bits_equal(_split_rne(y, m), _bit_rne(y, m), f"split m={m}")
+
+
+def test_split_rne_equals_bit_rne_on_bf16_lane_values():
+    """The bf16 lane's rounding (m = 7) on float32 values of every binade the lane holds (2^-40 .. 2^12), random
+    significands plus every midpoint and its neighbours."""
+    rng = np.random.default_rng(7)
+    e = rng.integers(-40, 12, 400000)
+    sig = rng.integers(1 << 23, 1 << 24, 400000)
+    y = (np.ldexp(sig.astype(np.float64), e - 23) * rng.choice([-1.0, 1.0], 400000)).astype(np.float32)
+    mids = np.ldexp(np.arange(256, 512, dtype=np.float64) + 0.5, -8)
+    mids = np.concatenate([np.ldexp(mids, k) for k in range(-40, 12, 5)]).astype(np.float32)
+    near = np.concatenate([mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0))])
+    y = np.concatenate([y, near, -near])
+    assert_bits_equal(_split_rne(y, 7), _bit_rne(y, 7), "split bf16")
