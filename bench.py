@@ -5,6 +5,7 @@ parity check of what was timed against the oracle.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
     python bench.py --copy-calibration        # only a 256 MiB device copy, 5 times (counter calibration)
+    python bench.py --valu-rates              # only the VALU issue-rate probe, one instruction kind at a time
     python bench.py --only LINE               # one extra line alone: quantize, lut, attend, mfma, trees, llm
 
 A step is one systolic call over the benchmark workload (A = x^T with x 512 x 4096 ~ N(0,1), B = W^T with
@@ -32,14 +33,16 @@ sys.path.insert(0, REPO)
 
 METRIC = "emulated MX GEMM GOP/s (systolic, bit-exact) + quantize GB/s vs HBM roofline"
 HBM_PEAK_GBS = 8000.0
-# MI355X's published vector FP32 peak, 157.3 TFLOP/s, is 78.6 T FMA lane-operations per second: the rate at which
-# its 1024 SIMDs retire 32-bit VALU lanes (256 CUs x 128 lanes/clk x 2.4 GHz).  The fast systolic kernel is
-# measured above the single-issue 64 lanes/clk/CU figure (SQ_INSTS_VALU x 64 / duration = 48.7 T lane-ops/s),
-# so the 128-lane rate is the ceiling it is held against.
+# MI355X's published vector FP32 peak, 157.3 TFLOP/s, is 78.6 T lane-operations per second: its 1024 SIMDs each
+# retiring one full-rate wave64 VALU instruction every 2 clocks at 2.4 GHz.  gfx950 issues v_add_f32, v_mul_f32
+# and v_and_b32 at that rate and v_rndne_f32, v_bfe_u32, v_add3_u32 at half of it (`--valu-rates`).
 VALU_LANE_OPS = 157.3e12 / 2
-VALU_SINGLE_ISSUE = 256 * 64 * 2.4e9        # one wave64 VALU instruction per SIMD per 4 clocks
-OPS_PER_MAC_MODEL = 10                      # the datapath's primitives per emulated MAC (a model, not a count)
-VALU_ROOF_TOPS = VALU_LANE_OPS / OPS_PER_MAC_MODEL * 2 / 1e12   # 15.73 TOP/s emulated
+# The emulated MAC's VALU issue on gfx950 in full-rate slots: an e4 lane step multiplies, masks the product,
+# rounds it to the lane grid (v_rndne_f32, half rate: 2 slots), adds exactly and rounds to nearest even at m
+# bits (three full-rate operations) = 8.  The roof prices every MAC at that step.
+SLOTS_PER_MAC_MODEL = 8
+VALU_ROOF_TOPS = VALU_LANE_OPS / SLOTS_PER_MAC_MODEL * 2 / 1e12   # 19.66 TOP/s emulated
+VALU_PROBE_KINDS = ("v_add_f32", "v_mul_f32", "v_and_b32", "v_rndne_f32", "v_bfe_u32", "v_add3_u32")
 FP8_PEAK_TFLOPS = 5000.0                    # MI355X dense FP8 matrix-core peak
 MAX_POOL = 16                               # host processes for the CPU baselines (one GPU's CPU share)
 
@@ -483,6 +486,28 @@ def mfma_line(torch, steps, P_A, X_A, P_B, X_B):
             "frac": round(k_tf / FP8_PEAK_TFLOPS, 4) if k_tf else None}
 
 
+def valu_rates():
+    """gfx950's VALU issue rate per instruction kind (mxq_valu_probe: 8192 workgroups x 256 threads, 64 x 2000
+    independent instructions each): lane-operations per second over the chip against the 78.6 T of the vector
+    FP32 peak."""
+    import torch
+
+    from mxq import _lib
+    wg, iters = 8192, 2000
+    out = torch.empty(wg * 256, device="cuda")
+    st = torch.cuda.current_stream()
+    res = {}
+    for kind, name in enumerate(VALU_PROBE_KINDS):
+        def f():
+            _lib.run("mxq_valu_probe", kind, iters, wg, _lib.ptr(out), _lib.stream(out.device))
+        f()
+        ms = _events_ms(f, 3, st)
+        rate = wg * 256 * 64 * iters / (ms / 1e3)
+        res[name] = {"ms": round(ms, 4), "lane_ops_per_s_T": round(rate / 1e12, 1),
+                     "frac_of_78.6T": round(rate / VALU_LANE_OPS, 3)}
+    print(json.dumps({"valu_rates": res}), flush=True)
+
+
 def copy_calibration():
     """A plain device copy of 256 MiB, five times: the reference point for the FETCH_SIZE / WRITE_SIZE
     counters (each launch reads and writes 262144 KiB)."""
@@ -532,6 +557,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines and the parity checks")
     ap.add_argument("--no-extra", action="store_true", help="only the systolic line (no quantize, LUT, attend)")
     ap.add_argument("--copy-calibration", action="store_true", help="run only the counter-calibration copy")
+    ap.add_argument("--valu-rates", action="store_true", help="run only the VALU issue-rate probe")
     ap.add_argument("--only", choices=("quantize", "lut", "attend", "mfma", "trees", "llm"),
                     help="run one extra line alone (for profiling) and print it; not the benchmark line")
     args = ap.parse_args()
@@ -539,6 +565,9 @@ def main():
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the systolic path "
               "would shard over output columns with one final all-gather)", file=sys.stderr)
         sys.exit(2)
+    if args.valu_rates:
+        valu_rates()
+        return
     if args.copy_calibration:
         copy_calibration()
         return
@@ -596,19 +625,19 @@ def main():
                      "peak": round(VALU_ROOF_TOPS, 3), "unit": "TOP/s",
                      "frac": round(k_tops / VALU_ROOF_TOPS, 4) if k_tops else None,
                      "traffic": _profile_value("systolic_fast_c2_traffic", "bytes_per_launch"),
-                     "kernel": "k_systolic_fast<16, true, 32, 32, HW_FINAL>", "kernel_ms": round(kms, 4) if kms else None,
+                     "kernel": "k_systolic_fast<16, true, 32, 64, HW_FINAL>", "kernel_ms": round(kms, 4) if kms else None,
                      "kernel_launches_timed": launches,
                      "executed": None if not (ops_per_mac and k_tops) else {
                          "valu_lane_ops_per_mac": ops_per_mac,
                          "valu_lane_ops_per_s_T": round(k_tops / 2 * ops_per_mac, 2),
                          "frac_of_78.6T_lane_rate": round(k_tops * 1e12 / 2 * ops_per_mac / VALU_LANE_OPS, 4),
-                         "frac_of_39.3T_single_issue": round(k_tops * 1e12 / 2 * ops_per_mac / VALU_SINGLE_ISSUE, 4),
                          "source": "SQ_INSTS_VALU x 64 / emulated MACs, profiles/systolic_fast_c2_valu.txt"},
                      "note": "VALU-bound emulation (neither HBM nor MFMA): achieved = 2 x 8,589,934,592 emulated "
-                             "MACs / the fast kernel's average duration; peak is a datapath MODEL: MI355X vector FP32 "
-                             "157.3 TFLOP/s = 78.6 T 32-bit lane-ops/s, / 10 lane-ops per emulated MAC (the "
-                             "datapath's primitive count, not the kernel's instruction count) x 2 ops per MAC; "
-                             "`executed` holds the counted instructions against the lane rates"},
+                             "MACs / the fast kernel's average duration; peak = MI355X vector FP32 157.3 TFLOP/s = "
+                             "78.6 T full-rate lane-slots/s, / 8 slots per emulated MAC (an e4 lane step on gfx950: "
+                             "multiply, mask, add and a 3-op nearest-even split at one slot each, round-to-integer "
+                             "at two as it issues at half rate) x 2 ops per MAC; `executed` holds the counted "
+                             "instructions (full- and half-rate alike) against the lane rate"},
     }
     extra = {}
     if not args.no_extra:

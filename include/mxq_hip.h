@@ -75,6 +75,12 @@ int mxq_version(void);
 int mxq_timer_enable(int32_t on);
 int mxq_timer_read(const char* kernel, double* total_ms, int64_t* launches);
 
+/* VALU issue-rate probe for measurement tools; no counterpart in the reference (the VALU roofline of the
+ * emulation kernels prices each instruction by its issue rate).  Launches `workgroups` x 256 threads, each
+ * issuing 64 * iters independent instructions of one kind: 0 v_add_f32, 1 v_mul_f32, 2 v_and_b32,
+ * 3 v_rndne_f32, 4 v_bfe_u32, 5 v_add3_u32.  out: workgroups * 256 floats (a sink for the results). */
+int mxq_valu_probe(int32_t kind, int32_t iters, int64_t workgroups, float* out, mxq_stream_t stream);
+
 /* Fused block quantization: per block, amax -> scale X (step 1) -> z = block / X -> P = element rule (step 2).
  * V: (outer, n, inner) of type v_dtype; P: float32, same shape; X: float32 (outer, ceil(n/bs), inner).
  * The last block along n is zero-padded for the amax.

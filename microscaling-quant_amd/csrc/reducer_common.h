@@ -6,6 +6,20 @@
 
 namespace mxq_red {
 
+// RNE of y at m fraction bits by Veltkamp's split with C = 2^(23 - m) + 1: c = y * C, then c - (c - y).  Three
+// full-rate float operations; the bit form, (u + 2^(22-m) - 1 + lsb) & mask, needs a bit-field extract and a
+// three-way add, which gfx950 issues at half rate.  Equal to the bit form for every integer |y| < 2^24 at
+// m = 1..9 (an exhaustive check), hence, the split commuting with powers of two, for every finite y whose
+// y * C stays finite and normal: the systolic e4 sums (integers in lane units, below 2^(15 + m)), the
+// systolic bf16 lane's sums (below 2^10 in magnitude, or the workgroup's results are discarded) and the adder
+// tree's level sums.  A subnormal y on the bf16 grid (a multiple of 2^-133) is returned unchanged, as by the
+// bit form.  Not contracted: an fma of y * C - y would leave c unrounded.
+__device__ __forceinline__ float split_rne(float y, float C) {
+#pragma clang fp contract(off)
+  const float c = y * C;
+  return c - (c - y);
+}
+
 // An operand matrix: row stride and problem stride in elements.
 struct Operand {
   const float* p;

@@ -116,19 +116,6 @@ struct FastLanes {
   uint32_t xs_lo, xs_hi; // scale magnitudes (bit patterns) for which the tile add needs no inner rounding
 };
 
-// RNE of y at m fraction bits by Veltkamp's split with C = 2^(23 - m) + 1: c = y * C, then c - (c - y).  Three
-// full-rate float operations; the bit form, (u + 2^(22-m) - 1 + lsb) & mask, needs a bit-field extract and a
-// three-way add, which gfx950 issues at half rate.  Equal to the bit form for every integer |y| < 2^24 at
-// m = 1..9 (an exhaustive check), hence, the split commuting with powers of two, for every finite y whose
-// y * C stays finite and normal: the e4 sums (integers in lane units, below 2^(15 + m)) and the bf16 lane's
-// sums (below 2^10 in magnitude, or the workgroup's results are discarded).  Not contracted: an fma of
-// y * C - y would leave c unrounded.
-__device__ __forceinline__ float split_rne(float y, float C) {
-#pragma clang fp contract(off)
-  const float c = y * C;
-  return c - (c - y);
-}
-
 // RNE of a float32 bit pattern at 7 fraction bits (bf16).  Finite values, infinities and the quiet NaNs the
 // ALU makes (0x7FC00000, 0xFFC00000) map as bf16_rne does; a NaN whose low 16 bits would carry is never
 // present (the workgroup's codes and scales are finite whenever its results are kept; every NaN is made by

@@ -23,10 +23,11 @@
 //   k_adder_fast         MXGEMMINI, levels: e4 levels (4, m) of non-decreasing m, then bf16 levels.  With an e4
 //                        first level A's rows are staged times 2^(6 + m_1), so a product is in units of that
 //                        level's subnormal step and lane(p) = rint(trunc(a' b)) (the flush under half a step is
-//                        subsumed).  Every add is one float32 add, exact on e4 levels (integers below 2^24), and a
-//                        bit RNE at the level's m, which needs no units (m never falls, so a later level's grid
-//                        is never coarser than its inputs'); on bf16 levels the float32 add of two 8-bit values
-//                        rounds once more, harmlessly (24 >= 2 * 8 + 1).  3 + 4 VALU operations per product.
+//                        subsumed).  Every add is one float32 add, exact on e4 levels (integers below 2^24), and
+//                        RNE at the level's m (Veltkamp's split, split_rne), which needs no units (m never falls,
+//                        so a later level's grid is never coarser than its inputs'); on bf16 levels the float32
+//                        add of two 8-bit values rounds once more, harmlessly (24 >= 2 * 8 + 1).  3 + 4 VALU
+//                        operations per product, all full-rate but the rint.
 //   k_anchor_fast        MXGEMMINI, no emin, equal level widths within each tree (no regridding: a tree is the
 //                        exact integer sum of its terms on one grid), bf16 tree lanes.  Pass 1 takes the anchor
 //                        from labels kept in LDS as 16-bit integers, two outputs per packed add and max; a zero
@@ -400,7 +401,7 @@ __device__ __forceinline__ void lds_row(const float (*src)[W], int r, int c, flo
 
 // Per-level constants of the fast adder tree, built on the host (make_fast_levels).
 struct FastLevels {
-  uint32_t half_m1[5], dsh[5], lmask[5];   // bit RNE at each level's m (bf16: 7)
+  float split[5];     // split_rne's constant 2^(23 - m) + 1 at each level's m (bf16: 7)
   float a_scale;      // A's rows are staged times this: 2^(6 + m_1) for an e4 first level, else 1
   float out_scale;    // root -> value: 1 / a_scale
   uint32_t pmask;     // product truncation to prod_m fraction bits
@@ -475,7 +476,7 @@ __global__ void __launch_bounds__(256) k_adder_fast(const TreeArgs args, const F
 #pragma unroll
             for (int l = 0; l < L; ++l) {
               if (carry) {
-                if ((i >> l) & 1) v = rne_bits(pend[l][x][y] + v, fl.half_m1[l], fl.dsh[l], fl.lmask[l]);
+                if ((i >> l) & 1) v = split_rne(pend[l][x][y] + v, fl.split[l]);
                 else {
                   pend[l][x][y] = v;
                   carry = false;
@@ -783,9 +784,7 @@ bool adder_fast_levels(const int32_t* e, const int32_t* m, int levels, const mxq
   *fl = FastLevels{};
   for (int l = 0; l < levels; ++l) {
     const int mm = e[l] == 8 ? 7 : m[l];
-    fl->half_m1[l] = (1u << (22 - mm)) - 1u;
-    fl->dsh[l] = (uint32_t)(23 - mm);
-    fl->lmask[l] = ~((1u << (23 - mm)) - 1u);
+    fl->split[l] = (float)((1u << (23 - mm)) + 1u);
   }
   fl->a_scale = first_e4 ? pow2_host(6 + m[0]) : 1.0f;
   fl->out_scale = first_e4 ? pow2_host(-(6 + m[0])) : 1.0f;

@@ -67,6 +67,7 @@ SIGNATURES = {
     "mxq_version": (c_i32, []),
     "mxq_timer_enable": (c_i32, [c_i32]),
     "mxq_timer_read": (c_i32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_i64)]),
+    "mxq_valu_probe": (c_i32, [c_i32, c_i32, c_i64, c_ptr, c_ptr]),
     "mxq_block_quantize": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64,
                                    ctypes.POINTER(BlockSpec), c_ptr]),
     "mxq_block_quantize_t": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, ctypes.POINTER(BlockSpec),

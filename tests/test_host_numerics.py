@@ -270,8 +270,9 @@ def test_split_rne_equals_bit_rne_on_lane_sums(m):
 
 
 def test_split_rne_equals_bit_rne_on_bf16_lane_values():
-    """The bf16 lane's rounding (m = 7) on float32 values of every binade the lane holds (2^-40 .. 2^12), random
-    significands plus every midpoint and its neighbours."""
+    """The bf16 lane's and the adder tree's bf16 levels' rounding (m = 7) on float32 values of every binade they
+    hold (2^-40 .. 2^12): random significands, every midpoint and its neighbours, and the subnormals on the bf16
+    grid (multiples of 2^-133), which both forms leave unchanged."""
     rng = np.random.default_rng(7)
     e = rng.integers(-40, 12, 400000)
     sig = rng.integers(1 << 23, 1 << 24, 400000)
@@ -279,5 +280,7 @@ def test_split_rne_equals_bit_rne_on_bf16_lane_values():
     mids = np.ldexp(np.arange(256, 512, dtype=np.float64) + 0.5, -8)
     mids = np.concatenate([np.ldexp(mids, k) for k in range(-40, 12, 5)]).astype(np.float32)
     near = np.concatenate([mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0))])
-    y = np.concatenate([y, near, -near])
+    sub = (np.arange(1, 128, dtype=np.float64) * 2.0 ** -133).astype(np.float32)   # subnormals on the bf16 grid
+    y = np.concatenate([y, near, -near, sub, -sub])
     assert_bits_equal(_split_rne(y, 7), _bit_rne(y, 7), "split bf16")
+    assert_bits_equal(_split_rne(sub, 7), sub, "split bf16 subnormal")
