@@ -5,15 +5,17 @@
 // float32 accumulator with about float32 precision.  The bound that follows is stated with mfma_accum.
 //
 //   k_mx_pack   codes (K x n float32, exact values of an FP8/FP6/FP4 element format) and power-of-two scales
-//               (ceil(K/32) x n) -> one byte per code in OCP FP8 (E4M3 holds every E4M3, E3M2, E2M3 and E2M1
-//               value; E5M2 codes stay E5M2) and one E8M0 byte per scale, in the instruction's lane order: for
-//               32-column tile t and 64-deep K step s, lane l = 32h + r (column 32t + r) holds 32 bytes, the codes
-//               [16h, 16h + 16) of block 2s then the same of block 2s + 1, at byte ((t * nk + s) * 64 + l) * 32
-//               (nk = K64 / 64, K padded to a multiple of 64 with zeros); its scale, block 2s + h's, is byte
-//               (t * nk + s) * 64 + l of the scale array.  Columns past n (up to the tile) are zero codes with
-//               scale 1.  So one wave's operand for one step is 2 KiB read contiguously.  A code the byte cannot
-//               hold exactly, or a scale that is not a power of two in [2^-127, 2^127] over a block with a
-//               nonzero code, sets the error word.
+//               (ceil(K/32) x n) -> the instruction's operand type (kind: 0 FP8 E4M3, 1 BF8 E5M2, 2 FP6 E2M3,
+//               3 BF6 E3M2, 4 FP4 E2M1; a code of a narrower format also fits E4M3) and one E8M0 byte per scale, in
+//               the instruction's lane order: for 32-column tile t and 64-deep K step s, lane l = 32h + r (column
+//               32t + r) holds 32 codes in BPL = 32 w / 8 bytes (w = 8, 6 or 4) at byte ((t * nk + s) * 64 + l) *
+//               BPL (nk = K64 / 64, K padded to a multiple of 64 with zeros), code j in bits [w j, w j + w): for FP8,
+//               codes [16h, 16h + 16) of block 2s then the same of block 2s + 1; for FP6 and FP4, the 32 codes of
+//               block 2s + h in order (each lane layout established on the device with single-product outputs).
+//               The lane's scale, block 2s + h's, is byte (t * nk + s) * 64 + l of the scale array.  Columns past n (up to the tile) are zero codes with
+//               scale 1.  So one wave's operand for one step is 64 BPL bytes read contiguously.  A code the
+//               type cannot hold exactly, or a scale that is not a power of two in [2^-127, 2^127] over a block
+//               with a nonzero code, sets the error word.
 //   k_mx_mfma   32 x 32 tiles of C, 64 K per instruction, lane layout as above (established on the device with
 //               exact integer data); lane l's 16 results are C[8(i/4) + 4h + i%4][l % 32], i = 0..15.
 #include "mxq_common.h"
@@ -25,21 +27,27 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int kE4M3 = 0, kE5M2 = 1;   // the MFMA operand type codes used here
+// The MFMA operand type codes (the instruction's cbsz / blgp values).
+constexpr int kE4M3 = 0, kE5M2 = 1, kE2M3 = 2, kE3M2 = 3, kE2M1 = 4;
 
-// OCP FP8 byte of an exact value: E4M3 (bias 7, no infinities, max 448) or E5M2 (bias 15, max 57344).
-// Returns false when x is not exactly representable.
-__device__ __forceinline__ bool fp8_byte(float x, int kind, uint32_t& out) {
+__host__ __device__ constexpr int code_bits(int kind) { return kind <= kE5M2 ? 8 : (kind <= kE3M2 ? 6 : 4); }
+__host__ __device__ constexpr int lane_bytes(int kind) { return 4 * code_bits(kind); }   // 32 codes
+
+// The OCP code of an exact value in operand type `kind`: E4M3 (bias 7, no infinities, max 448), E5M2 (bias 15,
+// max 57344), E2M3 (bias 1, max 7.5), E3M2 (bias 3, max 28), E2M1 (bias 1, max 6); the FP6 and FP4 types use
+// every exponent field for finite values.  Returns false when x is not exactly representable.
+__device__ __forceinline__ bool code_of(float x, int kind, uint32_t& out) {
+  const int man_bits = kind == kE4M3 || kind == kE2M3 ? 3 : (kind == kE2M1 ? 1 : 2);
+  const int exp_bits = code_bits(kind) - 1 - man_bits;
+  const int bias = (1 << (exp_bits - 1)) - 1;
   const uint32_t u = f2u(x);
-  const uint32_t sign = (u >> 31) << 7;
+  const uint32_t sign = (u >> 31) << (code_bits(kind) - 1);
   const uint32_t a = u & 0x7FFFFFFFu;
   if (a == 0u) {
     out = sign;
     return true;
   }
   if (a >= 0x7F800000u) return false;                      // Inf / NaN codes are outside the comparison path
-  const int man_bits = kind == kE4M3 ? 3 : 2;
-  const int bias = kind == kE4M3 ? 7 : 15;
   const int emin = 1 - bias;                               // smallest normal exponent
   const int e = (int)(a >> 23) - 127;                      // float32 exponent (subnormal float32 never fits)
   if (e < emin - man_bits) return false;                   // below the format's smallest subnormal
@@ -49,7 +57,9 @@ __device__ __forceinline__ bool fp8_byte(float x, int kind, uint32_t& out) {
     if (sig & ((1u << drop) - 1u)) return false;           // more significand bits than the format has
     const uint32_t man = (sig >> drop) & ((1u << man_bits) - 1u);
     const int field = e + bias;
-    if (kind == kE4M3 ? (field > 15 || (field == 15 && man == 7u)) : field > 30) return false;
+    const int fmax = (1 << exp_bits) - 1;
+    if (kind == kE4M3 ? (field > 15 || (field == 15 && man == 7u)) : (kind == kE5M2 ? field > 30 : field > fmax))
+      return false;
     out = sign | ((uint32_t)field << man_bits) | man;
     return true;
   }
@@ -72,34 +82,38 @@ __device__ __forceinline__ bool e8m0_byte(float x, uint32_t& out) {
   return true;
 }
 
-// One thread per (column c < n32, 32-row block g < K64/32): 32 bytes of codes and one scale byte, written
+// One thread per (column c < n32, 32-row block g < K64/32): the block's 32 codes and one scale byte, written
 // where the lane-ordered layout above puts them.  Consecutive threads take consecutive columns.
+template <int W>
 __global__ void __launch_bounds__(256) k_mx_pack(const float* __restrict__ P, const float* __restrict__ X,
                                                  int64_t K, int64_t n, int64_t n32, int64_t K64, int kind,
                                                  uint8_t* __restrict__ codes, uint8_t* __restrict__ scales,
                                                  int* __restrict__ err) {
+  constexpr int HW = 16 * W / 32;                          // words per half block (16 codes of W bits)
+  constexpr int BPL = 4 * W;                               // bytes per lane and K step
   const int64_t nb64 = K64 / 32, nk = K64 / 64;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n32 * nb64) return;
   const int64_t g = t / n32, c = t - (t / n32) * n32;
   const bool live = c < n;
-  uint32_t words[8];
+  uint32_t words[2 * HW];                                  // half h: words [h HW, h HW + HW)
+#pragma unroll
+  for (int w = 0; w < 2 * HW; ++w) words[w] = 0u;
   bool nonzero = false, bad = false;
 #pragma unroll
-  for (int w = 0; w < 8; ++w) {
-    uint32_t word = 0u;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t k = g * 32 + w * 4 + j;
-      uint32_t byte = 0u;
-      if (live && k < K) {
-        const float x = P[k * n + c];
-        nonzero |= (f2u(x) & 0x7FFFFFFFu) != 0u;
-        bad |= !fp8_byte(x, kind, byte);
-      }
-      word |= (byte & 0xFFu) << (8 * j);
+  for (int j = 0; j < 32; ++j) {
+    const int64_t k = g * 32 + j;
+    uint32_t code = 0u;
+    if (live && k < K) {
+      const float x = P[k * n + c];
+      nonzero |= (f2u(x) & 0x7FFFFFFFu) != 0u;
+      bad |= !code_of(x, kind, code);
     }
-    words[w] = word;
+    // FP8: code j % 16 of half j / 16 at bit W (j % 16) of that half's bits; FP6, FP4: code j at bit W j
+    const int bit = W == 8 ? 8 * (j % 16) : W * j;
+    const int wd = (W == 8 ? (j / 16) * HW : 0) + bit / 32, off = bit % 32;
+    words[wd] |= code << off;
+    if (off + W > 32) words[wd + 1] |= code >> (32 - off);
   }
   uint32_t sbyte = 127u;
   if (live && g * 32 < K) {
@@ -110,12 +124,21 @@ __global__ void __launch_bounds__(256) k_mx_pack(const float* __restrict__ P, co
   }
   const int64_t tile = c / 32, r = c % 32, step = g / 2, half = g % 2;
   const int64_t chunk = (tile * nk + step) * 64;           // lane 0 of this (tile, step)
-  // elements [0, 16) of the block go to lane r (h = 0), [16, 32) to lane 32 + r (h = 1); block 2s + half fills
-  // bytes [16 * half, 16 * half + 16) of each lane's 32
-  *reinterpret_cast<v4i*>(codes + (chunk + r) * 32 + half * 16) =
-      v4i{(int)words[0], (int)words[1], (int)words[2], (int)words[3]};
-  *reinterpret_cast<v4i*>(codes + (chunk + 32 + r) * 32 + half * 16) =
-      v4i{(int)words[4], (int)words[5], (int)words[6], (int)words[7]};
+  if constexpr (W == 8) {
+    // codes [0, 16) of the block go to lane r (h = 0), [16, 32) to lane 32 + r (h = 1); block 2s + half fills
+    // bytes [16 half, 16 half + 16) of each lane's 32
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(codes + (chunk + 32 * h + r) * BPL + half * (BPL / 2));
+#pragma unroll
+      for (int w = 0; w < HW; ++w) dst[w] = words[h * HW + w];
+    }
+  } else {
+    // the whole block to lane 32 half + r
+    uint32_t* dst = reinterpret_cast<uint32_t*>(codes + (chunk + 32 * half + r) * BPL);
+#pragma unroll
+    for (int w = 0; w < 2 * HW; ++w) dst[w] = words[w];
+  }
   scales[chunk + half * 32 + r] = (uint8_t)sbyte;          // lane 32 * half + r reads block 2s + half
   if (bad) atomicOr(err, 1);
 }
@@ -134,25 +157,37 @@ struct MxStep {
 
 constexpr int kDepth = 4;
 
-// (tile, step) chunk c: this lane's 32 bytes and scale byte
+// (tile, step) chunk c: this lane's BPL bytes of codes (the unused high registers of the operand are zero)
+template <int BPL>
 __device__ __forceinline__ v8i load_codes(const uint8_t* codes, int64_t chunk, int lane) {
-  const v4i* p = reinterpret_cast<const v4i*>(codes + (chunk * 64 + lane) * 32);
-  const v4i lo = p[0], hi = p[1];
-  return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  const uint8_t* q = codes + (chunk * 64 + lane) * BPL;
+  if constexpr (BPL == 32) {
+    const v4i* p = reinterpret_cast<const v4i*>(q);
+    const v4i lo = p[0], hi = p[1];
+    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  } else if constexpr (BPL == 24) {
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    const v2i* p = reinterpret_cast<const v2i*>(q);        // 8-byte aligned: 24 (chunk * 64 + lane)
+    const v2i x = p[0], y = p[1], z = p[2];
+    return v8i{x[0], x[1], y[0], y[1], z[0], z[1], 0, 0};
+  } else {
+    const v4i v = *reinterpret_cast<const v4i*>(q);
+    return v8i{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
+  }
 }
 
-template <int TA>
+template <int TA, int BA, int BB>
 __device__ __forceinline__ void load_step(MxStep<TA>& st, const uint8_t* A, const uint8_t* SA, const uint8_t* B,
                                           const uint8_t* SB, const int64_t (&ta)[TA], const int64_t (&tb)[2],
                                           int64_t nk, int64_t s, int lane) {
 #pragma unroll
   for (int t = 0; t < TA; ++t) {
-    st.a[t] = load_codes(A, ta[t] * nk + s, lane);
+    st.a[t] = load_codes<BA>(A, ta[t] * nk + s, lane);
     st.sa[t] = SA[(ta[t] * nk + s) * 64 + lane];
   }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    st.b[t] = load_codes(B, tb[t] * nk + s, lane);
+    st.b[t] = load_codes<BB>(B, tb[t] * nk + s, lane);
     st.sb[t] = SB[(tb[t] * nk + s) * 64 + lane];
   }
 }
@@ -161,6 +196,7 @@ template <int KA, int KB, int TA>
 __global__ void __launch_bounds__(256) k_mx_mfma(const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA,
                                                  const uint8_t* __restrict__ B, const uint8_t* __restrict__ SB,
                                                  float* __restrict__ C, int64_t K64, int64_t M, int64_t N) {
+  constexpr int BA = lane_bytes(KA), BB = lane_bytes(KB);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = lane & 31, h = lane >> 5;
   const int64_t m0 = (int64_t)blockIdx.y * (64 * TA) + (wave >> 1) * (32 * TA);
@@ -176,7 +212,8 @@ __global__ void __launch_bounds__(256) k_mx_mfma(const uint8_t* __restrict__ A, 
   // step kDepth ahead (past the end it re-reads the last step, whose values are never used).
   MxStep<TA> slot[kDepth];
 #pragma unroll
-  for (int s = 0; s < kDepth; ++s) load_step(slot[s], A, SA, B, SB, ta, tb, nk, min((int64_t)s, nk - 1), lane);
+  for (int s = 0; s < kDepth; ++s)
+    load_step<TA, BA, BB>(slot[s], A, SA, B, SB, ta, tb, nk, min((int64_t)s, nk - 1), lane);
   for (int64_t k = 0; k < nk; k += kDepth) {
 #pragma unroll
     for (int s = 0; s < kDepth; ++s) {
@@ -188,7 +225,7 @@ __global__ void __launch_bounds__(256) k_mx_mfma(const uint8_t* __restrict__ A, 
             acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(slot[s].a[i], slot[s].b[j], acc[i][j], KA, KB,
                                                                         0, slot[s].sa[i], 0, slot[s].sb[j]);
       }
-      load_step(slot[s], A, SA, B, SB, ta, tb, nk, min(k + s + kDepth, nk - 1), lane);
+      load_step<TA, BA, BB>(slot[s], A, SA, B, SB, ta, tb, nk, min(k + s + kDepth, nk - 1), lane);
     }
   }
 #pragma unroll
@@ -205,28 +242,46 @@ __global__ void __launch_bounds__(256) k_mx_mfma(const uint8_t* __restrict__ A, 
   }
 }
 
+template <int TA, int KA>
+void launch_mfma_b(int b_kind, dim3 grid, hipStream_t st, const uint8_t* A, const uint8_t* SA, const uint8_t* B,
+                   const uint8_t* SB, float* C, int64_t K64, int64_t M, int64_t N) {
+  switch (b_kind) {
+    case kE4M3: k_mx_mfma<KA, kE4M3, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+    case kE5M2: k_mx_mfma<KA, kE5M2, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+    case kE2M3: k_mx_mfma<KA, kE2M3, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+    case kE3M2: k_mx_mfma<KA, kE3M2, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+    default: k_mx_mfma<KA, kE2M1, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+  }
+}
+
 template <int TA>
 void launch_mfma(int a_kind, int b_kind, dim3 grid, hipStream_t st, const uint8_t* A, const uint8_t* SA,
                  const uint8_t* B, const uint8_t* SB, float* C, int64_t K64, int64_t M, int64_t N) {
-  if (a_kind == kE4M3 && b_kind == kE4M3) k_mx_mfma<kE4M3, kE4M3, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
-  else if (a_kind == kE4M3) k_mx_mfma<kE4M3, kE5M2, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
-  else if (b_kind == kE4M3) k_mx_mfma<kE5M2, kE4M3, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
-  else k_mx_mfma<kE5M2, kE5M2, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N);
+  switch (a_kind) {
+    case kE4M3: launch_mfma_b<TA, kE4M3>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+    case kE5M2: launch_mfma_b<TA, kE5M2>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+    case kE2M3: launch_mfma_b<TA, kE2M3>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+    case kE3M2: launch_mfma_b<TA, kE3M2>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+    default: launch_mfma_b<TA, kE2M1>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+  }
 }
 
 }  // namespace
 
 extern "C" int mxq_mx_pack(const float* P, const float* X, int64_t K, int64_t n, int32_t kind, uint8_t* codes,
                            uint8_t* scales, int32_t* err, mxq_stream_t stream) {
-  if (K < 0 || n < 0 || (kind != kE4M3 && kind != kE5M2)) return mxq::invalid("mxq_mx_pack: bad arguments");
+  if (K < 0 || n < 0 || kind < kE4M3 || kind > kE2M1) return mxq::invalid("mxq_mx_pack: bad arguments");
   const int64_t K64 = mxq::ceil_div(K, 64) * 64;
   if (n == 0 || K64 == 0) return MXQ_OK;
   if (!P || !X || !codes || !scales || !err) return mxq::invalid("mxq_mx_pack: NULL pointer");
   if (reinterpret_cast<uintptr_t>(codes) % 16) return mxq::invalid("mxq_mx_pack: codes must be 16-byte aligned");
   const int64_t n32 = mxq::ceil_div(n, 32) * 32;
   const int64_t threads = n32 * (K64 / 32);
-  k_mx_pack<<<mxq::grid_for(threads, 256), 256, 0, mxq::as_stream(stream)>>>(P, X, K, n, n32, K64, kind, codes,
-                                                                               scales, err);
+  const dim3 grid = mxq::grid_for(threads, 256);
+  hipStream_t st = mxq::as_stream(stream);
+  if (code_bits(kind) == 8) k_mx_pack<8><<<grid, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
+  else if (code_bits(kind) == 6) k_mx_pack<6><<<grid, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
+  else k_mx_pack<4><<<grid, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
   return mxq::check_launch("mxq_mx_pack");
 }
 
@@ -234,7 +289,7 @@ extern "C" int mxq_mx_mfma(const uint8_t* A, const uint8_t* SA, int32_t a_kind, 
                            int32_t b_kind, float* C, int64_t K64, int64_t M, int64_t N, mxq_stream_t stream) {
   // K64 == 0 is refused: the kernel's prologue reads its first K step before the loop tests the count
   if (K64 <= 0 || K64 % 64 || M < 0 || N < 0) return mxq::invalid("mxq_mx_mfma: bad shape (K64 must be a positive multiple of 64)");
-  if ((a_kind != kE4M3 && a_kind != kE5M2) || (b_kind != kE4M3 && b_kind != kE5M2))
+  if (a_kind < kE4M3 || a_kind > kE2M1 || b_kind < kE4M3 || b_kind > kE2M1)
     return mxq::invalid("mxq_mx_mfma: bad operand kind");
   if (M == 0 || N == 0) return MXQ_OK;
   if (!A || !SA || !B || !SB || !C) return mxq::invalid("mxq_mx_mfma: NULL pointer");
