@@ -44,6 +44,7 @@ SLOTS_PER_MAC_MODEL = 8
 VALU_ROOF_TOPS = VALU_LANE_OPS / SLOTS_PER_MAC_MODEL * 2 / 1e12   # 19.66 TOP/s emulated
 VALU_PROBE_KINDS = ("v_add_f32", "v_mul_f32", "v_and_b32", "v_rndne_f32", "v_bfe_u32", "v_add3_u32")
 FP8_PEAK_TFLOPS = 5000.0                    # MI355X dense FP8 matrix-core peak
+FP6_FP4_PEAK_TFLOPS = 10100.0               # MI355X dense FP6 and FP4 matrix-core peak
 MAX_POOL = 16                               # host processes for the CPU baselines (one GPU's CPU share)
 
 C3_FORMATS = ("MXFP8_E4M3", "MXFP8_E5M2", "MXFP6_E3M2", "MXFP6_E2M3", "MXFP4")
@@ -467,23 +468,34 @@ def trees_line(torch, steps, P_A, X_A, P_B, X_B):
     return out
 
 
-def mfma_line(torch, steps, P_A, X_A, P_B, X_B):
+def mfma_line(torch, steps, P_A, X_A, P_B, X_B, inp=None):
     """mfma_accum (the matrix-core comparison product) on the benchmark's own codes: pack both operands to FP8
     and E8M0 bytes, then V_MFMA_SCALE_F32_32X32X64_F8F6F4.  The kernel rate is held against MI355X's dense FP8
-    peak, 5.0 PFLOP/s."""
+    peak, 5.0 PFLOP/s.  With the inputs, the same x and W quantized to MXFP6_E2M3 and MXFP4 travel as FP6 and
+    FP4 operands, against the 10.1 PFLOP/s dense FP6/FP4 peak."""
     import mxq
+    from mxq import block
     dev = P_A.device
     s = torch.cuda.current_stream(dev)
-    fn = lambda: mxq.mfma_accum(P_A, X_A, P_B, X_B, "MXFP8_E4M3")                # noqa: E731
-    fn()
-    ms = _events_ms(fn, steps, s)
-    kms, _ = _kernel_ms(fn, steps, "mx_mfma")
     flops = 2 * P_A.shape[0] * P_A.shape[1] * P_B.shape[1]
-    k_tf = flops / (kms / 1e3) / 1e12 if kms else None
-    return {"workload": "mfma_accum on the same MXFP8_E4M3 codes (M = 512, N = 4096, K = 4096)",
-            "ms": round(ms, 4), "kernel": "k_mx_mfma", "kernel_ms": round(kms, 4) if kms else None,
-            "kernel_TFLOPs": round(k_tf, 2) if k_tf else None, "peak_TFLOPs": FP8_PEAK_TFLOPS,
-            "frac": round(k_tf / FP8_PEAK_TFLOPS, 4) if k_tf else None}
+
+    def timed(ops, fmt, peak):
+        fn = lambda: mxq.mfma_accum(*ops, fmt)                                    # noqa: E731
+        fn()
+        ms = _events_ms(fn, steps, s)
+        kms, _ = _kernel_ms(fn, steps, "mx_mfma")
+        k_tf = flops / (kms / 1e3) / 1e12 if kms else None
+        return {"ms": round(ms, 4), "kernel_ms": round(kms, 4) if kms else None,
+                "kernel_TFLOPs": round(k_tf, 2) if k_tf else None, "peak_TFLOPs": peak,
+                "frac": round(k_tf / peak, 4) if k_tf else None}
+    out = {"workload": "mfma_accum on the same MXFP8_E4M3 codes (M = 512, N = 4096, K = 4096)", "kernel": "k_mx_mfma",
+           **timed((P_A, X_A, P_B, X_B), "MXFP8_E4M3", FP8_PEAK_TFLOPS)}
+    if inp is not None:
+        xt, wt = inp["x"].t().contiguous().to(dev), inp["W"].t().contiguous().to(dev)
+        for fmt in ("MXFP6_E2M3", "MXFP4"):
+            a, b = block.mxgemmini.quantize(xt, fmt, axis=0), block.mxgemmini.quantize(wt, fmt, axis=0)
+            out[fmt] = timed((a[0], a[1], b[0], b[1]), fmt, FP6_FP4_PEAK_TFLOPS)
+    return out
 
 
 def valu_rates():
@@ -594,7 +606,7 @@ def main():
     P_B, X_B = block.mxgemmini.quantize(inp["W"].t().contiguous().to(dev), "MXFP8_E4M3", axis=0)
     ar = matmul.MXGEMMINI()
     if args.only in ("mfma", "trees"):
-        fn = {"mfma": lambda: mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B),
+        fn = {"mfma": lambda: mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B, inp),
               "trees": lambda: trees_line(torch, 3, P_A, X_A, P_B, X_B)}[args.only]
         print(json.dumps({"only": args.only, args.only: fn()}), flush=True)
         return
@@ -644,7 +656,7 @@ def main():
         line["quantize"], extra["quantize"] = quantize_lines(torch, max(5, args.steps // 2), inp)
         line["lut_c4"], extra["lut"] = lut_line(torch, 3, inp)
         line["attend_c5"], extra["attend"] = attend_line(torch, 3, inp)
-        line["mfma_c2"] = mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B)
+        line["mfma_c2"] = mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B, inp)
         line["trees_c2"] = trees_line(torch, 3, P_A, X_A, P_B, X_B)
     if cpu is not None:
         line["cpu_baseline"] = cpu["c2"]["cpu_baseline"]

@@ -108,25 +108,27 @@ struct FloatSink {
 
 template <int VEC>
 __device__ __forceinline__ void store_bytes(uint8_t* p, uint32_t w) {
-  if constexpr (VEC == 4) __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(p));
+  if constexpr (VEC == 4) *reinterpret_cast<uint32_t*>(p) = w;
   else if constexpr (VEC == 2) *reinterpret_cast<uint16_t*>(p) = (uint16_t)w;
   else *p = (uint8_t)w;
 }
 
-// W words of code bytes (1, 2 or 4: 4, 8 or 16 bytes, aligned), one streaming store.
+// W words of code bytes (1, 2 or 4: 4, 8 or 16 bytes, aligned), one store.
+// The byte sink's stores: plain, not streaming.  A wave writes 64 bytes of a code row and the next wave the rest of
+// its 128-byte line; streaming stores of those halves wrote 1.28x the code and scale bytes (C3: 88.4 MB for 69.2),
+// plain ones exactly them, in the same time.  (The float sink's rows are whole lines; its streaming stores keep
+// 268 MB of codes out of L2 and run faster than plain ones.)
 template <int W>
 __device__ __forceinline__ void store_words(uint8_t* p, const uint32_t (&w)[W]) {
   if constexpr (W == 1) {
-    __builtin_nontemporal_store(w[0], reinterpret_cast<uint32_t*>(p));
+    *reinterpret_cast<uint32_t*>(p) = w[0];
   } else if constexpr (W == 4) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 v = {w[0], w[1], w[2], w[3]};
-    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+    *reinterpret_cast<u32x4*>(p) = u32x4{w[0], w[1], w[2], w[3]};
   } else {
     static_assert(W == 2, "4, 8 or 16 bytes");
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    const u32x2 v = {w[0], w[1]};
-    __builtin_nontemporal_store(v, reinterpret_cast<u32x2*>(p));
+    *reinterpret_cast<u32x2*>(p) = u32x2{w[0], w[1]};
   }
 }
 
