@@ -28,6 +28,13 @@ __host__ __device__ inline bool has_hw(int e, int m) {
   return (e == 4 && m == 3) || (e == 5 && m == 2) || (e == 2 && m == 3) || (e == 3 && m == 2) || (e == 2 && m == 1);
 }
 
+// The formats whose conversion of N values a lane takes here: the FP6 forms convert 32 values at a time, whose
+// register vectors are not worth it for fewer than 16 (a kernel converting fewer leaves FP6 to the grid).
+template <int N>
+__host__ __device__ inline bool has_hw_n(int e, int m) {
+  return has_hw(e, m) && (N >= 16 || !((e == 2 && m == 3) || (e == 3 && m == 2)));
+}
+
 // |z| below this (and finite) converts as the grid rounds.
 __host__ __device__ inline float hw_limit(int e, int m) {
   return (e == 4 && m == 3) ? 464.0f : ((e == 5 && m == 2) ? 57344.0f : 3.0e38f);
@@ -68,7 +75,8 @@ __device__ __forceinline__ uint32_t field6(const u6v& p, int k) {
   return v & 63u;
 }
 
-// The element codes of N values (N % 4 == 0, N <= 32), code j in byte j % 4 of w[j / 4].
+// The element codes of N values (N % 4 == 0, N <= 32), code j in byte j % 4 of w[j / 4]; FP6 for N >= 16 only
+// (has_hw_n).
 template <int N>
 __device__ __forceinline__ void codes(const float (&z)[N], int e, int m, uint32_t (&w)[N / 4]) {
   static_assert(N % 4 == 0 && N <= 32, "N values in whole words");
@@ -94,7 +102,7 @@ __device__ __forceinline__ void codes(const float (&z)[N], int e, int m, uint32_
       // nibbles n0 n1 | n2 n3 in the low two bytes -> one code a byte
       w[q] = (r & 0xFu) | ((r & 0xF0u) << 4) | ((r & 0xF00u) << 8) | ((r & 0xF000u) << 12);
     }
-  } else {
+  } else if constexpr (N >= 16) {
     f16v even, odd;
     fp6_split<N>(z, even, odd);
     const u6v p = pack16x2(even, odd, e == 2);
@@ -104,7 +112,8 @@ __device__ __forceinline__ void codes(const float (&z)[N], int e, int m, uint32_
   }
 }
 
-// The grid values of N values (N even, N <= 32), in place: converted and converted back.
+// The grid values of N values (N even, N <= 32), in place: converted and converted back; FP6 for N >= 16 only
+// (has_hw_n).
 template <int N>
 __device__ __forceinline__ void values(float (&z)[N], int e, int m) {
   static_assert(N % 2 == 0 && N <= 32, "N values in pairs");
@@ -125,7 +134,7 @@ __device__ __forceinline__ void values(float (&z)[N], int e, int m) {
       z[2 * q] = r.x;
       z[2 * q + 1] = r.y;
     }
-  } else {
+  } else if constexpr (N >= 16) {
     f16v even, odd;
     fp6_split<N>(z, even, odd);
     const f32v r = unpack32(pack16x2(even, odd, e == 2), e == 2);

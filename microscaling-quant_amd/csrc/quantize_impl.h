@@ -440,9 +440,11 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, co
   }
   // the OCP grid at nearest even by the hardware conversions when every scaled value of the wave is finite
   // and within their range (a column's largest |z| is its maximum scaled, the division being monotone)
+  constexpr bool HW_OCP = ELEM == MXQ_ELEM_OCP && MODE == MXQ_RNE && VEC >= 4;
+  constexpr bool HW_MS = ELEM == MXQ_ELEM_MICROSOFT && MODE == MXQ_RNE && VEC >= 4;
   bool hw = false;
-  if constexpr (ELEM == MXQ_ELEM_OCP && MODE == MXQ_RNE && VEC >= 4) {
-    if (s.via_e == 0 && mxq_ocp_hw::has_hw(s.e, s.m) && out.hw_format(s)) {
+  if constexpr (HW_OCP) {
+    if (s.via_e == 0 && mxq_ocp_hw::has_hw_n<ROWS * VEC>(s.e, s.m) && out.hw_format(s)) {
       const float lim = mxq_ocp_hw::hw_limit(s.e, s.m);
       bool ok = true;
 #pragma unroll
@@ -454,10 +456,40 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, co
       hw = __all(ok);
     }
   }
+  // microxcaling's "even" (mxq/microxcaling/elemwise.py:29-60) is the OCP grid at nearest even, saturating at
+  // max_norm, with one exception: the float32 just below half the smallest subnormal step, which its float32
+  // floor(|A| + 0.5) rounds up to that step.  So with every value and scaled value finite and none of that
+  // magnitude, the values clamped to +-max_norm go to the hardware conversions.
+  mxq_block_spec hs = s;                             // the element format as the conversions name it
+  if constexpr (HW_MS) {
+    hs.m = s.m - 2;                                   // microxcaling's mbits count the sign and hidden bits
+    if (s.via_e == 0 && mxq_ocp_hw::has_hw_n<ROWS * VEC>(hs.e, hs.m) && out.hw_format(hs)) {
+      const int emin = 2 - (1 << (hs.e - 1));
+      const uint32_t odd = (uint32_t)(127 + emin - hs.m - 1) << 23;  // 2^(emin - m - 1), then one float below
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {               // finite inputs and finite scaled values (a NaN scale fails)
+        const float a = u2f(am[j]);
+        const float zm = !s.scale_rule ? a : (div ? apply_div(a, d[j]) : a * d[j].inv);
+        ok = ok && am[j] < 0x7F800000u && zm < INFINITY;
+      }
+#pragma unroll
+      for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) ok = ok && (f2u(v[i][j]) & 0x7FFFFFFFu) != odd - 1u;
+      hw = __all(ok);
+      if (hw) {
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) v[i][j] = fminf(fmaxf(v[i][j], -s.max_norm), s.max_norm);
+      }
+    }
+  }
   if (!live) return;
   const int64_t dst = (o * n + k0 + r * ROWS) * inner + cg * VEC;
-  if constexpr (ELEM == MXQ_ELEM_OCP && MODE == MXQ_RNE && VEC >= 4) {
-    if (hw) out.template hw_rows<ROWS, VEC>(dst, inner, v, rows == 32 ? ROWS : rows - r * ROWS, s);
+  if constexpr (HW_OCP || HW_MS) {
+    if (hw) out.template hw_rows<ROWS, VEC>(dst, inner, v, rows == 32 ? ROWS : rows - r * ROWS, hs);
   }
   if (!hw) {
 #pragma unroll

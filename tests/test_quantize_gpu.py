@@ -326,3 +326,49 @@ def test_mxgemmini_rne_grid_edges(cuda, fmt):
         assert not err
         assert np.array_equal(codes.cpu().numpy(), want_c), f"codes {fmt} {dt}"
         assert np.array_equal(scales.cpu().numpy(), want_s), f"scales {fmt} {dt}"
+
+
+def _ocp_edge_input(fmt, cols, seed):
+    """K = 96 rows (three blocks) by `cols` columns for block.ocp: every block's first row is 1.999 * 2^emax
+    (the OCP scale is then 1), the rest cycle through the format's grid, its ties and their float32 neighbours,
+    values between max_norm and 2^(emax + 1) (which saturate), the float32 just below half the smallest
+    subnormal step (which microxcaling's float32 rounding sends up a step), signed zeros and values that
+    round to zero, with random signs.  Column 5 holds a NaN and column 9 an Inf in the first block; two
+    elements hold the exceptional value, so that their waves, and only theirs, leave the conversions."""
+    from oracle import packed as op
+    e, m = op.FORMATS[fmt]
+    bias = (1 << (e - 1)) - 1
+    grid = sorted({(mf / (1 << m)) * 2.0 ** (1 - bias) if ef == 0 else (1 + mf / (1 << m)) * 2.0 ** (ef - bias)
+                   for ef in range(1 << e) for mf in range(1 << m)})
+    top = {"MXFP8_E4M3": 448.0, "MXFP8_E5M2": 57344.0, "MXFP6_E3M2": 28.0, "MXFP6_E2M3": 7.5, "MXFP4": 6.0}[fmt]
+    emax = int(np.floor(np.log2(top)))
+    grid = np.array([g for g in grid if g <= top], dtype=np.float64)
+    mids = ((grid[:-1] + grid[1:]) / 2).astype(np.float32)
+    over = np.linspace(top, 2.0 ** (emax + 1), 9)[1:-1].astype(np.float32)
+    odd = np.nextafter(np.float32(grid[1] / 2), np.float32(0))
+    pts = np.concatenate([grid.astype(np.float32), mids, np.nextafter(mids, np.float32(0)),
+                          np.nextafter(mids, np.float32(1e9)), over, np.float32([0.0, -0.0, 1e-30])])
+    rng = np.random.default_rng(seed)
+    V = rng.choice(pts, size=(96, cols)).astype(np.float32)
+    V *= np.where(rng.random(V.shape) < 0.5, np.float32(-1), np.float32(1))
+    V[::32, :] = np.float32(1.999 * 2.0 ** emax)
+    V[7, 5] = np.nan
+    V[3, 9] = np.inf
+    V[40, 20], V[70, cols - 3] = odd, -odd
+    return V
+
+
+@pytest.mark.parametrize("fmt", ["MXFP8_E4M3", "MXFP8_E5M2", "MXFP6_E3M2", "MXFP6_E2M3", "MXFP4"])
+@pytest.mark.parametrize("cols", [256, 90112], ids=["row_a_lane", "four_rows_a_lane"])
+def test_ocp_even_grid_edges(cuda, fmt, cols):
+    """block.ocp at "even" (microxcaling's rule), which runs on the hardware conversions, clamped to max_norm,
+    when a wave's values and scaled values are finite and none is the one value microxcaling rounds apart:
+    every tie, saturating value, signed zero and subnormal step of the format against the oracle.  256 columns
+    take one row a lane (4 values a lane: FP6 stays on the grid); 90112 take four rows a lane (16 values: FP6
+    converts too).  The NaN, Inf and exceptional-value waves take the general path in the same launches."""
+    from mxq import block
+    V = _ocp_edge_input(fmt, cols, 11)
+    P, X = block.ocp.quantize(torch.from_numpy(V).cuda(), fmt, axis=0, rounding_mode="even")
+    wP, wX = ob.ocp_quantize(V, fmt, 0)
+    assert_bits_equal(X.cpu().numpy(), wX, f"X {fmt}")
+    assert_bits_equal(P.cpu().numpy(), wP, f"P {fmt}")
