@@ -284,3 +284,30 @@ def test_split_rne_equals_bit_rne_on_bf16_lane_values():
     y = np.concatenate([y, near, -near, sub, -sub])
     assert_bits_equal(_split_rne(y, 7), _bit_rne(y, 7), "split bf16")
     assert_bits_equal(_split_rne(sub, 7), sub, "split bf16 subnormal")
+
+
+@pytest.mark.parametrize("fmt,e,m,top", [("MXFP8_E4M3", 4, 3, 448.0), ("MXFP8_E5M2", 5, 2, 57344.0),
+                                         ("MXFP6_E3M2", 3, 2, 28.0), ("MXFP6_E2M3", 2, 3, 7.5), ("MXFP4", 2, 1, 6.0)])
+def test_microsoft_even_is_clamped_ocp_rne(fmt, e, m, top):
+    """The identity behind block.ocp's hardware path: microxcaling's "even" equals the OCP grid at nearest even
+    after a clamp to +-max_norm (signed zeros included), except at the float32 just below half the smallest
+    subnormal step, which its float32 floor(|A| + 0.5) rounds up to that step.  Checked on every grid value,
+    tie and float32 neighbour, the saturating range and 10^6 random values per format."""
+    rng = np.random.default_rng(e * 10 + m)
+    span = 2.0 ** (np.floor(np.log2(top)) + 1)
+    bias = (1 << (e - 1)) - 1
+    g = np.array(sorted({(mf / (1 << m)) * 2.0 ** (1 - bias) if ef == 0 else (1 + mf / (1 << m)) * 2.0 ** (ef - bias)
+                         for ef in range(1 << e) for mf in range(1 << m)}), np.float64)
+    g = g[g <= top].astype(np.float32)
+    mids = ((g[1:].astype(np.float64) + g[:-1]) / 2).astype(np.float32)
+    near = np.concatenate([g, mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0)),
+                           np.nextafter(g, np.float32(np.inf)), np.nextafter(g, np.float32(0))])
+    z = np.concatenate([near, -near, rng.uniform(-1.2 * span, 1.2 * span, 10 ** 6).astype(np.float32),
+                        (rng.uniform(-1, 1, 10 ** 5) * 2.0 ** rng.integers(-40, 0, 10 ** 5)).astype(np.float32),
+                        np.float32([0.0, -0.0])])
+    ms = nx.microsoft_fmt(z, fmt, "even")
+    hw = nx.float_em(np.clip(z, np.float32(-top), np.float32(top)) + np.float32(0), e, m, "rne", "ocp")
+    odd = np.nextafter(np.float32(g[1] / 2), np.float32(0))
+    differ = ms.view(np.uint32) != hw.view(np.uint32)
+    assert set(np.abs(z[differ]).tolist()) == {float(odd)}
+    assert np.array_equal(ms[differ], np.sign(z[differ]) * np.float32(g[1]))
