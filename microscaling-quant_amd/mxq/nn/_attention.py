@@ -288,6 +288,20 @@ def _hints(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale: 
 
 
 @dataclass
+class _Prepared:
+    """One chunk of the batched path between its preparation and its launches."""
+    z0: int
+    z1: int
+    s0: int
+    e0: int
+    A_P: torch.Tensor
+    A_X: torch.Tensor
+    flags: Optional[torch.Tensor]
+    skip: Optional[torch.Tensor]
+    k_end: Optional[torch.Tensor]
+
+
+@dataclass
 class _Batched:
     """attend built from the library's own pieces (column-wise block quantizers, matmul.systolic with a kernel
     Arithmetic, no LUT rows) runs a query chunk of every (batch row, KV head) pair as one quantize call per
@@ -324,31 +338,29 @@ class _Batched:
         kv = (KT_P, KT_X, V_P, V_X)
         k_amax = _group_amax(KT_P, KT_X, qk.block_size, Z) if bias is not None else None
         qg = q.reshape(Z, n, dims.Tq, D)
-        pending = []                                     # (flags, z0, s0, e0) of chunks run on the batched path
+        # every chunk's operands, flags and hints first; the flags then come over in one transfer, before any
+        # matmul is queued, so the host queues the matmuls back to back and returns without waiting for them
+        chunks = []
         for s0 in range(0, dims.Tq, step):
             e0 = min(s0 + step, dims.Tq)
             for z0, z1 in _launch_ranges(B, Hkv, max(1, ELEMENTS_PER_LAUNCH // (n * (e0 - s0) * Tk))):
-                flags = self._chunk(qg, bias, kv, k_amax, scale, vector, dims, z0, z1, s0, e0, out)
-                if flags is not None:
-                    pending.append((flags, z0, s0, e0))
+                chunks.append(self._prepare(qg, bias, kv, k_amax, scale, dims, z0, z1, s0, e0))
+        every = torch.cat([c.flags for c in chunks]).cpu().tolist() if bias is not None else []
+        for c in chunks:
+            self._chunk(c, qg, bias, kv, scale, vector, dims, out)
         # a pair that would skip masked keys gets the reference's own call, on the same codes, over its outputs
-        if pending:
-            every = torch.cat([f for f, _, _, _ in pending]).cpu().tolist()
-            at = 0
-            for flags, z0, s0, e0 in pending:
-                for z in range(flags.numel()):
-                    if every[at + z] != 3:
-                        self._per_pair(q, bias, kv, scale, vector, rnd, dims, z0 + z, z0 + z + 1, s0, e0, out)
-                at += flags.numel()
+        at = 0
+        for c in chunks:
+            for z in range(c.z1 - c.z0 if bias is not None else 0):
+                if every[at + z] != 3:
+                    self._per_pair(q, bias, kv, scale, vector, rnd, dims, c.z0 + z, c.z0 + z + 1, c.s0, c.e0, out)
+            at += c.z1 - c.z0 if bias is not None else 0
 
-    def _chunk(self, qg, bias, kv, k_amax, scale, vector, dims: _Dims, z0, z1, s0, e0, out) -> Optional[torch.Tensor]:
-        """Pairs z0..z1, queries s0..e0 as two batched launches.  With a mask, returns each pair's flag (int32 on
-        the device): 3 when its call keeps every key (the batched result is the reference's); otherwise the
-        caller must redo it through the reference's call."""
-        from .. import _lib
-        from ..matmul._systolic import systolic_batched
+    def _prepare(self, qg, bias, kv, k_amax, scale, dims: _Dims, z0, z1, s0, e0) -> "_Prepared":
+        """Pairs z0..z1, queries s0..e0: Q^T's codes and, with a mask, each pair's flag (int32 on the device: 3
+        when its call keeps every key, so the batched result is the reference's; otherwise the caller redoes it
+        through the reference's call) and the two launches' hints."""
         qk, pv = self.qk, self.pv
-        KT_P, KT_X, V_P, V_X = kv
         Zc, n, m, Tk, D, Hkv = z1 - z0, dims.group, e0 - s0, dims.Tk, dims.D, dims.Hkv
         cols = n * m                                                              # one call's columns
         A_P, A_X = qk.a(qg[z0:z1, :, s0:e0].to(torch.float32).permute(3, 0, 1, 2).reshape(D, Zc * cols))
@@ -357,6 +369,17 @@ class _Batched:
             a_amax = _group_amax(A_P, A_X, qk.block_size, Zc)
             flags = _windows(a_amax, k_amax, z0, Zc, scale, bias, Hkv, s0, m, pv.block_size)
             skip, k_end = _hints(a_amax, k_amax, z0, Zc, scale, bias, Hkv, s0, m, cols, Tk)
+        return _Prepared(z0, z1, s0, e0, A_P, A_X, flags, skip, k_end)
+
+    def _chunk(self, c: "_Prepared", qg, bias, kv, scale, vector, dims: _Dims, out) -> None:
+        """A prepared chunk as two batched launches, its outputs into `out`."""
+        from .. import _lib
+        from ..matmul._systolic import systolic_batched
+        qk, pv = self.qk, self.pv
+        KT_P, KT_X, V_P, V_X = kv
+        z0, z1, s0, e0, A_P, A_X, skip, k_end = c.z0, c.z1, c.s0, c.e0, c.A_P, c.A_X, c.skip, c.k_end
+        Zc, n, m, Tk, D, Hkv = z1 - z0, dims.group, e0 - s0, dims.Tk, dims.D, dims.Hkv
+        cols = n * m                                                              # one call's columns
         arith, sched, size = self.qk_red
         S = torch.empty(Zc, cols, Tk, dtype=torch.float32, device=qg.device)
         # the score step r(r(S * scale) + mask row) is applied as the scores are stored (_scale_mask's step)
@@ -387,7 +410,6 @@ class _Batched:
             h0, h1 = max(z0, b * Hkv) - b * Hkv, min(z1, (b + 1) * Hkv) - b * Hkv
             part = O[b * Hkv + h0 - z0:b * Hkv + h1 - z0]                         # (h1 - h0) x n x m x D
             out[b, s0:e0, h0 * n:h1 * n] = part.permute(2, 0, 1, 3).reshape(m, (h1 - h0) * n, D).to(out.dtype)
-        return flags
 
     def _per_pair(self, q, bias, kv, scale, vector, rnd, dims: _Dims, z0, z1, s0, e0, out) -> None:
         KT_P, KT_X, V_P, V_X = kv
