@@ -164,10 +164,16 @@ typedef struct mxq_systolic_layout {
  *          columns hold a nonzero code.  Their reduction stops there (rounded up to 32 rows); the rows left out
  *          are checked by a pass over them (once per problem, not per tile), and unless A is +-0 there and B
  *          and the block scales finite, the tile is recomputed by the general kernel: a wrong k_end costs time,
- *          never bits.  Tiles are dispatched longest reduction first. */
+ *          never bits.  Tiles are dispatched longest reduction first.
+ *   a_live with k_end, the check's answer for A made by the caller (attention's softmax writes it with P^T,
+ *          mxq_softmax_quantize_t): per problem z, 32-row stage s and 32-column group g of A,
+ *          a_live[(z * ceil(K/32) + s) * ceil(M/32) + g] != 0 unless every code of A in those rows and columns
+ *          is +-0 and every block scale over them finite.  The pass then reads B only.  A byte that wrongly
+ *          says 0 for a stage some tile leaves out gives wrong results: this one is a promise, not a hint. */
 typedef struct mxq_systolic_hints {
   const uint8_t* skip;
   const int32_t* k_end;
+  const uint8_t* a_live;
 } mxq_systolic_hints;
 
 /* An elementwise step mxq_systolic_batched applies to every output as it is stored (no counterpart in the
@@ -237,9 +243,13 @@ int mxq_attend_windows(const double* amax_a, int64_t lda, const double* amax_k, 
  * element-to-lane order, reduction trees, expf and IEEE division), then P^T (T x R) block-quantized along T in
  * blocks of 32 by spec (MX-Gemmini's: the mxquant scale and the OCP element grid): PT_P (T x R float32 codes),
  * PT_X (ceil(T/32) x R float32 scales), as block.mxgemmini.quantize(softmax(S).t(), axis=0) gives them.
- * Replaces mxq/nn/_attention.py:136-139 (softmax, then pv.a(P.t())) for the batched path. */
+ * Replaces mxq/nn/_attention.py:136-139 (softmax, then pv.a(P.t())) for the batched path.  With stage_live
+ * (NULL for none), P^T's columns are R / cols problems of cols each (cols a multiple of 32 dividing R), and
+ * stage_live[(z * ceil(T/32) + s) * (cols / 32) + g] gets 1 when problem z's 32 rows s and 32 columns g of P^T
+ * hold a nonzero code or a non-finite scale, else 0: the a_live answer of mxq_systolic_hints for the P V
+ * product on these codes. */
 int mxq_softmax_quantize_t(const float* S, int64_t R, int64_t T, float* PT_P, float* PT_X,
-                           const mxq_block_spec* spec, mxq_stream_t stream);
+                           const mxq_block_spec* spec, uint8_t* stage_live, int64_t cols, mxq_stream_t stream);
 
 /* attend's two elementwise steps on the scores, in place: S (Z problems x n heads x m queries x Tk keys, float32,
  * contiguous) becomes r(r(S * scale) + mask_row), r the identity or (round_bf16 = 1) rounding.bf16; the add and its

@@ -11,7 +11,10 @@
 //                 the same bits.  Pass 1 takes those row statistics, one wave a row; in pass 2 a lane owns a row
 //                 and recomputes the probabilities of one 32-key block of it at a time, quantizes them as the
 //                 block they are (its maximum, the scale rule, the division, the element rule) and stores each
-//                 code at P^T[key][row], so a wave's store is a run of 64 rows.
+//                 code at P^T[key][row], so a wave's store is a run of 64 rows.  With `stage_live`, it also
+//                 writes, per 32 keys and 32 rows of P^T, whether any code there is nonzero or any scale
+//                 not finite: the answer the P V product's suffix pass would read P^T for (mxq_systolic_hints
+//                 a_live).
 #include <math.h>
 
 #include "mxq_common.h"
@@ -48,7 +51,8 @@ __device__ __forceinline__ void row_stats(const float* __restrict__ row, int T, 
 template <int ELEM, int MODE, int IT>
 __global__ void __launch_bounds__(256) k_softmax_pt(const float* __restrict__ S, int64_t R, int T,
                                                     float* __restrict__ PT_P, float* __restrict__ PT_X,
-                                                    mxq_block_spec s) {
+                                                    mxq_block_spec s, uint8_t* __restrict__ stage_live,
+                                                    int64_t cols) {
   __shared__ float mx_s[RB], sum_s[RB];
   const int64_t r0 = (int64_t)blockIdx.x * RB;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -93,37 +97,55 @@ __global__ void __launch_bounds__(256) k_softmax_pt(const float* __restrict__ S,
     }
     const float xs = block_scale(u2f(am), s);
     const Div d = make_div(xs);
+    uint32_t nz = 0u;                                  // the OR of this row's |code| bits over the block
     if (live) {
       PT_X[(int64_t)b * R + r] = xs;
 #pragma unroll
       for (int q = 0; q < 32; ++q)
-        if (k0 + q < T) PT_P[(int64_t)(k0 + q) * R + r] = elem_qm<ELEM, MODE>(s.scale_rule ? apply_div(v[q], d) : v[q], s);
+        if (k0 + q < T) {
+          const float code = elem_qm<ELEM, MODE>(s.scale_rule ? apply_div(v[q], d) : v[q], s);
+          PT_P[(int64_t)(k0 + q) * R + r] = code;
+          nz |= f2u(code) & 0x7FFFFFFFu;
+        }
+    }
+    if (stage_live) {
+      // per 32 rows (a half wave, inside one problem: cols % 32 == 0): any nonzero code or non-finite scale
+      const uint64_t bal = __ballot(live && (nz != 0u || !(fabsf(xs) < INFINITY)));
+      const int half = lane & 32;
+      const int64_t rh = r0 + half;
+      if ((lane & 31) == 0 && rh < R) {
+        const int64_t z = rh / cols, g = (rh - z * cols) / 32;
+        stage_live[(z * nb + b) * (cols / 32) + g] = ((bal >> half) & 0xFFFFFFFFull) != 0ull ? 1u : 0u;
+      }
     }
   }
 }
 
 template <int ELEM, int MODE>
 void launch_it(int it, dim3 grid, hipStream_t st, const float* S, int64_t R, int T, float* PT_P, float* PT_X,
-               const mxq_block_spec& s) {
+               const mxq_block_spec& s, uint8_t* live, int64_t cols) {
   switch (it) {
-    case 1: k_softmax_pt<ELEM, MODE, 1><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s); break;
-    case 2: k_softmax_pt<ELEM, MODE, 2><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s); break;
-    case 4: k_softmax_pt<ELEM, MODE, 4><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s); break;
-    case 8: k_softmax_pt<ELEM, MODE, 8><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s); break;
-    case 16: k_softmax_pt<ELEM, MODE, 16><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s); break;
-    default: k_softmax_pt<ELEM, MODE, 32><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s); break;
+    case 1: k_softmax_pt<ELEM, MODE, 1><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    case 2: k_softmax_pt<ELEM, MODE, 2><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    case 4: k_softmax_pt<ELEM, MODE, 4><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    case 8: k_softmax_pt<ELEM, MODE, 8><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    case 16: k_softmax_pt<ELEM, MODE, 16><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    default: k_softmax_pt<ELEM, MODE, 32><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
   }
 }
 
 }  // namespace
 
 extern "C" int mxq_softmax_quantize_t(const float* S, int64_t R, int64_t T, float* PT_P, float* PT_X,
-                                      const mxq_block_spec* spec, mxq_stream_t stream) {
+                                      const mxq_block_spec* spec, uint8_t* stage_live, int64_t cols,
+                                      mxq_stream_t stream) {
   if (!spec) return mxq::invalid("mxq_softmax_quantize_t: spec is NULL");
   if (R < 0 || T <= 32 || T > 2048) return mxq::invalid("mxq_softmax_quantize_t: needs 32 < T <= 2048 keys");
   if (spec->elem != MXQ_ELEM_OCP || spec->e < 2 || spec->e > 5 || spec->m < 1 || spec->m > 3 || spec->rounding < 0 ||
       spec->rounding > 2 || spec->scale_rule != MXQ_SCALE_MXQUANT || spec->via_e < 0 || spec->via_e > 8)
     return mxq::invalid("mxq_softmax_quantize_t: the spec must be MX-Gemmini's");
+  if (stage_live && (cols < 32 || cols % 32 || R % cols))
+    return mxq::invalid("mxq_softmax_quantize_t: stage_live needs cols a multiple of 32 dividing R");
   if (R == 0) return MXQ_OK;
   if (!S || !PT_P || !PT_X) return mxq::invalid("mxq_softmax_quantize_t: NULL pointer");
   int it = 1;
@@ -131,9 +153,9 @@ extern "C" int mxq_softmax_quantize_t(const float* S, int64_t R, int64_t T, floa
   const dim3 grid((unsigned)mxq::ceil_div(R, RB));
   hipStream_t st = mxq::as_stream(stream);
   switch (spec->rounding) {
-    case MXQ_RNE: launch_it<MXQ_ELEM_OCP, MXQ_RNE>(it, grid, st, S, R, (int)T, PT_P, PT_X, *spec); break;
-    case MXQ_TIES_AWAY: launch_it<MXQ_ELEM_OCP, MXQ_TIES_AWAY>(it, grid, st, S, R, (int)T, PT_P, PT_X, *spec); break;
-    default: launch_it<MXQ_ELEM_OCP, MXQ_TRUNC>(it, grid, st, S, R, (int)T, PT_P, PT_X, *spec); break;
+    case MXQ_RNE: launch_it<MXQ_ELEM_OCP, MXQ_RNE>(it, grid, st, S, R, (int)T, PT_P, PT_X, *spec, stage_live, cols); break;
+    case MXQ_TIES_AWAY: launch_it<MXQ_ELEM_OCP, MXQ_TIES_AWAY>(it, grid, st, S, R, (int)T, PT_P, PT_X, *spec, stage_live, cols); break;
+    default: launch_it<MXQ_ELEM_OCP, MXQ_TRUNC>(it, grid, st, S, R, (int)T, PT_P, PT_X, *spec, stage_live, cols); break;
   }
   return mxq::check_launch("mxq_softmax_quantize_t");
 }

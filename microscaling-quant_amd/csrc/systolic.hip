@@ -79,6 +79,7 @@ struct SysArgs {
   // of that stage may not be skipped (k_suffix_flags)
   const uint8_t* suf_a;
   const uint8_t* suf_b;
+  const uint8_t* a_live;      // the caller's suffix bytes of A (mxq_systolic_hints), NULL when absent
   int64_t stages;
   int epi_on;                 // apply `epi` to every output as it is stored
   mxq_systolic_epilogue epi;
@@ -248,13 +249,14 @@ __device__ __forceinline__ int64_t tile_kstop(const SysArgs& a, int64_t z, int64
 // those rows is finite; of B where codes and those scales are finite (0 * Inf would have made a NaN).  A byte
 // per answer, 1 = may not.  A's groups are checked only at stages at or past their kstop (no tile reads the
 // others).  One workgroup per stage and 256 columns (the first x blocks A's, the rest B's): a lane reads 4
-// adjacent columns of 8 rows, so each row is read as one 1 KB piece.
+// adjacent columns of 8 rows, so each row is read as one 1 KB piece.  With the caller's bytes for A
+// (a.a_live), the launch has B's workgroups only.
 constexpr int kSufCols = 256;
 __global__ void __launch_bounds__(256) k_suffix_flags(const SysArgs a, int64_t ga, int64_t gb, uint8_t* fa,
                                                       uint8_t* fb) {
   __shared__ uint32_t bad_g[kSufCols / 32];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t s = blockIdx.y, z = blockIdx.z, xa = (a.M + kSufCols - 1) / kSufCols;
+  const int64_t s = blockIdx.y, z = blockIdx.z, xa = a.a_live ? 0 : (a.M + kSufCols - 1) / kSufCols;
   const bool is_a = (int64_t)blockIdx.x < xa;
   const int64_t c0 = (is_a ? (int64_t)blockIdx.x : (int64_t)blockIdx.x - xa) * kSufCols;
   if (threadIdx.x < kSufCols / 32) bad_g[threadIdx.x] = 0u;
@@ -1013,9 +1015,9 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
         uint8_t* fa = reinterpret_cast<uint8_t*>(a.flags + 2 * W);
         uint8_t* fb = fa + count * stages * ga;
         a.stages = stages;
-        const int64_t blocks = mxq::ceil_div(a.M, kSufCols) + mxq::ceil_div(a.N, kSufCols);
+        const int64_t blocks = (a.a_live ? 0 : mxq::ceil_div(a.M, kSufCols)) + mxq::ceil_div(a.N, kSufCols);
         k_suffix_flags<<<dim3((unsigned)blocks, (unsigned)stages, (unsigned)count), 256, 0, st>>>(a, ga, gb, fa, fb);
-        a.suf_a = fa;
+        a.suf_a = a.a_live ? a.a_live : fa;
         a.suf_b = fb;
       } else {
         a.k_end = nullptr;   // the hint is dropped: every reduction runs to K
@@ -1104,6 +1106,7 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
     a.skip_cols = mxq::ceil_div(N, 32);
     a.k_end = hints->k_end;
     a.kend_groups = mxq::ceil_div(M, 64);
+    a.a_live = hints->k_end ? hints->a_live : nullptr;
   }
   if (epilogue) {
     a.epi_on = 1;

@@ -39,8 +39,9 @@ class ArithSpec(ctypes.Structure):
 
 
 class SystolicHints(ctypes.Structure):
-    """include/mxq_hip.h mxq_systolic_hints: device pointers (0 for none) to the skip map and the k_end bounds."""
-    _fields_ = [("skip", c_ptr), ("k_end", c_ptr)]
+    """include/mxq_hip.h mxq_systolic_hints: device pointers (0 for none) to the skip map, the k_end bounds and
+    the caller's suffix bytes of A."""
+    _fields_ = [("skip", c_ptr), ("k_end", c_ptr), ("a_live", c_ptr)]
 
 
 class SystolicEpilogue(ctypes.Structure):
@@ -107,7 +108,8 @@ SIGNATURES = {
     "mxq_lut_pick": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr]),
     "mxq_block_lut": (c_i32, [c_ptr, c_i32, c_i64, c_i64, ctypes.POINTER(BlockSpec), c_i32, c_i32, c_ptr, c_i32,
                               c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr]),
-    "mxq_softmax_quantize_t": (c_i32, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, ctypes.POINTER(BlockSpec), c_ptr]),
+    "mxq_softmax_quantize_t": (c_i32, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, ctypes.POINTER(BlockSpec), c_ptr, c_i64,
+                                       c_ptr]),
     "mxq_block_lut_workspace": (c_i32, [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, ctypes.POINTER(c_i64)]),
     "mxq_lut_lookup": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr]),
     "mxq_lut_finder": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_i64, c_ptr, c_ptr]),

@@ -73,14 +73,17 @@ def workspace_elements(K: int, M: int, N: int, count: int) -> int:
 def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: int, N: int, C: torch.Tensor,
                      arith: Arithmetic, schedule: Sequence[Tuple[int, int]], size: int = 16,
                      block_size: int = BLOCK, *, skip: Optional[torch.Tensor] = None,
-                     k_end: Optional[torch.Tensor] = None, epilogue: Optional["_lib.SystolicEpilogue"] = None) -> None:
+                     k_end: Optional[torch.Tensor] = None, a_live: Optional[torch.Tensor] = None,
+                     epilogue: Optional["_lib.SystolicEpilogue"] = None) -> None:
     """`count` problems of one shape in one launch, written into C (mxq_systolic_batched).  ops: the four
     device tensors the layout's strides address (codes A, scales X_A, codes B, scales X_B), float32 on C's
     device.  Each problem's result equals systolic() on that problem alone.  The Arithmetic must carry a
     kernel description (MXGEMMINI, MXQUANT, compiled).
     Hints (include/mxq_hip.h mxq_systolic_hints): `skip`, uint8 count x ceil(M/32) x ceil(N/32), nonzero where
     the caller does not need C's 32 x 32 group (such tiles come back +0); `k_end`, int32 count x ceil(M/64), a
-    bound on the rows of A holding nonzero codes in each 64-column group (checked: a wrong one costs time).
+    bound on the rows of A holding nonzero codes in each 64-column group (checked: a wrong one costs time);
+    `a_live`, with k_end, uint8 count x ceil(K/32) x ceil(M/32), the caller's answer to that check for A (nonzero
+    unless the 32 x 32 piece of A is +-0 with finite scales; trusted, so it must be exact).
     `epilogue` (mxq_systolic_epilogue): R(R(C * scale) + mask value) applied to every output as it is stored."""
     import ctypes
     kernel = getattr(arith, "kernel", None)
@@ -97,10 +100,11 @@ def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: 
     le = (ctypes.c_int32 * size)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
     for t, dt, shape in ((skip, torch.uint8, (count, -(-M // 32), -(-N // 32))),
-                         (k_end, torch.int32, (count, -(-M // 64)))):
+                         (k_end, torch.int32, (count, -(-M // 64))),
+                         (a_live, torch.uint8, (count, -(-K // 32), -(-M // 32)))):
         if t is not None and (t.dtype != dt or tuple(t.shape) != shape or t.device != dev or not t.is_contiguous()):
             raise ValueError(f"systolic_batched: a hint must be a contiguous {dt} tensor of shape {shape} on {dev}")
-    hints = _lib.SystolicHints(skip=_lib.ptr(skip), k_end=_lib.ptr(k_end))
+    hints = _lib.SystolicHints(skip=_lib.ptr(skip), k_end=_lib.ptr(k_end), a_live=_lib.ptr(a_live))
     work = torch.empty(workspace_elements(K, M, N, count), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_systolic_batched", *(_lib.ptr(t) for t in ops), _lib.ptr(C), ctypes.byref(layout), count,

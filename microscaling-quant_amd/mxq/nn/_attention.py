@@ -393,18 +393,20 @@ class _Batched:
                          Zc, D, cols, Tk, S, arith, sched, size, qk.block_size, skip=skip, epilogue=epi)
         # every call's P^T side by side: softmax and the quantizer in one kernel where they are torch's persistent
         # softmax and an MX-Gemmini quantizer; else P, quantized as it lies (a transposed view: no copy)
-        PT = _softmax_pt(S, pv.a, pv.block_size, vector)
+        PT = _softmax_pt(S, pv.a, pv.block_size, vector, cols if k_end is not None and cols % 32 == 0 else None)
+        a_live = None
         if PT is None:
             P = softmax(S, vector)
-            PT = pv.a(P.contiguous().view(Zc * cols, Tk).t())
-        PT_P, PT_X = PT
+            PT_P, PT_X = pv.a(P.contiguous().view(Zc * cols, Tk).t())
+        else:
+            PT_P, PT_X, a_live = PT
         arith, sched, size = self.pv_red
         O = torch.empty(Zc, cols, D, dtype=torch.float32, device=qg.device)
         systolic_batched((PT_P, PT_X, V_P[z0:], V_X[z0:]),
                          _lib.SystolicLayout(ld_a=Zc * cols, batch_a=cols, ld_xa=Zc * cols, batch_xa=cols,
                                              ld_b=D, batch_b=Tk * D, ld_xb=D, batch_xb=V_X.shape[1] * D,
                                              ld_c=D, batch_c=cols * D),
-                         Zc, Tk, cols, D, O, arith, sched, size, pv.block_size, k_end=k_end)
+                         Zc, Tk, cols, D, O, arith, sched, size, pv.block_size, k_end=k_end, a_live=a_live)
         O = O.view(Zc, n, m, D)
         for b in range(z0 // Hkv, (z1 - 1) // Hkv + 1):                          # pairs into B x Tq x H x D
             h0, h1 = max(z0, b * Hkv) - b * Hkv, min(z1, (b + 1) * Hkv) - b * Hkv
@@ -423,11 +425,12 @@ class _Batched:
                       s0, e0, out[b])
 
 
-def _softmax_pt(S: torch.Tensor, quantizer, block_size: int, vector: Optional[str]):
-    """(P^T codes, scales) of softmax(S) over its last dim through `quantizer` (mxq/nn/_attention.py:136-139),
-    as one kernel (mxq_softmax_quantize_t): for float32 rows of 32 < T <= 2048 keys, where torch.softmax runs its
-    persistent softmax, which the kernel reproduces bit for bit, and an MX-Gemmini quantizer of blocks of 32 along
-    the keys.  None where that does not hold."""
+def _softmax_pt(S: torch.Tensor, quantizer, block_size: int, vector: Optional[str], live_cols: Optional[int] = None):
+    """(P^T codes, scales, stage bytes) of softmax(S) over its last dim through `quantizer`
+    (mxq/nn/_attention.py:136-139), as one kernel (mxq_softmax_quantize_t): for float32 rows of 32 < T <= 2048
+    keys, where torch.softmax runs its persistent softmax, which the kernel reproduces bit for bit, and an
+    MX-Gemmini quantizer of blocks of 32 along the keys.  With live_cols (P^T's columns per problem), the third
+    item is the P V product's a_live hint for these codes, else None.  None where the kernel does not apply."""
     from .. import _lib
     from ..block import mxgemmini
     from ..element_quant.formats import get
@@ -446,10 +449,13 @@ def _softmax_pt(S: torch.Tensor, quantizer, block_size: int, vector: Optional[st
     R = Sc.numel() // T
     PT_P = torch.empty((T, R), dtype=torch.float32, device=S.device)
     PT_X = torch.empty((-(-T // 32), R), dtype=torch.float32, device=S.device)
+    live = None
+    if live_cols is not None:
+        live = torch.empty((R // live_cols, -(-T // 32), live_cols // 32), dtype=torch.uint8, device=S.device)
     with torch.cuda.device(S.device):
-        _lib.run("mxq_softmax_quantize_t", _lib.ptr(Sc), R, T, _lib.ptr(PT_P), _lib.ptr(PT_X), spec,
-                 _lib.stream(S.device))
-    return PT_P, PT_X
+        _lib.run("mxq_softmax_quantize_t", _lib.ptr(Sc), R, T, _lib.ptr(PT_P), _lib.ptr(PT_X), spec, _lib.ptr(live),
+                 live_cols or 0, _lib.stream(S.device))
+    return PT_P, PT_X, live
 
 
 def _launch_ranges(B: int, Hkv: int, per_launch: int):

@@ -379,3 +379,16 @@ def test_softmax_quantize_t_against_torch(cuda, T):
         want = q(torch.softmax(S, dim=-1).contiguous().t())
         assert_bits_equal(got[1].cpu().numpy(), want[1].cpu().numpy(), f"scales T={T} {fmt} {mode}")
         assert_bits_equal(got[0].cpu().numpy(), want[0].cpu().numpy(), f"codes T={T} {fmt} {mode}")
+        assert got[2] is None
+    # the stage bytes the P V product reads instead of a pass over P^T: per problem (96 columns each), 32 keys and
+    # 32 columns, whether any code is nonzero or any scale not finite
+    S2 = S[:288].contiguous()
+    q = partial(block.mxgemmini.quantize, fmt="MXFP8_E4M3", axis=0, rounding_mode="ties_away")
+    P, X, live = _attention._softmax_pt(S2, q, 32, None, 96)
+    want = q(torch.softmax(S2, dim=-1).contiguous().t())
+    assert_bits_equal(P.cpu().numpy(), want[0].cpu().numpy(), f"codes T={T} with stage bytes")
+    nb = -(-T // 32)
+    Pn = np.pad(P.cpu().numpy(), ((0, nb * 32 - T), (0, 0)))
+    nz = (Pn.reshape(nb, 32, 3, 3, 32) != 0).any(axis=(1, 4))                   # stage, problem, group
+    bad = ~np.isfinite(X.cpu().numpy()).reshape(nb, 3, 3, 32).all(axis=3)
+    assert np.array_equal(live.cpu().numpy(), (nz | bad).transpose(1, 0, 2).astype(np.uint8))
