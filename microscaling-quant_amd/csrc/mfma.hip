@@ -17,7 +17,8 @@
 //               type cannot hold exactly, or a scale that is not a power of two in [2^-127, 2^127] over a block
 //               with a nonzero code, sets the error word.
 //   k_mx_mfma   32 x 32 tiles of C, 64 K per instruction, lane layout as above (established on the device with
-//               exact integer data); lane l's 16 results are C[8(i/4) + 4h + i%4][l % 32], i = 0..15.
+//               exact integer data); lane l's 16 results are C[8(i/4) + 4h + i%4][l % 32], i = 0..15.  Each
+//               output is the sum, in a fixed order, of four float32 chains over every fourth K step.
 #include "mxq_common.h"
 #include "mxq_numerics.h"
 
@@ -143,19 +144,20 @@ __global__ void __launch_bounds__(256) k_mx_pack(const float* __restrict__ P, co
   if (bad) atomicOr(err, 1);
 }
 
-// One wave per (32 TA) x 64 block of C (TA x 2 instructions per K step, so each B load feeds TA of them and
-// each A load two); four waves per workgroup in a 2 x 2 arrangement ((64 TA) x 128).  TA = 2 where that still
-// gives the chip 1024 waves, else TA = 1: on C2's 512 x 4096 the 64 x 64 blocks leave half the SIMDs idle.
-// Tiles past the packed operand (M or N not reaching this wave's last tile) re-read the last tile: valid
-// bytes whose results are never stored.  Operands are loaded kDepth K steps ahead of the instructions that
-// use them.  A block's K order is the same for either TA, so the results are too.
-template <int TA>
-struct MxStep {
-  v8i a[TA], b[2];
-  int sa[TA], sb[2];
+// The product.  A workgroup of four waves owns a (32 TM) x (32 TN) block of C (TM x TN instruction tiles) and
+// splits K four ways: wave w runs K steps w, w + 4, w + 8, ... over the whole block, TM x TN instructions per
+// step, so every operand byte is loaded once per workgroup and feeds TN (A) or TM (B) instructions.  No wave
+// shares operands with another, so they go from global memory straight to the wave's registers (one
+// contiguous 64 BPL-byte chunk per 32-column tile and step), kDepth own steps ahead of the instructions.  At
+// the end the four partial blocks meet in LDS and each output is ((p0 + p1) + p2) + p3, p_w the float32 chain
+// of wave w's steps in K order.  The K split and the order of the sums do not depend on TM or TN, so neither do
+// the results.  Tiles past the packed operand (M or N not reaching the block's last tile) re-read its last
+// tile: valid bytes whose results are never stored.
+template <int TM, int TN>
+struct MxRegs {
+  v8i a[TM], b[TN];
+  int sa[TM], sb[TN];
 };
-
-constexpr int kDepth = 4;
 
 // (tile, step) chunk c: this lane's BPL bytes of codes (the unused high registers of the operand are zero)
 template <int BPL>
@@ -176,93 +178,140 @@ __device__ __forceinline__ v8i load_codes(const uint8_t* codes, int64_t chunk, i
   }
 }
 
-template <int TA, int BA, int BB>
-__device__ __forceinline__ void load_step(MxStep<TA>& st, const uint8_t* A, const uint8_t* SA, const uint8_t* B,
-                                          const uint8_t* SB, const int64_t (&ta)[TA], const int64_t (&tb)[2],
-                                          int64_t nk, int64_t s, int lane) {
+// Own steps in flight per wave: four when their operands take at most 200 VGPRs, else three (the TM TN
+// accumulators live in the 256 AGPRs).
+template <int BA, int BB, int TM, int TN>
+struct MxDepth {
+  static constexpr int kRegs = (TM * BA + TN * BB) / 4 + TM + TN;     // operand VGPRs of one step
+  static constexpr int kDepth = kRegs * 4 <= 200 ? 4 : 3;
+  static constexpr int kPhase = TM * TN <= 8 ? TM * TN : 8;          // tiles per wave and reduction phase
+  static constexpr int kReduce = 4 * kPhase * 16 * 64 * 4;           // the four waves' partial tiles, bytes
+  static_assert((TM * TN) % kPhase == 0 && kPhase % 4 == 0, "reduction phases");
+};
+
+template <int KA, int KB, int TM, int TN>
+__device__ __forceinline__ void mfma_step(v16f (&acc)[TM][TN], const MxRegs<TM, TN>& g) {
 #pragma unroll
-  for (int t = 0; t < TA; ++t) {
-    st.a[t] = load_codes<BA>(A, ta[t] * nk + s, lane);
-    st.sa[t] = SA[(ta[t] * nk + s) * 64 + lane];
-  }
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    st.b[t] = load_codes<BB>(B, tb[t] * nk + s, lane);
-    st.sb[t] = SB[(tb[t] * nk + s) * 64 + lane];
-  }
+    for (int j = 0; j < TN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(g.a[i], g.b[j], acc[i][j], KA, KB, 0, g.sa[i], 0,
+                                                                  g.sb[j]);
 }
 
-template <int KA, int KB, int TA>
-__global__ void __launch_bounds__(256) k_mx_mfma(const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA,
-                                                 const uint8_t* __restrict__ B, const uint8_t* __restrict__ SB,
-                                                 float* __restrict__ C, int64_t K64, int64_t M, int64_t N) {
+template <int KA, int KB, int TM, int TN>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+k_mx_mfma(const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA, const uint8_t* __restrict__ B,
+          const uint8_t* __restrict__ SB, float* __restrict__ C, int64_t K64, int64_t M, int64_t N) {
+  // (the reduction's LDS leaves one workgroup per CU, so one wave per SIMD: every register is the wave's)
   constexpr int BA = lane_bytes(KA), BB = lane_bytes(KB);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r = lane & 31, h = lane >> 5;
-  const int64_t m0 = (int64_t)blockIdx.y * (64 * TA) + (wave >> 1) * (32 * TA);
-  const int64_t n0 = (int64_t)blockIdx.x * 128 + (wave & 1) * 64;
+  using D = MxDepth<BA, BB, TM, TN>;
+  constexpr int kDepth = D::kDepth;
+  __shared__ __align__(16) float red[D::kReduce / 4];
+  // the wave index as a scalar, so the own-step count and its branches are the wave's, not per lane
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t nk = K64 / 64, tiles_m = (M + 31) / 32, tiles_n = (N + 31) / 32;
-  int64_t ta[TA], tb[2];
+  const int64_t m0 = (int64_t)blockIdx.y * (32 * TM), n0 = (int64_t)blockIdx.x * (32 * TN);
+  int64_t ta[TM], tb[TN];
 #pragma unroll
-  for (int t = 0; t < TA; ++t) ta[t] = min(m0 / 32 + t, tiles_m - 1);
+  for (int i = 0; i < TM; ++i) ta[i] = min(m0 / 32 + i, tiles_m - 1) * nk;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) tb[t] = min(n0 / 32 + t, tiles_n - 1);
-  v16f acc[TA][2] = {};
-  // kDepth K steps in flight: step s of each round issues its instructions, then refills its slot with the
-  // step kDepth ahead (past the end it re-reads the last step, whose values are never used).
-  MxStep<TA> slot[kDepth];
+  for (int j = 0; j < TN; ++j) tb[j] = min(n0 / 32 + j, tiles_n - 1) * nk;
+  // own step j is K step 4 j + wave; loads past the last K step re-read it (never used)
+  auto load = [&](MxRegs<TM, TN>& g, int64_t j) {
+    int64_t s = 4 * j + wave;
+    s = s < nk ? s : nk - 1;
 #pragma unroll
-  for (int s = 0; s < kDepth; ++s)
-    load_step<TA, BA, BB>(slot[s], A, SA, B, SB, ta, tb, nk, min((int64_t)s, nk - 1), lane);
-  for (int64_t k = 0; k < nk; k += kDepth) {
+    for (int i = 0; i < TM; ++i) {
+      g.a[i] = load_codes<BA>(A, ta[i] + s, lane);
+      g.sa[i] = SA[(ta[i] + s) * 64 + lane];
+    }
 #pragma unroll
-    for (int s = 0; s < kDepth; ++s) {
-      if (k + s < nk) {
+    for (int j = 0; j < TN; ++j) {
+      g.b[j] = load_codes<BB>(B, tb[j] + s, lane);
+      g.sb[j] = SB[(tb[j] + s) * 64 + lane];
+    }
+  };
+  const int64_t own = nk > wave ? (nk - wave + 3) / 4 : 0;
+  v16f acc[TM][TN] = {};
+  MxRegs<TM, TN> slot[kDepth];
 #pragma unroll
-        for (int i = 0; i < TA; ++i)
+  for (int d = 0; d < kDepth; ++d) load(slot[d], d);
+  int64_t j = 0;
+  for (; j + kDepth <= own; j += kDepth) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(slot[s].a[i], slot[s].b[j], acc[i][j], KA, KB,
-                                                                        0, slot[s].sa[i], 0, slot[s].sb[j]);
-      }
-      load_step<TA, BA, BB>(slot[s], A, SA, B, SB, ta, tb, nk, min(k + s + kDepth, nk - 1), lane);
+    for (int d = 0; d < kDepth; ++d) {
+      mfma_step<KA, KB>(acc, slot[d]);
+      load(slot[d], j + d + kDepth);
     }
   }
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t n = n0 + 32 * j + r;
-    if (n >= N) continue;
+  for (int d = 0; d < kDepth - 1; ++d)   // the last own - j < kDepth steps
+    if (j + d < own) mfma_step<KA, KB>(acc, slot[d]);
+  // the partial blocks meet in LDS kPhase tiles at a time: wave w's tile t (of the phase), elements
+  // [4 e, 4 e + 4) of every lane, 16 bytes at ((w kPhase + t) 4 + e) 256 + 4 l floats; then wave v sums and
+  // stores the phase's tiles v, v + 4, ...: lane l = 32 h + r, element 4 e + k of tile (i, jj) is
+  // C[m0 + 32 i + 8 e + 4 h + k][n0 + 32 jj + r]
+  constexpr int P = D::kPhase;
+  const int r = lane & 31, h = lane >> 5;
 #pragma unroll
-    for (int i = 0; i < TA; ++i)
+  for (int ph = 0; ph < TM * TN / P; ++ph) {
+    if (ph > 0) __syncthreads();   // the previous phase's sums have read their tiles
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t m = m0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
-        if (m < M) C[m * N + n] = acc[i][j][e];
+    for (int t = 0; t < P; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = (ph * P + t) / TN, jj = (ph * P + t) % TN;
+        *reinterpret_cast<float4*>(red + (((wave * P + t) * 4 + e) * 64 + lane) * 4) =
+            make_float4(acc[i][jj][4 * e], acc[i][jj][4 * e + 1], acc[i][jj][4 * e + 2], acc[i][jj][4 * e + 3]);
       }
+    __syncthreads();
+#pragma unroll
+    for (int t = wave; t < P; t += 4) {
+      const int i = (ph * P + t) / TN, jj = (ph * P + t) % TN;
+      const int64_t n = n0 + 32 * jj + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float4 v = *reinterpret_cast<const float4*>(red + ((t * 4 + e) * 64 + lane) * 4);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+          const float4 u = *reinterpret_cast<const float4*>(red + (((w * P + t) * 4 + e) * 64 + lane) * 4);
+          v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+        }
+        const int64_t m = m0 + 32 * i + 8 * e + 4 * h;
+        if (n < N) {
+          if (m < M) C[m * N + n] = v.x;
+          if (m + 1 < M) C[(m + 1) * N + n] = v.y;
+          if (m + 2 < M) C[(m + 2) * N + n] = v.z;
+          if (m + 3 < M) C[(m + 3) * N + n] = v.w;
+        }
+      }
+    }
   }
 }
 
-template <int TA, int KA>
+template <int TM, int TN, int KA>
 void launch_mfma_b(int b_kind, dim3 grid, hipStream_t st, const uint8_t* A, const uint8_t* SA, const uint8_t* B,
                    const uint8_t* SB, float* C, int64_t K64, int64_t M, int64_t N) {
   switch (b_kind) {
-    case kE4M3: k_mx_mfma<KA, kE4M3, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
-    case kE5M2: k_mx_mfma<KA, kE5M2, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
-    case kE2M3: k_mx_mfma<KA, kE2M3, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
-    case kE3M2: k_mx_mfma<KA, kE3M2, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
-    default: k_mx_mfma<KA, kE2M1, TA><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+    case kE4M3: k_mx_mfma<KA, kE4M3, TM, TN><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+    case kE5M2: k_mx_mfma<KA, kE5M2, TM, TN><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+    case kE2M3: k_mx_mfma<KA, kE2M3, TM, TN><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+    case kE3M2: k_mx_mfma<KA, kE3M2, TM, TN><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
+    default: k_mx_mfma<KA, kE2M1, TM, TN><<<grid, 256, 0, st>>>(A, SA, B, SB, C, K64, M, N); break;
   }
 }
 
-template <int TA>
-void launch_mfma(int a_kind, int b_kind, dim3 grid, hipStream_t st, const uint8_t* A, const uint8_t* SA,
-                 const uint8_t* B, const uint8_t* SB, float* C, int64_t K64, int64_t M, int64_t N) {
+template <int TM, int TN>
+void launch_mfma(int a_kind, int b_kind, hipStream_t st, const uint8_t* A, const uint8_t* SA, const uint8_t* B,
+                 const uint8_t* SB, float* C, int64_t K64, int64_t M, int64_t N) {
+  const dim3 grid((unsigned)mxq::ceil_div(N, 32 * TN), (unsigned)mxq::ceil_div(M, 32 * TM));
   switch (a_kind) {
-    case kE4M3: launch_mfma_b<TA, kE4M3>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
-    case kE5M2: launch_mfma_b<TA, kE5M2>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
-    case kE2M3: launch_mfma_b<TA, kE2M3>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
-    case kE3M2: launch_mfma_b<TA, kE3M2>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
-    default: launch_mfma_b<TA, kE2M1>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+    case kE4M3: launch_mfma_b<TM, TN, kE4M3>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+    case kE5M2: launch_mfma_b<TM, TN, kE5M2>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+    case kE2M3: launch_mfma_b<TM, TN, kE2M3>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+    case kE3M2: launch_mfma_b<TM, TN, kE3M2>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
+    default: launch_mfma_b<TM, TN, kE2M1>(b_kind, grid, st, A, SA, B, SB, C, K64, M, N); break;
   }
 }
 
@@ -295,13 +344,14 @@ extern "C" int mxq_mx_mfma(const uint8_t* A, const uint8_t* SA, int32_t a_kind, 
   if (!A || !SA || !B || !SB || !C) return mxq::invalid("mxq_mx_mfma: NULL pointer");
   if (reinterpret_cast<uintptr_t>(A) % 16 || reinterpret_cast<uintptr_t>(B) % 16)
     return mxq::invalid("mxq_mx_mfma: codes must be 16-byte aligned");
-  // 64 x 64 blocks per wave while they give at least 1024 waves, else 32 x 64
-  const bool two = mxq::ceil_div(N, 128) * mxq::ceil_div(M, 128) * 4 >= 1024;
-  if (mxq::ceil_div(M, two ? 128 : 64) > 65535) return mxq::invalid("mxq_mx_mfma: M too large");
-  const dim3 grid((unsigned)mxq::ceil_div(N, 128), (unsigned)mxq::ceil_div(M, two ? 128 : 64));
+  // the largest block of 128 x 128, 64 x 128 or 64 x 64 outputs that still gives every CU a workgroup (an
+  // operand byte feeds as many instructions as the block is wide or tall)
+  const int64_t b44 = mxq::ceil_div(M, 128) * mxq::ceil_div(N, 128), b24 = mxq::ceil_div(M, 64) * mxq::ceil_div(N, 128);
+  if (mxq::ceil_div(M, 64) > 65535) return mxq::invalid("mxq_mx_mfma: M too large");
   hipStream_t st = mxq::as_stream(stream);
   mxq::KernelTimer timer("mx_mfma", st);
-  if (two) launch_mfma<2>(a_kind, b_kind, grid, st, A, SA, B, SB, C, K64, M, N);
-  else launch_mfma<1>(a_kind, b_kind, grid, st, A, SA, B, SB, C, K64, M, N);
+  if (b44 >= 256) launch_mfma<4, 4>(a_kind, b_kind, st, A, SA, B, SB, C, K64, M, N);
+  else if (b24 >= 256) launch_mfma<2, 4>(a_kind, b_kind, st, A, SA, B, SB, C, K64, M, N);
+  else launch_mfma<2, 2>(a_kind, b_kind, st, A, SA, B, SB, C, K64, M, N);
   return mxq::check_launch("mxq_mx_mfma");
 }

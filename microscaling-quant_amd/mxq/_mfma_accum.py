@@ -11,7 +11,10 @@ the 64 products of one instruction are summed in groups of 8 consecutive k; with
 truncated toward zero to a multiple of 2^(E_g - 13), where E_g is the group's largest exponent sum
 e(a_k) + e(b_k) (e = the exponent field's value, a subnormal counting as its type's smallest normal exponent,
 plus the block scale's exponent); the group sums are then combined and added into the float32 accumulator
-with about float32 precision.  The stated tolerance follows:
+with about float32 precision.  The kernel keeps four float32 accumulators per output, over every fourth
+64-deep K step (steps 0, 4, 8, ...; 1, 5, 9, ...; ...), and adds them in that order at the end, whatever the
+shape, so a slice of M or N gives the same bits; the three extra additions fit in the last term below, which
+allows 2^-22 per step against the 2^-24 a float32 addition rounds by.  The stated tolerance follows:
 
     |Y - exact| <= sum over groups g of 7 * 2^(E_g - 13)
                    + sum over instructions i of 8 * 2^(E_i - 23) + ceil(K/64) * 2^-23 * sum_k |a_k b_k|

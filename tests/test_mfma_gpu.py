@@ -272,19 +272,25 @@ def test_rejects(cuda):
         mxq.mfma_accum(ones, X, ones, X, "FP32")
 
 
-def test_wave_block_shapes_agree(cuda):
-    """2048 x 2048 outputs run on 64 x 64 blocks per wave, 128-column slices of them on 32 x 64 blocks (too few
-    larger ones to fill the chip): every output identical, each keeping its K order."""
+@pytest.mark.parametrize("fmt", ["MXFP8_E4M3", "MXFP4"])
+def test_wave_block_shapes_agree(cuda, fmt):
+    """2048 x 2048 outputs run on 128 x 128 workgroup blocks, their 1024-row halves on 64 x 128 blocks and
+    128-column slices on 64 x 64 blocks (too few larger ones to fill the chip): every output identical, since
+    the four-way K split (K = 320: five steps, so the waves' chains differ in length) and the order of the
+    partial sums do not depend on the block."""
     from mxq import _mfma_accum as mfa
     rng = np.random.default_rng(12)
-    K, M, N = 128, 2048, 2048
-    PA, XA = ob.mxgemmini_quantize(rng.standard_normal((K, M)).astype(np.float32), "MXFP8_E4M3", 0)
-    PB, XB = ob.mxgemmini_quantize(rng.standard_normal((K, N)).astype(np.float32), "MXFP8_E4M3", 0)
+    K, M, N = 320, 2048, 2048
+    PA, XA = ob.mxgemmini_quantize(rng.standard_normal((K, M)).astype(np.float32), fmt, 0)
+    PB, XB = ob.mxgemmini_quantize(rng.standard_normal((K, N)).astype(np.float32), fmt, 0)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()          # noqa: E731
-    whole = mfa.mfma_accum(t(PA), t(XA), t(PB), t(XB), "MXFP8_E4M3").cpu().numpy()
+    whole = mfa.mfma_accum(t(PA), t(XA), t(PB), t(XB), fmt).cpu().numpy()
     for c in (0, 1024, 1920):
-        part = mfa.mfma_accum(t(PA), t(XA), t(PB[:, c:c + 128]), t(XB[:, c:c + 128]), "MXFP8_E4M3").cpu().numpy()
+        part = mfa.mfma_accum(t(PA), t(XA), t(PB[:, c:c + 128]), t(XB[:, c:c + 128]), fmt).cpu().numpy()
         assert np.array_equal(part.view(np.uint32), whole[:, c:c + 128].view(np.uint32)), c
+    for r in (0, 1024):
+        part = mfa.mfma_accum(t(PA[:, r:r + 1024]), t(XA[:, r:r + 1024]), t(PB), t(XB), fmt).cpu().numpy()
+        assert np.array_equal(part.view(np.uint32), whole[r:r + 1024].view(np.uint32)), r
 
 
 @pytest.mark.parametrize("K, M, N", [(4096, 96, 160), (1000, 33, 70)])
