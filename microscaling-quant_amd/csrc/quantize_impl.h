@@ -364,21 +364,24 @@ __global__ void __launch_bounds__(256) k_quant_strided(const T* __restrict__ V, 
 //     instead of VEC).
 template <typename T, int ELEM, int MODE, int VEC, int R, typename SINK>
 __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, const SINK out, int64_t outer,
-                                                     int64_t n, int64_t inner, int64_t nb, int64_t waves_per_row,
-                                                     mxq_block_spec s) {
+                                                     int64_t n, int64_t inner, mxq::DivU31 nb_div,
+                                                     mxq::DivU31 wpr_div, mxq_block_spec s) {
   constexpr int CPW = 64 / R;          // column groups per wave
   constexpr int ROWS = 32 / R;         // rows per lane
   constexpr int PER = (VEC + R - 1) / R;  // scales each lane evaluates
   const int64_t groups = inner / VEC;
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * (256 / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (wave >= outer * nb * waves_per_row) return;    // whole waves only: the exchanges below see every lane
-  const int64_t wr = wave / waves_per_row;           // (o, b) flattened
-  const int64_t o = wr / nb, b = wr - o * nb;
+  const int64_t nb = nb_div.d, waves_per_row = wpr_div.d;
+  // the launch keeps the wave count below 2^31
+  const uint32_t wave = blockIdx.x * (256 / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if ((int64_t)wave >= outer * nb * waves_per_row) return;   // whole waves only: the exchanges below see every lane
+  const uint32_t wr = mxq::divu31(wave, wpr_div);      // (o, b) flattened
+  const uint32_t o32 = mxq::divu31(wr, nb_div);
+  const int64_t o = o32, b = wr - o32 * nb_div.d;
   const int64_t k0 = b * 32;
   const int rows = (int)((n - k0 < 32) ? n - k0 : 32);
   const int c = lane % CPW, r = lane / CPW;
-  const int64_t cg = (wave - wr * waves_per_row) * CPW + c;
+  const int64_t cg = (int64_t)(wave - wr * wpr_div.d) * CPW + c;
   const bool live = cg < groups;
   const T* src = V + (o * n + k0 + r * ROWS) * inner + (live ? cg : 0) * VEC;
 
@@ -492,9 +495,23 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, co
     if (hw) out.template hw_rows<ROWS, VEC>(dst, inner, v, rows == 32 ? ROWS : rows - r * ROWS, hs);
   }
   if (!hw) {
-#pragma unroll
+    // the element grid in software, one row at a time from a second read of the row (the same loads and the
+    // same scaling give the same values): the registers of this rare path are one row's, so the kernel's
+    // count is the conversions' path's and more waves fit on a SIMD
+#pragma unroll 1
     for (int i = 0; i < ROWS; ++i) {
-      if (rows == 32 || r * ROWS + i < rows) out.template elems<ELEM, MODE, VEC>(dst + (int64_t)i * inner, v[i], s);
+      if (rows == 32 || r * ROWS + i < rows) {
+        float z[VEC];
+        load_vec<T, VEC>(src + (int64_t)i * inner, z);
+        if (div) {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) z[j] = apply_div(z[j], d[j]);
+        } else if (s.scale_rule) {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) z[j] = z[j] * d[j].inv;
+        }
+        out.template elems<ELEM, MODE, VEC>(dst + (int64_t)i * inner, z, s);
+      }
     }
   }
   if (r == 0) {
@@ -687,16 +704,20 @@ int launch_quant(const T* V, const SINK& out, int64_t outer, int64_t n, int64_t 
       constexpr int R = decltype(r_const)::value;
       const int64_t wpr = mxq::ceil_div(inner / kvec, 64 / R);
       const dim3 grid = mxq::grid_for(outer * nb * wpr * 64, 256);
+      const mxq::DivU31 dnb = mxq::make_divu31((uint32_t)nb), dwpr = mxq::make_divu31((uint32_t)wpr);
       if constexpr (SINK::kBytes == 1) {
         if (bvec == 8) {
-          k_quant_split<T, ELEM, MODE, 8, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
+          k_quant_split<T, ELEM, MODE, 8, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, dnb, dwpr, q);
           return;
         }
       }
-      if (vec == 4) k_quant_split<T, ELEM, MODE, 4, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
-      else if (vec == 2) k_quant_split<T, ELEM, MODE, 2, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
-      else k_quant_split<T, ELEM, MODE, 1, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, nb, wpr, q);
+      if (vec == 4) k_quant_split<T, ELEM, MODE, 4, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, dnb, dwpr, q);
+      else if (vec == 2) k_quant_split<T, ELEM, MODE, 2, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, dnb, dwpr, q);
+      else k_quant_split<T, ELEM, MODE, 1, R, SINK><<<grid, 256, 0, st>>>(V, out, outer, n, inner, dnb, dwpr, q);
     };
+    // the kernel indexes waves in 32 bits
+    if (outer * nb * mxq::ceil_div(inner / kvec, 64 / 32) >= (int64_t(1) << 31))
+      return mxq::invalid("block quantize: tensor too large (2^31 waves of 2048 elements)");
     if (waves8 >= 8 * 1024) go(std::integral_constant<int, 8>{});
     else go(std::integral_constant<int, 32>{});
     return mxq::check_launch("mxq_block_quantize");
