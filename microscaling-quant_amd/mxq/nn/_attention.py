@@ -338,16 +338,27 @@ class _Batched:
         kv = (KT_P, KT_X, V_P, V_X)
         k_amax = _group_amax(KT_P, KT_X, qk.block_size, Z) if bias is not None else None
         qg = q.reshape(Z, n, dims.Tq, D)
-        # every chunk's operands, flags and hints first; the flags then come over in one transfer, before any
-        # matmul is queued, so the host queues the matmuls back to back and returns without waiting for them
+        # every chunk's operands, flags and hints first; the flags then come over in one transfer into pinned
+        # memory, queued ahead of the matmuls with an event behind it, so the host queues the matmuls while the
+        # GPU works, then waits for the copy alone and returns without waiting for the matmuls
         chunks = []
         for s0 in range(0, dims.Tq, step):
             e0 = min(s0 + step, dims.Tq)
             for z0, z1 in _launch_ranges(B, Hkv, max(1, ELEMENTS_PER_LAUNCH // (n * (e0 - s0) * Tk))):
                 chunks.append(self._prepare(qg, bias, kv, k_amax, scale, dims, z0, z1, s0, e0))
-        every = torch.cat([c.flags for c in chunks]).cpu().tolist() if bias is not None else []
+        if bias is not None:
+            flags = torch.cat([c.flags for c in chunks])
+            host = torch.empty(flags.shape, dtype=flags.dtype, pin_memory=True)
+            host.copy_(flags, non_blocking=True)
+            copied = torch.cuda.Event()
+            copied.record(torch.cuda.current_stream(flags.device))
         for c in chunks:
             self._chunk(c, qg, bias, kv, scale, vector, dims, out)
+        if bias is not None:
+            copied.synchronize()
+            every = host.tolist()
+        else:
+            every = []
         # a pair that would skip masked keys gets the reference's own call, on the same codes, over its outputs
         at = 0
         for c in chunks:
