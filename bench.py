@@ -704,7 +704,7 @@ def main():
     dev = torch.device("cuda", 0)
     if args.only in ("quantize", "lut", "attend", "llm"):
         fn = {"quantize": lambda: quantize_lines(torch, max(5, args.steps // 2), inp)[0],
-              "lut": lambda: lut_line(torch, 3, inp)[0], "attend": lambda: attend_line(torch, 3, inp)[0],
+              "lut": lambda: lut_line(torch, 3, inp)[0], "attend": lambda: attend_line(torch, 10, inp)[0],
               "llm": lambda: llm_line(torch, 2)}[args.only]
         print(json.dumps({"only": args.only, args.only: fn()}), flush=True)
         return
@@ -762,7 +762,7 @@ def main():
     if not args.no_extra:
         line["quantize"], extra["quantize"] = quantize_lines(torch, max(5, args.steps // 2), inp)
         line["lut_c4"], extra["lut"] = lut_line(torch, 3, inp)
-        line["attend_c5"], extra["attend"] = attend_line(torch, 3, inp)
+        line["attend_c5"], extra["attend"] = attend_line(torch, 10, inp)
         line["mfma_c2"] = mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B, inp)
         line["trees_c2"] = trees_line(torch, 3, P_A, X_A, P_B, X_B)
         line["c2_variants"], extra["c2_variants"] = c2_variants_line(torch, 10, inp)
