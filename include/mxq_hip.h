@@ -181,7 +181,8 @@ typedef struct mxq_systolic_hints {
  * are written instead of in a pass of its own).  Output (r, c) of problem z becomes R(R(C * scale) + mask value)
  * in float32, R the identity (bf16 == 0) or bf16 RNE (bf16 != 0); without a mask, R(C * scale).  The mask value
  * is mask[b * mask_b_stride + (r % m) * mask_row_stride + c] with b = (z0 + z) / z_per_b - z0 / z_per_b.  Tiles
- * the skip hint marks take C = +0.  The same step as mxq_scores_scale_mask, bit for bit. */
+ * the skip hint marks take C = +0.  The same step as mxq_scores_scale_mask, bit for bit.  m and z_per_b are at
+ * least 1, z0 at least 0, and m, z_per_b and z0 + count below 2^31 (MXQ_EINVAL otherwise). */
 typedef struct mxq_systolic_epilogue {
   float scale;
   int32_t bf16;

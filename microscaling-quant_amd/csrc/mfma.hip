@@ -203,7 +203,8 @@ template <int KA, int KB, int TM, int TN>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 k_mx_mfma(const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA, const uint8_t* __restrict__ B,
           const uint8_t* __restrict__ SB, float* __restrict__ C, int64_t K64, int64_t M, int64_t N) {
-  // (the reduction's LDS leaves one workgroup per CU, so one wave per SIMD: every register is the wave's)
+  // (registers for one wave per SIMD: the 128 x 128 and 64 x 128 blocks' reduction takes 128 KiB of LDS, one
+  // workgroup per CU, and the operands in flight take what the accumulators leave)
   constexpr int BA = lane_bytes(KA), BB = lane_bytes(KB);
   using D = MxDepth<BA, BB, TM, TN>;
   constexpr int kDepth = D::kDepth;

@@ -86,12 +86,22 @@ struct SysArgs {
 };
 
 // The caller's epilogue, per output row: the mask row of output row r of problem z (NULL without a mask), then
-// R(R(v * scale) + row[c]) per output, R = bf16 RNE or identity.  Rows and m fit 32 bits (M / 32 <= 65535).
-__device__ __forceinline__ const float* epi_row(const SysArgs& a, int64_t z, int64_t r) {
+// R(R(v * scale) + row[c]) per output, R = bf16 RNE or identity.  Rows, m, z_per_b and z0 + z fit 31 bits
+// (M / 32 <= 65535; the launch checks the rest), so both divisions are 32-bit: as 64-bit divisions on the scalar
+// unit they were some hundred instructions in every workgroup's stores.
+__device__ __forceinline__ const float* epi_mask(const SysArgs& a, int64_t z) {   // problem z's mask rows
   const mxq_systolic_epilogue& e = a.epi;
   if (!e.mask) return nullptr;
-  const int64_t b = (e.z0 + z) / e.z_per_b - e.z0 / e.z_per_b;
-  return e.mask + b * e.mask_b_stride + (int64_t)((uint32_t)r % (uint32_t)e.m) * e.mask_row_stride;
+  const uint32_t zb = (uint32_t)e.z_per_b;
+  const int64_t b = (int64_t)((uint32_t)(e.z0 + z) / zb) - (int64_t)((uint32_t)e.z0 / zb);
+  return e.mask + b * e.mask_b_stride;
+}
+__device__ __forceinline__ uint32_t epi_rm(const SysArgs& a, int64_t r) {             // r % m
+  return (uint32_t)r % (uint32_t)a.epi.m;
+}
+__device__ __forceinline__ const float* epi_row(const SysArgs& a, int64_t z, int64_t r) {
+  const float* mz = epi_mask(a, z);
+  return mz ? mz + (int64_t)epi_rm(a, r) * a.epi.mask_row_stride : nullptr;
 }
 
 __device__ __forceinline__ float epi_apply(const SysArgs& a, const float* row, int64_t c, float v) {
@@ -186,11 +196,19 @@ template <int TM, int TN>
 __device__ __forceinline__ void write_tile(const SysArgs& a, int64_t z, int64_t mr, int64_t nc,
                                            const float (&C)[TM][TN]) {
   float* Cz = a.C + z * a.batch_c;
+  // the epilogue's mask rows: problem z's base once, then (mr + x) % m stepped row by row (below m, so one
+  // subtraction wraps it)
+  const float* mz = a.epi_on ? epi_mask(a, z) : nullptr;
+  uint32_t rm = mz ? epi_rm(a, mr) : 0u;
 #pragma unroll
   for (int x = 0; x < TM; ++x) {
+    if (x > 0) {
+      rm += 1u;
+      rm = rm >= (uint32_t)a.epi.m ? rm - (uint32_t)a.epi.m : rm;
+    }
     if (mr + x >= a.M) continue;
     if (a.epi_on) {
-      const float* row = epi_row(a, z, mr + x);
+      const float* row = mz ? mz + (int64_t)rm * a.epi.mask_row_stride : nullptr;
 #pragma unroll
       for (int y = 0; y < TN; ++y)
         if (nc + y < a.N) Cz[(mr + x) * a.ldc + nc + y] = epi_apply(a, row, nc + y, C[x][y]);
@@ -1091,8 +1109,10 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
     return mxq::invalid("mxq_systolic_batched: negative batch stride");
   if (count > 1 && M > 0 && N > 0 && L.batch_c < (M - 1) * L.ld_c + N)
     return mxq::invalid("mxq_systolic_batched: outputs of two problems overlap");
-  if (epilogue && (epilogue->m < 1 || epilogue->m > 0x7FFFFFFF || epilogue->z_per_b < 1 || epilogue->z0 < 0))
-    return mxq::invalid("mxq_systolic_batched: epilogue needs m >= 1 (below 2^31), z_per_b >= 1, z0 >= 0");
+  if (epilogue && (epilogue->m < 1 || epilogue->m > 0x7FFFFFFF || epilogue->z_per_b < 1 ||
+                   epilogue->z_per_b > 0x7FFFFFFF || epilogue->z0 < 0 || epilogue->z0 + count > 0x7FFFFFFF))
+    return mxq::invalid("mxq_systolic_batched: epilogue needs m >= 1 and z_per_b >= 1 (below 2^31), z0 >= 0 and "
+                        "z0 + count below 2^31");
   if (M == 0 || N == 0 || count == 0) return MXQ_OK;
   if (!P_A || !X_A || !P_B || !X_B || !C || !workspace) return mxq::invalid("mxq_systolic_batched: NULL pointer");
   SysArgs a{};
