@@ -454,3 +454,7 @@ def test_batched_hint_and_epilogue_errors(cuda):
     with pytest.raises(Exception, match="epilogue needs m >= 1"):
         systolic_batched(ops, lay, 2, 64, 40, 50, C, ar, HW_FINAL,
                          epilogue=_lib.SystolicEpilogue(scale=1.0, m=0, z_per_b=1))
+    # the epilogue divides in 32 bits: z0 + count must stay below 2^31
+    with pytest.raises(Exception, match="z0 \\+ count below 2\\^31"):
+        systolic_batched(ops, lay, 2, 64, 40, 50, C, ar, HW_FINAL,
+                         epilogue=_lib.SystolicEpilogue(scale=1.0, m=1, z_per_b=1, z0=2 ** 31 - 2))
