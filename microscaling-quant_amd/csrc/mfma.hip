@@ -21,55 +21,21 @@
 //               output is the sum, in a fixed order, of four float32 chains over every fourth K step.
 #include "mxq_common.h"
 #include "mxq_numerics.h"
+#include "ocp_hw.h"
 
 namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+using mxq_ocp_hw::f2v;
+using mxq_ocp_hw::s2v;
 
 // The MFMA operand type codes (the instruction's cbsz / blgp values).
 constexpr int kE4M3 = 0, kE5M2 = 1, kE2M3 = 2, kE3M2 = 3, kE2M1 = 4;
 
 __host__ __device__ constexpr int code_bits(int kind) { return kind <= kE5M2 ? 8 : (kind <= kE3M2 ? 6 : 4); }
 __host__ __device__ constexpr int lane_bytes(int kind) { return 4 * code_bits(kind); }   // 32 codes
-
-// The OCP code of an exact value in operand type `kind`: E4M3 (bias 7, no infinities, max 448), E5M2 (bias 15,
-// max 57344), E2M3 (bias 1, max 7.5), E3M2 (bias 3, max 28), E2M1 (bias 1, max 6); the FP6 and FP4 types use
-// every exponent field for finite values.  Returns false when x is not exactly representable.
-__device__ __forceinline__ bool code_of(float x, int kind, uint32_t& out) {
-  const int man_bits = kind == kE4M3 || kind == kE2M3 ? 3 : (kind == kE2M1 ? 1 : 2);
-  const int exp_bits = code_bits(kind) - 1 - man_bits;
-  const int bias = (1 << (exp_bits - 1)) - 1;
-  const uint32_t u = f2u(x);
-  const uint32_t sign = (u >> 31) << (code_bits(kind) - 1);
-  const uint32_t a = u & 0x7FFFFFFFu;
-  if (a == 0u) {
-    out = sign;
-    return true;
-  }
-  if (a >= 0x7F800000u) return false;                      // Inf / NaN codes are outside the comparison path
-  const int emin = 1 - bias;                               // smallest normal exponent
-  const int e = (int)(a >> 23) - 127;                      // float32 exponent (subnormal float32 never fits)
-  if (e < emin - man_bits) return false;                   // below the format's smallest subnormal
-  const uint32_t sig = (a & 0x007FFFFFu) | 0x00800000u;    // 24-bit significand (a is a normal float32 here)
-  if (e >= emin) {
-    const int drop = 23 - man_bits;
-    if (sig & ((1u << drop) - 1u)) return false;           // more significand bits than the format has
-    const uint32_t man = (sig >> drop) & ((1u << man_bits) - 1u);
-    const int field = e + bias;
-    const int fmax = (1 << exp_bits) - 1;
-    if (kind == kE4M3 ? (field > 15 || (field == 15 && man == 7u)) : (kind == kE5M2 ? field > 30 : field > fmax))
-      return false;
-    out = sign | ((uint32_t)field << man_bits) | man;
-    return true;
-  }
-  // subnormal in the format: value = man * 2^(emin - man_bits)
-  const int shift = 23 - (e - (emin - man_bits));          // sig >> shift = man
-  if (shift > 31 || (sig & ((1u << shift) - 1u))) return false;
-  out = sign | (sig >> shift);
-  return true;
-}
 
 // E8M0 byte of a power-of-two scale in [2^-127, 2^127]; false otherwise.
 __device__ __forceinline__ bool e8m0_byte(float x, uint32_t& out) {
@@ -84,7 +50,12 @@ __device__ __forceinline__ bool e8m0_byte(float x, uint32_t& out) {
 }
 
 // One thread per (column c < n32, 32-row block g < K64/32): the block's 32 codes and one scale byte, written
-// where the lane-ordered layout above puts them.  Consecutive threads take consecutive columns.
+// where the lane-ordered layout above puts them.  Consecutive threads take consecutive columns.  The codes come
+// from gfx950's conversions (V_CVT_SCALEF32_PK_*, scale 1), whose fields are already in the lane order (FP8 byte
+// j, FP6 field j at bit 6 j, FP4 nibble j at bit 4 j), and a value is a code of the type exactly when it is
+// finite and converts back to itself, bit for bit: an exact value converts to its own code (-0 keeping its
+// sign, as the OCP code of -0 does), and anything else to a different value (rounded, saturated, or E4M3's NaN
+// and E5M2's Inf past their ranges).
 template <int W>
 __global__ void __launch_bounds__(256) k_mx_pack(const float* __restrict__ P, const float* __restrict__ X,
                                                  int64_t K, int64_t n, int64_t n32, int64_t K64, int kind,
@@ -93,29 +64,74 @@ __global__ void __launch_bounds__(256) k_mx_pack(const float* __restrict__ P, co
   constexpr int HW = 16 * W / 32;                          // words per half block (16 codes of W bits)
   constexpr int BPL = 4 * W;                               // bytes per lane and K step
   const int64_t nb64 = K64 / 32, nk = K64 / 64;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n32 * nb64) return;
-  const int64_t g = t / n32, c = t - (t / n32) * n32;
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;   // the launch keeps n32 * nb64 below 2^31
+  if ((int64_t)t >= n32 * nb64) return;
+  const uint32_t gq = t / (uint32_t)n32;
+  const int64_t g = gq, c = t - gq * (uint32_t)n32;
   const bool live = c < n;
-  uint32_t words[2 * HW];                                  // half h: words [h HW, h HW + HW)
-#pragma unroll
-  for (int w = 0; w < 2 * HW; ++w) words[w] = 0u;
-  bool nonzero = false, bad = false;
+  float x[32];
+  bool nonzero = false, finite = true;
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
     const int64_t k = g * 32 + j;
-    uint32_t code = 0u;
-    if (live && k < K) {
-      const float x = P[k * n + c];
-      nonzero |= (f2u(x) & 0x7FFFFFFFu) != 0u;
-      bad |= !code_of(x, kind, code);
-    }
-    // FP8: code j % 16 of half j / 16 at bit W (j % 16) of that half's bits; FP6, FP4: code j at bit W j
-    const int bit = W == 8 ? 8 * (j % 16) : W * j;
-    const int wd = (W == 8 ? (j / 16) * HW : 0) + bit / 32, off = bit % 32;
-    words[wd] |= code << off;
-    if (off + W > 32) words[wd + 1] |= code >> (32 - off);
+    x[j] = live && k < K ? P[k * n + c] : 0.0f;
+    nonzero |= (f2u(x[j]) & 0x7FFFFFFFu) != 0u;
+    finite &= (f2u(x[j]) & 0x7FFFFFFFu) < 0x7F800000u;
   }
+  uint32_t words[2 * HW];                                  // code j at bit W j (FP8: half j / 16 in words [h HW, ..))
+  bool same = true;                                        // every value came back from its code
+  if constexpr (W == 8) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      s2v r = {0, 0};
+      f2v lo, hi;
+      if (kind == kE4M3) {
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, x[4 * q], x[4 * q + 1], 1.0f, false);
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, x[4 * q + 2], x[4 * q + 3], 1.0f, true);
+        lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(__builtin_bit_cast(uint32_t, r), 1.0f, false);
+        hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(__builtin_bit_cast(uint32_t, r), 1.0f, true);
+      } else {
+        r = __builtin_amdgcn_cvt_scalef32_pk_bf8_f32(r, x[4 * q], x[4 * q + 1], 1.0f, false);
+        r = __builtin_amdgcn_cvt_scalef32_pk_bf8_f32(r, x[4 * q + 2], x[4 * q + 3], 1.0f, true);
+        lo = __builtin_amdgcn_cvt_scalef32_pk_f32_bf8(__builtin_bit_cast(uint32_t, r), 1.0f, false);
+        hi = __builtin_amdgcn_cvt_scalef32_pk_f32_bf8(__builtin_bit_cast(uint32_t, r), 1.0f, true);
+      }
+      words[q] = __builtin_bit_cast(uint32_t, r);
+      same &= f2u(lo.x) == f2u(x[4 * q]) && f2u(lo.y) == f2u(x[4 * q + 1]) && f2u(hi.x) == f2u(x[4 * q + 2]) &&
+              f2u(hi.y) == f2u(x[4 * q + 3]);
+    }
+  } else if constexpr (W == 6) {
+    mxq_ocp_hw::f16v even, odd;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      even[k] = x[2 * k];
+      odd[k] = x[2 * k + 1];
+    }
+    const mxq_ocp_hw::u6v pk = mxq_ocp_hw::pack16x2(even, odd, kind == kE2M3);
+    const mxq_ocp_hw::f32v back = mxq_ocp_hw::unpack32(pk, kind == kE2M3);
+#pragma unroll
+    for (int w = 0; w < 6; ++w) words[w] = pk[w];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) same &= f2u(back[j]) == f2u(x[j]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t w = 0u;
+      w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[8 * q], x[8 * q + 1], 1.0f, 0);
+      w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[8 * q + 2], x[8 * q + 3], 1.0f, 1);
+      w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[8 * q + 4], x[8 * q + 5], 1.0f, 2);
+      w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, x[8 * q + 6], x[8 * q + 7], 1.0f, 3);
+      words[q] = w;
+      const f2v b0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+      const f2v b1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+      const f2v b2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+      const f2v b3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+      same &= f2u(b0.x) == f2u(x[8 * q]) && f2u(b0.y) == f2u(x[8 * q + 1]) && f2u(b1.x) == f2u(x[8 * q + 2]) &&
+              f2u(b1.y) == f2u(x[8 * q + 3]) && f2u(b2.x) == f2u(x[8 * q + 4]) && f2u(b2.y) == f2u(x[8 * q + 5]) &&
+              f2u(b3.x) == f2u(x[8 * q + 6]) && f2u(b3.y) == f2u(x[8 * q + 7]);
+    }
+  }
+  bool bad = !(finite && same);
   uint32_t sbyte = 127u;
   if (live && g * 32 < K) {
     if (!e8m0_byte(X[g * n + c], sbyte)) {
@@ -327,6 +343,7 @@ extern "C" int mxq_mx_pack(const float* P, const float* X, int64_t K, int64_t n,
   if (reinterpret_cast<uintptr_t>(codes) % 16) return mxq::invalid("mxq_mx_pack: codes must be 16-byte aligned");
   const int64_t n32 = mxq::ceil_div(n, 32) * 32;
   const int64_t threads = n32 * (K64 / 32);
+  if (threads >= (int64_t(1) << 31)) return mxq::invalid("mxq_mx_pack: operand too large (2^31 blocks of 32)");
   const dim3 grid = mxq::grid_for(threads, 256);
   hipStream_t st = mxq::as_stream(stream);
   if (code_bits(kind) == 8) k_mx_pack<8><<<grid, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
