@@ -22,7 +22,9 @@
 
 namespace {
 
-constexpr int RB = 64;   // rows per workgroup
+constexpr int H = 2;          // 64-row groups per workgroup
+constexpr int RB = 64 * H;    // rows per workgroup
+constexpr int NT = 256 * H;   // threads per workgroup: 4 waves per row group
 
 // torch's statistics of one row (lane l's elements l + 64 it)
 template <int IT>
@@ -49,15 +51,15 @@ __device__ __forceinline__ void row_stats(const float* __restrict__ row, int T, 
 }
 
 template <int ELEM, int MODE, int IT>
-__global__ void __launch_bounds__(256) k_softmax_pt(const float* __restrict__ S, int64_t R, int T,
+__global__ void __launch_bounds__(NT) k_softmax_pt(const float* __restrict__ S, int64_t R, int T,
                                                     float* __restrict__ PT_P, float* __restrict__ PT_X,
                                                     mxq_block_spec s, uint8_t* __restrict__ stage_live,
                                                     int64_t cols) {
   __shared__ float mx_s[RB], sum_s[RB];
   const int64_t r0 = (int64_t)blockIdx.x * RB;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  // pass 1: each wave takes every fourth row
-  for (int j = w; j < RB; j += 4) {
+  // pass 1: each wave takes every (4 H)th row
+  for (int j = w; j < RB; j += 4 * H) {
     if (r0 + j >= R) break;
     float mx, sm;
     row_stats<IT>(S + (r0 + j) * T, T, lane, mx, sm);
@@ -67,15 +69,17 @@ __global__ void __launch_bounds__(256) k_softmax_pt(const float* __restrict__ S,
     }
   }
   __syncthreads();
-  // pass 2: lane m of each wave takes row r0 + m, wave w the key blocks w, w + 4, ...: the block's 32
-  // probabilities recomputed, its maximum, scale and codes in the lane, and each code stored as P^T[key][row],
-  // a run of 64 rows per store across the wave
-  const int64_t r = r0 + lane;
+  // pass 2: lane m of wave w takes row r0 + 64 (w % H) + m and the key blocks w / H, w / H + 4, ...: the
+  // block's 32 probabilities recomputed, its maximum, scale and codes in the lane, and each code stored as
+  // P^T[key][row], a run of 64 rows per store across the wave and of 64 H rows across the H waves that take
+  // the same blocks (128 rows: 382.5 us per C5 call against 387.5 with 64, no gain at 256)
+  const int hg = w % H, wb = w / H;                 // row group, and first key block, of the wave
+  const int64_t r = r0 + 64 * hg + lane;
   const bool live = r < R;
-  const float mx = mx_s[lane], sm = sum_s[lane];
+  const float mx = mx_s[64 * hg + lane], sm = sum_s[64 * hg + lane];
   const float* src = S + (live ? r : r0) * T;
   const int nb = (T + 31) / 32;
-  for (int b = w; b < nb; b += 4) {
+  for (int b = wb; b < nb; b += 4) {
     const int k0 = b * 32;
     float v[32];
     if ((T & 3) == 0 && k0 + 32 <= T) {               // rows 16-byte aligned: 16-byte loads
@@ -112,7 +116,7 @@ __global__ void __launch_bounds__(256) k_softmax_pt(const float* __restrict__ S,
       // per 32 rows (a half wave, inside one problem: cols % 32 == 0): any nonzero code or non-finite scale
       const uint64_t bal = __ballot(live && (nz != 0u || !(fabsf(xs) < INFINITY)));
       const int half = lane & 32;
-      const int64_t rh = r0 + half;
+      const int64_t rh = r0 + 64 * hg + half;
       if ((lane & 31) == 0 && rh < R) {
         const int64_t z = rh / cols, g = (rh - z * cols) / 32;
         stage_live[(z * nb + b) * (cols / 32) + g] = ((bal >> half) & 0xFFFFFFFFull) != 0ull ? 1u : 0u;
@@ -125,12 +129,12 @@ template <int ELEM, int MODE>
 void launch_it(int it, dim3 grid, hipStream_t st, const float* S, int64_t R, int T, float* PT_P, float* PT_X,
                const mxq_block_spec& s, uint8_t* live, int64_t cols) {
   switch (it) {
-    case 1: k_softmax_pt<ELEM, MODE, 1><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
-    case 2: k_softmax_pt<ELEM, MODE, 2><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
-    case 4: k_softmax_pt<ELEM, MODE, 4><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
-    case 8: k_softmax_pt<ELEM, MODE, 8><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
-    case 16: k_softmax_pt<ELEM, MODE, 16><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
-    default: k_softmax_pt<ELEM, MODE, 32><<<grid, 256, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    case 1: k_softmax_pt<ELEM, MODE, 1><<<grid, NT, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    case 2: k_softmax_pt<ELEM, MODE, 2><<<grid, NT, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    case 4: k_softmax_pt<ELEM, MODE, 4><<<grid, NT, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    case 8: k_softmax_pt<ELEM, MODE, 8><<<grid, NT, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    case 16: k_softmax_pt<ELEM, MODE, 16><<<grid, NT, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
+    default: k_softmax_pt<ELEM, MODE, 32><<<grid, NT, 0, st>>>(S, R, T, PT_P, PT_X, s, live, cols); break;
   }
 }
 
