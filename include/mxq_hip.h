@@ -27,6 +27,12 @@ extern "C" {
 
 typedef void* mxq_stream_t;
 
+/* ABI revision, returned by mxq_version().  A caller checks it against the header it was built with.
+ *   1  the first release.
+ *   2  mxq_lut_tables takes the code format (fmt_e, fmt_m) before the grid; mxq_systolic_hints gained
+ *      a_live. */
+#define MXQ_ABI_VERSION 2
+
 enum { MXQ_OK = 0, MXQ_EINVAL = 1, MXQ_EHIP = 2 };
 
 /* Input element types of the block quantizer. */
@@ -62,7 +68,8 @@ typedef struct mxq_arith_spec {
   float sat_value;
 } mxq_arith_spec;
 
-/* Library identity and the last error of the calling thread. */
+/* Library identity (MXQ_ABI_VERSION of the header the library was built from) and the last error of the
+ * calling thread. */
 const char* mxq_last_error(void);
 int mxq_version(void);
 
@@ -369,9 +376,10 @@ int mxq_lut_lookup_packed(const uint8_t* I4, int64_t K, int64_t n, int32_t group
                           float* out, mxq_stream_t stream);
 
 /* block.lut along axis 0 in one call: V (K x n, row-major, float32 / bf16 / f16 by v_dtype) block-quantized
- * in blocks of 32 rows by spec (mxgemmini's: the OCP element grid of a LUT format, no via), the element codes
- * kept as bytes in the workspace while their grid bins are counted per column group, the tables fitted as
- * mxq_lut_tables fits them (T: ceil(n / 2^group) x 16), and every code replaced by its nearest entry: P_lut
+ * in blocks of 32 rows by spec (mxgemmini's: the OCP element grid of a LUT format at its own max_norm, no via),
+ * the element codes kept as bytes in the workspace while their grid bins are counted per column group, the
+ * tables fitted as mxq_lut_tables fits them (T: ceil(n / 2^group) x 16), and every code replaced by its nearest
+ * entry: P_lut
  * (K x n float32) and X (ceil(K / 32) x n float32 scales) are what block.lut returns.  grid, nv, safe, ns,
  * safe_order: as mxq_lut_tables, for spec's format.  K >= 1, n % 16 == 0, V, P_lut and X 16-byte aligned.
  * workspace: device memory of mxq_block_lut_workspace bytes, 256-byte aligned.  *err (device) gets bit 0 set

@@ -102,4 +102,4 @@ extern "C" int mxq_timer_read(const char* kernel, double* total_ms, int64_t* lau
 
 extern "C" const char* mxq_last_error(void) { return mxq::g_last_error.c_str(); }
 
-extern "C" int mxq_version(void) { return 1; }
+extern "C" int mxq_version(void) { return MXQ_ABI_VERSION; }

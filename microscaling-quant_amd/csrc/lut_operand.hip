@@ -165,8 +165,9 @@ extern "C" int mxq_block_lut(const void* V, int32_t v_dtype, int64_t K, int64_t 
   if (!spec) return mxq::invalid("mxq_block_lut: spec is NULL");
   if (int rc = mxq_quant::validate(*spec)) return rc;
   if (spec->scale_rule != MXQ_SCALE_MXQUANT || spec->elem != MXQ_ELEM_OCP || spec->via_e != 0 ||
-      !mxq_ocp_hw::has_hw(spec->e, spec->m))
-    return mxq::invalid("mxq_block_lut: the spec must be MX-Gemmini's (its scale, the OCP element grid, no via)");
+      !mxq_ocp_hw::has_hw(spec->e, spec->m) || spec->max_norm != mxq_ocp_hw::fmt_max(spec->e, spec->m))
+    return mxq::invalid("mxq_block_lut: the spec must be MX-Gemmini's (its scale, the OCP element grid at the format's own "
+                         "max_norm, no via)");
   CodeGrid cg;
   if (int rc = check_args(K, n, group, spec->e, spec->m, nv, &cg, "mxq_block_lut")) return rc;
   if (max_iters < 0 || ns < 1 || ns > mxq_lut::kMaxGrid) return mxq::invalid("mxq_block_lut: bad max_iters or ns");

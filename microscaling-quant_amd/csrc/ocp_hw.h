@@ -35,6 +35,17 @@ __host__ __device__ inline bool has_hw_n(int e, int m) {
   return has_hw(e, m) && (N >= 16 || !((e == 2 && m == 3) || (e == 3 && m == 2)));
 }
 
+// The format's largest finite value, where the conversions saturate (E4M3 448, E5M2 57344, E2M3 7.5, E3M2 28,
+// E2M1 6).  A grid clamped at another max_norm is not theirs, so the callers gate on max_norm equal to this.
+__host__ __device__ inline float fmt_max(int e, int m) {
+  if (e == 4 && m == 3) return 448.0f;
+  if (e == 5 && m == 2) return 57344.0f;
+  if (e == 2 && m == 3) return 7.5f;
+  if (e == 3 && m == 2) return 28.0f;
+  if (e == 2 && m == 1) return 6.0f;
+  return 0.0f;
+}
+
 // |z| below this (and finite) converts as the grid rounds.
 __host__ __device__ inline float hw_limit(int e, int m) {
   return (e == 4 && m == 3) ? 464.0f : ((e == 5 && m == 2) ? 57344.0f : 3.0e38f);

@@ -442,12 +442,14 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, co
       for (int j = 0; j < VEC; ++j) v[i][j] = v[i][j] * d[j].inv;
   }
   // the OCP grid at nearest even by the hardware conversions when every scaled value of the wave is finite
-  // and within their range (a column's largest |z| is its maximum scaled, the division being monotone)
+  // and within their range (a column's largest |z| is its maximum scaled, the division being monotone) and the
+  // grid saturates where they do (max_norm the format's own)
   constexpr bool HW_OCP = ELEM == MXQ_ELEM_OCP && MODE == MXQ_RNE && VEC >= 4;
   constexpr bool HW_MS = ELEM == MXQ_ELEM_MICROSOFT && MODE == MXQ_RNE && VEC >= 4;
   bool hw = false;
   if constexpr (HW_OCP) {
-    if (s.via_e == 0 && mxq_ocp_hw::has_hw_n<ROWS * VEC>(s.e, s.m) && out.hw_format(s)) {
+    if (s.via_e == 0 && mxq_ocp_hw::has_hw_n<ROWS * VEC>(s.e, s.m) && out.hw_format(s) &&
+        s.max_norm == mxq_ocp_hw::fmt_max(s.e, s.m)) {
       const float lim = mxq_ocp_hw::hw_limit(s.e, s.m);
       bool ok = true;
 #pragma unroll
@@ -466,7 +468,8 @@ __global__ void __launch_bounds__(256) k_quant_split(const T* __restrict__ V, co
   mxq_block_spec hs = s;                             // the element format as the conversions name it
   if constexpr (HW_MS) {
     hs.m = s.m - 2;                                   // microxcaling's mbits count the sign and hidden bits
-    if (s.via_e == 0 && mxq_ocp_hw::has_hw_n<ROWS * VEC>(hs.e, hs.m) && out.hw_format(hs)) {
+    if (s.via_e == 0 && mxq_ocp_hw::has_hw_n<ROWS * VEC>(hs.e, hs.m) && out.hw_format(hs) &&
+        s.max_norm == mxq_ocp_hw::fmt_max(hs.e, hs.m)) {
       const int emin = 2 - (1 << (hs.e - 1));
       const uint32_t odd = (uint32_t)(127 + emin - hs.m - 1) << 23;  // 2^(emin - m - 1), then one float below
       bool ok = true;

@@ -22,6 +22,9 @@ LIB_PATH = os.environ.get("MXQ_HIP_LIB", os.path.join(_HERE, "libmxq_hip.so"))
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
 
+#: the MXQ_ABI_VERSION of include/mxq_hip.h these signatures follow; a library reporting another is refused
+ABI_VERSION = 2
+
 c_i32, c_i64, c_f32, c_f64, c_ptr = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
 
 
@@ -146,6 +149,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             for name, (res, args) in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.restype, fn.argtypes = res, args
+            if lib.mxq_version() != ABI_VERSION:
+                raise RuntimeError(f"mxq: {path} has C ABI revision {lib.mxq_version()}, this package binds "
+                                   f"revision {ABI_VERSION}; rebuild the library")
             _lib = lib
     return _lib
 
@@ -177,6 +183,13 @@ def stream(dev: torch.device) -> ctypes.c_void_p:
 
 def ptr(t: Optional[torch.Tensor]) -> ctypes.c_void_p:
     return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def aligned(t: torch.Tensor, nbytes: int = 16) -> torch.Tensor:
+    """t itself when its first element sits on an nbytes boundary, else a fresh contiguous copy (torch's
+    allocator hands out 256-byte aligned blocks).  Views at an odd offset into a larger storage are valid
+    inputs; kernels that load 16 bytes a lane need the copy."""
+    return t if t.data_ptr() % nbytes == 0 else torch.empty_like(t, memory_format=torch.contiguous_format).copy_(t)
 
 
 def back(t: torch.Tensor, like: torch.Tensor) -> torch.Tensor:

@@ -78,7 +78,7 @@ def mfma_accum(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: tor
     K, M, N = check_operands(P_A, X_A, P_B, X_B, block_size)
     ka, kb = _kind(fmt_a), _kind(fmt_a if fmt_b is None else fmt_b)
     dev = _lib.compute_device(P_A)
-    ops = [_lib.to_device(t.detach(), dev).contiguous() for t in (P_A, X_A, P_B, X_B)]
+    ops = [_lib.aligned(_lib.to_device(t.detach(), dev).contiguous()) for t in (P_A, X_A, P_B, X_B)]
     C = torch.zeros((M, N), dtype=torch.float32, device=dev)
     if K == 0 or M == 0 or N == 0:
         return _lib.back(C, P_A)

@@ -37,7 +37,9 @@ def test_version_and_error_without_gpu():
     """mxq_version and mxq_last_error touch no device."""
     from mxq import _lib
     lib = _lib.load()
-    assert lib.mxq_version() >= 1
+    text = open(HEADER).read()
+    assert f"#define MXQ_ABI_VERSION {_lib.ABI_VERSION}\n" in text
+    assert lib.mxq_version() == _lib.ABI_VERSION
     lib.mxq_last_error.restype = ctypes.c_char_p
     assert isinstance(lib.mxq_last_error(), bytes)
 

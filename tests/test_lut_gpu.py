@@ -212,6 +212,22 @@ def test_block_lut_one_call_against_oracle(cuda, fmt):
         assert_bits_equal(P.cpu().numpy(), wP, f"P {fmt} {shape}")
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_block_lut_one_call_misaligned_view(cuda, dt):
+    """A contiguous view at an element offset that is not a 16-byte boundary (a slice of a flat buffer, as flat
+    parameter storage hands out) quantizes as a fresh copy of it does, on the one-call path."""
+    from mxq import block
+    K, n = 96, 64
+    flat = torch.randn(K * n + 3, generator=torch.Generator().manual_seed(5)).to(dt).cuda()
+    V = flat[1:1 + K * n].view(K, n)
+    assert V.is_contiguous() and V.data_ptr() % 16
+    kw = dict(rounding_mode="rne", scale_floor=2.0 ** -23, group=1, max_iters=50)
+    P, X = block.lut.quantize(V, "MXFP6_E3M2", 0, 32, **kw)
+    wP, wX = block.lut.quantize(V.clone(), "MXFP6_E3M2", 0, 32, **kw)
+    assert_bits_equal(X.cpu().numpy(), wX.cpu().numpy(), f"X of a misaligned {dt} view")
+    assert_bits_equal(P.cpu().numpy(), wP.cpu().numpy(), f"P of a misaligned {dt} view")
+
+
 def test_block_lut_one_call_errors(cuda):
     """A non-finite V gives codes that are not values of the format: the one-call path raises what the tables
     raise (E3M2 has no NaN or Inf code: the encoder flags it; E5M2 has them: the count flags it), and the

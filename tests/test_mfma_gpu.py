@@ -272,6 +272,22 @@ def test_rejects(cuda):
         mxq.mfma_accum(ones, X, ones, X, "FP32")
 
 
+def test_misaligned_code_views(cuda):
+    """Codes handed in as a contiguous view at an element offset off the 16-byte grid give the bits of a fresh
+    copy of them."""
+    import mxq
+    rng = np.random.default_rng(3)
+    PA, XA = ob.mxgemmini_quantize(rng.standard_normal((96, 40)).astype(np.float32), "MXFP8_E4M3", 0)
+    flat = torch.zeros(PA.size + 1, device="cuda")
+    flat[1:] = torch.from_numpy(PA).reshape(-1).cuda()
+    view = flat[1:].view(PA.shape)
+    assert view.data_ptr() % 16
+    X = torch.from_numpy(XA).cuda()
+    got = mxq.mfma_accum(view, X, view, X, "MXFP8_E4M3")
+    want = mxq.mfma_accum(view.clone(), X, view.clone(), X, "MXFP8_E4M3")
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("fmt", ["MXFP8_E4M3", "MXFP4"])
 def test_wave_block_shapes_agree(cuda, fmt):
     """2048 x 2048 outputs run on 128 x 128 workgroup blocks, their 1024-row halves on 64 x 128 blocks and

@@ -372,3 +372,34 @@ def test_ocp_even_grid_edges(cuda, fmt, cols):
     wP, wX = ob.ocp_quantize(V, fmt, 0)
     assert_bits_equal(X.cpu().numpy(), wX, f"X {fmt}")
     assert_bits_equal(P.cpu().numpy(), wP, f"P {fmt}")
+
+
+@pytest.mark.parametrize("elem", ["ocp", "microsoft"])
+def test_c_abi_own_max_norm(cuda, elem):
+    """A C caller's spec with a max_norm other than the format's own (the Python quantizers always pass the
+    format's): E4M3 at nearest even, unscaled, saturating at 240, where the hardware conversions would saturate at
+    448.  The kernel keeps such waves on the software grid: the grid clamped at 240 (OCP), and microxcaling's
+    element step with max_norm 240, bit for bit; then the same values at the format's own 448 against the
+    oracle's grids (the conversions' path)."""
+    import ctypes
+
+    from mxq import _lib
+    rng = np.random.default_rng(17)
+    V = (rng.standard_normal((64, 256)) * 150).astype(np.float32)
+    V[3, :8] = [239.9, 240.0, 241.0, 300.0, -300.0, 447.0, 0.0, -0.0]
+    Vd = torch.from_numpy(V).cuda()
+    for max_norm in (240.0, 448.0):
+        if elem == "ocp":
+            spec = _lib.BlockSpec(scale_rule=_lib.SCALE_NONE, elem=_lib.ELEM_OCP, e=4, m=3, rounding=1,
+                                  max_norm=max_norm)
+            g = nx._ocp(V, 4, 3, "rne")
+            want = np.where(np.abs(g) > max_norm, np.copysign(np.float32(max_norm), g), g).astype(np.float32)
+        else:
+            spec = _lib.BlockSpec(scale_rule=_lib.SCALE_NONE, elem=_lib.ELEM_MICROSOFT, e=4, m=5, rounding=1,
+                                  max_norm=max_norm)
+            want = nx.microsoft(V, 4, 5, max_norm, "even")
+        P = torch.empty_like(Vd)
+        X = torch.empty(2, 256, device="cuda")
+        _lib.run("mxq_block_quantize", _lib.ptr(Vd), 0, _lib.ptr(P), _lib.ptr(X), 1, 64, 256, 32,
+                 ctypes.byref(spec), _lib.stream(Vd.device))
+        assert_bits_equal(P.cpu().numpy(), want, f"{elem} E4M3 codes saturating at {max_norm}")
