@@ -29,8 +29,9 @@ typedef void* mxq_stream_t;
 
 /* ABI revision, returned by mxq_version().  A caller checks it against the header it was built with.
  *   1  the first release.
- *   2  mxq_lut_tables takes the code format (fmt_e, fmt_m) before the grid; mxq_systolic_hints gained
- *      a_live. */
+ *   2  mxq_lut_tables takes the code format (fmt_e, fmt_m) before the grid; mxq_systolic_hints gained a_live
+ *      and c_end; mxq_softmax_quantize_t takes a tail; mxq_mask_minabs and mxq_attend_hints give the largest
+ *      mask values; mxq_systolic_fast_lanes. */
 #define MXQ_ABI_VERSION 2
 
 enum { MXQ_OK = 0, MXQ_EINVAL = 1, MXQ_EHIP = 2 };
@@ -176,12 +177,25 @@ typedef struct mxq_systolic_layout {
  *          mxq_softmax_quantize_t): per problem z, 32-row stage s and 32-column group g of A,
  *          a_live[(z * ceil(K/32) + s) * ceil(M/32) + g] != 0 unless every code of A in those rows and columns
  *          is +-0 and every block scale over them finite.  The pass then reads B only.  A byte that wrongly
- *          says 0 for a stage some tile leaves out gives wrong results: this one is a promise, not a hint. */
+ *          says 0 for a stage some tile leaves out gives wrong results: this one is a promise, not a hint.
+ *          When the fast kernel runs (mxq_systolic_fast_lanes), a tile it hands to the general kernel for
+ *          another reason is recomputed over the same rows when its left-out rows passed the check, so rows of
+ *          A past k_end whose a_live bytes are 0 are never read: they need not hold codes or scales at all.
+ *   c_end  with skip: per problem z and 64-row group t of C, a fast tile made only of skipped groups whose first
+ *          column is at or past c_end[z * ceil(M/64) + t] is not stored at all (those outputs keep what the
+ *          buffer held).  Attention's scores past a 64-row group's last seen key are never read: the softmax
+ *          takes them from the mask (mxq_softmax_quantize_t's tail). */
 typedef struct mxq_systolic_hints {
   const uint8_t* skip;
   const int32_t* k_end;
   const uint8_t* a_live;
+  const int32_t* c_end;
 } mxq_systolic_hints;
+
+/* 1 when mxq_systolic and mxq_systolic_batched run the fast kernel for these lanes and this arithmetic (any
+ * other case runs the general kernel alone, which reads every row of A and computes every tile), else 0.  No
+ * counterpart in the reference: a caller that leaves rows of A unwritten under k_end asks this first. */
+int mxq_systolic_fast_lanes(const int32_t* lane_e, const int32_t* lane_m, int32_t size, const mxq_arith_spec* arith);
 
 /* An elementwise step mxq_systolic_batched applies to every output as it is stored (no counterpart in the
  * reference as a fused step: it is attention's score step, mxq/nn/_attention.py:128-135, done where the scores
@@ -255,9 +269,24 @@ int mxq_attend_windows(const double* amax_a, int64_t lda, const double* amax_k, 
  * (NULL for none), P^T's columns are R / cols problems of cols each (cols a multiple of 32 dividing R), and
  * stage_live[(z * ceil(T/32) + s) * (cols / 32) + g] gets 1 when problem z's 32 rows s and 32 columns g of P^T
  * hold a nonzero code or a non-finite scale, else 0: the a_live answer of mxq_systolic_hints for the P V
- * product on these codes. */
+ * product on these codes.
+ * With `tail` (NULL for none; needs stage_live and cols a multiple of 64), S holds of each row only the keys
+ * below k_end of its 64-row group; a key at or past it has the score R(R(+0 * score.scale) + mask value) of
+ * the epilogue `score` (bf16 = 0), whose largest value over the group is tail_max.  A row whose largest stored
+ * score s is finite and exceeds tail_max by at least 128 (tail_max - s <= -128 in float32) has every such
+ * probability exp(tail - s) / sum = +0 and its maximum and sum over the stored keys alone: it reads nothing
+ * else.  Any other row reads those scores from the mask.  When every row of a 64-row group is of the first
+ * kind, P^T's rows at and past k_end for those columns are not written (codes +0 and scales of a zero block,
+ * which a reader bound by k_end and these stage_live bytes, all 0 there, never reads); otherwise they are. */
+typedef struct mxq_softmax_tail {
+  const int32_t* k_end;          /* per problem and 64-row group: [z * (cols / 64) + t] */
+  const float* tail_max;         /* the same layout */
+  mxq_systolic_epilogue score;   /* how the scores were stored: scale, mask rows, z0, z_per_b, m (bf16 = 0) */
+} mxq_softmax_tail;
+
 int mxq_softmax_quantize_t(const float* S, int64_t R, int64_t T, float* PT_P, float* PT_X,
-                           const mxq_block_spec* spec, uint8_t* stage_live, int64_t cols, mxq_stream_t stream);
+                           const mxq_block_spec* spec, uint8_t* stage_live, int64_t cols,
+                           const mxq_softmax_tail* tail, mxq_stream_t stream);
 
 /* attend's two elementwise steps on the scores, in place: S (Z problems x n heads x m queries x Tk keys, float32,
  * contiguous) becomes r(r(S * scale) + mask_row), r the identity or (round_bf16 = 1) rounding.bf16; the add and its
@@ -273,16 +302,19 @@ int mxq_scores_scale_mask(float* S, int64_t Z, int64_t n, int64_t m, int64_t Tk,
  * work its computation makes moot, without changing a bit).  mxq_mask_minabs: per mask batch row, 32-row group
  * of the call's `rows` = n*m score rows (row r reads the mask row of query r % m) and 32-key group, the
  * smallest |mask| (0 for a NaN) into out[(batch * ceil(rows/32) + group) * ceil(Tk/32) + key group].
- * mxq_attend_hints: per call z (mask batch row (z0 + z) / z_per_b - z0 / z_per_b when `batched`, else 0), its
- * masked-key bound b as mxq_attend_windows takes it; skip[(z * ceil(rows/32) + g) * ceil(Tk/32) + j] = 1 when
- * that group's smallest |mask| c absorbs 2b in float32 (scores there do not matter: the mask absorbs any the
- * call can produce); k_end[z * ceil(rows/64) + t] = 32 * (1 + the last key group some row of 64-row group t
- * still sees), 0 when none. */
+ * With maxval (NULL for none), also the largest mask value of each group, NaN aside (-Inf for none), in the same
+ * layout.  mxq_attend_hints: per call z (mask batch row (z0 + z) / z_per_b - z0 / z_per_b when `batched`, else
+ * 0), its masked-key bound b as mxq_attend_windows takes it; skip[(z * ceil(rows/32) + g) * ceil(Tk/32) + j] = 1
+ * when that group's smallest |mask| c absorbs 2b in float32 (scores there do not matter: the mask absorbs any
+ * the call can produce); k_end[z * ceil(rows/64) + t] = 32 * (1 + the last key group some row of 64-row group t
+ * still sees), 0 when none; with tail_max (NULL for none; needs maxval), tail_max[z * ceil(rows/64) + t] = the
+ * largest maxval of the groups of t past k_end (all of them skipped), -Inf when there are none. */
 int mxq_mask_minabs(const float* mask, int64_t mask_b_stride, int64_t mask_row_stride, int64_t batches, int64_t rows,
-                    int64_t m, int64_t Tk, float* out, mxq_stream_t stream);
+                    int64_t m, int64_t Tk, float* out, float* maxval, mxq_stream_t stream);
 int mxq_attend_hints(const double* amax_a, int64_t lda, const double* amax_k, int64_t ldk, int64_t D, int64_t Z,
                      double slack_scale, const float* minabs, int64_t z0, int64_t z_per_b, int32_t batched,
-                     int64_t rows, int64_t Tk, uint8_t* skip, int32_t* k_end, mxq_stream_t stream);
+                     int64_t rows, int64_t Tk, uint8_t* skip, int32_t* k_end, const float* maxval, float* tail_max,
+                     mxq_stream_t stream);
 
 /* The adder tree: the operands, Arithmetic, scales and output of mxq_systolic; each reduction of `size` products
  * (zeros past a K tail) summed by log2(size) levels of adjacent-pair acc_adds, level l in (level_e[l],

@@ -8,13 +8,14 @@
 //                        add of the query's mask row, r again -- the reference's two elementwise steps with their
 //                        two roundings, read and written once.
 //   k_mask_minabs        per mask batch row, 32-row group of a call's n*m score rows and 32-key group, the
-//                        smallest |mask| (0 for a NaN)
+//                        smallest |mask| (0 for a NaN) and the largest mask value
 //   k_attend_hints       the two batched launches' hints (include/mxq_hip.h mxq_systolic_hints) from those and
 //                        each call's masked-key bound b: a 32 x 32 group of scores is not needed when its
 //                        smallest |mask| c absorbs 2b (c + 2b == c and c - 2b == c in float32), for then every
 //                        mask value there absorbs every score the call can produce, r(r(s * scale) + mask) is
 //                        r(mask) whatever s is, and a +0 score gives the same; k_end of a 64-row group is the
-//                        end of its last key group that some of its rows still see.  Where every key of a row is
+//                        end of its last key group that some of its rows still see, and the largest mask value
+//                        past it (the largest score there, for the softmax).  Where every key of a row is
 //                        masked softmax is uniform, not zero, and the systolic kernel's check of the rows past
 //                        k_end sends that tile to the general kernel.
 #include "mxq_common.h"
@@ -186,20 +187,28 @@ __global__ void __launch_bounds__(256) k_attend_windows(const double* __restrict
 
 __global__ void __launch_bounds__(256) k_mask_minabs(const float* __restrict__ mask, int64_t mask_b_stride,
                                                      int64_t mask_row_stride, int64_t rows, int64_t m, int64_t Tk,
-                                                     int64_t rgroups, int64_t kgroups, float* __restrict__ out) {
+                                                     int64_t rgroups, int64_t kgroups, float* __restrict__ out,
+                                                     float* __restrict__ maxval) {
   const int64_t bb = blockIdx.z, rg = blockIdx.y, key = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  float mn = f_inf();                                          // keys past Tk take no part
+  float mn = f_inf(), mx = -f_inf();                           // keys past Tk take no part
   if (key < Tk) {
     for (int i = 0; i < 32; ++i) {
       const int64_t r = rg * 32 + i;
       if (r >= rows) break;
       const float c = mask[bb * mask_b_stride + (r % m) * mask_row_stride + key];
       mn = fminf(mn, c != c ? 0.0f : fabsf(c));
+      mx = fmaxf(mx, c);                                       // a NaN takes no part
     }
   }
-  for (int off = 16; off > 0; off >>= 1) mn = fminf(mn, __shfl_xor(mn, off, 32));
+  for (int off = 16; off > 0; off >>= 1) {
+    mn = fminf(mn, __shfl_xor(mn, off, 32));
+    mx = fmaxf(mx, __shfl_xor(mx, off, 32));
+  }
   const int64_t kg = key >> 5;
-  if ((threadIdx.x & 31) == 0 && kg < kgroups) out[(bb * rgroups + rg) * kgroups + kg] = mn;
+  if ((threadIdx.x & 31) == 0 && kg < kgroups) {
+    out[(bb * rgroups + rg) * kgroups + kg] = mn;
+    if (maxval) maxval[(bb * rgroups + rg) * kgroups + kg] = mx;
+  }
 }
 
 // Workgroup (t, z): 64-row group t of call z.  The bound as k_attend_windows takes it.
@@ -208,9 +217,11 @@ __global__ void __launch_bounds__(256) k_attend_hints(const double* __restrict__
                                                       double slack_scale, const float* __restrict__ minabs,
                                                       int64_t z0, int64_t z_per_b, int batched, int64_t rgroups,
                                                       int64_t kgroups, int64_t tgroups, uint8_t* __restrict__ skip,
-                                                      int32_t* __restrict__ k_end) {
+                                                      int32_t* __restrict__ k_end, const float* __restrict__ maxval,
+                                                      float* __restrict__ tail_max) {
   __shared__ float b2;
   __shared__ int last;
+  __shared__ float tmax[4];
   const int64_t t = blockIdx.x, z = blockIdx.y;
   __shared__ double terms[256];
   const double bound = call_bound(amax_a, lda, amax_k, ldk, D, z, slack_scale, terms);
@@ -236,6 +247,17 @@ __global__ void __launch_bounds__(256) k_attend_hints(const double* __restrict__
   atomicMax(&last, mine);
   __syncthreads();
   if (threadIdx.x == 0) k_end[z * tgroups + t] = (int32_t)((last + 1) * 32);
+  if (!tail_max) return;
+  // the largest mask value of the groups past k_end (every one of them skipped): the largest score there
+  float tm = -f_inf();
+  for (int64_t rg = 2 * t; rg < 2 * t + 2 && rg < rgroups; ++rg) {
+    const float* vrow = maxval + (bb * rgroups + rg) * kgroups;
+    for (int64_t kg = last + 1 + threadIdx.x; kg < kgroups; kg += 256) tm = fmaxf(tm, vrow[kg]);
+  }
+  for (int off = 32; off > 0; off >>= 1) tm = fmaxf(tm, __shfl_xor(tm, off, 64));
+  if ((threadIdx.x & 63) == 0) tmax[threadIdx.x >> 6] = tm;
+  __syncthreads();
+  if (threadIdx.x == 0) tail_max[z * tgroups + t] = fmaxf(fmaxf(tmax[0], tmax[1]), fmaxf(tmax[2], tmax[3]));
 }
 
 }  // namespace
@@ -291,7 +313,7 @@ extern "C" int mxq_attend_windows(const double* amax_a, int64_t lda, const doubl
 }
 
 extern "C" int mxq_mask_minabs(const float* mask, int64_t mask_b_stride, int64_t mask_row_stride, int64_t batches,
-                               int64_t rows, int64_t m, int64_t Tk, float* out, mxq_stream_t stream) {
+                               int64_t rows, int64_t m, int64_t Tk, float* out, float* maxval, mxq_stream_t stream) {
   if (batches < 0 || rows < 0 || m < 1 || Tk < 0 || mask_b_stride < 0 || mask_row_stride < 0)
     return mxq::invalid("mxq_mask_minabs: bad shape");
   if (batches == 0 || rows == 0 || Tk == 0) return MXQ_OK;
@@ -301,22 +323,23 @@ extern "C" int mxq_mask_minabs(const float* mask, int64_t mask_b_stride, int64_t
     return mxq::invalid("mxq_mask_minabs: too large");
   const dim3 grid((unsigned)mxq::ceil_div(Tk, 256), (unsigned)rgroups, (unsigned)batches);
   k_mask_minabs<<<grid, 256, 0, mxq::as_stream(stream)>>>(mask, mask_b_stride, mask_row_stride, rows, m, Tk, rgroups,
-                                                          kgroups, out);
+                                                          kgroups, out, maxval);
   return mxq::check_launch("mxq_mask_minabs");
 }
 
 extern "C" int mxq_attend_hints(const double* amax_a, int64_t lda, const double* amax_k, int64_t ldk, int64_t D,
                                 int64_t Z, double slack_scale, const float* minabs, int64_t z0, int64_t z_per_b,
                                 int32_t batched, int64_t rows, int64_t Tk, uint8_t* skip, int32_t* k_end,
-                                mxq_stream_t stream) {
+                                const float* maxval, float* tail_max, mxq_stream_t stream) {
   if (D < 0 || Z < 0 || rows < 0 || Tk < 0 || z0 < 0 || z_per_b < 1 || lda < Z || ldk < Z)
     return mxq::invalid("mxq_attend_hints: bad shape");
   if (Z == 0 || rows == 0) return MXQ_OK;
   if (!amax_a || !amax_k || !minabs || !skip || !k_end) return mxq::invalid("mxq_attend_hints: NULL pointer");
+  if (tail_max && !maxval) return mxq::invalid("mxq_attend_hints: tail_max needs maxval");
   const int64_t rgroups = mxq::ceil_div(rows, 32), kgroups = mxq::ceil_div(Tk, 32), tgroups = mxq::ceil_div(rows, 64);
   if (tgroups > INT32_MAX || Z > 65535 || kgroups > INT32_MAX / 32) return mxq::invalid("mxq_attend_hints: too large");
   k_attend_hints<<<dim3((unsigned)tgroups, (unsigned)Z), 256, 0, mxq::as_stream(stream)>>>(
       amax_a, lda, amax_k, ldk, D, slack_scale, minabs, z0, z_per_b, batched ? 1 : 0, rgroups, kgroups, tgroups, skip,
-      k_end);
+      k_end, maxval, tail_max);
   return mxq::check_launch("mxq_attend_hints");
 }

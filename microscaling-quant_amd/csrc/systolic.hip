@@ -70,7 +70,8 @@ struct SysArgs {
   const uint8_t* skip;    // per problem, 32-row group and 32-column group of C: nonzero = not needed
   int64_t skip_rows, skip_cols;
   const int32_t* k_end;   // per problem and 64-column group of A: rows at and past it hold only +-0 codes
-  int64_t kend_groups;
+  int64_t kend_groups;    // ceil(M / 64): 64-column groups of A, 64-row groups of C
+  const int32_t* c_end;   // per problem and 64-row group of C: skipped tiles from this column on are not stored
   // dispatch position (blockIdx.x + tiles_x * (blockIdx.y + tiles_y * blockIdx.z)) -> fast tile
   // (z * tiles_y + ty) * tiles_x + tx, by descending work (k_tile_order); NULL: the grid's own tile, rows last
   // first
@@ -469,7 +470,7 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   const LaneConsts<HWF> lc{fl};
   static_assert((BM / TM) * (BN / TN) == NT, "256 threads");
   __shared__ __align__(16) Smem<BM, BN> sm;
-  __shared__ uint32_t red[3][4];
+  __shared__ uint32_t red[4][4];
   __shared__ uint32_t live[2][4];   // per staged buffer and wave: bit 0, A has a nonzero code; bit 1, B has;
                                     // bit 2, a staged block scale does not allow the short tile add
   __shared__ float xs_a[2][BM], xs_b[2][BN];   // the stage's block scales (block size 32)
@@ -514,7 +515,8 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   if (args.skip) {
     if (tile_skipped(args, z, m0, n0, BM, BN)) {
       if (threadIdx.x == 0) args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = 0u;
-      write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
+      if (!args.c_end || n0 < args.c_end[z * args.kend_groups + m0 / 64])
+        write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
       return;
     }
   }
@@ -575,8 +577,10 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
     lb.store(sm.b[to], vb);
   };
   int buf = 0;
-  load_stage(0);
-  store_stage(0);
+  if (kstop > 0) {                                // rows at and past kstop are never read
+    load_stage(0);
+    store_stage(0);
+  }
   __syncthreads();
 
   float scale[TM][TN];
@@ -723,23 +727,25 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   }
 
   // rows past kstop: the results are exact only if A holds +-0 there, B and every remaining block scale are
-  // finite (k_suffix_flags' bytes for this tile's groups and the stages it left out)
+  // finite (k_suffix_flags' bytes for this tile's groups and the stages it left out); bit j of `bad` for the
+  // tile's 32-column group j of A (j < BM / 32), then of B
+  constexpr int GT = BM / 32 + BN / 32;
+  uint32_t bad = 0u;
   if (kstop < K) {
-    constexpr int GT = BM / 32 + BN / 32;
     const int64_t s0 = kstop / KT, ga = (M + 31) / 32, gb = (N + 31) / 32;
-    bool bad = false;
     for (int64_t i = threadIdx.x; i < (args.stages - s0) * GT; i += 256) {
       const int64_t st = s0 + i / GT;
       const int j = (int)(i % GT);
+      bool b;
       if (j < BM / 32) {
         const int64_t g = m0 / 32 + j;
-        bad = bad || (g < ga && args.suf_a[(z * args.stages + st) * ga + g]);
+        b = g < ga && args.suf_a[(z * args.stages + st) * ga + g];
       } else {
         const int64_t g = n0 / 32 + (j - BM / 32);
-        bad = bad || (g < gb && args.suf_b[(z * args.stages + st) * gb + g]);
+        b = g < gb && args.suf_b[(z * args.stages + st) * gb + g];
       }
+      bad |= b ? 1u << j : 0u;
     }
-    max_b = umax(max_b, bad ? 0x7F800000u : 0u);
   }
 
   // the workgroup's verdict: its maxima over everything it read
@@ -747,29 +753,36 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
     max_a = umax(max_a, (uint32_t)__shfl_xor((int)max_a, off, 64));
     max_b = umax(max_b, (uint32_t)__shfl_xor((int)max_b, off, 64));
     max_x = umax(max_x, (uint32_t)__shfl_xor((int)max_x, off, 64));
+    bad |= (uint32_t)__shfl_xor((int)bad, off, 64);
   }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     red[0][wave] = max_a;
     red[1][wave] = max_b;
     red[2][wave] = max_x;
+    red[3][wave] = bad;
   }
   __syncthreads();
   const uint32_t wa = umax(umax(red[0][0], red[0][1]), umax(red[0][2], red[0][3]));
   const uint32_t wb = umax(umax(red[1][0], red[1][1]), umax(red[1][2], red[1][3]));
   const uint32_t wx = umax(umax(red[2][0], red[2][1]), umax(red[2][2], red[2][3]));
-  const bool ok = wa < kFastAMaxBits && wb < 0x7F800000u && wx < 0x7F800000u &&
+  const uint32_t wbad = red[3][0] | red[3][1] | red[3][2] | red[3][3];
+  const bool ok = wbad == 0u && wa < kFastAMaxBits && wb < 0x7F800000u && wx < 0x7F800000u &&
                   u2f(wa) * u2f(wb) <= args.fast_prod_max;
+  // the flag: bit 0, the general kernel computes the tile; bits 1..GT, which groups' left-out rows failed
+  // their check (a piece of the tile reduces over all of K when its group of A or of B did, else to kstop)
   if (threadIdx.x == 0)
-    args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = ok ? 0u : 1u;
+    args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = ok ? 0u : 1u | (wbad << 1);
   if (!ok) return;
   write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
 }
 
 // ------------------------------------------------------------------------------- general datapath
 // The BM x BN outputs at (m0, n0) of problem z.
+// The reduction runs over rows [0, kstop) of A and B (kstop = K, or a multiple of 32 the fast kernel's check
+// allows to stop at).
 template <int BM, int BN, int TM, int TN>
-__device__ __forceinline__ void gen_tile_at(const SysArgs& args, int64_t z, int64_t m0, int64_t n0,
+__device__ __forceinline__ void gen_tile_at(const SysArgs& args, int64_t z, int64_t m0, int64_t n0, int64_t kstop,
                                             Smem<BM, BN>& sm) {
   constexpr int NT = (BM / TM) * (BN / TN);
   const int tn = threadIdx.x % (BN / TN), tm = threadIdx.x / (BN / TN);
@@ -788,16 +801,17 @@ __device__ __forceinline__ void gen_tile_at(const SysArgs& args, int64_t z, int6
   TileLoader<BM, NT> la;
   TileLoader<BN, NT> lb;
   int buf = 0;
-  la.load(A, args.A.ld, K, M, 0, m0, va);
-  lb.load(B, args.B.ld, K, N, 0, n0, vb);
+  const int64_t kl = kstop < K ? kstop : K;       // rows at and past kstop are never read (they load as zeros)
+  la.load(A, args.A.ld, kl, M, 0, m0, va);
+  lb.load(B, args.B.ld, kl, N, 0, n0, vb);
   la.store(sm.a[0], va);
   lb.store(sm.b[0], vb);
   __syncthreads();
   float scale[TM][TN];
   int in_block = 0;
   int64_t g = 0;
-  for (int64_t k0 = 0; k0 < K; k0 += KT) {
-    const bool more = k0 + KT < K;
+  for (int64_t k0 = 0; k0 < kstop; k0 += KT) {
+    const bool more = k0 + KT < kstop;
     if (more) {
       la.load(A, args.A.ld, K, M, k0 + KT, m0, va);
       lb.load(B, args.B.ld, K, N, k0 + KT, n0, vb);
@@ -870,23 +884,38 @@ __device__ __forceinline__ void gen_tile_at(const SysArgs& args, int64_t z, int6
   }
 }
 
+// Where a general piece of a tile the fast kernel flagged (flag bits as it writes them) stops: at the fast
+// kernel's stop under k_end when the rows left out passed the check for this piece's own columns of A and B
+// (A +-0 there, B and the scales finite), else at K.  The fast lanes' arithmetic adds nothing for a +-0 code of
+// A (its product flushes to +0, the lanes keep the sum, the tile add keeps C), the premise of the fast kernel's
+// own stop; so the piece's bits are the same either way, and rows past k_end that passed are never read.
+__device__ __forceinline__ int64_t piece_kstop(const SysArgs& a, uint32_t flag, int64_t z, int64_t m0, int64_t n0,
+                                               int64_t tm0, int64_t tn0) {
+  if (!a.k_end) return a.K;
+  const int64_t ks = tile_kstop(a, z, tm0);
+  if (ks >= a.K) return a.K;
+  const uint32_t bad = flag >> 1;                 // bit j: group j of A (j < fbm / 32), then of B
+  const int ja = (int)((m0 - tm0) / 32), jb = a.fbm / 32 + (int)((n0 - tn0) / 32);
+  return ((bad >> ja) & 1u) || ((bad >> jb) & 1u) ? a.K : ks;
+}
+
 // only_flagged: the grid is the fast kernel's tiles (it ran first); a workgroup whose tile has its flag set
 // computes that tile's BM x BN pieces in turn, the others return at once.  Otherwise one piece per workgroup.
 template <int BM, int BN, int TM, int TN>
-__global__ void __launch_bounds__((BM / TM) * (BN / TN)) k_systolic_gen(const SysArgs args, int only_flagged) {
+__global__ void __launch_bounds__((BM / TM) * (BN / TN), 4) k_systolic_gen(const SysArgs args, int only_flagged) {
   static_assert(32 % BM == 0 && 32 % BN == 0, "a general tile lies inside one fast tile");
   __shared__ Smem<BM, BN> sm;
   const int64_t z = blockIdx.z;
   if (!only_flagged) {
-    gen_tile_at<BM, BN, TM, TN>(args, z, (int64_t)blockIdx.y * BM, (int64_t)blockIdx.x * BN, sm);
+    gen_tile_at<BM, BN, TM, TN>(args, z, (int64_t)blockIdx.y * BM, (int64_t)blockIdx.x * BN, args.K, sm);
     return;
   }
-  if (args.flags[(z * args.tiles_y + blockIdx.y) * args.tiles_x + blockIdx.x] == 0u) return;
-  for (int64_t m0 = (int64_t)blockIdx.y * args.fbm; m0 < (int64_t)(blockIdx.y + 1) * args.fbm && m0 < args.M;
-       m0 += BM)
-    for (int64_t n0 = (int64_t)blockIdx.x * args.fbn; n0 < (int64_t)(blockIdx.x + 1) * args.fbn && n0 < args.N;
-         n0 += BN) {
-      gen_tile_at<BM, BN, TM, TN>(args, z, m0, n0, sm);
+  const uint32_t flag = args.flags[(z * args.tiles_y + blockIdx.y) * args.tiles_x + blockIdx.x];
+  if (flag == 0u) return;
+  const int64_t tm0 = (int64_t)blockIdx.y * args.fbm, tn0 = (int64_t)blockIdx.x * args.fbn;
+  for (int64_t m0 = tm0; m0 < tm0 + args.fbm && m0 < args.M; m0 += BM)
+    for (int64_t n0 = tn0; n0 < tn0 + args.fbn && n0 < args.N; n0 += BN) {
+      gen_tile_at<BM, BN, TM, TN>(args, z, m0, n0, piece_kstop(args, flag, z, m0, n0, tm0, tn0), sm);
       __syncthreads();   // the next piece restages sm
     }
 }
@@ -1080,6 +1109,12 @@ int check_common(int64_t K, int64_t M, int64_t N, int64_t count, const int32_t* 
 
 }  // namespace
 
+extern "C" int mxq_systolic_fast_lanes(const int32_t* lane_e, const int32_t* lane_m, int32_t size,
+                                       const mxq_arith_spec* arith) {
+  if (!arith || !lane_e || !lane_m || size < 1 || size > kMaxLanes || !lanes_valid(lane_e, lane_m, size)) return 0;
+  return lanes_fast(lane_e, lane_m, size, *arith) ? 1 : 0;
+}
+
 extern "C" int mxq_systolic(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C,
                             int64_t K, int64_t M, int64_t N, const int32_t* lane_e, const int32_t* lane_m,
                             int32_t size, int32_t block_size, const mxq_arith_spec* arith, uint32_t* workspace,
@@ -1127,6 +1162,7 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
     a.k_end = hints->k_end;
     a.kend_groups = mxq::ceil_div(M, 64);
     a.a_live = hints->k_end ? hints->a_live : nullptr;
+    a.c_end = hints->skip ? hints->c_end : nullptr;
   }
   if (epilogue) {
     a.epi_on = 1;

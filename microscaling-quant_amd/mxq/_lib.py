@@ -42,9 +42,9 @@ class ArithSpec(ctypes.Structure):
 
 
 class SystolicHints(ctypes.Structure):
-    """include/mxq_hip.h mxq_systolic_hints: device pointers (0 for none) to the skip map, the k_end bounds and
-    the caller's suffix bytes of A."""
-    _fields_ = [("skip", c_ptr), ("k_end", c_ptr), ("a_live", c_ptr)]
+    """include/mxq_hip.h mxq_systolic_hints: device pointers (0 for none) to the skip map, the k_end bounds, the
+    caller's suffix bytes of A and the column bounds past which skipped tiles are not stored."""
+    _fields_ = [("skip", c_ptr), ("k_end", c_ptr), ("a_live", c_ptr), ("c_end", c_ptr)]
 
 
 class SystolicEpilogue(ctypes.Structure):
@@ -52,6 +52,12 @@ class SystolicEpilogue(ctypes.Structure):
     _fields_ = [("scale", ctypes.c_float), ("bf16", ctypes.c_int32), ("mask", c_ptr),
                 ("mask_b_stride", ctypes.c_int64), ("mask_row_stride", ctypes.c_int64), ("z0", ctypes.c_int64),
                 ("z_per_b", ctypes.c_int64), ("m", ctypes.c_int64)]
+
+
+class SoftmaxTail(ctypes.Structure):
+    """include/mxq_hip.h mxq_softmax_tail: per 64-row group the keys S holds (k_end) and the largest score past
+    them (tail_max), and the score step that gives those scores from the mask."""
+    _fields_ = [("k_end", c_ptr), ("tail_max", c_ptr), ("score", SystolicEpilogue)]
 
 
 class SystolicLayout(ctypes.Structure):
@@ -95,9 +101,9 @@ SIGNATURES = {
     "mxq_scores_scale_mask": (c_i32, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_f32, c_ptr, c_i64, c_i64, c_i64, c_i64,
                                       c_i32, c_ptr]),
     "mxq_group_amax": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
-    "mxq_mask_minabs": (c_i32, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
+    "mxq_mask_minabs": (c_i32, [c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr]),
     "mxq_attend_hints": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_f64, c_ptr, c_i64, c_i64, c_i32, c_i64,
-                                 c_i64, c_ptr, c_ptr, c_ptr]),
+                                 c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
     "mxq_attend_windows": (c_i32, [c_ptr, c_i64, c_ptr, c_i64, c_i64, c_i64, c_f64, c_ptr, c_i64, c_i64, c_i64,
                                    c_i64, c_i64, c_i64, c_i64, c_ptr, c_ptr]),
     "mxq_adder_tree": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i32, c_i32,
@@ -112,7 +118,8 @@ SIGNATURES = {
     "mxq_block_lut": (c_i32, [c_ptr, c_i32, c_i64, c_i64, ctypes.POINTER(BlockSpec), c_i32, c_i32, c_ptr, c_i32,
                               c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr, c_ptr]),
     "mxq_softmax_quantize_t": (c_i32, [c_ptr, c_i64, c_i64, c_ptr, c_ptr, ctypes.POINTER(BlockSpec), c_ptr, c_i64,
-                                       c_ptr]),
+                                       ctypes.POINTER(SoftmaxTail), c_ptr]),
+    "mxq_systolic_fast_lanes": (c_i32, [c_ptr, c_ptr, c_i32, ctypes.POINTER(ArithSpec)]),
     "mxq_block_lut_workspace": (c_i32, [c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, ctypes.POINTER(c_i64)]),
     "mxq_lut_lookup": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_ptr]),
     "mxq_lut_finder": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_ptr, c_i32, c_ptr, c_i64, c_ptr, c_ptr]),

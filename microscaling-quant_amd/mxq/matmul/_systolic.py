@@ -74,6 +74,7 @@ def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: 
                      arith: Arithmetic, schedule: Sequence[Tuple[int, int]], size: int = 16,
                      block_size: int = BLOCK, *, skip: Optional[torch.Tensor] = None,
                      k_end: Optional[torch.Tensor] = None, a_live: Optional[torch.Tensor] = None,
+                     c_end: Optional[torch.Tensor] = None,
                      epilogue: Optional["_lib.SystolicEpilogue"] = None) -> None:
     """`count` problems of one shape in one launch, written into C (mxq_systolic_batched).  ops: the four
     device tensors the layout's strides address (codes A, scales X_A, codes B, scales X_B), float32 on C's
@@ -83,7 +84,8 @@ def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: 
     the caller does not need C's 32 x 32 group (such tiles come back +0); `k_end`, int32 count x ceil(M/64), a
     bound on the rows of A holding nonzero codes in each 64-column group (checked: a wrong one costs time);
     `a_live`, with k_end, uint8 count x ceil(K/32) x ceil(M/32), the caller's answer to that check for A (nonzero
-    unless the 32 x 32 piece of A is +-0 with finite scales; trusted, so it must be exact).
+    unless the 32 x 32 piece of A is +-0 with finite scales; trusted, so it must be exact); `c_end`, with skip,
+    int32 count x ceil(M/64): skipped tiles whose columns start at or past it are not stored at all.
     `epilogue` (mxq_systolic_epilogue): R(R(C * scale) + mask value) applied to every output as it is stored."""
     import ctypes
     kernel = getattr(arith, "kernel", None)
@@ -101,15 +103,29 @@ def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: 
     lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
     for t, dt, shape in ((skip, torch.uint8, (count, -(-M // 32), -(-N // 32))),
                          (k_end, torch.int32, (count, -(-M // 64))),
-                         (a_live, torch.uint8, (count, -(-K // 32), -(-M // 32)))):
+                         (a_live, torch.uint8, (count, -(-K // 32), -(-M // 32))),
+                         (c_end, torch.int32, (count, -(-M // 64)))):
         if t is not None and (t.dtype != dt or tuple(t.shape) != shape or t.device != dev or not t.is_contiguous()):
             raise ValueError(f"systolic_batched: a hint must be a contiguous {dt} tensor of shape {shape} on {dev}")
-    hints = _lib.SystolicHints(skip=_lib.ptr(skip), k_end=_lib.ptr(k_end), a_live=_lib.ptr(a_live))
+    hints = _lib.SystolicHints(skip=_lib.ptr(skip), k_end=_lib.ptr(k_end), a_live=_lib.ptr(a_live),
+                               c_end=_lib.ptr(c_end))
     work = torch.empty(workspace_elements(K, M, N, count), dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         _lib.run("mxq_systolic_batched", *(_lib.ptr(t) for t in ops), _lib.ptr(C), ctypes.byref(layout), count,
                  K, M, N, le, lm, size, block_size, kernel.ctype(), ctypes.byref(hints),
                  None if epilogue is None else ctypes.byref(epilogue), _lib.ptr(work), 0, _lib.stream(dev))
+
+
+def fast_lanes(arith: Arithmetic, schedule: Sequence[Tuple[int, int]], size: int = 16) -> bool:
+    """Whether the library runs its fast kernel for this Arithmetic and lane schedule (mxq_systolic_fast_lanes):
+    then a launch under k_end never reads rows of A past it that its check passes."""
+    import ctypes
+    kernel = getattr(arith, "kernel", None)
+    if kernel is None or len(schedule) != size:
+        return False
+    le = (ctypes.c_int32 * size)(*[int(e) for e, _ in schedule])
+    lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
+    return bool(_lib.load().mxq_systolic_fast_lanes(le, lm, size, kernel.ctype()))
 
 
 def _reference_loop(P_A, X_A, P_B, X_B, arith, schedule, size, block_size, K, M, N):

@@ -22,6 +22,7 @@ first and last key some query of the call still sees, widened to pv.block_size b
 P V then runs over the same key blocks, provided P is exactly zero on every key outside them; otherwise over
 all keys.  Outside keys contribute whole all-zero blocks, which add nothing to any reducer's tile sum.
 """
+import ctypes
 from dataclasses import dataclass
 from functools import partial
 from typing import Iterator, Optional, Tuple
@@ -262,12 +263,13 @@ def _windows(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale
 
 
 def _hints(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale: float, bias: torch.Tensor,
-           Hkv: int, s0: int, m: int, rows: int, Tk: int):
+           Hkv: int, s0: int, m: int, rows: int, Tk: int, with_tail: bool = False):
     """The two batched launches' hints from the mask rows s0.. of pairs z0..z0+Zc and each call's bound
     (include/mxq_hip.h mxq_attend_hints): the 32 x 32 score groups whose mask absorbs every score the call can
     produce, where a +0 score gives the reference's r(r(s * scale) + mask) (skip, for Q K^T), and per 64 rows
     the end of the keys some row still sees (k_end, for P V; checked by the kernel, so a row whose every key
-    is masked, where softmax is uniform, costs time, not bits)."""
+    is masked, where softmax is uniform, costs time, not bits).  with_tail: also the largest mask value past
+    k_end per 64 rows (tail_max, for the softmax's tail), else None."""
     from .. import _lib
     D = a_amax.shape[0]
     mask, b_stride, r_stride = _mask_rows(bias, z0, Hkv, s0)
@@ -276,15 +278,17 @@ def _hints(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale: 
     rg, kg, tg = -(-rows // 32), -(-Tk // 32), -(-rows // 64)
     dev = a_amax.device
     minabs = torch.empty(batches, rg, kg, dtype=torch.float32, device=dev)
+    maxval = torch.empty(batches, rg, kg, dtype=torch.float32, device=dev) if with_tail else None
     skip = torch.empty(Zc, rg, kg, dtype=torch.uint8, device=dev)
     k_end = torch.empty(Zc, tg, dtype=torch.int32, device=dev)
+    tail_max = torch.empty(Zc, tg, dtype=torch.float32, device=dev) if with_tail else None
     with torch.cuda.device(dev):
         _lib.run("mxq_mask_minabs", _lib.ptr(mask), b_stride, r_stride, batches, rows, m, Tk, _lib.ptr(minabs),
-                 _lib.stream(dev))
+                 _lib.ptr(maxval), _lib.stream(dev))
         _lib.run("mxq_attend_hints", _lib.ptr(a_amax), a_amax.shape[1], _lib.ptr(k_amax[:, z0:]), k_amax.shape[1],
                  D, Zc, SLACK * abs(scale), _lib.ptr(minabs), z0, Hkv, int(batched), rows, Tk, _lib.ptr(skip),
-                 _lib.ptr(k_end), _lib.stream(dev))
-    return skip, k_end
+                 _lib.ptr(k_end), _lib.ptr(maxval), _lib.ptr(tail_max), _lib.stream(dev))
+    return skip, k_end, tail_max
 
 
 @dataclass
@@ -299,6 +303,7 @@ class _Prepared:
     flags: Optional[torch.Tensor]
     skip: Optional[torch.Tensor]
     k_end: Optional[torch.Tensor]
+    tail_max: Optional[torch.Tensor]
 
 
 @dataclass
@@ -313,6 +318,7 @@ class _Batched:
     pv: Scheme
     qk_red: tuple
     pv_red: tuple
+    pv_fast: bool    # the P V launch runs the fast kernel, which never reads P^T past k_end where it is +0
 
     @staticmethod
     def of(qk: Scheme, pv: Scheme, q: torch.Tensor) -> Optional["_Batched"]:
@@ -323,7 +329,9 @@ class _Batched:
         qk_red, pv_red = _systolic_reducer(qk.reduce, qk.block_size), _systolic_reducer(pv.reduce, pv.block_size)
         if qk_red is None or pv_red is None:
             return None
-        return _Batched(qk, pv, qk_red, pv_red)
+        from ..matmul._systolic import fast_lanes
+        arith, sched, size = pv_red
+        return _Batched(qk, pv, qk_red, pv_red, fast_lanes(arith, sched, size))
 
     def run(self, q, k, v, bias, scale, step, vector, rnd, dims: _Dims, out) -> None:
         qk, pv = self.qk, self.pv
@@ -345,7 +353,7 @@ class _Batched:
         for s0 in range(0, dims.Tq, step):
             e0 = min(s0 + step, dims.Tq)
             for z0, z1 in _launch_ranges(B, Hkv, max(1, ELEMENTS_PER_LAUNCH // (n * (e0 - s0) * Tk))):
-                chunks.append(self._prepare(qg, bias, kv, k_amax, scale, dims, z0, z1, s0, e0))
+                chunks.append(self._prepare(qg, bias, kv, k_amax, scale, vector, dims, z0, z1, s0, e0))
         if bias is not None:
             flags = torch.cat([c.flags for c in chunks])
             host = torch.empty(flags.shape, dtype=flags.dtype, pin_memory=True)
@@ -367,7 +375,7 @@ class _Batched:
                     self._per_pair(q, bias, kv, scale, vector, rnd, dims, c.z0 + z, c.z0 + z + 1, c.s0, c.e0, out)
             at += c.z1 - c.z0 if bias is not None else 0
 
-    def _prepare(self, qg, bias, kv, k_amax, scale, dims: _Dims, z0, z1, s0, e0) -> "_Prepared":
+    def _prepare(self, qg, bias, kv, k_amax, scale, vector, dims: _Dims, z0, z1, s0, e0) -> "_Prepared":
         """Pairs z0..z1, queries s0..e0: Q^T's codes and, with a mask, each pair's flag (int32 on the device: 3
         when its call keeps every key, so the batched result is the reference's; otherwise the caller redoes it
         through the reference's call) and the two launches' hints."""
@@ -375,12 +383,20 @@ class _Batched:
         Zc, n, m, Tk, D, Hkv = z1 - z0, dims.group, e0 - s0, dims.Tk, dims.D, dims.Hkv
         cols = n * m                                                              # one call's columns
         A_P, A_X = qk.a(qg[z0:z1, :, s0:e0].to(torch.float32).permute(3, 0, 1, 2).reshape(D, Zc * cols))
-        flags = skip = k_end = None
+        flags = skip = k_end = tail_max = None
         if bias is not None:
             a_amax = _group_amax(A_P, A_X, qk.block_size, Zc)
             flags = _windows(a_amax, k_amax, z0, Zc, scale, bias, Hkv, s0, m, pv.block_size)
-            skip, k_end = _hints(a_amax, k_amax, z0, Zc, scale, bias, Hkv, s0, m, cols, Tk)
-        return _Prepared(z0, z1, s0, e0, A_P, A_X, flags, skip, k_end)
+            skip, k_end, tail_max = _hints(a_amax, k_amax, z0, Zc, scale, bias, Hkv, s0, m, cols, Tk,
+                                           self._tail_ok(cols, Tk, vector))
+        return _Prepared(z0, z1, s0, e0, A_P, A_X, flags, skip, k_end, tail_max)
+
+    def _tail_ok(self, cols: int, Tk: int, vector) -> bool:
+        """Whether the scores past each 64-row group's k_end may go unstored and P^T unwritten there: the
+        softmax kernel takes them from the mask, and the P V launch's fast kernel reads P^T only below k_end
+        where the softmax's stage bytes say the rest is +0 (64-row groups inside one call: cols % 64 == 0)."""
+        return (self.pv_fast and cols % 64 == 0 and
+                _softmax_pt_spec(self.pv.a, self.pv.block_size, vector, Tk) is not None)
 
     def _chunk(self, c: "_Prepared", qg, bias, kv, scale, vector, dims: _Dims, out) -> None:
         """A prepared chunk as two batched launches, its outputs into `out`."""
@@ -397,14 +413,22 @@ class _Batched:
         mask, b_stride, r_stride = (None, 0, 0) if bias is None else _mask_rows(bias, z0, Hkv, s0)
         epi = _lib.SystolicEpilogue(scale=float(scale), bf16=int(vector == "bf16"), mask=_lib.ptr(mask),
                                     mask_b_stride=b_stride, mask_row_stride=r_stride, z0=z0, z_per_b=Hkv, m=m)
+        # with a tail, the scores past each 64-row group's k_end are never stored: the softmax reads what it
+        # needs of them from the mask through the same score step
+        tail = None
+        if c.tail_max is not None:
+            tail = _lib.SoftmaxTail(k_end=_lib.ptr(k_end), tail_max=_lib.ptr(c.tail_max), score=epi)
         systolic_batched((A_P, A_X, KT_P[:, z0 * Tk:], KT_X[:, z0 * Tk:]),
                          _lib.SystolicLayout(ld_a=Zc * cols, batch_a=cols, ld_xa=Zc * cols, batch_xa=cols,
                                              ld_b=KT_P.shape[1], batch_b=Tk, ld_xb=KT_X.shape[1], batch_xb=Tk,
                                              ld_c=Tk, batch_c=cols * Tk),
-                         Zc, D, cols, Tk, S, arith, sched, size, qk.block_size, skip=skip, epilogue=epi)
+                         Zc, D, cols, Tk, S, arith, sched, size, qk.block_size, skip=skip,
+                         c_end=None if tail is None else k_end, epilogue=epi)
         # every call's P^T side by side: softmax and the quantizer in one kernel where they are torch's persistent
         # softmax and an MX-Gemmini quantizer; else P, quantized as it lies (a transposed view: no copy)
-        PT = _softmax_pt(S, pv.a, pv.block_size, vector, cols if k_end is not None and cols % 32 == 0 else None)
+        PT = _softmax_pt(S, pv.a, pv.block_size, vector, cols if k_end is not None and cols % 32 == 0 else None,
+                         tail)
+        assert tail is None or PT is not None, "a tail needs the softmax kernel"
         a_live = None
         if PT is None:
             P = softmax(S, vector)
@@ -436,26 +460,39 @@ class _Batched:
                       s0, e0, out[b])
 
 
-def _softmax_pt(S: torch.Tensor, quantizer, block_size: int, vector: Optional[str], live_cols: Optional[int] = None):
-    """(P^T codes, scales, stage bytes) of softmax(S) over its last dim through `quantizer`
-    (mxq/nn/_attention.py:136-139), as one kernel (mxq_softmax_quantize_t): for float32 rows of 32 < T <= 2048
-    keys, where torch.softmax runs its persistent softmax, which the kernel reproduces bit for bit, and an
-    MX-Gemmini quantizer of blocks of 32 along the keys.  With live_cols (P^T's columns per problem), the third
-    item is the P V product's a_live hint for these codes, else None.  None where the kernel does not apply."""
-    from .. import _lib
+def _softmax_pt_spec(quantizer, block_size: int, vector: Optional[str], T: int):
+    """The kernel's block spec when mxq_softmax_quantize_t computes softmax over T keys and `quantizer`'s P^T
+    (torch's persistent softmax, for 32 < T <= 2048 keys, and an MX-Gemmini quantizer of blocks of 32 along the
+    keys), else None."""
     from ..block import mxgemmini
     from ..element_quant.formats import get
     from ..scale_factor import MXQUANT_FLOOR
-    T = S.shape[-1]
-    if vector is not None or S.dtype != torch.float32 or not 32 < T <= 2048 or block_size != 32:
+    if vector is not None or not 32 < T <= 2048 or block_size != 32:
         return None
-    if quantizer.func is not mxgemmini.quantize or quantizer.keywords.get("block_size", 32) != 32:
+    if not isinstance(quantizer, partial) or quantizer.func is not mxgemmini.quantize or \
+            quantizer.keywords.get("block_size", 32) != 32:
         return None
     kw = quantizer.keywords
     f = get(kw["fmt"])
     if f is None:
         return None
-    spec = mxgemmini.spec(f, kw.get("rounding_mode", "ties_away"), kw.get("scale_floor", MXQUANT_FLOOR), kw.get("via"))
+    return mxgemmini.spec(f, kw.get("rounding_mode", "ties_away"), kw.get("scale_floor", MXQUANT_FLOOR), kw.get("via"))
+
+
+def _softmax_pt(S: torch.Tensor, quantizer, block_size: int, vector: Optional[str], live_cols: Optional[int] = None,
+                tail: Optional["_lib.SoftmaxTail"] = None):
+    """(P^T codes, scales, stage bytes) of softmax(S) over its last dim through `quantizer`
+    (mxq/nn/_attention.py:136-139), as one kernel (mxq_softmax_quantize_t): for float32 rows of 32 < T <= 2048
+    keys, where torch.softmax runs its persistent softmax, which the kernel reproduces bit for bit, and an
+    MX-Gemmini quantizer of blocks of 32 along the keys.  With live_cols (P^T's columns per problem), the third
+    item is the P V product's a_live hint for these codes, else None.  With a tail (include/mxq_hip.h
+    mxq_softmax_tail), S holds each 64-row group's keys below its k_end only.  None where the kernel does not
+    apply."""
+    from .. import _lib
+    T = S.shape[-1]
+    spec = _softmax_pt_spec(quantizer, block_size, vector, T) if S.dtype == torch.float32 else None
+    if spec is None:
+        return None
     Sc = S.contiguous()
     R = Sc.numel() // T
     PT_P = torch.empty((T, R), dtype=torch.float32, device=S.device)
@@ -465,7 +502,7 @@ def _softmax_pt(S: torch.Tensor, quantizer, block_size: int, vector: Optional[st
         live = torch.empty((R // live_cols, -(-T // 32), live_cols // 32), dtype=torch.uint8, device=S.device)
     with torch.cuda.device(S.device):
         _lib.run("mxq_softmax_quantize_t", _lib.ptr(Sc), R, T, _lib.ptr(PT_P), _lib.ptr(PT_X), spec, _lib.ptr(live),
-                 live_cols or 0, _lib.stream(S.device))
+                 live_cols or 0, None if tail is None else ctypes.byref(tail), _lib.stream(S.device))
     return PT_P, PT_X, live
 
 

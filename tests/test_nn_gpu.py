@@ -287,13 +287,14 @@ def test_attend_skip_hints(cuda, monkeypatch, kind):
         mask = torch.where(j > i, -30.0, 0.0)[None, None]
     else:
         mask = torch.where((j > i) | (j < i - 96), low, 0.0)[None, None]
-    marked = []
+    marked, tails = [], []
     orig = at._hints
 
     def spy(*a, **kw):
-        skip, k_end = orig(*a, **kw)
+        skip, k_end, tail_max = orig(*a, **kw)
         marked.append(0 if skip is None else int(skip.sum()))
-        return skip, k_end
+        tails.append(tail_max is not None)
+        return skip, k_end, tail_max
 
     monkeypatch.setattr(at, "_hints", spy)
     hw, hwo = _hw(mxq), _hw_oracle()
@@ -302,6 +303,45 @@ def test_attend_skip_hints(cuda, monkeypatch, kind):
     assert_bits_equal(got, want, f"attend with {kind} mask")
     assert marked, "the batched path ran"
     assert (sum(marked) == 0) if kind == "causal_weak" else (sum(marked) > 0), marked
+    assert all(tails), "scores past k_end are left unstored (256 query rows per call, a multiple of 64)"
+
+
+@pytest.mark.parametrize("kind", ["query_row_masked", "positive_tail", "mixed_group"])
+def test_attend_tail_full_rows(cuda, monkeypatch, kind):
+    """Rows for which the keys past their 64-row group's k_end matter, so the softmax reads those scores from
+    the mask and the group writes P^T there: a query row whose every key is masked (softmax uniform over all
+    keys), a mask whose masked value is +max (the masked keys win), and one such row inside a group of ordinary
+    causal rows (the group's other rows keep +0 past k_end).  Every output bit for bit against the oracle; the
+    tail path taken."""
+    import mxq
+    from mxq.nn import _attention as at
+    B, H, Hkv, T, D = 1, 2, 1, 256, 64
+    g = torch.Generator().manual_seed(13)
+    q, k, v = (torch.randn(B, h, T, D, generator=g) for h in (H, Hkv, Hkv))
+    low, high = torch.finfo(torch.float32).min, torch.finfo(torch.float32).max
+    i, j = torch.arange(T)[:, None], torch.arange(T)[None, :]
+    if kind == "query_row_masked":
+        mask = torch.where(j > i, low, 0.0)[None, None].clone()
+        mask[0, 0, 70] = low
+    elif kind == "positive_tail":
+        mask = torch.where(j > i, high, 0.0)[None, None]
+    else:
+        mask = torch.where(j > i, low, 0.0)[None, None].clone()
+        mask[0, 0, 100, 200:] = high                       # row 100 of group 64..127 prefers its masked keys
+    tails = []
+    orig = at._hints
+
+    def spy(*a, **kw):
+        out = orig(*a, **kw)
+        tails.append(out[2] is not None)
+        return out
+
+    monkeypatch.setattr(at, "_hints", spy)
+    hw, hwo = _hw(mxq), _hw_oracle()
+    got = mxq.nn.attend(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), D ** -0.5, hw, hw).cpu().numpy()
+    want = oatt.attend(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), D ** -0.5, hwo, hwo, _gpu_softmax)
+    assert_bits_equal(got, want, f"attend, {kind}")
+    assert tails and all(tails)
 
 
 def _c5_inputs(Hkv=32):
