@@ -31,7 +31,7 @@ typedef void* mxq_stream_t;
  *   1  the first release.
  *   2  mxq_lut_tables takes the code format (fmt_e, fmt_m) before the grid; mxq_systolic_hints gained a_live
  *      and c_end; mxq_softmax_quantize_t takes a tail; mxq_mask_minabs and mxq_attend_hints give the largest
- *      mask values; mxq_systolic_fast_lanes. */
+ *      mask values; mxq_systolic_fast_lanes; the dither entry points. */
 #define MXQ_ABI_VERSION 2
 
 enum { MXQ_OK = 0, MXQ_EINVAL = 1, MXQ_EHIP = 2 };
@@ -461,6 +461,24 @@ int mxq_microsoft(const float* z, float* out, int64_t n, int32_t ebits, int32_t 
 /* A scale-factor rule of `spec` (MXQUANT, OCP or OCP_NO_CLIP with the MICROSOFT element fields) applied to
  * block maxima.  Replaces mxq/scale_factor.py:40-81. */
 int mxq_scale_factor(const float* amax, float* out, int64_t n, const mxq_block_spec* spec, mxq_stream_t stream);
+
+/* microxcaling's "dither" rounding, sign(A) * floor(|A| + u), with the uniforms the caller drew as the reference
+ * does (torch.rand_like of the tensor it rounds, in [0, 1)).  mxq_microsoft_dither: mxq_microsoft with u[i]
+ * for element i (replaces mxq/element_quant/microsoft.py:18-23 with round="dither",
+ * mxq/microxcaling/elemwise.py:41-43).  mxq_scale_factor_dither: OCP_NO_CLIP's rule with u[i] for maximum i
+ * (replaces mxq/scale_factor.py:68-81 with rounding_mode="dither").  mxq_block_quantize_dither:
+ * mxq_block_quantize for spec's MICROSOFT element rule (its `rounding` field ignored) rounding by dither: element
+ * (o, k, i) of V viewed as (outer, n, inner) takes u[((o * inner + i) * nb + k / block_size) * block_size +
+ * k % block_size], nb = ceil(n / block_size), the order of the reference's blocked tensor (the block axis moved
+ * last, then zero-padded); with OCP_NO_CLIP its block's rounding of amax / X takes u_amax[(o * inner + i) * nb +
+ * k / block_size] (NULL otherwise).  Replaces mxq/block/ocp.py:35-49 with rounding_mode="dither". */
+int mxq_microsoft_dither(const float* z, const float* u, float* out, int64_t n, int32_t ebits, int32_t mbits,
+                         float max_norm, int32_t saturate, mxq_stream_t stream);
+int mxq_scale_factor_dither(const float* amax, const float* u, float* out, int64_t n, const mxq_block_spec* spec,
+                            mxq_stream_t stream);
+int mxq_block_quantize_dither(const void* V, int32_t v_dtype, const float* u_amax, const float* u, float* P,
+                              float* X, int64_t outer, int64_t n, int64_t inner, int64_t block_size,
+                              const mxq_block_spec* spec, mxq_stream_t stream);
 
 /* arith.exact_add (float32 operands).  Replaces mxq/arith.py:68-103. */
 int mxq_exact_add(const float* a, const float* b, float* out, int64_t n, int32_t e, int32_t m, int32_t mode,

@@ -227,7 +227,7 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
                                                    const float* __restrict__ safe, int ns,
                                                    const int* __restrict__ safe_order, int max_iters,
                                                    float* __restrict__ T, uint32_t* __restrict__ code_map,
-                                                   mxq_lut::CodeGrid cg) {
+                                                   mxq_lut::CodeGrid cg, int exact) {
   constexpr int kRounds = kMaxGrid / 64;
   __shared__ double x_s[kMaxGrid];
   __shared__ double w_s[kMaxGrid];
@@ -235,6 +235,7 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
   __shared__ double sums[kSize], wsum[kSize];
   __shared__ double pw[kMaxGrid], pwx[kMaxGrid];     // inclusive prefix sums of the counts and counts x values
   __shared__ int lo_s[kSize], hi_s[kSize];           // a pass's cluster ranges of bins (lo -1: empty)
+  __shared__ int lab_s[kMaxGrid];                    // a pass's cluster of each bin (sums not exact)
   __shared__ float safe_s[kMaxGrid];
   __shared__ int order_s[kMaxGrid];
   __shared__ unsigned char member[kMaxGrid];
@@ -378,8 +379,9 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
   // ---- Lloyd passes
   // A pass assigns each bin its nearest centre (first minimum).  The centres are ascending and the bins too, so
   // the assignment is non-decreasing along the bins and every cluster is a run of bins: its sums are then
-  // differences of the prefix sums (exact, as every sum here is).  A pass whose assignment is not monotone
-  // (rounding at a near-tie could make one) adds its bins into the sums by LDS atomics instead.  The new
+  // differences of the prefix sums (exact while sums_exact holds).  A pass whose assignment is not monotone
+  // (rounding at a near-tie could make one) adds its bins into the sums by LDS atomics instead; groups whose
+  // sums may round add each cluster's bins in bin order, a lane a cluster, as the reference does.  The new
   // centres are sorted and deduplicated only when they need it (a stable sort of ascending, distinct values
   // is the identity).
   for (int it = 0; it < max_iters && !stop; ++it) {
@@ -423,8 +425,15 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
     }
     if (lane < kSize) { lo_s[lane] = -1; hi_s[lane] = -1; sums[lane] = 0.0; wsum[lane] = 0.0; }
     __syncthreads();
-    const bool runs = __all(mono);
-    if (runs) {
+    const bool all_runs = __all(mono);
+    const bool runs = exact && all_runs;
+    if (!exact) {
+#pragma unroll
+      for (int r = 0; r < kRounds; ++r) {
+        const int i = r * 64 + lane;
+        if (r < nr && i < nv) lab_s[i] = best[r];
+      }
+    } else if (runs) {
 #pragma unroll
       for (int r = 0; r < kRounds; ++r) {
         if (r >= nr) break;
@@ -457,6 +466,15 @@ __global__ void __launch_bounds__(64) k_lut_kmeans(mxq_lut::CountSource src, int
         const int lo = lo_s[lane], hi = hi_s[lane];
         sw = lo < 0 ? 0.0 : pw[hi] - (lo > 0 ? pw[lo - 1] : 0.0);
         swx = lo < 0 ? 0.0 : pwx[hi] - (lo > 0 ? pwx[lo - 1] : 0.0);
+      } else if (!exact) {
+        // the reference's scatter_add order: the cluster's bins one by one, in bin order
+        sw = 0.0;
+        swx = 0.0;
+        for (int i = 0; i < nv; ++i)
+          if (lab_s[i] == lane) {
+            sw += w_s[i];
+            swx += w_s[i] * x_s[i];
+          }
       }
       cn = (sw > 0.0) ? swx / sw : C[lane];
     }
@@ -754,10 +772,11 @@ namespace mxq_lut {
 
 int launch_kmeans(const CountSource& src, int64_t ng, int nv, const float* grid, const float* safe, int ns,
                   const int* safe_order, int max_iters, float* T, uint32_t* code_map, const CodeGrid& cg,
-                  hipStream_t st) {
+                  bool exact_sums, hipStream_t st) {
   if (code_map && !cg.ok) return mxq::invalid("k-means: a code map needs the format's code grid");
   mxq::KernelTimer timer("lut_kmeans", st);
-  k_lut_kmeans<<<dim3((unsigned)ng), 64, 0, st>>>(src, nv, grid, safe, ns, safe_order, max_iters, T, code_map, cg);
+  k_lut_kmeans<<<dim3((unsigned)ng), 64, 0, st>>>(src, nv, grid, safe, ns, safe_order, max_iters, T, code_map, cg,
+                                                  exact_sums ? 1 : 0);
   return mxq::check_launch("mxq_lut k-means");
 }
 
@@ -799,7 +818,9 @@ extern "C" int mxq_lut_tables(const float* P, int64_t K, int64_t n, int32_t grou
     if (int rc = mxq::check_launch("mxq_lut_tables histogram")) return rc;
   }
   const mxq_lut::CountSource src{counts, 1, 0, ng, 0};
-  return mxq_lut::launch_kmeans(src, ng, nv, grid, safe, ns, safe_order, max_iters, T, nullptr, mxq_lut::CodeGrid{}, st);
+  const int64_t per_group = K * ((int64_t(1) << group) < n ? (int64_t(1) << group) : n);
+  return mxq_lut::launch_kmeans(src, ng, nv, grid, safe, ns, safe_order, max_iters, T, nullptr, mxq_lut::CodeGrid{},
+                                mxq_lut::sums_exact(per_group, fmt_e, fmt_m), st);
 }
 
 extern "C" int mxq_lut_pick(const float* P, int64_t K, int64_t n, int32_t group, const float* T, int32_t width,

@@ -1,6 +1,8 @@
 // Shared by the LUT translation units: table sizes, where a code sits in its format's value grid, and the
 // k-means launch (lut.hip) that both the standalone tables and the fused LUT operand path use.
 #pragma once
+#include <cmath>
+
 #include "mxq_common.h"
 #include "mxq_numerics.h"
 
@@ -19,6 +21,22 @@ struct CodeGrid {
   int sign_at;       // e + m
   int cmax;
 };
+
+// Whether a group's float64 sums of count x value are exact in any order: every such sum is a multiple of the
+// format's smallest step and at most per_group x its largest value in magnitude, so it is exact while that bound
+// over the step stays below 2^53 (always for E4M3, E3M2 and E2M3; for E5M2 up to about 2.4 M codes a group).
+// Past it, k-means adds each cluster's bins one by one in bin order, as the reference's scatter_add does.
+inline bool sums_exact(int64_t per_group, int e, int m) {
+  double top = 0.0;
+  if (e == 4 && m == 3) top = 448.0;
+  else if (e == 5 && m == 2) top = 57344.0;
+  else if (e == 3 && m == 2) top = 28.0;
+  else if (e == 2 && m == 3) top = 7.5;
+  if (top == 0.0) return false;
+  const int bias = (1 << (e - 1)) - 1;
+  const double step = std::ldexp(1.0, 1 - bias - m);
+  return (double)per_group * top / step < 9007199254740992.0;
+}
 
 inline CodeGrid code_grid_of(int e, int m, int nv) {
   CodeGrid g{};
@@ -85,9 +103,9 @@ inline int64_t stripe_rows(int64_t K, int64_t col_blocks, int64_t target) {
 
 // k-means over each of ng groups (one 64-lane workgroup each): T (ng x kSize) and, when code_map is not NULL,
 // per group and element code c < 2^(e+m+1) the bits of the entry pick chooses for the code's value (NaN for a
-// code with no bin) at code_map[g * ncodes + c].
+// code with no bin) at code_map[g * ncodes + c].  exact_sums: sums_exact() holds for the groups.
 int launch_kmeans(const CountSource& src, int64_t ng, int nv, const float* grid, const float* safe, int ns,
                   const int* safe_order, int max_iters, float* T, uint32_t* code_map, const CodeGrid& cg,
-                  hipStream_t st);
+                  bool exact_sums, hipStream_t st);
 
 }  // namespace mxq_lut

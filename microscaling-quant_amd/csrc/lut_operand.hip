@@ -202,7 +202,10 @@ extern "C" int mxq_block_lut(const void* V, int32_t v_dtype, int64_t K, int64_t 
     if (rc) return rc;
   }
   const mxq_lut::CountSource src{partial, (int)p.nsplit, p.split_stride, p.nunits, p.shift};
-  if (int rc = mxq_lut::launch_kmeans(src, p.ng, nv, grid, safe, ns, safe_order, max_iters, T, map, cg, st)) return rc;
+  const int64_t per_group = K * ((int64_t(1) << group) < n ? (int64_t(1) << group) : n);
+  if (int rc = mxq_lut::launch_kmeans(src, p.ng, nv, grid, safe, ns, safe_order, max_iters, T, map, cg,
+                                      mxq_lut::sums_exact(per_group, spec->e, spec->m), st))
+    return rc;
   {
     mxq::KernelTimer timer("lut_pick_codes", st);
     const int64_t col_blocks = mxq::ceil_div(n, p.pick_cw);

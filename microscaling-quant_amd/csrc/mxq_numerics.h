@@ -27,6 +27,8 @@
 #include "../../include/mxq_hip.h"
 
 enum { MXQ_TIES_AWAY = 0, MXQ_RNE = 1, MXQ_TRUNC = 2 };
+// microxcaling's "dither" (floor(|A| + u) with a uniform u per element): its element step only
+enum { MXQ_DITHER = 3 };
 enum { MXQ_GRID_QTORCH = 0, MXQ_GRID_IEEE = 1, MXQ_GRID_OCP = 2 };
 
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -280,11 +282,13 @@ MXQ_HD float float_em_quantize64(double z, int e, int m, int mode, int grid, flo
 // order: private_exp = floor(log2(|A| + (A == 0))) clipped at min_exp; out = A / 2^pe * 2^(bits-2); round;
 // out / 2^(bits-2) * 2^pe; saturate (clamp) or overflow to Inf; +-Inf inputs restored.
 template <int MODE>
-MXQ_HD float ms_round_mantissa_t(float A) {
+MXQ_HD float ms_round_mantissa_t(float A, float u = 0.0f) {
   const float absA = fabsf(A);
   const float sgn = (A > 0.0f) ? 1.0f : ((A < 0.0f) ? -1.0f : 0.0f);   // torch.sign (0 for NaN and +-0)
   if constexpr (MODE == MXQ_TRUNC) {
     return sgn * floorf(absA);
+  } else if constexpr (MODE == MXQ_DITHER) {
+    return sgn * floorf(absA + u);                   // u: the element's draw of torch.rand_like, in [0, 1)
   } else if constexpr (MODE == MXQ_TIES_AWAY) {
     return sgn * floorf(absA + 0.5f);
   } else {
@@ -298,7 +302,7 @@ MXQ_HD float ms_round_mantissa_t(float A) {
 }
 
 template <int MODE>
-MXQ_HD float microsoft_quantize_t(float A, int ebits, int mbits, float max_norm, bool saturate) {
+MXQ_HD float microsoft_quantize_t(float A, int ebits, int mbits, float max_norm, bool saturate, float u = 0.0f) {
   const uint32_t ua = f2u(A), aa = ua & 0x7FFFFFFFu;
   if (aa >= 0x7F800000u) return A;                       // NaN stays NaN; +-Inf is restored at the end
   const int min_exp = -(1 << (ebits - 1)) + 2;
@@ -310,7 +314,7 @@ MXQ_HD float microsoft_quantize_t(float A, int ebits, int mbits, float max_norm,
   const float p2 = pow2f(pe);                            // 2 ** private_exp, exact or Inf
   float out = (pe <= 127) ? A * pow2f(-pe) : A / p2;
   out = out * (float)(1 << (mbits - 2));
-  out = ms_round_mantissa_t<MODE>(out);
+  out = ms_round_mantissa_t<MODE>(out, u);
   out = out * pow2f(2 - mbits);
   out = out * p2;
   if (saturate) {
@@ -360,9 +364,12 @@ MXQ_HD float scale_ocp(float amax, int emax, int scale_bits) {
 }
 
 // mxq/scale_factor.py:68-81 `ocp_no_clip`: ocp's X, doubled where microsoft(amax / X) without saturation is Inf.
-MXQ_HD float scale_ocp_no_clip(float amax, int emax, int scale_bits, int ebits, int mbits, float max_norm, int mode) {
+// Mode MXQ_DITHER rounds with u, the block's draw.
+MXQ_HD float scale_ocp_no_clip(float amax, int emax, int scale_bits, int ebits, int mbits, float max_norm, int mode,
+                               float u = 0.0f) {
   const float X = scale_ocp(amax, emax, scale_bits);
-  const float r = microsoft_quantize(amax / X, ebits, mbits, max_norm, mode, false);
+  const float r = mode == MXQ_DITHER ? microsoft_quantize_t<MXQ_DITHER>(amax / X, ebits, mbits, max_norm, false, u)
+                                     : microsoft_quantize(amax / X, ebits, mbits, max_norm, mode, false);
   const bool inf = (f2u(r) & 0x7FFFFFFFu) == 0x7F800000u;
   return inf ? X * 2.0f : X;
 }

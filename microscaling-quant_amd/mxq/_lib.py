@@ -129,6 +129,10 @@ SIGNATURES = {
     "mxq_float_em": (c_i32, [c_ptr, c_i32, c_ptr, c_i64, c_i32, c_i32, c_i32, c_i32, c_f32, c_ptr]),
     "mxq_microsoft": (c_i32, [c_ptr, c_ptr, c_i64, c_i32, c_i32, c_f32, c_i32, c_i32, c_ptr]),
     "mxq_scale_factor": (c_i32, [c_ptr, c_ptr, c_i64, ctypes.POINTER(BlockSpec), c_ptr]),
+    "mxq_microsoft_dither": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i32, c_i32, c_f32, c_i32, c_ptr]),
+    "mxq_scale_factor_dither": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, ctypes.POINTER(BlockSpec), c_ptr]),
+    "mxq_block_quantize_dither": (c_i32, [c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64,
+                                          ctypes.POINTER(BlockSpec), c_ptr]),
     "mxq_exact_add": (c_i32, [c_ptr, c_ptr, c_ptr, c_i64, c_i32, c_i32, c_i32, c_i32, c_f32, c_ptr]),
     "mxq_truncate_significand": (c_i32, [c_ptr, c_ptr, c_i64, c_i32, c_ptr]),
     "mxq_flush_product": (c_i32, [c_ptr, c_ptr, c_i64, c_f32, c_ptr]),
@@ -139,7 +143,7 @@ SIGNATURES = {
 SCALE_NONE, SCALE_MXQUANT, SCALE_OCP, SCALE_OCP_NO_CLIP = 0, 1, 2, 3
 ELEM_NONE, ELEM_QTORCH, ELEM_IEEE, ELEM_OCP, ELEM_MICROSOFT = 0, 1, 2, 3, 4
 MODE_CODE = {"ties_away": 0, "rne": 1, "truncate": 2}
-MS_MODE_CODE = {"nearest": 0, "even": 1, "floor": 2}
+MS_MODE_CODE = {"nearest": 0, "even": 1, "floor": 2, "dither": 3}
 GRID_CODE = {"qtorch": 0, "ieee": 1, "ocp": 2}
 ARITH_MXGEMMINI, ARITH_MXQUANT = 0, 1
 

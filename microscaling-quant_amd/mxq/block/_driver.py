@@ -100,6 +100,35 @@ def quantize_fused(V: torch.Tensor, axis: int, block_size: int, spec: _lib.Block
     return _lib.back(P, V), _lib.back(X, V)
 
 
+def quantize_dither(V: torch.Tensor, axis: int, block_size: int, spec: _lib.BlockSpec) -> Tuple[torch.Tensor, torch.Tensor]:
+    """quantize_fused for microxcaling's element step rounding by dither (mxq_block_quantize_dither).  The
+    uniforms are drawn on V's device in the reference's order: one per block maximum when the scale rule rounds
+    the maximum (ocp_no_clip), then one per element of the blocked tensor (..., nblocks, block_size), padding
+    included."""
+    from ..element_quant.microsoft import draws
+    axis = _axis(V, axis)
+    _check_block(block_size)
+    outer, n, inner = _view3(V.shape, axis)
+    nb = -(-n // block_size)
+    u_amax = draws(V, outer * inner * nb) if spec.scale_rule == _lib.SCALE_OCP_NO_CLIP else None
+    u = draws(V, outer * inner * nb * block_size)
+    dev = _lib.compute_device(V)
+    Vd = _lib.to_device(V.detach(), dev)
+    if Vd.dtype not in _NATIVE:
+        Vd = Vd.to(torch.float32)
+    Vd = Vd.contiguous()
+    xshape = list(Vd.shape)
+    xshape[axis] = nb
+    P = torch.empty(Vd.shape, dtype=torch.float32, device=dev)
+    X = torch.empty(xshape, dtype=torch.float32, device=dev)
+    u_amax = None if u_amax is None else _lib.to_device(u_amax, dev)
+    u = _lib.to_device(u, dev)
+    with torch.cuda.device(dev):
+        _lib.run("mxq_block_quantize_dither", _lib.ptr(Vd), _NATIVE[Vd.dtype], _lib.ptr(u_amax), _lib.ptr(u),
+                 _lib.ptr(P), _lib.ptr(X), outer, n, inner, block_size, spec, _lib.stream(dev))
+    return _lib.back(P, V), _lib.back(X, V)
+
+
 def _transposed_view(V: torch.Tensor, axis: int, block_size: int) -> bool:
     """V (n x inner) is the transpose of a row-major matrix and is quantized along axis 0 in blocks of 32."""
     return (V.ndim == 2 and axis == 0 and block_size == 32 and not V.is_contiguous()

@@ -4,7 +4,9 @@
 
 = scale_factor.ocp (shared exponent floor(log2 amax) - emax, E8M0) then microxcaling's element step
 (saturate, subnormals kept); one fused kernel.  P * expand(X) equals microxcaling's _quantize_mx.
-`rounding_mode`: "even" (RNE), "nearest" (ties away), "floor".  `placement` picks step 1:
+`rounding_mode`: "even" (RNE), "nearest" (ties away), "floor", "dither" (uniforms drawn as the reference draws
+them: for no_clip one per block maximum first, then one per element of the blocked, zero-padded tensor, on V's
+device).  `placement` picks step 1:
     top         the spec: block max in the format's top binade, clipped to max_norm when it rounds above
     below_top   one binade down: never clips, the top binade unused
     no_clip     top, except the blocks that would clip go one binade down
@@ -43,7 +45,10 @@ def quantize(V: torch.Tensor, fmt: Union[str, Format], axis: int = 0, block_size
     if f is None:
         return _driver.quantize_fused(V, axis, block_size, _lib.BlockSpec())
     _driver._axis(V, axis)
-    return _driver.quantize_fused(V, axis, block_size, spec(f, rounding_mode, scale_bits, placement))
+    sp = spec(f, rounding_mode, scale_bits, placement)
+    if rounding_mode == "dither":
+        return _driver.quantize_dither(V, axis, block_size, sp)
+    return _driver.quantize_fused(V, axis, block_size, sp)
 
 
 def dequantize(P: torch.Tensor, X: torch.Tensor, axis: int = 0, block_size: int = _driver.BLOCK) -> torch.Tensor:

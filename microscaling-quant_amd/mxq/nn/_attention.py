@@ -198,6 +198,9 @@ def _one_call(q_b, ops: _KVOperands, bias, scale, qk: Scheme, pv: Scheme, vector
 #: score entries per batched launch (problems x n*m x Tk float32): 4 GiB
 ELEMENTS_PER_LAUNCH = 1 << 30
 
+#: bytes of prepared query codes and scales (Q^T of the chunks waiting for their launches) held at once
+PREPARED_BYTES = 1 << 28
+
 
 def _columnwise(quantizer, block_size: int) -> bool:
     """A library block quantizer with blocks along axis 0: every column is quantized on its own, so the columns
@@ -346,14 +349,25 @@ class _Batched:
         kv = (KT_P, KT_X, V_P, V_X)
         k_amax = _group_amax(KT_P, KT_X, qk.block_size, Z) if bias is not None else None
         qg = q.reshape(Z, n, dims.Tq, D)
-        # every chunk's operands, flags and hints first; the flags then come over in one transfer into pinned
-        # memory, queued ahead of the matmuls with an event behind it, so the host queues the matmuls while the
-        # GPU works, then waits for the copy alone and returns without waiting for the matmuls
-        chunks = []
+        # chunks are prepared (Q^T's codes, flags, hints) in batches that stop once they hold PREPARED_BYTES of
+        # codes and scales, so the prepared operands stay bounded (by that plus one chunk) however long the input
+        batch, held = [], 0
         for s0 in range(0, dims.Tq, step):
             e0 = min(s0 + step, dims.Tq)
             for z0, z1 in _launch_ranges(B, Hkv, max(1, ELEMENTS_PER_LAUNCH // (n * (e0 - s0) * Tk))):
-                chunks.append(self._prepare(qg, bias, kv, k_amax, scale, vector, dims, z0, z1, s0, e0))
+                c = self._prepare(qg, bias, kv, k_amax, scale, vector, dims, z0, z1, s0, e0)
+                batch.append(c)
+                held += (c.A_P.numel() + c.A_X.numel()) * 4
+                if held >= PREPARED_BYTES:
+                    self._launch(batch, q, qg, bias, kv, scale, vector, rnd, dims, out)
+                    batch, held = [], 0
+        if batch:
+            self._launch(batch, q, qg, bias, kv, scale, vector, rnd, dims, out)
+
+    def _launch(self, chunks, q, qg, bias, kv, scale, vector, rnd, dims: _Dims, out) -> None:
+        """Prepared chunks' launches.  Their flags come over in one transfer into pinned memory, queued ahead of
+        the matmuls with an event behind it, so the host queues the matmuls while the GPU works, then waits for
+        the copy alone and returns without waiting for the matmuls."""
         if bias is not None:
             flags = torch.cat([c.flags for c in chunks])
             host = torch.empty(flags.shape, dtype=flags.dtype, pin_memory=True)

@@ -88,4 +88,17 @@ def ocp_no_clip(amax: torch.Tensor, fmt, rounding_mode: str = "even", scale_bits
     if f is None:
         raise ValueError(f"{fmt!r} is pass-through (no element format); it has no scale")
     check_mode(rounding_mode)
-    return _apply(amax, ocp_no_clip_spec(f, rounding_mode, scale_bits))
+    spec = ocp_no_clip_spec(f, rounding_mode, scale_bits)
+    if rounding_mode != "dither":
+        return _apply(amax, spec)
+    # dither rounds amax / X with one draw per maximum, as rand_like(amax / X) (mxq/scale_factor.py:78-80)
+    from .element_quant.microsoft import draws
+    if amax.dtype != torch.float32:
+        raise TypeError(f"mxq.scale_factor: float32 block maxima required, got {amax.dtype}")
+    u = draws(amax, amax.numel())
+    dev, a = _lib.ew_prepare(amax, torch.float32)
+    out = torch.empty_like(a)
+    with torch.cuda.device(dev):
+        _lib.run("mxq_scale_factor_dither", _lib.ptr(a), _lib.ptr(_lib.to_device(u, dev)), _lib.ptr(out),
+                 out.numel(), spec, _lib.stream(dev))
+    return _lib.back(out, amax)

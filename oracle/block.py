@@ -87,19 +87,23 @@ def mxgemmini_quantize(V, fmt, axis=0, block_size=BLOCK, rounding_mode="ties_awa
     return compose(V, lambda a: nx.scale_mxquant(a, scale_floor), elem, axis, block_size)
 
 
-def ocp_quantize(V, fmt, axis=0, block_size=BLOCK, rounding_mode="even", scale_bits=8, placement="top"):
-    """mxq/block/ocp.py:35-49."""
+def ocp_quantize(V, fmt, axis=0, block_size=BLOCK, rounding_mode="even", scale_bits=8, placement="top",
+                 draws=None):
+    """mxq/block/ocp.py:35-49.  draws = (u_amax, u) for rounding_mode "dither": the uniforms rand_like drew for
+    the block maxima (no_clip only, else None) and for the blocked tensor (..., nblocks, block_size), flat in
+    those tensors' order."""
     f = _fmt(fmt)
     if f is None:
         return compose(V, None, None, axis, block_size)
+    u_amax, u = draws if draws is not None else (None, None)
     emax = nx.FORMATS[f][2]
     if placement == "top":
         scale = lambda a: nx.scale_ocp(a, emax, scale_bits)                       # noqa: E731
     elif placement == "below_top":
         scale = lambda a: nx.scale_ocp_below_top(a, emax, scale_bits)             # noqa: E731
     else:
-        scale = lambda a: nx.scale_ocp_no_clip(a, f, rounding_mode, scale_bits)   # noqa: E731
-    return compose(V, scale, lambda z: nx.microsoft_fmt(z, f, rounding_mode), axis, block_size)
+        scale = lambda a: nx.scale_ocp_no_clip(a, f, rounding_mode, scale_bits, u_amax)   # noqa: E731
+    return compose(V, scale, lambda z: nx.microsoft_fmt(z, f, rounding_mode, u), axis, block_size)
 
 
 def nblocks(n, block_size=BLOCK):

@@ -198,8 +198,11 @@ def _ocp(z, e, m, rounding_mode):
 
 
 # --------------------------------------------------------------------------- microxcaling element step
-def _ms_round_mantissa(A, mode):
-    """mxq/microxcaling/elemwise.py:29-60 (names: nearest = ties_away, even = rne, floor = truncate)."""
+def _ms_round_mantissa(A, mode, u=None):
+    """mxq/microxcaling/elemwise.py:29-60 (names: nearest = ties_away, even = rne, floor = truncate).  "dither"
+    (:41-43) rounds with u, the uniforms torch.rand_like drew for A (float32, A's shape)."""
+    if mode == "dither":
+        return tsign(A) * np.floor(np.abs(A) + f32(u).reshape(A.shape))
     if mode == "floor":
         return tsign(A) * np.floor(np.abs(A))
     if mode == "nearest":
@@ -211,8 +214,9 @@ def _ms_round_mantissa(A, mode):
     raise ValueError(mode)
 
 
-def microsoft(A, ebits, mbits, max_norm, mode="even", saturate_normals=True):
-    """mxq/microxcaling/elemwise.py:63-151 `_quantize_elemwise_core` (float formats, allow_denorm=True) on float32."""
+def microsoft(A, ebits, mbits, max_norm, mode="even", saturate_normals=True, u=None):
+    """mxq/microxcaling/elemwise.py:63-151 `_quantize_elemwise_core` (float formats, allow_denorm=True) on float32;
+    u: the draws for mode "dither"."""
     A = f32(A)
     with np.errstate(all="ignore"):
         private_exp = np.floor(log2_f32(np.abs(A) + (A == 0).astype(F32)))
@@ -220,7 +224,7 @@ def microsoft(A, ebits, mbits, max_norm, mode="even", saturate_normals=True):
         private_exp = np.maximum(private_exp, F32(min_exp))          # torch clip(min): NaN stays NaN
         p2 = exp2_int(private_exp)
         out = A / p2 * F32(2 ** (mbits - 2))
-        out = _ms_round_mantissa(out, mode)
+        out = _ms_round_mantissa(out, mode, u)
         out = out / F32(2 ** (mbits - 2)) * p2
         if saturate_normals:
             out = np.clip(out, F32(-max_norm), F32(max_norm))
@@ -231,10 +235,10 @@ def microsoft(A, ebits, mbits, max_norm, mode="even", saturate_normals=True):
     return out.astype(F32)
 
 
-def microsoft_fmt(z, fmt, rounding_mode="even"):
+def microsoft_fmt(z, fmt, rounding_mode="even", u=None):
     """mxq/element_quant/microsoft.py:18-23."""
     eb, mb, _, mn = FORMATS[fmt][4]
-    return microsoft(z, eb, mb, mn, rounding_mode, True)
+    return microsoft(z, eb, mb, mn, rounding_mode, True, u)
 
 
 # ---------------------------------------------------------------------------------------- scale factors
@@ -270,12 +274,12 @@ def scale_ocp_below_top(amax, emax, scale_bits=8):
     return scale_ocp(amax, emax - 1, scale_bits)
 
 
-def scale_ocp_no_clip(amax, fmt, rounding_mode="even", scale_bits=8):
-    """mxq/scale_factor.py:68-81."""
+def scale_ocp_no_clip(amax, fmt, rounding_mode="even", scale_bits=8, u=None):
+    """mxq/scale_factor.py:68-81 (u: the draws for rounding_mode "dither", one per maximum)."""
     e, m, emax, mn, (eb, mb, _, _) = FORMATS[fmt]
     X = scale_ocp(amax, emax, scale_bits)
     with np.errstate(all="ignore"):
-        rounded = microsoft(f32(amax) / X, eb, mb, mn, rounding_mode, saturate_normals=False)
+        rounded = microsoft(f32(amax) / X, eb, mb, mn, rounding_mode, saturate_normals=False, u=u)
         return np.where(np.isinf(rounded), X * F32(2), X).astype(F32)
 
 

@@ -59,6 +59,24 @@ def test_tables_pick_against_oracle(cuda, fmt):
         assert np.array_equal(I, ol.pick(P, wT, G)), f"pick {shape}"
 
 
+def test_tables_past_exact_sums(cuda):
+    """lut.tables on E5M2 codes with 4 M codes in one group (4096 x 1024, group 10): past about 2.4 M codes of a
+    format reaching 57344 in steps of 2^-16, float64 sums of count x value can round, so the k-means adds each
+    cluster's bins in bin order (the reference's scatter_add order) instead of by prefix differences.  Tables and
+    picks against the oracle (numpy's add.at, also in bin order); the input is checked to be past the bound."""
+    from mxq import lut
+    rng = np.random.default_rng(41)
+    vals, _, _ = ol.tables_of("MXFP8_E5M2")
+    grid = np.unique(vals[np.isfinite(vals)])
+    K, n, G = 4096, 1024, 10
+    P = grid[rng.integers(0, grid.size, (K, n))].astype(np.float32)
+    P[rng.random((K, n)) < 0.6] = -57344.0
+    assert K * n * 57344.0 / 2.0 ** -16 >= 2.0 ** 53
+    T = lut.tables(torch.from_numpy(P).cuda(), "MXFP8_E5M2", group=G, max_iters=50)
+    wT = ol.tables(P, "MXFP8_E5M2", G, 50)
+    assert_bits_equal(T.cpu().numpy(), wT, "tables of one 4 M-code E5M2 group")
+
+
 def test_c4_shape(cuda):
     """The LUT benchmark shape: block.lut MXFP6_E3M2 on 4096 x 4096, group 1, 50 iterations (2048 tables)."""
     from mxq import block

@@ -233,11 +233,13 @@ def test_exact_core_matches_eager(cuda):
 
 
 def test_attend_batched_launch_ranges(cuda, monkeypatch):
-    """The batched path split into launches of fewer pairs than a batch row holds, two batch rows with their
-    own left-padding masks, GQA 2:1: bit for bit against the oracle's per-call loop."""
+    """The batched path split into launches of fewer pairs than a batch row holds, each launched as soon as it
+    is prepared (a budget of one byte of prepared codes), two batch rows with their own left-padding masks, GQA
+    2:1: bit for bit against the oracle's per-call loop."""
     import mxq
     from mxq.nn import _attention
     monkeypatch.setattr(_attention, "ELEMENTS_PER_LAUNCH", 3 * 2 * 48 * 48)
+    monkeypatch.setattr(_attention, "PREPARED_BYTES", 1)
     B, H, Hkv, T, D = 2, 8, 4, 48, 32
     g = torch.Generator().manual_seed(9)
     q, k, v = (torch.randn(B, h, T, D, generator=g) for h in (H, Hkv, Hkv))
@@ -448,3 +450,63 @@ def test_softmax_quantize_t_against_torch(cuda, T):
     nz = (Pn.reshape(nb, 32, 3, 3, 32) != 0).any(axis=(1, 4))                   # stage, problem, group
     bad = ~np.isfinite(X.cpu().numpy()).reshape(nb, 3, 3, 32).all(axis=3)
     assert np.array_equal(live.cpu().numpy(), (nz | bad).transpose(1, 0, 2).astype(np.uint8))
+
+
+def test_exp_underflows_past_minus_128(cuda):
+    """The softmax kernel's tail rule rests on exp(x) = +0 on the device for every float32 x <= -128 (e^-103.98 is
+    already below half the smallest subnormal): every float32 in [-512, -128] and a strided sample of the rest down
+    to -Inf, through torch.exp on the GPU (the same expf the kernel reproduces bit for bit)."""
+    lo, hi = 0xC3000000, 0xC4000000                       # -128 .. -512 as bit patterns
+    dense = torch.arange(lo, hi + 1, dtype=torch.int64, device="cuda").to(torch.int32).view(torch.float32)
+    sparse = torch.arange(hi, 0xFF800001, 4099, dtype=torch.int64, device="cuda").to(torch.int32).view(torch.float32)
+    for x in (dense, sparse, torch.tensor([float("-inf")], device="cuda")):
+        e = torch.exp(x)
+        assert int(e.view(torch.int32).ne(0).sum()) == 0
+
+
+@pytest.mark.parametrize("fmt", ["MXFP8_E4M3", "MXFP4"])
+def test_softmax_tail_against_full_scores(cuda, fmt):
+    """mxq_softmax_quantize_t with a tail (S stored below each 64-row group's k_end only, NaN past it, which it must
+    not read) against the same kernel on the whole S: three problems of 128 rows x 256 keys with their own mask
+    rows, a causal mask (every group takes the short path), one with a query row masked everywhere (its group reads
+    the mask and writes every key) and one with a row whose masked keys carry +max (the same).  Codes, scales and
+    stage bytes bit for bit wherever the tailed call writes them; where it does not (past k_end of a short-path
+    group), the whole-S call has +0 codes and stage bytes 0, so the P V product never reads them."""
+    from functools import partial
+
+    from mxq import _lib, block
+    from mxq.nn import _attention
+    Z, cols, T, scale = 3, 128, 256, 0.125
+    g = torch.Generator(device="cuda").manual_seed(31)
+    low, high = torch.finfo(torch.float32).min, torch.finfo(torch.float32).max
+    i, j = torch.arange(cols, device="cuda")[:, None], torch.arange(T, device="cuda")[None, :]
+    mask = torch.where(j > i + 64, low, 0.0).repeat(Z, 1, 1).contiguous()     # Z x cols x T
+    mask[1, 70] = low
+    mask[2, 10, 200:] = high
+    k_end = torch.tensor([[128, 192]] * Z, dtype=torch.int32, device="cuda")  # group t sees keys < 64 (t + 2)
+    tail_max = torch.empty(Z, 2, device="cuda")
+    for z in range(Z):
+        for t in range(2):
+            tail_max[z, t] = mask[z, 64 * t:64 * t + 64, int(k_end[z, t]):].max()
+    raw = torch.randn(Z, cols, T, device="cuda", generator=g) * 4
+    S_full = (raw * scale + mask).contiguous()
+    kk = torch.arange(T, device="cuda")[None, None, :]
+    ke_row = k_end.repeat_interleave(64, dim=1)[:, :, None]                      # Z x cols x 1
+    S_full = torch.where(kk >= ke_row, 0.0 * scale + mask, S_full)             # what the score step stores there
+    S_part = torch.where(kk >= ke_row, torch.full_like(S_full, float("nan")), S_full)
+    q = partial(block.mxgemmini.quantize, fmt=fmt, axis=0, rounding_mode="rne")
+    epi = _lib.SystolicEpilogue(scale=scale, bf16=0, mask=_lib.ptr(mask), mask_b_stride=cols * T, mask_row_stride=T,
+                                z0=0, z_per_b=1, m=cols)
+    tail = _lib.SoftmaxTail(k_end=_lib.ptr(k_end), tail_max=_lib.ptr(tail_max), score=epi)
+    P, X, live = (t.cpu().numpy() for t in _attention._softmax_pt(S_part.view(Z * cols, T), q, 32, None, cols, tail))
+    wP, wX, wlive = (t.cpu().numpy() for t in _attention._softmax_pt(S_full.view(Z * cols, T), q, 32, None, cols))
+    assert_bits_equal(live, wlive, "stage bytes")
+    full_groups = {(1, 1), (2, 0)}
+    for z in range(Z):
+        for t in range(2):
+            c0, ke = z * cols + 64 * t, int(k_end[z, t])
+            kw = T if (z, t) in full_groups else ke
+            assert_bits_equal(P[:kw, c0:c0 + 64], wP[:kw, c0:c0 + 64], f"codes z{z} t{t}")
+            assert_bits_equal(X[:kw // 32, c0:c0 + 64], wX[:kw // 32, c0:c0 + 64], f"scales z{z} t{t}")
+            if kw < T:
+                assert not wP[kw:, c0:c0 + 64].any() and not wlive[z, kw // 32:, t * 2:t * 2 + 2].any()

@@ -168,6 +168,31 @@ def test_microsoft_nearest_is_ocp_grid_ties_away():
         assert_bits_equal(fl[~band], want[~band], f"{fmt} floor")
 
 
+@pytest.mark.parametrize("fmt", list(nx.FORMATS))
+def test_microsoft_dither_pins(fmt):
+    """microxcaling's dither (floor(|A| + u)) pinned without retyping it: u = 0.5 everywhere is its "nearest";
+    u = 0 is its "floor"; every result is the floor or the next value up (the floor with u just below 1); and
+    stochastic rounding is unbiased, the mean over uniform draws of u being A itself (within 6 standard errors of
+    the grid step) for values inside the format's range."""
+    eb, mb, _, mn = nx.FORMATS[fmt][4]
+    rng = np.random.default_rng(7)
+    A = (rng.standard_normal(4000) * np.exp2(rng.integers(-10, 6, 4000))).astype(np.float32)
+    A = A[np.abs(A) < mn / 2]
+    half, zero = np.full(A.shape, 0.5, np.float32), np.zeros(A.shape, np.float32)
+    top = np.full(A.shape, np.nextafter(np.float32(1), np.float32(0)), np.float32)
+    assert_bits_equal(nx.microsoft(A, eb, mb, mn, "dither", True, half), nx.microsoft(A, eb, mb, mn, "nearest"), "u=1/2")
+    assert_bits_equal(nx.microsoft(A, eb, mb, mn, "dither", True, zero), nx.microsoft(A, eb, mb, mn, "floor"), "u=0")
+    lo, hi = nx.microsoft(A, eb, mb, mn, "floor"), nx.microsoft(A, eb, mb, mn, "dither", True, top)
+    u = rng.random(A.shape).astype(np.float32)
+    d = nx.microsoft(A, eb, mb, mn, "dither", True, u)
+    assert np.all((d == lo) | (d == hi)) and np.all(np.abs(hi) >= np.abs(lo))
+    draws = 400
+    mean = np.mean([nx.microsoft(A, eb, mb, mn, "dither", True, rng.random(A.shape).astype(np.float32))
+                    for _ in range(draws)], axis=0, dtype=np.float64)
+    step = np.abs(hi.astype(np.float64) - lo.astype(np.float64))
+    assert np.all(np.abs(mean - A) <= 6 * step * 0.5 / np.sqrt(draws) + 1e-30)
+
+
 # ---- exact rationals ------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("em", [(4, 3), (4, 4), (4, 6), (6, 9), (5, 10), (8, 7)], ids=lambda em: f"e{em[0]}m{em[1]}")

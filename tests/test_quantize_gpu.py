@@ -403,3 +403,56 @@ def test_c_abi_own_max_norm(cuda, elem):
         _lib.run("mxq_block_quantize", _lib.ptr(Vd), 0, _lib.ptr(P), _lib.ptr(X), 1, 64, 256, 32,
                  ctypes.byref(spec), _lib.stream(Vd.device))
         assert_bits_equal(P.cpu().numpy(), want, f"{elem} E4M3 codes saturating at {max_norm}")
+
+
+@pytest.mark.parametrize("placement", ["top", "below_top", "no_clip"])
+@pytest.mark.parametrize("on", ["cuda", "cpu"])
+def test_ocp_dither(cuda, placement, on):
+    """block.ocp with rounding_mode="dither" (mxq/microxcaling/elemwise.py:41-43): the uniforms are drawn as the
+    reference draws them, on V's device (the GPU's or the CPU's default generator): for no_clip one per block
+    maximum first, then one per element of the blocked, zero-padded tensor.  Reseeding and drawing the same
+    tensors in that order gives the oracle the same draws: codes and scales bit for bit, every format, both
+    layouts, tails."""
+    from mxq import block
+    rng = np.random.default_rng(23)
+    for fmt in FMTS:
+        for shape, axis, bs in [((100, 33), 0, 32), ((5, 70, 3), 1, 16)]:
+            V = (rng.standard_normal(shape) * np.exp2(rng.integers(-8, 8, shape))).astype(np.float32)
+            V.flat[:3] = [0.0, -0.0, 1e-40]
+            torch.manual_seed(1234)
+            P, X = block.ocp.quantize(torch.from_numpy(V).to(on), fmt, axis=axis, block_size=bs,
+                                      rounding_mode="dither", placement=placement)
+            assert P.device.type == on
+            torch.manual_seed(1234)
+            outer, n, inner = int(np.prod(shape[:axis])), shape[axis], int(np.prod(shape[axis + 1:]))
+            nb = -(-n // bs)
+            ua = torch.rand(outer * inner * nb, device=on) if placement == "no_clip" else None
+            u = torch.rand(outer * inner * nb * bs, device=on)
+            wP, wX = ob.ocp_quantize(V, fmt, axis, bs, "dither", 8, placement,
+                                     draws=(None if ua is None else ua.cpu().numpy(), u.cpu().numpy()))
+            assert_bits_equal(X.cpu().numpy(), wX, f"X {fmt} {shape} {placement} dither on {on}")
+            assert_bits_equal(P.cpu().numpy(), wP, f"P {fmt} {shape} {placement} dither on {on}")
+
+
+def test_microsoft_and_no_clip_dither(cuda):
+    """element_quant.microsoft.quantize and scale_factor.ocp_no_clip with "dither": one draw per element (per
+    maximum), torch.rand_like of the rounded tensor on its device; against the oracle given the same draws."""
+    from mxq import scale_factor
+    from mxq.element_quant import microsoft
+    rng = np.random.default_rng(29)
+    for fmt in FMTS:
+        eb, mb, _, mn = nx.FORMATS[fmt][4]
+        z = (rng.standard_normal((64, 48)) * np.exp2(rng.integers(-6, 4, (64, 48)))).astype(np.float32)
+        zt = torch.from_numpy(z).cuda()
+        torch.manual_seed(77)
+        got = microsoft.quantize(zt, fmt, rounding_mode="dither").cpu().numpy()
+        torch.manual_seed(77)
+        u = torch.rand_like(zt).cpu().numpy()
+        assert_bits_equal(got, nx.microsoft(z, eb, mb, mn, "dither", True, u), f"microsoft dither {fmt}")
+        amax = np.abs(z).max(axis=1, keepdims=True)
+        at = torch.from_numpy(amax).cuda()
+        torch.manual_seed(78)
+        X = scale_factor.ocp_no_clip(at, fmt, rounding_mode="dither").cpu().numpy()
+        torch.manual_seed(78)
+        ua = torch.rand_like(at).cpu().numpy()
+        assert_bits_equal(X, nx.scale_ocp_no_clip(amax, fmt, "dither", 8, ua), f"ocp_no_clip dither {fmt}")
