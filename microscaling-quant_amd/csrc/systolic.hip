@@ -122,6 +122,7 @@ struct FastLanes {
   int32_t a_exp[32];     // A's rows of lane i are staged times 2^a_exp[i]: 6 + m_i (e4 lanes), 0 (bf16 lane)
   float rescale[32];     // before e4 lane i the scaled sum is multiplied by 2^(m_i - m_{i-1}) (1: unchanged)
   float split[32];       // 2^(23 - m_i) + 1: split_rne's constant for RNE at m_i fraction bits
+  float magic[32];       // 1.5 * 2^(17 - m_i): (p + magic) - magic rounds p to a multiple of 2^-(6 + m_i)
   float out_scale;       // scaled sum -> sum after the last e4 lane: 2^-(6 + m_last)
   uint32_t pmask;        // product truncation to prod_m fraction bits
   float flush_thr;       // bf16 lane: |product| below this becomes zero
@@ -161,6 +162,11 @@ struct LaneConsts {
   __device__ __forceinline__ float out_scale() const {
     if constexpr (HWF) return 0x1p-12f;                      // 2^-(6 + m of lane 14)
     else return fl.out_scale;
+  }
+  // 1.5 * 2^(17 - m_i): adding and subtracting it rounds a product in value units to the lane's subnormal step
+  __device__ __forceinline__ float magic(int i) const {
+    if constexpr (HWF) return 1.5f * (float)(1u << (17 - hw_final_m(i)));
+    else return fl.magic[i];
   }
 };
 
@@ -777,6 +783,197 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
 }
 
+// ------------------------------------------------------------------------- fast datapath, small grids
+// k_systolic_fast64: k_systolic_fast's datapath for grids too small to give every CU 4 workgroups of 64 x 64
+// outputs (e.g. 512 x 4096 outputs: 512 workgroups), where a workgroup must carry more work per staged byte.
+// Its operands lie whole inside the matrices (M, N and K multiples of 64, rows 16-byte aligned, blocks of 32),
+// so every stage of 64 rows moves straight from global memory into LDS (global_load_lds_dwordx4: no registers,
+// no LDS stores, 1 KB per instruction per wave) while the previous stage is reduced; one barrier per two
+// blocks.  The lanes work in value units: a product is rounded to its lane's subnormal step 2^-(6+m) by adding
+// and subtracting 1.5 * 2^(17-m) (exact: |p| stays far below 2^(16-m) whenever the tile's results are kept),
+// so A is staged as it is, no sum is rescaled between lanes, and every operation issues at full rate.  The
+// sums, roundings and tile adds are k_systolic_fast's, value for value.  The workgroup's operand maxima are
+// read back from LDS once per stage; its verdict and flag are k_systolic_fast's.  No hints, no epilogue.
+constexpr int KS64 = 64;                            // rows per stage
+
+template <int SIZE, bool BF16_LAST, bool HWF>
+__global__ void __launch_bounds__(256) k_systolic_fast64(const SysArgs args, const FastLanes fl) {
+  constexpr int BM = 64, BN = 64, TM = 4, TN = 4, NBS = KS64 / KT;
+  typedef __attribute__((address_space(3))) void* lds_t;
+  static_assert(!HWF || (SIZE == 16 && BF16_LAST), "HW_FINAL has 16 lanes, the last bf16");
+  const LaneConsts<HWF> lc{fl};
+  // the two stage buffers are distinct arrays, each named where it is used: the compiler can then tell the
+  // direct-to-LDS loads into one from the reads of the other, and does not wait for the loads before them
+  __shared__ __align__(16) float sa0[KS64][BM], sa1[KS64][BM];
+  __shared__ __align__(16) float sb0[KS64][BN], sb1[KS64][BN];
+  __shared__ __align__(16) float xs_a[2][NBS][BM];
+  __shared__ __align__(16) float xs_b[2][NBS][BN];
+  __shared__ uint32_t inexact_w[2][NBS][4];         // per buffer, block and wave: a scale denies the short add
+  __shared__ uint32_t red[3][4];
+  const int tn = threadIdx.x % (BN / TN), tm = threadIdx.x / (BN / TN);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t z = blockIdx.z, ty = blockIdx.y, tx = blockIdx.x;
+  const int64_t m0 = ty * BM, n0 = tx * BN;
+  const float* A = args.A.p + z * args.A.batch + m0;
+  const float* B = args.B.p + z * args.B.batch + n0;
+  const float* XA = args.XA.p + z * args.XA.batch + m0;
+  const float* XB = args.XB.p + z * args.XB.batch + n0;
+  const int64_t K = args.K;
+  // a wave instruction moves 64 lanes x 16 bytes = 4 rows of 64 floats; a stage is 16 such row quads per
+  // operand, 4 per wave
+  constexpr int INST = KS64 / 4 / 4;
+  float xv[NBS];
+  // the scales' loads go first: a wait the compiler places before rewriting their registers then does not
+  // wait for the stage's direct-to-LDS loads too
+  auto load_stage = [&](int64_t k, float (&da)[KS64][BM], float (&db)[KS64][BN]) __attribute__((always_inline)) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int q = 0; q < NBS; ++q) {
+      const int64_t g = k / KT + q;
+      xv[q] = t < BM ? XA[g * args.XA.ld + t] : (t < BM + BN ? XB[g * args.XB.ld + t - BM] : 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < INST; ++j) {
+      const int r0 = (wave * INST + j) * 4;
+      const int64_t r = k + r0 + lane / 16;
+      const int c = 4 * (lane % 16);
+      __builtin_amdgcn_global_load_lds(A + r * args.A.ld + c, (lds_t)&da[r0][0], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(B + r * args.B.ld + c, (lds_t)&db[r0][0], 16, 0, 0);
+    }
+  };
+  uint32_t max_a = 0u, max_b = 0u, max_x = 0u;
+  // the stage's scales into LDS with their short-add verdicts, then the barrier once this wave's loads landed
+  auto finish_stage = [&](int buf) __attribute__((always_inline)) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int q = 0; q < NBS; ++q) {
+      bool inexact = false;
+      if (t < BM + BN) {
+        max_x = umax(max_x, f2u(xv[q]) & 0x7FFFFFFFu);
+        if constexpr (BF16_LAST) inexact = !exact_scale(xv[q], fl.xs_lo, fl.xs_hi);
+        if (t < BM) xs_a[buf][q][t] = xv[q];
+        else xs_b[buf][q][t - BM] = xv[q];
+      }
+      const uint64_t bal = __ballot(inexact);
+      if (lane == 0) inexact_w[buf][q][wave] = bal != 0ull ? 1u : 0u;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): the direct-to-LDS loads of this wave landed
+    __syncthreads();
+  };
+
+  float C[TM][TN];
+#pragma unroll
+  for (int x = 0; x < TM; ++x)
+#pragma unroll
+    for (int y = 0; y < TN; ++y) C[x][y] = 0.0f;
+
+  // one stage: its operand maxima read back from LDS, then its blocks reduced into C
+  auto reduce_stage = [&](const float (&ca)[KS64][BM], const float (&cb)[KS64][BN], int buf)
+                          __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < KS64 * BM / 4 / 256; ++j) {
+      const float4 qa = reinterpret_cast<const float4*>(&ca[0][0])[threadIdx.x + 256 * j];
+      const float4 qb = reinterpret_cast<const float4*>(&cb[0][0])[threadIdx.x + 256 * j];
+      max_a = umax(max_a, umax(umax(f2u(qa.x) & 0x7FFFFFFFu, f2u(qa.y) & 0x7FFFFFFFu),
+                               umax(f2u(qa.z) & 0x7FFFFFFFu, f2u(qa.w) & 0x7FFFFFFFu)));
+      max_b = umax(max_b, umax(umax(f2u(qb.x) & 0x7FFFFFFFu, f2u(qb.y) & 0x7FFFFFFFu),
+                               umax(f2u(qb.z) & 0x7FFFFFFFu, f2u(qb.w) & 0x7FFFFFFFu)));
+    }
+#pragma unroll
+    for (int q = 0; q < NBS; ++q) {
+      const bool short_add = BF16_LAST && (inexact_w[buf][q][0] | inexact_w[buf][q][1] | inexact_w[buf][q][2] |
+                                           inexact_w[buf][q][3]) == 0u;
+      float scale[TM][TN];
+      {
+        const float4 xa = *reinterpret_cast<const float4*>(&xs_a[buf][q][tm * TM]);
+        const float4 xb = *reinterpret_cast<const float4*>(&xs_b[buf][q][tn * TN]);
+        const float fa[TM] = {xa.x, xa.y, xa.z, xa.w}, fb[TN] = {xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+        for (int x = 0; x < TM; ++x)
+#pragma unroll
+          for (int y = 0; y < TN; ++y) scale[x][y] = fa[x] * fb[y];
+      }
+#pragma unroll
+      for (int r0 = KT * q; r0 < KT * q + KT; r0 += SIZE) {
+        float S[TM][TN];
+#pragma unroll
+        for (int i = 0; i < SIZE; ++i) {
+          const float4 a4 = *reinterpret_cast<const float4*>(&ca[r0 + i][tm * TM]);
+          const float4 b4 = *reinterpret_cast<const float4*>(&cb[r0 + i][tn * TN]);
+          const float a[TM] = {a4.x, a4.y, a4.z, a4.w}, b[TN] = {b4.x, b4.y, b4.z, b4.w};
+          if (BF16_LAST && i == SIZE - 1) {
+            // bf16 lane: S plus the truncated product flushed below the threshold, RNE to bf16
+#pragma unroll
+            for (int x = 0; x < TM; ++x)
+#pragma unroll
+              for (int y = 0; y < TN; ++y) {
+                float t = u2f(f2u(a[x] * b[y]) & fl.pmask);
+                t = fabsf(t) < fl.flush_thr ? 0.0f : t;
+                S[x][y] = split_rne(S[x][y] + t, 65537.0f);
+              }
+          } else {
+            const float mg = lc.magic(i);
+#pragma unroll
+            for (int x = 0; x < TM; ++x)
+#pragma unroll
+              for (int y = 0; y < TN; ++y) {
+#pragma clang fp contract(off)
+                const float p = (u2f(f2u(a[x] * b[y]) & fl.pmask) + mg) - mg;    // lane(p)
+                S[x][y] = i == 0 ? p : split_rne(S[x][y] + p, lc.split(i));
+              }
+          }
+        }
+        if (short_add) {
+#pragma unroll
+          for (int x = 0; x < TM; ++x)
+#pragma unroll
+            for (int y = 0; y < TN; ++y) C[x][y] = bf16_bits(C[x][y] + S[x][y] * scale[x][y]);
+        } else {
+#pragma unroll
+          for (int x = 0; x < TM; ++x)
+#pragma unroll
+            for (int y = 0; y < TN; ++y) C[x][y] = bf16_bits(C[x][y] + bf16_bits(S[x][y] * scale[x][y]));
+        }
+      }
+    }
+  };
+
+  load_stage(0, sa0, sb0);
+  finish_stage(0);
+  for (int64_t k0 = 0; k0 < K; k0 += 2 * KS64) {
+    // even stage: buffer 0 reduced while stage k0 + 64 lands in buffer 1; odd stage: the other way round
+    const bool more1 = k0 + KS64 < K;
+    if (more1) load_stage(k0 + KS64, sa1, sb1);
+    reduce_stage(sa0, sb0, 0);
+    if (!more1) break;
+    finish_stage(1);
+    const bool more2 = k0 + 2 * KS64 < K;
+    if (more2) load_stage(k0 + 2 * KS64, sa0, sb0);
+    reduce_stage(sa1, sb1, 1);
+    if (more2) finish_stage(0);
+  }
+
+  for (int off = 32; off > 0; off >>= 1) {
+    max_a = umax(max_a, (uint32_t)__shfl_xor((int)max_a, off, 64));
+    max_b = umax(max_b, (uint32_t)__shfl_xor((int)max_b, off, 64));
+    max_x = umax(max_x, (uint32_t)__shfl_xor((int)max_x, off, 64));
+  }
+  if (lane == 0) {
+    red[0][wave] = max_a;
+    red[1][wave] = max_b;
+    red[2][wave] = max_x;
+  }
+  __syncthreads();
+  const uint32_t wa = umax(umax(red[0][0], red[0][1]), umax(red[0][2], red[0][3]));
+  const uint32_t wb = umax(umax(red[1][0], red[1][1]), umax(red[1][2], red[1][3]));
+  const uint32_t wx = umax(umax(red[2][0], red[2][1]), umax(red[2][2], red[2][3]));
+  const bool ok = wa < kFastAMaxBits && wb < 0x7F800000u && wx < 0x7F800000u &&
+                  u2f(wa) * u2f(wb) <= args.fast_prod_max;
+  if (threadIdx.x == 0) args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = ok ? 0u : 1u;
+  if (!ok) return;
+  write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
+}
+
 // ------------------------------------------------------------------------------- general datapath
 // The BM x BN outputs at (m0, n0) of problem z.
 // The reduction runs over rows [0, kstop) of A and B (kstop = K, or a multiple of 32 the fast kernel's check
@@ -970,6 +1167,7 @@ FastLanes make_fast_lanes(const int32_t* e, const int32_t* m, int size, const mx
     fl.a_exp[i] = 6 + mi;
     if (prev >= 0) fl.rescale[i] = pow2f(mi - prev);
     fl.split[i] = (float)((1u << (23 - mi)) + 1u);
+    fl.magic[i] = 1.5f * pow2f(17 - mi);
     prev = mi;
   }
   fl.out_scale = pow2f(-(6 + prev));
@@ -1026,6 +1224,35 @@ void launch_fast(int size, bool bf16_last, bool hwf, dim3 grid, hipStream_t st, 
   }
 }
 
+// Ladders with a last bf16 lane (HW_FINAL among them); without one the compiler's schedule of this kernel
+// spills, and k_systolic_fast takes them.
+void launch_fast64(int size, bool hwf, dim3 grid, hipStream_t st, const SysArgs& a, const FastLanes& fl) {
+  if (hwf) {
+    k_systolic_fast64<16, true, true><<<grid, 256, 0, st>>>(a, fl);
+    return;
+  }
+  switch (size) {
+    case 4: k_systolic_fast64<4, true, false><<<grid, 256, 0, st>>>(a, fl); break;
+    case 8: k_systolic_fast64<8, true, false><<<grid, 256, 0, st>>>(a, fl); break;
+    case 16: k_systolic_fast64<16, true, false><<<grid, 256, 0, st>>>(a, fl); break;
+    default: k_systolic_fast64<32, true, false><<<grid, 256, 0, st>>>(a, fl); break;
+  }
+}
+
+// Whether k_systolic_fast64 takes the launch: a ladder ending in a bf16 lane, a grid of 64 x 64 tiles that
+// gives every CU at least 2 but fewer than 4 workgroups, every 64-row stage inside the operands and 16-byte
+// aligned, blocks of 32, no hints and no epilogue (on 512 x 4096 outputs, K = 4096: 1.06 ms against 1.16 for
+// k_systolic_fast on 32 x 64 tiles).
+bool takes_fast64(const SysArgs& a, int64_t count) {
+  const int64_t tiles = mxq::ceil_div(a.M, 64) * mxq::ceil_div(a.N, 64) * count;
+  auto aligned = [](const Operand& o) {
+    return o.ld % 4 == 0 && o.batch % 4 == 0 && reinterpret_cast<uintptr_t>(o.p) % 16 == 0;
+  };
+  return a.lane_e[a.size - 1] == 8 && !a.skip && !a.k_end && !a.epi_on && a.block_size == KT && a.K > 0 &&
+         a.M % 64 == 0 && a.N % 64 == 0 &&
+         a.K % KS64 == 0 && tiles >= 2 * 256 && tiles < 4 * 256 && aligned(a.A) && aligned(a.B);
+}
+
 bool lanes_valid(const int32_t* e, const int32_t* m, int size) {
   for (int i = 0; i < size; ++i) {
     const bool ok = (e[i] == 8 && m[i] == 23) || (e[i] >= 1 && e[i] <= 8 && m[i] >= 1 && m[i] <= 22);
@@ -1044,10 +1271,12 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
   if (mxq::ceil_div(a.M, 64) * mxq::ceil_div(a.N, 64) * count >= want) { a.fbm = 64; a.fbn = 64; }
   else if (mxq::ceil_div(a.M, 32) * mxq::ceil_div(a.N, 64) * count >= want) { a.fbm = 32; a.fbn = 64; }
   else { a.fbm = 32; a.fbn = 32; }
+  const bool fast_lanes = !force_general && a.K > 0 && lanes_fast(lane_e, lane_m, a.size, ar);
+  const bool fast64 = fast_lanes && takes_fast64(a, count);
+  if (fast64) { a.fbm = 64; a.fbn = 64; }
   a.tiles_x = mxq::ceil_div(a.N, a.fbn);
   a.tiles_y = mxq::ceil_div(a.M, a.fbm);
   a.fast_prod_max = 0.0f;
-  const bool fast_lanes = !force_general && a.K > 0 && lanes_fast(lane_e, lane_m, a.size, ar);
   const dim3 grid_f((unsigned)a.tiles_x, (unsigned)a.tiles_y, (unsigned)count);
   const dim3 grid_g((unsigned)mxq::ceil_div(a.N, 32), (unsigned)mxq::ceil_div(a.M, 32), (unsigned)count);
   const dim3 grid_gf((unsigned)a.tiles_x, (unsigned)a.tiles_y, (unsigned)count);   // after the fast kernel
@@ -1080,8 +1309,12 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
     }
     {
       mxq::KernelTimer timer("systolic_fast", st);
-      launch_fast(a.size, lane_e[a.size - 1] == 8, is_hw_final(lane_e, lane_m, a.size), grid_f, st, a,
-                  make_fast_lanes(lane_e, lane_m, a.size, ar));
+      if (fast64)
+        launch_fast64(a.size, is_hw_final(lane_e, lane_m, a.size), grid_f, st, a,
+                      make_fast_lanes(lane_e, lane_m, a.size, ar));
+      else
+        launch_fast(a.size, lane_e[a.size - 1] == 8, is_hw_final(lane_e, lane_m, a.size), grid_f, st, a,
+                    make_fast_lanes(lane_e, lane_m, a.size, ar));
     }
     if (int rc = mxq::check_launch("mxq_systolic fast")) return rc;
     mxq::KernelTimer timer("systolic_general", st);

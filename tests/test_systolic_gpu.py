@@ -287,6 +287,34 @@ def test_all_fast_tile_shapes(cuda):
                 assert_bits_equal(Y[:, cols], want, f"{M}x{N} cols {cols}")
 
 
+@pytest.mark.parametrize("case", [0, 1, 3, 4, 5], ids=lambda i: f"l{i}")
+def test_small_grid_fast_kernel(cuda, case):
+    """Grids of 512 to 1023 tiles of 64 x 64 outputs (512 x 4096 and 1024 x 2048 here) run on the fast kernel
+    that stages 64 rows per step straight into LDS and rounds in value units: every ladder with a last bf16
+    lane, K = 128 and K = 192 (an odd count of 64-row stages), two columns of A past the fast bound (their
+    tiles go to the general kernel).  Every output equal to the general kernel's alone, edge column slices
+    equal to the oracle's.  K = 96 (not a multiple of 64) takes the 32-row kernel, checked the same way."""
+    from mxq import matmul
+    size, sched, (pe, pm) = FAST_LADDERS[case]
+    rng = np.random.default_rng(40 + case)
+    ar, orc = _arith("MXGEMMINI", pe, pm)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()          # noqa: E731
+    for M, N, K in ((512, 4096, 128), (1024, 2048, 192), (512, 4096, 96)):
+        P_A, X_A = _codes(rng, K, M, scale=2.0)
+        P_B, X_B = _codes(rng, K, N, scale=0.3)
+        for r, c in ((5, 70), (K - 1, M - 3)):
+            P_A[r, c] = 448.0
+            X_A[0, c] = np.float32(2.0 ** 20)
+        ops = [t(x) for x in (P_A, X_A, P_B, X_B)]
+        Y = matmul.systolic(*ops, ar, sched, size)
+        G = matmul.systolic(*ops, ar, sched, size, force_general=True)
+        assert_bits_equal(Y.cpu().numpy(), G.cpu().numpy(), f"{M}x{N}x{K} fast vs general")
+        Y = Y.cpu().numpy()
+        for cols in (slice(0, 6), slice(N - 6, N)):
+            want = osys.systolic(P_A, X_A, P_B[:, cols], X_B[:, cols], orc, sched, size)
+            assert_bits_equal(Y[:, cols], want, f"{M}x{N}x{K} cols {cols}")
+
+
 def test_zero_stages_skip_exactly(cuda):
     """Stages (32 K rows) whose A or B tile is all +-0 are skipped by the fast kernel: a zero block for every
     tile, zero blocks for some row or column tiles only, -0 codes, a zero stage whose block scale is not a power
