@@ -265,6 +265,14 @@ def _events_ms(fn, steps, stream):
     return start.elapsed_time(end) / steps
 
 
+def _warm(fn, calls=10):
+    """Untimed calls, so the timed ones start with the clocks up after the host-side work between lines."""
+    import torch
+    for _ in range(calls):
+        fn()
+    torch.cuda.synchronize()
+
+
 def _kernel_ms(fn, steps, kernel):
     """Average duration of the library kernel `kernel` over `steps` calls of fn (library HIP events)."""
     import torch
@@ -352,6 +360,7 @@ def quantize_lines(torch, steps, inp):
     for fmt in C3_FORMATS:
         fn = lambda: block.mxgemmini.quantize(V, fmt, axis=0, rounding_mode="rne")   # noqa: E731
         outputs[fmt] = _slice_digests(*(t.cpu().numpy() for t in fn()), 512)
+        _warm(fn)
         ms = _events_ms(fn, steps, s)
         out[fmt] = round(bytes_c3 / ms / 1e6, 1)
         res, calls, held = _capture(fn, "mxq_block_quantize")
@@ -364,7 +373,7 @@ def quantize_lines(torch, steps, inp):
     pk, pk_kern = {}, {}
     for fmt in C3_FORMATS:
         fn = lambda: mxq.packed.quantize(V, fmt, rounding_mode="rne", check=False)            # noqa: E731
-        fn()
+        _warm(fn)
         ms = _events_ms(fn, steps, s)
         pk[fmt] = round(bytes_pk / ms / 1e6, 1)
         res, calls, held = _capture(fn, "mxq_block_quantize_packed")
@@ -383,8 +392,8 @@ def quantize_lines(torch, steps, inp):
         r = block.ocp.quantize(rot[i[0] % 64], "MXFP8_E4M3", axis=0)
         i[0] += 1
         return r
-    q1()
-    ms1 = _events_ms(q1, 64, s)
+    _warm(q1, 64)
+    ms1 = _events_ms(q1, 256, s)
     c1_calls, c1_keep = [], []
     for k in range(64):
         res, calls, held = _capture(q1, "mxq_block_quantize")
@@ -710,7 +719,7 @@ def main():
     from mxq import block, matmul
     dev = torch.device("cuda", 0)
     if args.only in ("quantize", "lut", "attend", "llm"):
-        fn = {"quantize": lambda: quantize_lines(torch, max(5, args.steps // 2), inp)[0],
+        fn = {"quantize": lambda: quantize_lines(torch, max(10, args.steps), inp)[0],
               "lut": lambda: lut_line(torch, 3, inp)[0], "attend": lambda: attend_line(torch, 10, inp)[0],
               "llm": lambda: llm_line(torch, 2)}[args.only]
         print(json.dumps({"only": args.only, args.only: fn()}), flush=True)
@@ -770,7 +779,7 @@ def main():
     }
     extra = {}
     if not args.no_extra:
-        line["quantize"], extra["quantize"] = quantize_lines(torch, max(5, args.steps // 2), inp)
+        line["quantize"], extra["quantize"] = quantize_lines(torch, max(10, args.steps), inp)
         line["lut_c4"], extra["lut"] = lut_line(torch, 3, inp)
         line["attend_c5"], extra["attend"] = attend_line(torch, 10, inp)
         line["mfma_c2"] = mfma_line(torch, max(5, args.steps // 2), P_A, X_A, P_B, X_B, inp)

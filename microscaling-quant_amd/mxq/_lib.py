@@ -9,7 +9,9 @@ There is no CPU implementation behind this package.  CPU tensors are copied to t
 there, and copied back (the reference returns outputs on the input's device).  Without a GPU, or without the
 built library, every computing call raises RuntimeError.
 """
+import contextlib
 import ctypes
+import functools
 import os
 import threading
 from typing import Optional, Sequence
@@ -21,6 +23,7 @@ LIB_PATH = os.environ.get("MXQ_HIP_LIB", os.path.join(_HERE, "libmxq_hip.so"))
 
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
+_FN = {}            # entry point name -> its ctypes function, filled by load()
 
 #: the MXQ_ABI_VERSION of include/mxq_hip.h these signatures follow; a library reporting another is refused
 ABI_VERSION = 2
@@ -151,6 +154,8 @@ ARITH_MXGEMMINI, ARITH_MXQUANT = 0, 1
 def load(path: str = LIB_PATH) -> ctypes.CDLL:
     """Open the library (once) and declare every entry point's C signature."""
     global _lib
+    if _lib is not None:
+        return _lib
     with _lock:
         if _lib is None:
             if not os.path.exists(path):
@@ -160,11 +165,28 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             for name, (res, args) in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.restype, fn.argtypes = res, args
+                _FN[name] = fn
             if lib.mxq_version() != ABI_VERSION:
+                _FN.clear()
                 raise RuntimeError(f"mxq: {path} has C ABI revision {lib.mxq_version()}, this package binds "
                                    f"revision {ABI_VERSION}; rebuild the library")
             _lib = lib
     return _lib
+
+
+def memo_spec(make):
+    """make, remembered per positional arguments (their types included): a spec struct is only read once built,
+    and building one, with the reference's argument checks, costs about a microsecond of every call.  Arguments
+    that cannot be hashed are built afresh; errors are raised as make raises them."""
+    cached = functools.lru_cache(maxsize=512, typed=True)(make)
+
+    @functools.wraps(make)
+    def spec(*args):
+        try:
+            return cached(*args)
+        except TypeError:
+            return make(*args)
+    return spec
 
 
 def check(rc: int, what: str) -> None:
@@ -188,12 +210,29 @@ def to_device(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
     return t if t.device == dev else t.to(dev)
 
 
-def stream(dev: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
-def ptr(t: Optional[torch.Tensor]) -> ctypes.c_void_p:
-    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+def stream(dev: torch.device) -> int:
+    """torch's current stream of `dev` as a hipStream_t handle (an int)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+_SAME_DEVICE = contextlib.nullcontext()
+
+
+def on(dev: torch.device):
+    """A context in which `dev` is the current device: torch.cuda.device(dev), or nothing to do when it already
+    is (the common case, and a microsecond less per call)."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return _SAME_DEVICE
+    return torch.cuda.device(dev)
+
+
+def ptr(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else t.data_ptr()
 
 
 def aligned(t: torch.Tensor, nbytes: int = 16) -> torch.Tensor:
@@ -217,7 +256,13 @@ def numel(shape: Sequence[int]) -> int:
 
 def run(name: str, *args) -> None:
     """Call entry point `name` with args; raise RuntimeError on a nonzero status."""
-    check(getattr(load(), name)(*args), name)
+    fn = _FN.get(name)
+    if fn is None:
+        load()
+        fn = _FN[name] if name in _FN else getattr(load(), name)
+    rc = fn(*args)
+    if rc != 0:
+        check(rc, name)
 
 
 def ew_prepare(x: torch.Tensor, dtype: torch.dtype):

@@ -83,7 +83,7 @@ def mfma_accum(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: tor
     if K == 0 or M == 0 or N == 0:
         return _lib.back(C, P_A)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         A8, SA, K64 = _pack(ops[0], ops[1], ka, K, err, dev)
         B8, SB, _ = _pack(ops[2], ops[3], kb, K, err, dev)
         if int(err.item()):

@@ -22,7 +22,7 @@ __all__ = ["exact_add", "truncate_significand", "flush_product", "saturate"]
 def _unary(name: str, x: torch.Tensor, *args) -> torch.Tensor:
     dev, xd = _lib.ew_prepare(x, torch.float32)
     out = torch.empty_like(xd)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run(name, _lib.ptr(xd), _lib.ptr(out), out.numel(), *args, _lib.stream(dev))
     return _lib.back(out, x)
 
@@ -37,7 +37,7 @@ def exact_add(a: torch.Tensor, b: torch.Tensor, e: int, m: int, rounding_mode: s
     ad = _lib.to_device(a.detach(), dev).to(torch.float32).expand(shape).contiguous()
     bd = _lib.to_device(b.detach(), dev).to(torch.float32).expand(shape).contiguous()
     out = torch.empty(shape, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_exact_add", _lib.ptr(ad), _lib.ptr(bd), _lib.ptr(out), out.numel(), e, m,
                  _lib.MODE_CODE[rounding_mode], _lib.GRID_CODE[grid], max_norm, _lib.stream(dev))
     return _lib.back(out, a)

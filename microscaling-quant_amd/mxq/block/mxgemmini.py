@@ -22,6 +22,7 @@ from . import _driver
 __all__ = ["quantize", "dequantize"]
 
 
+@_lib.memo_spec
 def spec(f: Format, rounding_mode: str, scale_floor: float, via: Optional[Tuple[int, int]]) -> _lib.BlockSpec:
     """The fused kernel's spec, after the reference's own checks (made when its element step runs)."""
     if via is not None:

@@ -18,6 +18,7 @@ from . import _driver
 __all__ = ["quantize", "dequantize"]
 
 
+@_lib.memo_spec
 def spec(f: Format) -> _lib.BlockSpec:
     return _lib.BlockSpec(scale_rule=_lib.SCALE_MXQUANT, scale_floor=f32_scalar(MXQUANT_FLOOR),
                           elem=_lib.ELEM_QTORCH, e=f.e, m=f.m, rounding=_lib.MODE_CODE["ties_away"])

@@ -26,6 +26,7 @@ __all__ = ["quantize", "dequantize", "PLACEMENTS"]
 PLACEMENTS = ("top", "below_top", "no_clip")
 
 
+@_lib.memo_spec
 def spec(f: Format, rounding_mode: str, scale_bits: int, placement: str) -> _lib.BlockSpec:
     _check_bits(scale_bits)
     check_mode(rounding_mode)

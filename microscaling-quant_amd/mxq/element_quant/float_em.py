@@ -51,7 +51,7 @@ def quantize(z: torch.Tensor, e: int, m: int, rounding_mode: str = "ties_away", 
     f64 = z.dtype == torch.float64
     dev, zd = _lib.ew_prepare(z, torch.float64 if f64 else torch.float32)
     out = torch.empty(zd.shape, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_float_em", _lib.ptr(zd), 3 if f64 else 0, _lib.ptr(out), out.numel(), e, m,
                  _lib.MODE_CODE[rounding_mode], _lib.GRID_CODE[grid], max_norm, _lib.stream(dev))
     return _lib.back(out, z)

@@ -40,7 +40,7 @@ def elementwise(z: torch.Tensor, f: Format, rounding_mode: str, saturate_normals
     u = draws(z, z.numel()) if rounding_mode == "dither" else None
     dev, zd = _lib.ew_prepare(z, torch.float32)
     out = torch.empty_like(zd)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         if u is None:
             _lib.run("mxq_microsoft", _lib.ptr(zd), _lib.ptr(out), out.numel(), f.e, f.ms_bits, f.max_norm,
                      _lib.MS_MODE_CODE[rounding_mode], int(saturate_normals), _lib.stream(dev))

@@ -166,7 +166,7 @@ def finder(codes: torch.Tensor, T: torch.Tensor, fmt: Union[str, Format], *, gro
     fxd, lfd = fx_all.to(dev), lut_fx.to(dev).contiguous()
     out = torch.empty(c.shape, dtype=torch.int64, device=dev)
     K = c.shape[0]
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_lut_finder", _lib.ptr(c), K, n, group, _lib.ptr(fxd), ncodes, _lib.ptr(lfd),
                  0 if mask is None else mask, _lib.ptr(out), _lib.stream(dev))
     return _lib.back(out, codes)

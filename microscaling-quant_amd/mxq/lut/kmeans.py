@@ -65,7 +65,7 @@ def fit(P: torch.Tensor, fmt, group: int, max_iters: int):
     work = torch.empty(ng * nv + 1, dtype=torch.int32, device=dev)
     if n == 0:
         work.zero_()
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_lut_tables", _lib.ptr(Pd), K, n, group, max_iters, _lib.ptr(g_d), nv, _lib.ptr(s_d),
                  s_d.numel(), _lib.ptr(o_d), f.e, f.m, _lib.ptr(T), _lib.ptr(work), _lib.stream(dev))
     return T, work[-1:]
@@ -86,7 +86,7 @@ def _pick(P: torch.Tensor, T: torch.Tensor, group: int, values: bool) -> torch.T
     Td = _lib.to_device(T.detach(), dev).to(torch.float32).contiguous()
     K, n = Pd.shape
     out = torch.empty((K, n), dtype=torch.float32 if values else torch.int64, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_lut_pick", _lib.ptr(Pd), K, n, group, _lib.ptr(Td), Td.shape[1],
                  _lib.ptr(None if values else out), _lib.ptr(out if values else None), _lib.stream(dev))
     return _lib.back(out, P)
@@ -119,6 +119,6 @@ def lookup(I: torch.Tensor, T: torch.Tensor, *, group: int) -> torch.Tensor:
         raise IndexError(f"mxq.lut.lookup: index out of range for tables of width {width}")
     K, n = Id.shape
     out = torch.empty((K, n), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_lut_lookup", _lib.ptr(Id), K, n, group, _lib.ptr(Td), width, _lib.ptr(out), _lib.stream(dev))
     return _lib.back(out, I)

@@ -51,7 +51,7 @@ def adder_tree(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: tor
     le = (ctypes.c_int32 * levels)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * levels)(*[int(m) for _, m in schedule])
     work = torch.empty(workspace_elements(K, M, N, 1), dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_adder_tree", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, le, lm, size, block_size,
                  kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))
     return _lib.back(C, P_A)

@@ -90,7 +90,7 @@ def anchor_tree(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: to
     spec = _lib.AnchorSpec(width=width, drop=DROPS.index(drop), headroom=head, has_emin=int(emin is not None),
                            emin=0 if emin is None else emin, nbits=lg + 1)
     work = torch.empty(workspace_elements(K, M, N, 1), dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_anchor_tree", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, te, tm, tb, size, block_size,
                  ctypes.byref(spec), kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))
     return _lib.back(C, P_A)

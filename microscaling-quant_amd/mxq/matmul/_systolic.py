@@ -58,7 +58,7 @@ def systolic(P_A: torch.Tensor, X_A: torch.Tensor, P_B: torch.Tensor, X_B: torch
     le = (ctypes.c_int32 * size)(*[int(e) for e, _ in schedule])
     lm = (ctypes.c_int32 * size)(*[int(m) for _, m in schedule])
     work = torch.empty(workspace_elements(K, M, N, 1), dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_systolic", *(_lib.ptr(t) for t in ops), _lib.ptr(C), K, M, N, le, lm, size, block_size,
                  kernel.ctype(), _lib.ptr(work), int(force_general), _lib.stream(dev))
     return _lib.back(C, P_A)
@@ -110,7 +110,7 @@ def systolic_batched(ops, layout: "_lib.SystolicLayout", count: int, K: int, M: 
     hints = _lib.SystolicHints(skip=_lib.ptr(skip), k_end=_lib.ptr(k_end), a_live=_lib.ptr(a_live),
                                c_end=_lib.ptr(c_end))
     work = torch.empty(workspace_elements(K, M, N, count), dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_systolic_batched", *(_lib.ptr(t) for t in ops), _lib.ptr(C), ctypes.byref(layout), count,
                  K, M, N, le, lm, size, block_size, kernel.ctype(), ctypes.byref(hints),
                  None if epilogue is None else ctypes.byref(epilogue), _lib.ptr(work), 0, _lib.stream(dev))

@@ -235,7 +235,7 @@ def _group_amax(codes: torch.Tensor, scales: torch.Tensor, block_size: int, grou
     from .. import _lib
     K, cols = codes.shape
     out = torch.empty(K, groups, dtype=torch.float64, device=codes.device)
-    with torch.cuda.device(codes.device):
+    with _lib.on(codes.device):
         _lib.run("mxq_group_amax", _lib.ptr(codes.contiguous()), _lib.ptr(scales.contiguous()), K, cols, groups,
                  block_size, _lib.ptr(out), _lib.stream(codes.device))
     return out
@@ -258,7 +258,7 @@ def _windows(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale
     D, Tk = a_amax.shape[0], bias.shape[2]
     flags = torch.zeros(Zc, dtype=torch.int32, device=a_amax.device)
     mask, b_stride, r_stride = _mask_rows(bias, z0, Hkv, s0)
-    with torch.cuda.device(a_amax.device):
+    with _lib.on(a_amax.device):
         _lib.run("mxq_attend_windows", _lib.ptr(a_amax), a_amax.shape[1], _lib.ptr(k_amax[:, z0:]), k_amax.shape[1],
                  D, Zc, SLACK * abs(scale), _lib.ptr(mask), b_stride, r_stride, z0, Hkv, m, Tk, block,
                  _lib.ptr(flags), _lib.stream(a_amax.device))
@@ -285,7 +285,7 @@ def _hints(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale: 
     skip = torch.empty(Zc, rg, kg, dtype=torch.uint8, device=dev)
     k_end = torch.empty(Zc, tg, dtype=torch.int32, device=dev)
     tail_max = torch.empty(Zc, tg, dtype=torch.float32, device=dev) if with_tail else None
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_mask_minabs", _lib.ptr(mask), b_stride, r_stride, batches, rows, m, Tk, _lib.ptr(minabs),
                  _lib.ptr(maxval), _lib.stream(dev))
         _lib.run("mxq_attend_hints", _lib.ptr(a_amax), a_amax.shape[1], _lib.ptr(k_amax[:, z0:]), k_amax.shape[1],
@@ -514,7 +514,7 @@ def _softmax_pt(S: torch.Tensor, quantizer, block_size: int, vector: Optional[st
     live = None
     if live_cols is not None:
         live = torch.empty((R // live_cols, -(-T // 32), live_cols // 32), dtype=torch.uint8, device=S.device)
-    with torch.cuda.device(S.device):
+    with _lib.on(S.device):
         _lib.run("mxq_softmax_quantize_t", _lib.ptr(Sc), R, T, _lib.ptr(PT_P), _lib.ptr(PT_X), spec, _lib.ptr(live),
                  live_cols or 0, None if tail is None else ctypes.byref(tail), _lib.stream(S.device))
     return PT_P, PT_X, live
@@ -539,7 +539,7 @@ def _scale_mask(S: torch.Tensor, bias: Optional[torch.Tensor], scale: float, vec
     from .. import _lib
     Zc, _, Tk = S.shape
     mask, b_stride, r_stride = (None, 0, 0) if bias is None else _mask_rows(bias, z0, Hkv, s0)
-    with torch.cuda.device(S.device):
+    with _lib.on(S.device):
         _lib.run("mxq_scores_scale_mask", _lib.ptr(S), Zc, n, m, Tk, float(scale), _lib.ptr(mask), b_stride,
                  r_stride, z0, Hkv, int(vector == "bf16"),
                  _lib.stream(S.device))

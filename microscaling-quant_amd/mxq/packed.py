@@ -101,7 +101,7 @@ def quantize(V: torch.Tensor, fmt: Union[str, Format], method: str = "mxgemmini"
     codes = torch.empty(Vd.shape, dtype=torch.uint8, device=dev)
     scales = torch.empty(xshape, dtype=torch.uint8, device=dev)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_block_quantize_packed", _lib.ptr(Vd), _driver._NATIVE[Vd.dtype], _lib.ptr(codes),
                  _lib.ptr(scales), _lib.ptr(err), outer, n, inner, block_size, spec, _lib.stream(dev))
     if check:
@@ -124,7 +124,7 @@ def pack(P: torch.Tensor, X: torch.Tensor, fmt: Union[str, Format], axis: int = 
     codes = torch.empty(Pd.shape, dtype=torch.uint8, device=dev)
     scales = torch.empty(xshape, dtype=torch.uint8, device=dev)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_pack", _lib.ptr(Pd), _lib.ptr(Xd), _lib.ptr(codes), _lib.ptr(scales), _lib.ptr(err), outer, n,
                  inner, block_size, f.e, f.m, _lib.stream(dev))
     if check:
@@ -152,7 +152,7 @@ def unpack(codes: torch.Tensor, scales: torch.Tensor, fmt: Union[str, Format], a
     Cd, Sd, dev, outer, n, inner, xshape = _byte_operands(codes, scales, axis, block_size, "unpack")
     P = torch.empty(Cd.shape, dtype=torch.float32, device=dev)
     X = torch.empty(xshape, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_unpack", _lib.ptr(Cd), _lib.ptr(Sd), _lib.ptr(P), _lib.ptr(X), outer, n, inner, block_size,
                  f.e, f.m, _lib.stream(dev))
     return _lib.back(P, codes), _lib.back(X, codes)
@@ -165,7 +165,7 @@ def dequantize(codes: torch.Tensor, scales: torch.Tensor, fmt: Union[str, Format
     f = _format(fmt)
     Cd, Sd, dev, outer, n, inner, _ = _byte_operands(codes, scales, axis, block_size, "dequantize")
     out = torch.empty(Cd.shape, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_dequantize_packed", _lib.ptr(Cd), _lib.ptr(Sd), _lib.ptr(out), outer, n, inner, block_size,
                  f.e, f.m, _lib.stream(dev))
     return _lib.back(out, codes)
@@ -182,7 +182,7 @@ def pick(P: torch.Tensor, T: torch.Tensor, *, group: int) -> torch.Tensor:
     Td = _lib.to_device(T.detach(), dev).to(torch.float32).contiguous()
     K, n = Pd.shape
     out = torch.empty((K, (n + 1) // 2), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_lut_pick_packed", _lib.ptr(Pd), K, n, group, _lib.ptr(Td), Td.shape[1], _lib.ptr(out),
                  _lib.stream(dev))
     return _lib.back(out, P)
@@ -208,7 +208,7 @@ def lookup(I4: torch.Tensor, T: torch.Tensor, *, group: int, n: int) -> torch.Te
         raise IndexError(f"mxq.packed.lookup: index out of range for tables of width {width}")
     K = Id.shape[0]
     out = torch.empty((K, n), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_lut_lookup_packed", _lib.ptr(Id), K, n, group, _lib.ptr(Td), width, _lib.ptr(out),
                  _lib.stream(dev))
     return _lib.back(out, I4)

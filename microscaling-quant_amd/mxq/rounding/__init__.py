@@ -48,7 +48,7 @@ def round_bits(bits: torch.Tensor, keep: Union[int, torch.Tensor], mode: str) ->
     kd = None
     if keep_t is not None:
         kd = _lib.to_device(keep_t, dev).expand(shape).contiguous()
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_round_bits", _lib.ptr(b), _lib.ptr(kd), int(keep) if keep_t is None else 0, _lib.ptr(out),
                  out.numel(), _lib.MODE_CODE[mode], _lib.stream(dev))
     return _lib.back(out, bits)
@@ -60,7 +60,7 @@ def round_int(k: torch.Tensor, mode: str) -> torch.Tensor:
         raise TypeError(f"mxq.rounding.round_int: float32 or float64 input required, got {k.dtype}")
     dev, kd = _lib.ew_prepare(k, k.dtype)
     out = torch.empty_like(kd)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_round_int", _lib.ptr(kd), 0 if k.dtype == torch.float32 else 3, _lib.ptr(out), out.numel(),
                  _lib.MODE_CODE[mode], _lib.stream(dev))
     return _lib.back(out, k)
@@ -76,7 +76,7 @@ def bf16(x: torch.Tensor) -> torch.Tensor:
     does, keeps the sign of +-0 and passes NaN through.)"""
     dev, xd = _lib.ew_prepare(x, torch.float32)
     out = torch.empty_like(xd)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_bf16", _lib.ptr(xd), _lib.ptr(out), out.numel(), _lib.stream(dev))
     return _lib.back(out, x)
 

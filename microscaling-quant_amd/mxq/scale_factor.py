@@ -58,7 +58,7 @@ def _apply(amax: torch.Tensor, spec: _lib.BlockSpec) -> torch.Tensor:
         raise TypeError(f"mxq.scale_factor: float32 block maxima required, got {amax.dtype}")
     dev, a = _lib.ew_prepare(amax, torch.float32)
     out = torch.empty_like(a)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_scale_factor", _lib.ptr(a), _lib.ptr(out), out.numel(), spec, _lib.stream(dev))
     return _lib.back(out, amax)
 
@@ -98,7 +98,7 @@ def ocp_no_clip(amax: torch.Tensor, fmt, rounding_mode: str = "even", scale_bits
     u = draws(amax, amax.numel())
     dev, a = _lib.ew_prepare(amax, torch.float32)
     out = torch.empty_like(a)
-    with torch.cuda.device(dev):
+    with _lib.on(dev):
         _lib.run("mxq_scale_factor_dither", _lib.ptr(a), _lib.ptr(_lib.to_device(u, dev)), _lib.ptr(out),
                  out.numel(), spec, _lib.stream(dev))
     return _lib.back(out, amax)
