@@ -556,6 +556,235 @@ __global__ void __launch_bounds__(256) k_quant_contig32(const T* __restrict__ V,
   }
 }
 
+// ------------------------------------------------------ code bytes of the OCP grid at nearest even, one pass
+// k_pack_rne: the byte sink for the OCP element grid rounded to nearest even and saturating at the format's own
+// largest value (block.mxgemmini's rounding_mode="rne" without `via`), blocks of 32 along the axis, eight
+// adjacent columns a lane, R lanes of a wave per block column (32 / R rows each), as k_quant_split lays them out.
+// Written for the instruction count of the common wave, whose inputs and scaled values are finite and whose
+// block scales are normal powers of two:
+//   * 16-bit inputs stay packed two to a register; the column maxima are packed 16-bit maxima (|x| patterns
+//     order as the values do, a NaN above Inf, as in float32).
+//   * one lane of each column's R evaluates the scale rule and hands the others its E8M0 byte, which is all
+//     they need: the reciprocal of a normal power of two 2^k is 2^-k, read off the byte.
+//   * z = fma(v, 1/X, +0): v / X correctly rounded, -0 made +0 (the grid's sign for an exact zero);
+//     clamped to +-max (the grid saturates: rounding a clamped value gives the saturated one), then converted
+//     by gfx950's scaled conversions at scale 1, which round to nearest even with true subnormals.
+//   * FP6 through the FP8 conversions: E2M3 is E4M3's grid on z * 2^-6 and E3M2 is E5M2's on z * 2^-12 (the
+//     same mantissa widths; the exponent offsets map one format's subnormal step and binades onto the other's),
+//     whose code bytes, with the top exponent bits zero, move the sign from bit 7 to bit 5.  FP4 converts two
+//     values into a byte, spread to one a byte.
+// A wave with any other block (a non-finite value, a scale that is not a normal power of two) takes
+// k_quant_split's software element path for all of its blocks.
+namespace pkr {
+
+template <typename T>
+struct In;                                            // a lane's row of eight values: loads and maxima
+template <>
+struct In<float> {
+  static constexpr int NW = 8, NA = 8;                // words per row, words of column maxima
+  static constexpr uint32_t kFin = 0x7F800000u;       // |x| patterns below this are finite
+  __device__ static void load(const float* p, uint32_t (&w)[NW]) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 4);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  }
+  __device__ static void amax(uint32_t (&am)[NA], const uint32_t (&w)[NW]) {
+#pragma unroll
+    for (int j = 0; j < NW; ++j) am[j] = max(am[j], w[j] & 0x7FFFFFFFu);
+  }
+  __device__ static uint32_t column(const uint32_t (&am)[NA], int j) { return am[j]; }
+  __device__ static float f32(uint32_t a) { return u2f(a); }
+  __device__ static float value(const uint32_t (&w)[NW], int j) { return u2f(w[j]); }
+};
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t max_u16x2(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                               __builtin_bit_cast(u16x2, b)));
+}
+struct In16 {
+  static constexpr int NW = 4, NA = 4;
+  template <typename T>
+  __device__ static void load(const T* p, uint32_t (&w)[NW]) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  }
+  __device__ static void amax(uint32_t (&am)[NA], const uint32_t (&w)[NW]) {
+#pragma unroll
+    for (int j = 0; j < NW; ++j) am[j] = max_u16x2(am[j], w[j] & 0x7FFF7FFFu);
+  }
+  __device__ static uint32_t column(const uint32_t (&am)[NA], int j) { return (am[j >> 1] >> (16 * (j & 1))) & 0xFFFFu; }
+};
+template <>
+struct In<bf16_t> : In16 {
+  static constexpr uint32_t kFin = 0x7F80u;
+  __device__ static float f32(uint32_t a) { return u2f(a << 16); }
+  __device__ static float value(const uint32_t (&w)[NW], int j) {
+    return (j & 1) ? u2f(w[j >> 1] & 0xFFFF0000u) : u2f(w[j >> 1] << 16);
+  }
+};
+template <>
+struct In<f16_t> : In16 {
+  static constexpr uint32_t kFin = 0x7C00u;
+  __device__ static float f32(uint32_t a) { return (float)__builtin_bit_cast(_Float16, (uint16_t)a); }
+  __device__ static float value(const uint32_t (&w)[NW], int j) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j >> 1] >> (16 * (j & 1))));
+  }
+};
+
+// Per element format (e, m): the pre-scale exponent of the conversion used, the clamp, the four codes.
+template <int E, int M>
+struct Code {
+  static_assert((E == 4 && M == 3) || (E == 5 && M == 2) || (E == 2 && M == 3) || (E == 3 && M == 2) ||
+                (E == 2 && M == 1), "an OCP MX element format");
+  static constexpr int SH = (E == 2 && M == 3) ? 6 : ((E == 3 && M == 2) ? 12 : 0);   // z * 2^-SH converted
+  static constexpr float MAXV = (E == 4) ? 448.0f : (E == 5) ? 57344.0f : (M == 3) ? 7.5f : (E == 3) ? 28.0f : 6.0f;
+  static constexpr float CLAMP = MAXV / (float)(1u << SH);
+  __device__ static uint32_t four(float z0, float z1, float z2, float z3) {
+    if constexpr (E == 2 && M == 1) {
+      uint32_t r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, z0, z1, 1.0f, 0);     // byte 0: z1 z0 nibbles
+      r = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(r, z2, z3, 1.0f, 2);              // byte 2: z3 z2
+      return (r & 0x000F000Fu) | ((r & 0x00F000F0u) << 4);
+    } else {
+      mxq_ocp_hw::s2v r = {0, 0};
+      if constexpr (M == 3) {                                                         // E4M3, E2M3
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, z0, z1, 1.0f, false);
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, z2, z3, 1.0f, true);
+      } else {                                                                        // E5M2, E3M2
+        r = __builtin_amdgcn_cvt_scalef32_pk_bf8_f32(r, z0, z1, 1.0f, false);
+        r = __builtin_amdgcn_cvt_scalef32_pk_bf8_f32(r, z2, z3, 1.0f, true);
+      }
+      const uint32_t w = __builtin_bit_cast(uint32_t, r);
+      if constexpr (SH != 0) return (w & 0x1F1F1F1Fu) | ((w >> 2) & 0x20202020u);   // sign: bit 7 -> bit 5
+      else return w;
+    }
+  }
+};
+
+}  // namespace pkr
+
+template <typename T, int E, int M, int R>
+__global__ void __launch_bounds__(256) k_pack_rne(const T* __restrict__ V, const ByteSink out, int64_t outer, int64_t n,
+                                                  int64_t inner, mxq::DivU31 nb_div, mxq::DivU31 wpr_div,
+                                                  mxq_block_spec s) {
+  using In = pkr::In<T>;
+  using Cd = pkr::Code<E, M>;
+  constexpr int VEC = 8, CPW = 64 / R, ROWS = 32 / R, PER = VEC / R;
+  static_assert(R == 4 || R == 8, "4 or 8 lanes per block column");
+  const int64_t groups = inner / VEC;
+  const int lane = threadIdx.x & 63;
+  const int64_t nb = nb_div.d;
+  const uint32_t wave = blockIdx.x * (256 / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if ((int64_t)wave >= outer * nb * wpr_div.d) return;   // whole waves only: the exchanges below see every lane
+  const uint32_t wr = mxq::divu31(wave, wpr_div);
+  const uint32_t o32 = mxq::divu31(wr, nb_div);
+  const int64_t o = o32, b = wr - o32 * nb_div.d;
+  const int64_t k0 = b * 32;
+  const int rows = (int)((n - k0 < 32) ? n - k0 : 32);
+  const int c = lane % CPW, r = lane / CPW;
+  const int64_t cg = (int64_t)(wave - wr * wpr_div.d) * CPW + c;
+  const bool live = cg < groups;
+  const T* src = V + (o * n + k0 + r * ROWS) * inner + (live ? cg : 0) * VEC;
+
+  uint32_t w[ROWS][In::NW];
+  uint32_t am[In::NA];
+#pragma unroll
+  for (int j = 0; j < In::NA; ++j) am[j] = 0u;
+#pragma unroll
+  for (int i = 0; i < ROWS; ++i) {
+    if (rows == 32 || r * ROWS + i < rows) {
+      In::load(src + (int64_t)i * inner, w[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < In::NW; ++j) w[i][j] = 0u;
+    }
+    In::amax(am, w[i]);
+  }
+#pragma unroll
+  for (int step = CPW; step < 64; step <<= 1)
+#pragma unroll
+    for (int j = 0; j < In::NA; ++j) {
+      const uint32_t other = (uint32_t)__shfl_xor((int)am[j], step, 64);
+      if constexpr (In::NA == 8) am[j] = max(am[j], other);
+      else am[j] = pkr::max_u16x2(am[j], other);
+    }
+  // lane r evaluates the scales of columns r, r + R, ...; a column's E8M0 byte when its maximum is finite and
+  // its scale a normal power of two, else 0
+  float own_x[PER];
+  uint32_t own_b[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    uint32_t mine = In::column(am, q * R);
+#pragma unroll
+    for (int jj = 1; jj < R; ++jj) mine = (r == jj) ? In::column(am, q * R + jj) : mine;
+    own_x[q] = block_scale(In::f32(mine), s);
+    const uint32_t u = f2u(own_x[q]), be = u >> 23;
+    own_b[q] = (mine < In::kFin && (u & 0x807FFFFFu) == 0u && be >= 1u && be <= 254u) ? be : 0u;
+  }
+  uint32_t eb[VEC];
+  bool fast = true;
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    eb[j] = (uint32_t)__shfl((int)own_b[j / R], c + (j % R) * CPW, 64);
+    fast = fast && eb[j] != 0u;
+  }
+  const int64_t dst = (o * n + k0 + r * ROWS) * inner + cg * VEC;
+  const int64_t xat = (o * nb + b) * inner + cg * VEC;
+  if (__all(fast)) {
+    if (!live) return;
+    float inv[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const int ex = 254 - (int)eb[j] - Cd::SH;                     // 2^-(k + SH), normal or subnormal
+      inv[j] = u2f(ex >= 1 ? (uint32_t)ex << 23 : 1u << (22 + ex));
+    }
+#pragma unroll
+    for (int i = 0; i < ROWS; ++i) {
+      float z[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        z[j] = __builtin_amdgcn_fmed3f(__builtin_fmaf(In::value(w[i], j), inv[j], 0.0f), -Cd::CLAMP, Cd::CLAMP);
+      const uint32_t w0 = Cd::four(z[0], z[1], z[2], z[3]), w1 = Cd::four(z[4], z[5], z[6], z[7]);
+      if (rows == 32 || r * ROWS + i < rows) store_words<2>(out.P + dst + (int64_t)i * inner, {w0, w1});
+    }
+    if (r == 0)
+      store_words<2>(out.X + xat, {eb[0] | eb[1] << 8 | eb[2] << 16 | eb[3] << 24,
+                                   eb[4] | eb[5] << 8 | eb[6] << 16 | eb[7] << 24});
+    return;
+  }
+  // the software element path for the whole wave (k_quant_split's, on the same scales and divisions)
+  float xs[VEC];
+  Div d[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j) {
+    xs[j] = __shfl(own_x[j / R], c + (j % R) * CPW, 64);
+    d[j] = make_div(xs[j]);
+  }
+  if (!live) return;
+  // rows read again from memory (the same values), so that this rare path holds one row's registers
+#pragma unroll 1
+  for (int i = 0; i < ROWS; ++i) {
+    if (rows == 32 || r * ROWS + i < rows) {
+      uint32_t wi[In::NW];
+      In::load(src + (int64_t)i * inner, wi);
+#pragma unroll 1
+      for (int h = 0; h < VEC; h += 4) {                 // four codes at a time: fewer registers again
+        float z[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v = In::value(wi, h + j);
+          z[j] = s.scale_rule ? apply_div(v, d[h + j]) : v;
+        }
+        out.template elems<MXQ_ELEM_OCP, MXQ_RNE, 4>(dst + (int64_t)i * inner + h, z, s);
+      }
+    }
+  }
+  if (r == 0) {
+    bool zero[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) zero[j] = In::column(am, j) == 0u;
+    out.template scales<VEC>(xat, xs, zero);
+  }
+}
+
 // V = M^T with M (inner x n) row-major in memory, blocks of 32 along n: every block is 32 contiguous elements
 // of a row of M.  A workgroup quantizes a tile of 64 rows of M x 64 of n (two blocks per row): loads along M's
 // rows (coalesced), eight lanes of four elements per block whose maxima meet through exchanges, and the codes
@@ -670,6 +899,32 @@ inline int validate(const mxq_block_spec& s) {
   return MXQ_OK;
 }
 
+// k_pack_rne for blocks of 32 along the axis, inner % 8 == 0, V 16-byte aligned, codes and scales 8-byte
+// aligned: four lanes per block column (eight rows each) while that gives the chip at least 2048 waves,
+// else eight (four rows each).
+template <typename T>
+int launch_pack_rne(const T* V, const ByteSink& out, int64_t outer, int64_t n, int64_t inner, int64_t nb,
+                    const mxq_block_spec& q, hipStream_t st) {
+  const int64_t groups = inner / 8;
+  if (outer * nb * mxq::ceil_div(groups, 8) >= (int64_t(1) << 31))
+    return mxq::invalid("block quantize: tensor too large (2^31 waves of 2048 elements)");
+  auto go = [&](auto r_const) {
+    constexpr int R = decltype(r_const)::value;
+    const int64_t wpr = mxq::ceil_div(groups, 64 / R);
+    const dim3 grid = mxq::grid_for(outer * nb * wpr * 64, 256);
+    const mxq::DivU31 dnb = mxq::make_divu31((uint32_t)nb), dwpr = mxq::make_divu31((uint32_t)wpr);
+    auto run = [&](auto kern) { kern<<<grid, 256, 0, st>>>(V, out, outer, n, inner, dnb, dwpr, q); };
+    if (q.e == 4) run(k_pack_rne<T, 4, 3, R>);
+    else if (q.e == 5) run(k_pack_rne<T, 5, 2, R>);
+    else if (q.e == 3) run(k_pack_rne<T, 3, 2, R>);
+    else if (q.m == 3) run(k_pack_rne<T, 2, 3, R>);
+    else run(k_pack_rne<T, 2, 1, R>);
+  };
+  if (outer * nb * mxq::ceil_div(groups, 16) >= 2048) go(std::integral_constant<int, 4>{});
+  else go(std::integral_constant<int, 8>{});
+  return mxq::check_launch("mxq_block_quantize_packed");
+}
+
 // bs < 0: the transposed layout (outer 1, block 32, V read as M^T), k_quant_t (float32 outputs only).
 template <typename T, int ELEM, int MODE, typename SINK>
 int launch_quant(const T* V, const SINK& out, int64_t outer, int64_t n, int64_t inner, int64_t bs,
@@ -693,6 +948,11 @@ int launch_quant(const T* V, const SINK& out, int64_t outer, int64_t n, int64_t 
     return inner % vec == 0 && av % (vec * sizeof(T)) == 0 && ap % (vec * OB) == 0 && ax % (vec * OB) == 0;
   };
   const int vec = aligned(4) ? 4 : (aligned(2) ? 2 : 1);
+  if constexpr (SINK::kBytes == 1 && ELEM == MXQ_ELEM_OCP && MODE == MXQ_RNE) {
+    if (bs == 32 && q.via_e == 0 && out.e == q.e && out.m == q.m && mxq_ocp_hw::has_hw(q.e, q.m) &&
+        q.max_norm == mxq_ocp_hw::fmt_max(q.e, q.m) && aligned(8) && av % 16 == 0)
+      return launch_pack_rne(V, out, outer, n, inner, nb, q, st);
+  }
   if (bs == 32) {
     // code bytes: eight columns a lane when they align (8-byte stores: a wave's eight lanes write 64 contiguous
     // bytes of a row, the next wave the other half of the line; sixteen would keep 64 values a lane, which

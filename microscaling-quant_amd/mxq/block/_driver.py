@@ -82,7 +82,7 @@ def quantize_fused(V: torch.Tensor, axis: int, block_size: int, spec: _lib.Block
     axis = _axis(V, axis)
     _check_block(block_size)
     if V.is_cuda:
-        dev, Vd = V.device, V.detach()
+        dev, Vd = V.device, V                           # only its memory is read: no autograd record needed
     else:
         dev = _lib.compute_device(V)
         Vd = V.detach().to(dev)
@@ -92,7 +92,12 @@ def quantize_fused(V: torch.Tensor, axis: int, block_size: int, spec: _lib.Block
         if _transposed_view(Vd, axis, block_size):
             return _quantize_transposed(Vd, dev, spec, V)
         Vd = Vd.contiguous()
-    outer, n, inner = _view3(Vd.shape, axis)
+    n = Vd.shape[axis]
+    if n > 1 and Vd.numel():
+        inner = Vd.stride(axis)                         # contiguous, numel > 0, length > 1: the inner size
+        outer = Vd.numel() // (n * inner)
+    else:
+        outer, n, inner = _view3(Vd.shape, axis)
     nb = -(-n // block_size)
     xshape = list(Vd.shape)
     xshape[axis] = nb

@@ -112,6 +112,51 @@ def test_packed_specials_and_errors(cuda):
         mxq.packed.quantize(V, "MXFP4", "mxquant", rounding_mode="rne")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fmt", FMTS)
+def test_quantize_packed_rne_kernel(cuda, dtype, fmt):
+    """block.mxgemmini rne bytes with inner % 8 == 0 (the one-pass kernel for the OCP grid at nearest even):
+    eight lanes per block column with partial waves and tail blocks against the oracle everywhere; four lanes
+    (4128 x 2048) against pack() of the float32 quantizer everywhere and the oracle on the columns around the
+    planted values; both floors (1e-38 divides, 2^-23 is a power of two), waves with NaN, Inf, huge, subnormal
+    and all-zero blocks (the software path)."""
+    import mxq
+    rng = np.random.default_rng(len(fmt) * 7 + {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}[dtype])
+    for shape, axis in [((4100, 136), 0), ((3, 70, 40), 1), ((4128, 2048), 0)]:
+        V = rng.standard_normal(shape).astype(np.float32) * np.float32(2.0)
+        flat = V.reshape(-1)
+        sp = [np.nan, np.inf, -np.inf, 6.0e4, 2.0 ** -140, -0.0]
+        at = rng.choice(flat.size, len(sp), replace=False)
+        flat[at] = sp
+        if axis == 0:
+            V[64:96, 16:24] = 0.0                                    # all-zero blocks in one lane's columns
+        Vt = torch.from_numpy(V).to(dtype)
+        Vd = Vt.cuda()
+        for floor in (1e-38, 2.0 ** -23):
+            codes, scales = mxq.packed.quantize(Vd, fmt, "mxgemmini", axis, 32, check=False,
+                                                rounding_mode="rne", scale_floor=floor)
+            got_c, got_s = codes.cpu().numpy(), scales.cpu().numpy()
+            if V.size <= 600_000:
+                P, X = ob.mxgemmini_quantize(Vt.float().numpy(), fmt, axis, 32, "rne", floor)
+                want_c, want_s, _ = op.pack(P, X, fmt, axis, 32)
+                _, c_ok = op.encode(P, *op.FORMATS[fmt])
+                assert np.array_equal(got_c[c_ok], want_c[c_ok]), f"codes {dtype} {fmt} {shape} floor {floor}"
+                assert np.array_equal(got_s, want_s), f"scales {dtype} {fmt} {shape} floor {floor}"
+                continue
+            P, X = mxq.block.mxgemmini.quantize(Vd, fmt, axis=axis, rounding_mode="rne", scale_floor=floor)
+            _, c_ok = op.encode(P.cpu().numpy(), *op.FORMATS[fmt])
+            pc, ps = mxq.packed.pack(P, X, fmt, axis, 32, check=False)
+            assert np.array_equal(got_c[c_ok], pc.cpu().numpy()[c_ok]), f"codes {dtype} {fmt} {shape} floor {floor}"
+            assert np.array_equal(got_s, ps.cpu().numpy()), f"scales {dtype} {fmt} {shape} floor {floor}"
+            for col in sorted({int(a) % shape[1] for a in at} | {20}):
+                cols = slice(col - col % 8, col - col % 8 + 8)
+                Po, Xo = ob.mxgemmini_quantize(Vt[:, cols].float().numpy(), fmt, 0, 32, "rne", floor)
+                wc, ws, _ = op.pack(Po, Xo, fmt)
+                _, ok = op.encode(Po, *op.FORMATS[fmt])
+                assert np.array_equal(got_c[:, cols][ok], wc[ok]), f"codes {dtype} {fmt} cols {cols} floor {floor}"
+                assert np.array_equal(got_s[:, cols], ws), f"scales {dtype} {fmt} cols {cols} floor {floor}"
+
+
 @pytest.mark.parametrize("n,group,width", [(40, 0, 16), (41, 1, 16), (7, 0, 5)])
 def test_pick_lookup_packed(cuda, n, group, width):
     """Nibbles equal lut.pick's int64 indices packed two to a byte; lookup of them equals lut.lookup."""

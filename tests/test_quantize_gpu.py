@@ -132,6 +132,23 @@ def test_transposed_view_layout(cuda, dtype):
                 assert P.is_contiguous() and P.shape == (n, inner) and X.shape == (-(-n // 32), inner)
 
 
+def test_contiguous_views_with_length_one_axes(cuda):
+    """Contiguous views whose length-one axes carry strides other than a fresh tensor's (torch ignores those
+    strides when it calls a view contiguous): every axis of each, the same codes and scales as the oracle."""
+    from mxq import block
+    rng = np.random.default_rng(12)
+    base = torch.from_numpy(_edge_matrix(rng, 40, 70)).cuda()
+    views = [base[:, :33][:1], base[:1, :64].unsqueeze(1), base.t()[:, :1], base.t()[:, 3:4].unsqueeze(0)]
+    for V in views:
+        assert V.is_contiguous()
+        V32 = V.cpu().numpy().copy()
+        for axis in range(V.ndim):
+            P, X = block.mxgemmini.quantize(V, "MXFP8_E4M3", axis=axis)
+            wP, wX = ob.mxgemmini_quantize(V32, "MXFP8_E4M3", axis)
+            assert_bits_equal(P.cpu().numpy(), wP, f"P {tuple(V.shape)} {V.stride()} axis {axis}")
+            assert_bits_equal(X.cpu().numpy(), wX, f"X {tuple(V.shape)} {V.stride()} axis {axis}")
+
+
 def test_cpu_tensors_round_trip_through_gpu(cuda):
     from mxq import block
     V = torch.randn(64, 8)
