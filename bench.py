@@ -587,7 +587,7 @@ def c2_variants_line(torch, steps, inp):
     return out, cols
 
 
-def mfma_line(torch, steps, P_A, X_A, P_B, X_B, inp=None):
+def mfma_line(torch, steps, P_A, X_A, P_B, X_B, inp):
     """mfma_accum (the matrix-core comparison product) on the benchmark's own codes: pack both operands to FP8
     and E8M0 bytes, then V_MFMA_SCALE_F32_32X32X64_F8F6F4.  The kernel rate is held against MI355X's dense FP8
     peak, 5.0 PFLOP/s.  With the inputs, the same x and W quantized to MXFP6_E2M3 and MXFP4 travel as FP6 and
@@ -598,24 +598,30 @@ def mfma_line(torch, steps, P_A, X_A, P_B, X_B, inp=None):
     s = torch.cuda.current_stream(dev)
     flops = 2 * P_A.shape[0] * P_A.shape[1] * P_B.shape[1]
 
-    def timed(ops, fmt, peak):
+    def timed(ops, fmt, peak, packed=None):
         fn = lambda: mxq.mfma_accum(*ops, fmt)                                    # noqa: E731
-        fn()
+        _warm(fn)
         ms = _events_ms(fn, steps, s)
         res, calls, held = _capture(fn, "mxq_mx_mfma")           # held: the packed operands
         kms = _replay_ms(calls, "mxq_mx_mfma", steps, s)
         del res, calls, held
         k_tf = flops / (kms / 1e3) / 1e12 if kms else None
-        return {"ms": round(ms, 4), "kernel_ms": round(kms, 4) if kms else None,
+        line = {"ms": round(ms, 4), "kernel_ms": round(kms, 4) if kms else None,
                 "kernel_TFLOPs": round(k_tf, 2) if k_tf else None, "peak_TFLOPs": peak,
                 "frac": round(k_tf / peak, 4) if k_tf else None}
-    out = {"workload": "mfma_accum on the same MXFP8_E4M3 codes (M = 512, N = 4096, K = 4096)", "kernel": "k_mx_mfma",
-           **timed((P_A, X_A, P_B, X_B), "MXFP8_E4M3", FP8_PEAK_TFLOPS)}
-    if inp is not None:
-        xt, wt = inp["x"].t().contiguous().to(dev), inp["W"].t().contiguous().to(dev)
-        for fmt in ("MXFP6_E2M3", "MXFP4"):
-            a, b = block.mxgemmini.quantize(xt, fmt, axis=0), block.mxgemmini.quantize(wt, fmt, axis=0)
-            out[fmt] = timed((a[0], a[1], b[0], b[1]), fmt, FP6_FP4_PEAK_TFLOPS)
+        if packed is not None:                                   # the same operands as mxq.packed bytes
+            fb = lambda: mxq.mfma_accum_packed(*packed, fmt, check=False)        # noqa: E731
+            _warm(fb)
+            line["from_bytes_ms"] = round(_events_ms(fb, steps, s), 4)
+        return line
+    xt, wt = inp["x"].t().contiguous().to(dev), inp["W"].t().contiguous().to(dev)
+    by = lambda fmt: (*mxq.packed.quantize(xt, fmt), *mxq.packed.quantize(wt, fmt))    # noqa: E731
+    out = {"workload": "mfma_accum on the same MXFP8_E4M3 codes (M = 512, N = 4096, K = 4096); from_bytes_ms: "
+                       "mfma_accum_packed on the same codes and scales as mxq.packed bytes", "kernel": "k_mx_mfma",
+           **timed((P_A, X_A, P_B, X_B), "MXFP8_E4M3", FP8_PEAK_TFLOPS, by("MXFP8_E4M3"))}
+    for fmt in ("MXFP6_E2M3", "MXFP4"):
+        a, b = block.mxgemmini.quantize(xt, fmt, axis=0), block.mxgemmini.quantize(wt, fmt, axis=0)
+        out[fmt] = timed((a[0], a[1], b[0], b[1]), fmt, FP6_FP4_PEAK_TFLOPS, by(fmt))
     return out
 
 

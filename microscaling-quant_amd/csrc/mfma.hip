@@ -49,20 +49,45 @@ __device__ __forceinline__ bool e8m0_byte(float x, uint32_t& out) {
   return true;
 }
 
-// One thread per (column c < n32, 32-row block g < K64/32): the block's 32 codes and one scale byte, written
-// where the lane-ordered layout above puts them.  Consecutive threads take consecutive columns.  The codes come
-// from gfx950's conversions (V_CVT_SCALEF32_PK_*, scale 1), whose fields are already in the lane order (FP8 byte
-// j, FP6 field j at bit 6 j, FP4 nibble j at bit 4 j), and a value is a code of the type exactly when it is
-// finite and converts back to itself, bit for bit: an exact value converts to its own code (-0 keeping its
-// sign, as the OCP code of -0 does), and anything else to a different value (rounded, saturated, or E4M3's NaN
-// and E5M2's Inf past their ranges).
+// Writes one (column c < n32, 32-row block g < K64/32) block: its 32 codes as the instruction's fields (code j
+// at bit W j of words[], FP8: half j / 16 in words [h HW, ..)) and its scale byte, where the lane-ordered layout
+// above puts them.
+template <int W>
+__device__ __forceinline__ void put_block(const uint32_t (&words)[W], uint32_t sbyte, int64_t c, int64_t g,
+                                          int64_t nk, uint8_t* __restrict__ codes, uint8_t* __restrict__ scales) {
+  constexpr int HW = 16 * W / 32;                          // words per half block (16 codes of W bits)
+  constexpr int BPL = 4 * W;                               // bytes per lane and K step
+  const int64_t tile = c / 32, r = c % 32, step = g / 2, half = g % 2;
+  const int64_t chunk = (tile * nk + step) * 64;           // lane 0 of this (tile, step)
+  if constexpr (W == 8) {
+    // codes [0, 16) of the block go to lane r (h = 0), [16, 32) to lane 32 + r (h = 1); block 2s + half fills
+    // bytes [16 half, 16 half + 16) of each lane's 32
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(codes + (chunk + 32 * h + r) * BPL + half * (BPL / 2));
+#pragma unroll
+      for (int w = 0; w < HW; ++w) dst[w] = words[h * HW + w];
+    }
+  } else {
+    // the whole block to lane 32 half + r
+    uint32_t* dst = reinterpret_cast<uint32_t*>(codes + (chunk + 32 * half + r) * BPL);
+#pragma unroll
+    for (int w = 0; w < 2 * HW; ++w) dst[w] = words[w];
+  }
+  scales[chunk + half * 32 + r] = (uint8_t)sbyte;          // lane 32 * half + r reads block 2s + half
+}
+
+// One thread per (column c < n32, 32-row block g < K64/32): the block's 32 codes and one scale byte.
+// Consecutive threads take consecutive columns.  The codes come from gfx950's conversions (V_CVT_SCALEF32_PK_*,
+// scale 1), whose fields are already in the lane order (FP8 byte j, FP6 field j at bit 6 j, FP4 nibble j at
+// bit 4 j), and a value is a code of the type exactly when it is finite and converts back to itself, bit for
+// bit: an exact value converts to its own code (-0 keeping its sign, as the OCP code of -0 does), and anything
+// else to a different value (rounded, saturated, or E4M3's NaN and E5M2's Inf past their ranges).
 template <int W>
 __global__ void __launch_bounds__(256) k_mx_pack(const float* __restrict__ P, const float* __restrict__ X,
                                                  int64_t K, int64_t n, int64_t n32, int64_t K64, int kind,
                                                  uint8_t* __restrict__ codes, uint8_t* __restrict__ scales,
                                                  int* __restrict__ err) {
-  constexpr int HW = 16 * W / 32;                          // words per half block (16 codes of W bits)
-  constexpr int BPL = 4 * W;                               // bytes per lane and K step
   const int64_t nb64 = K64 / 32, nk = K64 / 64;
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;   // the launch keeps n32 * nb64 below 2^31
   if ((int64_t)t >= n32 * nb64) return;
@@ -78,7 +103,7 @@ __global__ void __launch_bounds__(256) k_mx_pack(const float* __restrict__ P, co
     nonzero |= (f2u(x[j]) & 0x7FFFFFFFu) != 0u;
     finite &= (f2u(x[j]) & 0x7FFFFFFFu) < 0x7F800000u;
   }
-  uint32_t words[2 * HW];                                  // code j at bit W j (FP8: half j / 16 in words [h HW, ..))
+  uint32_t words[W];                                       // code j at bit W j (FP8: half j / 16 in words [h HW, ..))
   bool same = true;                                        // every value came back from its code
   if constexpr (W == 8) {
 #pragma unroll
@@ -139,24 +164,139 @@ __global__ void __launch_bounds__(256) k_mx_pack(const float* __restrict__ P, co
       if (nonzero) bad = true;                             // a non-power-of-two scale only over zero codes
     }
   }
-  const int64_t tile = c / 32, r = c % 32, step = g / 2, half = g % 2;
-  const int64_t chunk = (tile * nk + step) * 64;           // lane 0 of this (tile, step)
-  if constexpr (W == 8) {
-    // codes [0, 16) of the block go to lane r (h = 0), [16, 32) to lane 32 + r (h = 1); block 2s + half fills
-    // bytes [16 half, 16 half + 16) of each lane's 32
+  put_block<W>(words, sbyte, c, g, nk, codes, scales);
+  if (bad) atomicOr(err, 1);
+}
+
+// k_mx_pack's layout from the byte wire format (mxq.packed: K x n code bytes, the code in the low w bits with
+// the OCP MX numbering, and ceil(K/32) x n E8M0 bytes), one thread per (column, block): the fields are the codes
+// themselves, so no conversion.  A byte that is no finite code of the type (E4M3 S.1111.111, E5M2's exponent
+// field all ones, FP6 and FP4 bits above w) or a scale of 0xFF (NaN) over a block with a nonzero code sets
+// the error word; the matrix cores then see what the low bits say.
+template <int W>
+__global__ void __launch_bounds__(256) k_mx_pack_bytes(const uint8_t* __restrict__ P, const uint8_t* __restrict__ X,
+                                                       int64_t K, int64_t n, int64_t n32, int64_t K64, int kind,
+                                                       uint8_t* __restrict__ codes, uint8_t* __restrict__ scales,
+                                                       int* __restrict__ err) {
+  const int64_t nb64 = K64 / 32, nk = K64 / 64;
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;   // the launch keeps n32 * nb64 below 2^31
+  if ((int64_t)t >= n32 * nb64) return;
+  const uint32_t gq = t / (uint32_t)n32;
+  const int64_t g = gq, c = t - gq * (uint32_t)n32;
+  const bool live = c < n;
+  const uint32_t fmask = (1u << W) - 1u;                   // the field (FP8: the whole byte)
+  const uint32_t mag = W == 8 ? 0x7Fu : (fmask >> 1);      // the field without its sign bit
+  uint32_t words[W] = {};
+  bool nonzero = false, bad = false;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      uint32_t* dst = reinterpret_cast<uint32_t*>(codes + (chunk + 32 * h + r) * BPL + half * (BPL / 2));
-#pragma unroll
-      for (int w = 0; w < HW; ++w) dst[w] = words[h * HW + w];
-    }
-  } else {
-    // the whole block to lane 32 half + r
-    uint32_t* dst = reinterpret_cast<uint32_t*>(codes + (chunk + 32 * half + r) * BPL);
-#pragma unroll
-    for (int w = 0; w < 2 * HW; ++w) dst[w] = words[w];
+  for (int j = 0; j < 32; ++j) {
+    const int64_t k = g * 32 + j;
+    const uint32_t b = live && k < K ? P[k * n + c] : 0u;
+    nonzero |= (b & mag) != 0u;
+    if constexpr (W == 8) bad |= kind == kE4M3 ? (b & 0x7Fu) == 0x7Fu : (b & 0x7Cu) == 0x7Cu;
+    else bad |= b > fmask;
+    const int bit = W * j;                                 // field j at bit W j of the 32 codes' W words
+    words[bit / 32] |= (b & fmask) << (bit % 32);
+    if (bit % 32 + W > 32) words[bit / 32 + 1] |= (b & fmask) >> (32 - bit % 32);
   }
-  scales[chunk + half * 32 + r] = (uint8_t)sbyte;          // lane 32 * half + r reads block 2s + half
+  uint32_t sbyte = 127u;
+  if (live && g * 32 < K) {
+    sbyte = X[g * n + c];
+    if (sbyte == 0xFFu) {
+      if (nonzero) bad = true;                             // a NaN scale only over zero codes
+      sbyte = 127u;
+    }
+  }
+  put_block<W>(words, sbyte, c, g, nk, codes, scales);
+  if (bad) atomicOr(err, 1);
+}
+
+// k_mx_pack_bytes for four adjacent columns of one block a thread, n % 4 == 0 and the byte arrays 4-byte
+// aligned: the block's 32 rows load as one word each (the four columns' bytes; eight consecutive threads read
+// 32 contiguous bytes of a row), a byte transpose of each 4 x 4 square by permutes gives each column's codes
+// four rows to a word, and each column's lane bytes leave in 16- or 8-byte stores.  Same checks, fields and
+// layout as k_mx_pack_bytes.
+__device__ __forceinline__ void transpose4x4(uint32_t& a, uint32_t& b, uint32_t& c, uint32_t& d) {
+  // rows a, b, c, d of four bytes (byte q = column q) -> columns: a = column 0's four rows, ...
+  const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);   // a0 b0 a1 b1
+  const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);   // a2 b2 a3 b3
+  const uint32_t cd_lo = __builtin_amdgcn_perm(d, c, 0x05010400u);   // c0 d0 c1 d1
+  const uint32_t cd_hi = __builtin_amdgcn_perm(d, c, 0x07030602u);   // c2 d2 c3 d3
+  a = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);             // a0 b0 c0 d0
+  b = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);             // a1 b1 c1 d1
+  c = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);             // a2 b2 c2 d2
+  d = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);             // a3 b3 c3 d3
+}
+
+template <int W>
+__global__ void __launch_bounds__(256) k_mx_pack_bytes4(const uint8_t* __restrict__ P, const uint8_t* __restrict__ X,
+                                                        int64_t K, int64_t n, int64_t n32, int64_t K64, int kind,
+                                                        uint8_t* __restrict__ codes, uint8_t* __restrict__ scales,
+                                                        int* __restrict__ err) {
+  constexpr int BPL = 4 * W;
+  const int64_t nk = K64 / 64, nq = n32 / 4;
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;   // the launch keeps nq * K64 / 32 below 2^31
+  if ((int64_t)t >= nq * (K64 / 32)) return;
+  const uint32_t gq = t / (uint32_t)nq;
+  const int64_t g = gq, c0 = (int64_t)(t - gq * (uint32_t)nq) * 4;
+  const bool live = c0 < n;                                // n % 4 == 0: the quad is whole or past n
+  const int64_t tile = c0 / 32, r0 = c0 % 32, step = g / 2, half = g % 2;
+  const int64_t chunk = (tile * nk + step) * 64;
+  uint32_t w[32];                                          // row k's four bytes, then column-major (below)
+  bool bad = false;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    const int64_t row = g * 32 + k;
+    w[k] = live && row < K ? *reinterpret_cast<const uint32_t*>(P + row * n + c0) : 0u;
+    if constexpr (W == 8) {
+      const uint32_t y = kind == kE4M3 ? (w[k] & 0x7F7F7F7Fu) + 0x01010101u : (w[k] & 0x7C7C7C7Cu) + 0x04040404u;
+      bad |= (y & 0x80808080u) != 0u;                      // E4M3 S.1111.111, E5M2 S.11111.xx
+    } else {
+      bad |= (w[k] & (W == 6 ? 0xC0C0C0C0u : 0xF0F0F0F0u)) != 0u;
+    }
+  }
+  uint32_t sw = live && g * 32 < K ? *reinterpret_cast<const uint32_t*>(X + g * n + c0) : 0x7F7F7F7Fu;
+  // after the transposes, w[4 i + q] holds column q's rows 4 i .. 4 i + 3
+#pragma unroll
+  for (int i = 0; i < 8; ++i) transpose4x4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  const uint32_t mag = W == 8 ? 0x7F7F7F7Fu : (W == 6 ? 0x1F1F1F1Fu : 0x07070707u);
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    bool nonzero = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) nonzero |= (w[4 * i + q] & mag) != 0u;
+    if (((sw >> (8 * q)) & 0xFFu) == 0xFFu) {
+      bad |= nonzero;                                      // a NaN scale only over zero codes
+      sw = (sw & ~(0xFFu << (8 * q))) | (127u << (8 * q));
+    }
+    if constexpr (W == 8) {
+      // codes [0, 16) to lane r (h = 0), [16, 32) to lane 32 + r, at bytes [16 half, 16 half + 16)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<u32x4*>(codes + (chunk + 32 * h + r0 + q) * BPL + half * (BPL / 2)) =
+            u32x4{w[4 * (4 * h) + q], w[4 * (4 * h + 1) + q], w[4 * (4 * h + 2) + q], w[4 * (4 * h + 3) + q]};
+    } else {
+      // the whole block to lane 32 half + r, code j at bit W j
+      uint32_t f[W] = {};
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const uint32_t b = (w[4 * (j / 4) + q] >> (8 * (j % 4))) & 0xFFu;
+        const int bit = W * j;
+        f[bit / 32] |= b << (bit % 32);
+        if (bit % 32 + W > 32) f[bit / 32 + 1] |= b >> (32 - bit % 32);
+      }
+      uint8_t* dst = codes + (chunk + 32 * half + r0 + q) * BPL;
+      if constexpr (W == 4) {
+        *reinterpret_cast<u32x4*>(dst) = u32x4{f[0], f[1], f[2], f[3]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) reinterpret_cast<u32x2*>(dst)[j] = u32x2{f[2 * j], f[2 * j + 1]};
+      }
+    }
+  }
+  *reinterpret_cast<uint32_t*>(scales + chunk + half * 32 + r0) = sw;
   if (bad) atomicOr(err, 1);
 }
 
@@ -350,6 +490,32 @@ extern "C" int mxq_mx_pack(const float* P, const float* X, int64_t K, int64_t n,
   else if (code_bits(kind) == 6) k_mx_pack<6><<<grid, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
   else k_mx_pack<4><<<grid, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
   return mxq::check_launch("mxq_mx_pack");
+}
+
+extern "C" int mxq_mx_pack_bytes(const uint8_t* P, const uint8_t* X, int64_t K, int64_t n, int32_t kind,
+                                 uint8_t* codes, uint8_t* scales, int32_t* err, mxq_stream_t stream) {
+  if (K < 0 || n < 0 || kind < kE4M3 || kind > kE2M1) return mxq::invalid("mxq_mx_pack_bytes: bad arguments");
+  const int64_t K64 = mxq::ceil_div(K, 64) * 64;
+  if (n == 0 || K64 == 0) return MXQ_OK;
+  if (!P || !X || !codes || !scales || !err) return mxq::invalid("mxq_mx_pack_bytes: NULL pointer");
+  if (reinterpret_cast<uintptr_t>(codes) % 16) return mxq::invalid("mxq_mx_pack_bytes: codes must be 16-byte aligned");
+  const int64_t n32 = mxq::ceil_div(n, 32) * 32;
+  const int64_t threads = n32 * (K64 / 32);
+  if (threads >= (int64_t(1) << 31)) return mxq::invalid("mxq_mx_pack_bytes: operand too large (2^31 blocks of 32)");
+  const dim3 grid = mxq::grid_for(threads, 256);
+  hipStream_t st = mxq::as_stream(stream);
+  mxq::KernelTimer timer("mx_pack_bytes", st);
+  if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(P) | reinterpret_cast<uintptr_t>(X)) % 4 == 0) {
+    const dim3 g4 = mxq::grid_for(n32 / 4 * (K64 / 32), 256);
+    if (code_bits(kind) == 8) k_mx_pack_bytes4<8><<<g4, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
+    else if (code_bits(kind) == 6) k_mx_pack_bytes4<6><<<g4, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
+    else k_mx_pack_bytes4<4><<<g4, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
+    return mxq::check_launch("mxq_mx_pack_bytes");
+  }
+  if (code_bits(kind) == 8) k_mx_pack_bytes<8><<<grid, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
+  else if (code_bits(kind) == 6) k_mx_pack_bytes<6><<<grid, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
+  else k_mx_pack_bytes<4><<<grid, 256, 0, st>>>(P, X, K, n, n32, K64, kind, codes, scales, err);
+  return mxq::check_launch("mxq_mx_pack_bytes");
 }
 
 extern "C" int mxq_mx_mfma(const uint8_t* A, const uint8_t* SA, int32_t a_kind, const uint8_t* B, const uint8_t* SB,

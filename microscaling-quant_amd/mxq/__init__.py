@@ -12,7 +12,8 @@ hand-written HIP kernel of libmxq_hip.so on an AMD Instinct MI355X.
     matmul            systolic: Y = A^T B from codes and scales in the hardware's summation order, with the
                       MXGEMMINI or MXQUANT Arithmetic and a per-lane accumulator schedule
     fp64_accum        the same codes with no rounding inside the multiply: the error floor
-    mfma_accum        the same comparison on the gfx950 matrix cores, within mfma_tolerance(K) * sum |a b|
+    mfma_accum        the same comparison on the gfx950 matrix cores, within mfma_tolerance(K) * sum |a b|;
+                      mfma_accum_packed takes the codes and scales as mxq.packed bytes
     schedule          one float(e, m) per accumulator position: load(csv), fixed(e, m), HW_FINAL
     scheme            Scheme(name, a, b, reduce): one explicit chain for one matmul
     nn                MXLinear, patch, attend: Schemes inside a model
@@ -24,9 +25,9 @@ import torch  # noqa: F401  (first: libmxq_hip.so binds to the HIP runtime torch
 from . import rounding, arith, schedule, scale_factor, element_quant, lut, block, matmul, scheme, nn, packed
 from .block import BLOCK
 from ._fp64_accum import fp64_accum
-from ._mfma_accum import mfma_accum, mfma_tolerance
+from ._mfma_accum import mfma_accum, mfma_accum_packed, mfma_tolerance
 from .element_quant.formats import Format
 from .scheme import Scheme
 
 __all__ = ["rounding", "arith", "schedule", "scale_factor", "element_quant", "lut", "block", "matmul", "scheme", "nn",
-           "packed", "BLOCK", "Format", "Scheme", "fp64_accum", "mfma_accum", "mfma_tolerance"]
+           "packed", "BLOCK", "Format", "Scheme", "fp64_accum", "mfma_accum", "mfma_accum_packed", "mfma_tolerance"]

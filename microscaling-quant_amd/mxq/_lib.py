@@ -114,6 +114,7 @@ SIGNATURES = {
     "mxq_anchor_tree": (c_i32, [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i32,
                                 c_i32, ctypes.POINTER(AnchorSpec), ctypes.POINTER(ArithSpec), c_ptr, c_i32, c_ptr]),
     "mxq_mx_pack": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "mxq_mx_pack_bytes": (c_i32, [c_ptr, c_ptr, c_i64, c_i64, c_i32, c_ptr, c_ptr, c_ptr, c_ptr]),
     "mxq_mx_mfma": (c_i32, [c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr]),
     "mxq_lut_tables": (c_i32, [c_ptr, c_i64, c_i64, c_i32, c_i32, c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_i32, c_i32,
                                c_ptr, c_ptr, c_ptr]),

@@ -37,7 +37,7 @@ from . import _lib
 from .element_quant.formats import Format, get
 from .matmul._common import check_operands
 
-__all__ = ["mfma_accum", "mfma_tolerance"]
+__all__ = ["mfma_accum", "mfma_accum_packed", "mfma_tolerance"]
 
 # the instruction's operand types (cbsz / blgp) and their code widths in bits
 _E4M3, _E5M2, _E2M3, _E3M2, _E2M1 = 0, 1, 2, 3, 4
@@ -66,6 +66,56 @@ def _pack(P: torch.Tensor, X: torch.Tensor, kind: int, K: int, err: torch.Tensor
     _lib.run("mxq_mx_pack", _lib.ptr(P), _lib.ptr(X), K, n, kind, _lib.ptr(codes), _lib.ptr(scales), _lib.ptr(err),
              _lib.stream(dev))
     return codes, scales, K64
+
+
+def _pack_bytes(codes: torch.Tensor, scales: torch.Tensor, kind: int, K: int, err: torch.Tensor, dev):
+    n = codes.shape[1]
+    n32 = -(-n // 32) * 32
+    K64 = -(-K // 64) * 64
+    out = torch.empty(n32 * K64 * _BITS[kind] // 8, dtype=torch.uint8, device=dev)
+    sc = torch.empty(n32 * K64 // 32, dtype=torch.uint8, device=dev)
+    _lib.run("mxq_mx_pack_bytes", _lib.ptr(codes), _lib.ptr(scales), K, n, kind, _lib.ptr(out), _lib.ptr(sc),
+             _lib.ptr(err), _lib.stream(dev))
+    return out, sc, K64
+
+
+@torch.no_grad()
+def mfma_accum_packed(codes_A: torch.Tensor, scales_A: torch.Tensor, codes_B: torch.Tensor, scales_B: torch.Tensor,
+                      fmt_a: Union[str, Format], fmt_b: Optional[Union[str, Format]] = None, *,
+                      check: bool = True) -> torch.Tensor:
+    """mfma_accum from the byte wire format of mxq.packed: A's codes (K x M uint8, mxq.packed.quantize(A, fmt,
+    axis=0)) and E8M0 scales (ceil(K/32) x M uint8), the same of B (K x N).  The bytes are the matrix cores'
+    fields already, so no float32 codes are read.  A byte that is no finite code of its format, or a NaN scale
+    over a block with a nonzero code, raises ValueError; check=False skips that test (one host synchronisation)
+    and the matrix cores then read what the low bits say."""
+    for name, t in (("codes_A", codes_A), ("scales_A", scales_A), ("codes_B", codes_B), ("scales_B", scales_B)):
+        if t.dtype != torch.uint8 or t.ndim != 2:
+            raise ValueError(f"mfma_accum_packed: {name} must be a 2-D uint8 tensor, got {t.dtype} {tuple(t.shape)}")
+    K, M = codes_A.shape
+    N = codes_B.shape[1]
+    nb = -(-K // 32)
+    if codes_B.shape[0] != K:
+        raise ValueError(f"mfma_accum_packed: codes_B has {codes_B.shape[0]} rows, codes_A {K}")
+    if tuple(scales_A.shape) != (nb, M) or tuple(scales_B.shape) != (nb, N):
+        raise ValueError(f"mfma_accum_packed: scales must be ({nb}, M) and ({nb}, N), got {tuple(scales_A.shape)} "
+                         f"and {tuple(scales_B.shape)}")
+    ka, kb = _kind(fmt_a), _kind(fmt_a if fmt_b is None else fmt_b)
+    dev = _lib.compute_device(codes_A)
+    ops = [_lib.to_device(t.detach(), dev).contiguous() for t in (codes_A, scales_A, codes_B, scales_B)]
+    C = torch.zeros((M, N), dtype=torch.float32, device=dev) if K == 0 else \
+        torch.empty((M, N), dtype=torch.float32, device=dev)
+    if K == 0 or M == 0 or N == 0:
+        return _lib.back(C, codes_A)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    with _lib.on(dev):
+        A8, SA, K64 = _pack_bytes(ops[0], ops[1], ka, K, err, dev)
+        B8, SB, _ = _pack_bytes(ops[2], ops[3], kb, K, err, dev)
+        if check and int(err.item()):
+            raise ValueError("mfma_accum_packed: a byte is no finite code of its format, or a block with nonzero "
+                             "codes has a NaN scale")
+        _lib.run("mxq_mx_mfma", _lib.ptr(A8), _lib.ptr(SA), ka, _lib.ptr(B8), _lib.ptr(SB), kb, _lib.ptr(C), K64, M,
+                 N, _lib.stream(dev))
+    return _lib.back(C, codes_A)
 
 
 @torch.no_grad()

@@ -272,6 +272,66 @@ def test_rejects(cuda):
         mxq.mfma_accum(ones, X, ones, X, "FP32")
 
 
+@pytest.mark.parametrize("fmt_a,fmt_b", [("MXFP8_E4M3", "MXFP8_E4M3"), ("MXFP8_E5M2", "MXFP8_E5M2"),
+                                         ("MXFP6_E3M2", "MXFP6_E2M3"), ("MXFP4", "MXFP8_E5M2"),
+                                         ("MXFP8_E4M3", "MXFP4")])
+@pytest.mark.parametrize("shape", [(1000, 70, 130), (4096, 512, 256)])
+def test_packed_bytes_equal_float_codes(cuda, fmt_a, fmt_b, shape):
+    """mfma_accum_packed on mxq.packed's code and E8M0 bytes gives the bits mfma_accum gives on the same
+    quantizer's float32 codes and scales (the matrix cores see the same fields), with and without the check."""
+    import mxq
+    K, M, N = shape
+    g = torch.Generator(device="cuda").manual_seed(K + M)
+    A = torch.randn(K, M, device="cuda", generator=g)
+    B = torch.randn(K, N, device="cuda", generator=g) * 0.1
+    kw = dict(rounding_mode="rne", scale_floor=2.0 ** -23)
+    ca, sa = mxq.packed.quantize(A, fmt_a, "mxgemmini", 0, **kw)
+    cb, sb = mxq.packed.quantize(B, fmt_b, "mxgemmini", 0, **kw)
+    PA, XA = mxq.block.mxgemmini.quantize(A, fmt_a, axis=0, **kw)
+    PB, XB = mxq.block.mxgemmini.quantize(B, fmt_b, axis=0, **kw)
+    want = mxq.mfma_accum(PA, XA, PB, XB, fmt_a, fmt_b)
+    assert torch.equal(mxq.mfma_accum_packed(ca, sa, cb, sb, fmt_a, fmt_b), want)
+    assert torch.equal(mxq.mfma_accum_packed(ca, sa, cb, sb, fmt_a, fmt_b, check=False), want)
+
+
+def test_packed_bytes_rejects(cuda):
+    """Bytes that are no finite code of the format, and a NaN scale over a block with a nonzero code, raise;
+    a NaN scale over an all-zero block does not; malformed tensors raise before any launch."""
+    import mxq
+    for n in (4, 5):                                          # four columns a thread, and one
+        _packed_rejects(mxq, n)
+    codes = torch.zeros(64, 4, dtype=torch.uint8, device="cuda")
+    scales = torch.full((2, 4), 127, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError, match="uint8"):
+        mxq.mfma_accum_packed(codes.float(), scales, codes, scales, "MXFP8_E4M3")
+    with pytest.raises(ValueError, match="scales must be"):
+        mxq.mfma_accum_packed(codes, scales[:1], codes, scales, "MXFP8_E4M3")
+    with pytest.raises(ValueError, match="rows"):
+        mxq.mfma_accum_packed(codes, scales, codes[:32], scales[:1], "MXFP8_E4M3")
+
+
+def _packed_rejects(mxq, n):
+    codes = torch.zeros(64, n, dtype=torch.uint8, device="cuda")
+    codes[5, 1] = 0x38                                                      # 1.0 in E4M3
+    scales = torch.full((2, n), 127, dtype=torch.uint8, device="cuda")
+    assert float(mxq.mfma_accum_packed(codes, scales, codes, scales, "MXFP8_E4M3")[1, 1]) == 1.0
+    for fmt, byte in (("MXFP8_E4M3", 0x7F), ("MXFP8_E4M3", 0xFF), ("MXFP8_E5M2", 0x7C), ("MXFP8_E5M2", 0xFE),
+                      ("MXFP6_E2M3", 0x40), ("MXFP6_E3M2", 0x80), ("MXFP4", 0x10)):
+        bad = codes.clone()
+        bad[7, 2] = byte
+        with pytest.raises(ValueError, match="no finite code"):
+            mxq.mfma_accum_packed(bad, scales, codes, scales, fmt)
+        mxq.mfma_accum_packed(bad, scales, codes, scales, fmt, check=False)
+    nan = scales.clone()
+    nan[0, 1] = 0xFF
+    with pytest.raises(ValueError, match="NaN scale"):
+        mxq.mfma_accum_packed(codes, nan, codes, scales, "MXFP8_E4M3")
+    nan = scales.clone()
+    nan[1, 3] = 0xFF                                                        # rows 32..63 of column 3: all zero
+    assert torch.equal(mxq.mfma_accum_packed(codes, nan, codes, scales, "MXFP8_E4M3"),
+                       mxq.mfma_accum_packed(codes, scales, codes, scales, "MXFP8_E4M3"))
+
+
 def test_misaligned_code_views(cuda):
     """Codes handed in as a contiguous view at an element offset off the 16-byte grid give the bits of a fresh
     copy of them."""
