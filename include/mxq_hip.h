@@ -34,7 +34,7 @@ typedef void* mxq_stream_t;
  *      mask values; mxq_systolic_fast_lanes; the dither entry points. */
 #define MXQ_ABI_VERSION 2
 
-enum { MXQ_OK = 0, MXQ_EINVAL = 1, MXQ_EHIP = 2 };
+enum { MXQ_OK = 0, MXQ_EINVAL = 1, MXQ_EHIP = 2, MXQ_EBUSY = 3 };
 
 /* Input element types of the block quantizer. */
 enum { MXQ_DT_F32 = 0, MXQ_DT_BF16 = 1, MXQ_DT_F16 = 2 };
@@ -230,8 +230,11 @@ int mxq_systolic_batched(const float* P_A, const float* X_A, const float* P_B, c
  * fast kernel's per-tile flags live in a 1 MiB array the library holds on each GPU (kept until the process
  * ends), so ceil(M/32) * ceil(N/32) may be at most 262144 (M * N up to 2^28 outputs); larger shapes return
  * MXQ_EINVAL.  The call allocates nothing and makes no host synchronisation; the current device must be the
- * stream's.  Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams or
- * threads) race and must be serialised by the caller.  Results are bit-identical to mxq_systolic's. */
+ * stream's.  Every call on one GPU shares that GPU's array, so calls must not overlap on one GPU: a call on
+ * another stream than the previous call's, made while that call's kernels may still run (an event recorded
+ * behind them is pending), is refused with MXQ_EBUSY before any launch; calls on one stream are ordered by it.
+ * Calls made while their stream is captured into a graph are not checked (the caller orders the replays).
+ * Results are bit-identical to mxq_systolic's. */
 int mxq_systolic_noalloc(const float* P_A, const float* X_A, const float* P_B, const float* X_B, float* C,
                          int64_t K, int64_t M, int64_t N, const int32_t* lane_e, const int32_t* lane_m, int32_t size,
                          int32_t block_size, const mxq_arith_spec* arith, int32_t force_general,

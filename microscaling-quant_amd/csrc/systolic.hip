@@ -1415,38 +1415,48 @@ static __device__ __align__(256) uint32_t scratch[kScratchWords];
 namespace {
 
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
-uint32_t* g_scratch[kMaxDevices] = {};
 
-// the scratch array's address on the current device (which must be the stream's device)
-int scratch_on_device(hipStream_t st, uint32_t** out) {
+// Per device: the scratch array's address, and the guard against calls that overlap on the GPU: an event
+// recorded behind each call's kernels on its stream.  A call on another stream while that event is pending
+// would share the array with a running call, so it is refused (MXQ_EBUSY); calls on one stream are ordered by
+// the stream and need no test.  Calls made while their stream is being captured into a graph neither test nor
+// record (the graph's replays are the caller's to order).
+struct ScratchSlot {
+  uint32_t* p = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool pending = false;        // `done` was recorded by a call outside capture
+};
+std::mutex g_scratch_mu;       // held from the guard's test through the launch and the record
+ScratchSlot g_scratch[kMaxDevices];
+
+int hip_fail(const char* what, hipError_t err) {
+  mxq::set_error(std::string("mxq_systolic_noalloc: ") + what + ": " + hipGetErrorString(err));
+  return MXQ_EHIP;
+}
+
+// The current device (which must be the stream's) and its slot, set up on the device's first call.
+int slot_on_device(hipStream_t st, ScratchSlot** out) {
   int dev = -1;
   hipError_t err = hipGetDevice(&dev);
-  if (err != hipSuccess) {
-    mxq::set_error(std::string("mxq_systolic_noalloc: hipGetDevice: ") + hipGetErrorString(err));
-    return MXQ_EHIP;
-  }
+  if (err != hipSuccess) return hip_fail("hipGetDevice", err);
   if (dev < 0 || dev >= kMaxDevices) return mxq::invalid("mxq_systolic_noalloc: device index out of range");
   if (st) {
     int sdev = -1;
     err = hipStreamGetDevice(st, &sdev);
-    if (err != hipSuccess) {
-      mxq::set_error(std::string("mxq_systolic_noalloc: hipStreamGetDevice: ") + hipGetErrorString(err));
-      return MXQ_EHIP;
-    }
+    if (err != hipSuccess) return hip_fail("hipStreamGetDevice", err);
     if (sdev != dev) return mxq::invalid("mxq_systolic_noalloc: the stream belongs to another device than the current one");
   }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch[dev]) {
+  ScratchSlot& sl = g_scratch[dev];
+  if (!sl.p) {
     void* p = nullptr;
     err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (err != hipSuccess || !p) {
-      mxq::set_error(std::string("mxq_systolic_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(err));
-      return MXQ_EHIP;
-    }
-    g_scratch[dev] = static_cast<uint32_t*>(p);
+    if (err != hipSuccess || !p) return hip_fail("hipGetSymbolAddress", err);
+    err = hipEventCreateWithFlags(&sl.done, hipEventDisableTiming);
+    if (err != hipSuccess) return hip_fail("hipEventCreateWithFlags", err);
+    sl.p = static_cast<uint32_t*>(p);
   }
-  *out = g_scratch[dev];
+  *out = &sl;
   return MXQ_OK;
 }
 
@@ -1463,15 +1473,36 @@ extern "C" int mxq_systolic_noalloc(const float* P_A, const float* X_A, const fl
     return mxq::invalid("mxq_systolic_noalloc: ceil(M/32) * ceil(N/32) exceeds its 262144 tile flags "
                         "(use mxq_systolic with a workspace)");
   hipStream_t st = mxq::as_stream(stream);
-  uint32_t* flags = nullptr;
-  if (int rc = scratch_on_device(st, &flags)) return rc;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchSlot* sl = nullptr;
+  if (int rc = slot_on_device(st, &sl)) return rc;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t err = hipStreamIsCapturing(st, &cap);
+  if (err != hipSuccess) return hip_fail("hipStreamIsCapturing", err);
+  const bool captured = cap != hipStreamCaptureStatusNone;
+  if (!captured && sl->pending && sl->last != st) {
+    err = hipEventQuery(sl->done);
+    if (err == hipErrorNotReady) {
+      mxq::set_error("mxq_systolic_noalloc: a call on another stream is still running on this GPU and holds its "
+                     "scratch array; order the calls (one stream, or an event between them)");
+      return MXQ_EBUSY;
+    }
+    if (err != hipSuccess) return hip_fail("hipEventQuery", err);
+  }
   // every flag the general kernel reads is written by the fast kernel of the same call first: nothing in the
   // array has to start at zero
   SysArgs a{};
   a.A = {P_A, M, 0}; a.XA = {X_A, M, 0}; a.B = {P_B, N, 0}; a.XB = {X_B, N, 0};
-  a.C = C; a.ldc = N; a.batch_c = 0; a.flags = flags;
+  a.C = C; a.ldc = N; a.batch_c = 0; a.flags = sl->p;
   a.K = K; a.M = M; a.N = N; a.size = size; a.block_size = block_size; a.ar = *arith;
-  return run_systolic(a, lane_e, lane_m, 1, force_general, st);
+  if (int rc = run_systolic(a, lane_e, lane_m, 1, force_general, st)) return rc;
+  if (!captured) {
+    err = hipEventRecord(sl->done, st);
+    if (err != hipSuccess) return hip_fail("hipEventRecord", err);
+    sl->last = st;
+    sl->pending = true;
+  }
+  return MXQ_OK;
 }
 
 extern "C" int64_t mxq_systolic_workspace(int64_t K, int64_t M, int64_t N, int64_t count) {

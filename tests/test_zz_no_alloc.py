@@ -77,3 +77,35 @@ def test_no_alloc_size_limit(cuda):
     p, le, lm, ar = _args([t, t, t, t], 32, 16416, 16416)
     rc = lib.mxq_systolic_noalloc(*p, _lib.ptr(t), 32, 16416, 16416, le, lm, 16, 32, ar, 0, _lib.stream(t.device))
     assert rc == 1 and b"262144" in lib.mxq_last_error()
+
+
+def test_no_alloc_refuses_overlapping_streams(cuda):
+    """A call on a second stream while the first stream's call (4096^3, milliseconds of kernels) may still run
+    is refused with MXQ_EBUSY and launches nothing; once that call is done, the second stream's call runs and
+    gives the same bits; calls on one stream back to back are never refused."""
+    from mxq import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(32)
+    K = M = N = 4096
+    ops = _operands(rng, K, M, N, [])
+    p, le, lm, ar = _args(ops, K, M, N)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    C1 = torch.empty(M, N, device="cuda")
+    C2 = torch.full((M, N), float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    call = lambda C, s: lib.mxq_systolic_noalloc(*p, _lib.ptr(C), K, M, N, le, lm, 16, 32, ar, 0,   # noqa: E731
+                                                 s.cuda_stream)
+    assert call(C1, s1) == 0
+    assert call(C1, s1) == 0                            # the same stream: ordered by it
+    rc = call(C2, s2)
+    busy = rc == 3
+    assert rc in (0, 3)
+    if busy:
+        assert b"another stream" in lib.mxq_last_error()
+        s2.synchronize()
+        assert torch.isnan(C2).all(), "a refused call launches nothing"
+    s1.synchronize()
+    assert busy, "the first stream's 4096^3 call was still queued when the second call came"
+    assert call(C2, s2) == 0
+    s2.synchronize()
+    assert torch.equal(C1, C2)
