@@ -767,7 +767,7 @@ def main():
                      "frac": round(k_tops / VALU_ROOF_TOPS, 4) if k_tops else None,
                      "frac_survey_model": round(k_tops / SURVEY_ROOF_TOPS, 4) if k_tops else None,
                      "traffic": _profile_value("systolic_fast_c2_traffic", "bytes_per_launch"),
-                     "kernel": "k_systolic_fast64<16, true, true>", "kernel_ms": round(kms, 4) if kms else None,
+                     "kernel": "k_systolic_fast64<16, true, true, 2>", "kernel_ms": round(kms, 4) if kms else None,
                      "kernel_launches_timed": launches,
                      "executed": None if not (ops_per_mac and k_tops) else {
                          "valu_lane_ops_per_mac": ops_per_mac,

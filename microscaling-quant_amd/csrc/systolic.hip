@@ -796,9 +796,13 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 // read back from LDS once per stage; its verdict and flag are k_systolic_fast's.  No hints, no epilogue.
 constexpr int KS64 = 64;                            // rows per stage
 
-template <int SIZE, bool BF16_LAST, bool HWF>
-__global__ void __launch_bounds__(256) k_systolic_fast64(const SysArgs args, const FastLanes fl) {
-  constexpr int BM = 64, BN = 64, TM = 4, TN = 4, NBS = KS64 / KT;
+template <int SIZE, bool BF16_LAST, bool HWF, int TN>
+__global__ void __launch_bounds__(64 * 64 / (4 * TN)) k_systolic_fast64(const SysArgs args, const FastLanes fl) {
+  constexpr int BM = 64, BN = 64, TM = 4, NBS = KS64 / KT;
+  constexpr int NT = (BM / TM) * (BN / TN), NWV = NT / 64;   // threads, waves
+  static_assert(TN == 4 || TN == 2 || TN == 1, "4 x 4, 4 x 2 or 4 x 1 outputs a thread (4, 8 or 16 waves)");
+  // (launched with TN = 2: on 512 x 4096 outputs, K = 4096, 1.062 ms a call against 1.112 with TN = 4 (two waves
+  // a SIMD at 172 VGPRs) and 1.243 with TN = 1 (79 VGPRs: one workgroup a CU), the same bits)
   typedef __attribute__((address_space(3))) void* lds_t;
   static_assert(!HWF || (SIZE == 16 && BF16_LAST), "HW_FINAL has 16 lanes, the last bf16");
   const LaneConsts<HWF> lc{fl};
@@ -808,8 +812,8 @@ __global__ void __launch_bounds__(256) k_systolic_fast64(const SysArgs args, con
   __shared__ __align__(16) float sb0[KS64][BN], sb1[KS64][BN];
   __shared__ __align__(16) float xs_a[2][NBS][BM];
   __shared__ __align__(16) float xs_b[2][NBS][BN];
-  __shared__ uint32_t inexact_w[2][NBS][4];         // per buffer, block and wave: a scale denies the short add
-  __shared__ uint32_t red[3][4];
+  __shared__ uint32_t inexact_w[2][NBS][NWV];       // per buffer, block and wave: a scale denies the short add
+  __shared__ uint32_t red[3][NWV];
   const int tn = threadIdx.x % (BN / TN), tm = threadIdx.x / (BN / TN);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t z = blockIdx.z, ty = blockIdx.y, tx = blockIdx.x;
@@ -820,8 +824,8 @@ __global__ void __launch_bounds__(256) k_systolic_fast64(const SysArgs args, con
   const float* XB = args.XB.p + z * args.XB.batch + n0;
   const int64_t K = args.K;
   // a wave instruction moves 64 lanes x 16 bytes = 4 rows of 64 floats; a stage is 16 such row quads per
-  // operand, 4 per wave
-  constexpr int INST = KS64 / 4 / 4;
+  // operand, 16 / NWV per wave
+  constexpr int INST = KS64 / 4 / NWV;
   float xv[NBS];
   // the scales' loads go first: a wait the compiler places before rewriting their registers then does not
   // wait for the stage's direct-to-LDS loads too
@@ -871,9 +875,9 @@ __global__ void __launch_bounds__(256) k_systolic_fast64(const SysArgs args, con
   auto reduce_stage = [&](const float (&ca)[KS64][BM], const float (&cb)[KS64][BN], int buf)
                           __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < KS64 * BM / 4 / 256; ++j) {
-      const float4 qa = reinterpret_cast<const float4*>(&ca[0][0])[threadIdx.x + 256 * j];
-      const float4 qb = reinterpret_cast<const float4*>(&cb[0][0])[threadIdx.x + 256 * j];
+    for (int j = 0; j < KS64 * BM / 4 / NT; ++j) {
+      const float4 qa = reinterpret_cast<const float4*>(&ca[0][0])[threadIdx.x + NT * j];
+      const float4 qb = reinterpret_cast<const float4*>(&cb[0][0])[threadIdx.x + NT * j];
       max_a = umax(max_a, umax(umax(f2u(qa.x) & 0x7FFFFFFFu, f2u(qa.y) & 0x7FFFFFFFu),
                                umax(f2u(qa.z) & 0x7FFFFFFFu, f2u(qa.w) & 0x7FFFFFFFu)));
       max_b = umax(max_b, umax(umax(f2u(qb.x) & 0x7FFFFFFFu, f2u(qb.y) & 0x7FFFFFFFu),
@@ -881,13 +885,24 @@ __global__ void __launch_bounds__(256) k_systolic_fast64(const SysArgs args, con
     }
 #pragma unroll
     for (int q = 0; q < NBS; ++q) {
-      const bool short_add = BF16_LAST && (inexact_w[buf][q][0] | inexact_w[buf][q][1] | inexact_w[buf][q][2] |
-                                           inexact_w[buf][q][3]) == 0u;
+      uint32_t inexact = 0u;
+#pragma unroll
+      for (int v = 0; v < NWV; ++v) inexact |= inexact_w[buf][q][v];
+      const bool short_add = BF16_LAST && inexact == 0u;
       float scale[TM][TN];
       {
         const float4 xa = *reinterpret_cast<const float4*>(&xs_a[buf][q][tm * TM]);
-        const float4 xb = *reinterpret_cast<const float4*>(&xs_b[buf][q][tn * TN]);
-        const float fa[TM] = {xa.x, xa.y, xa.z, xa.w}, fb[TN] = {xb.x, xb.y, xb.z, xb.w};
+        float fb[TN];
+        if constexpr (TN == 4) {
+          const float4 xb = *reinterpret_cast<const float4*>(&xs_b[buf][q][tn * TN]);
+          fb[0] = xb.x; fb[1] = xb.y; fb[2] = xb.z; fb[3] = xb.w;
+        } else if constexpr (TN == 2) {
+          const float2 xb = *reinterpret_cast<const float2*>(&xs_b[buf][q][tn * TN]);
+          fb[0] = xb.x; fb[1] = xb.y;
+        } else {
+          fb[0] = xs_b[buf][q][tn];
+        }
+        const float fa[TM] = {xa.x, xa.y, xa.z, xa.w};
 #pragma unroll
         for (int x = 0; x < TM; ++x)
 #pragma unroll
@@ -899,8 +914,17 @@ __global__ void __launch_bounds__(256) k_systolic_fast64(const SysArgs args, con
 #pragma unroll
         for (int i = 0; i < SIZE; ++i) {
           const float4 a4 = *reinterpret_cast<const float4*>(&ca[r0 + i][tm * TM]);
-          const float4 b4 = *reinterpret_cast<const float4*>(&cb[r0 + i][tn * TN]);
-          const float a[TM] = {a4.x, a4.y, a4.z, a4.w}, b[TN] = {b4.x, b4.y, b4.z, b4.w};
+          const float a[TM] = {a4.x, a4.y, a4.z, a4.w};
+          float b[TN];
+          if constexpr (TN == 4) {
+            const float4 b4 = *reinterpret_cast<const float4*>(&cb[r0 + i][tn * TN]);
+            b[0] = b4.x; b[1] = b4.y; b[2] = b4.z; b[3] = b4.w;
+          } else if constexpr (TN == 2) {
+            const float2 b2 = *reinterpret_cast<const float2*>(&cb[r0 + i][tn * TN]);
+            b[0] = b2.x; b[1] = b2.y;
+          } else {
+            b[0] = cb[r0 + i][tn];
+          }
           if (BF16_LAST && i == SIZE - 1) {
             // bf16 lane: S plus the truncated product flushed below the threshold, RNE to bf16
 #pragma unroll
@@ -964,9 +988,13 @@ __global__ void __launch_bounds__(256) k_systolic_fast64(const SysArgs args, con
     red[2][wave] = max_x;
   }
   __syncthreads();
-  const uint32_t wa = umax(umax(red[0][0], red[0][1]), umax(red[0][2], red[0][3]));
-  const uint32_t wb = umax(umax(red[1][0], red[1][1]), umax(red[1][2], red[1][3]));
-  const uint32_t wx = umax(umax(red[2][0], red[2][1]), umax(red[2][2], red[2][3]));
+  uint32_t wa = 0u, wb = 0u, wx = 0u;
+#pragma unroll
+  for (int v = 0; v < NWV; ++v) {
+    wa = umax(wa, red[0][v]);
+    wb = umax(wb, red[1][v]);
+    wx = umax(wx, red[2][v]);
+  }
   const bool ok = wa < kFastAMaxBits && wb < 0x7F800000u && wx < 0x7F800000u &&
                   u2f(wa) * u2f(wb) <= args.fast_prod_max;
   if (threadIdx.x == 0) args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = ok ? 0u : 1u;
@@ -1228,14 +1256,14 @@ void launch_fast(int size, bool bf16_last, bool hwf, dim3 grid, hipStream_t st, 
 // spills, and k_systolic_fast takes them.
 void launch_fast64(int size, bool hwf, dim3 grid, hipStream_t st, const SysArgs& a, const FastLanes& fl) {
   if (hwf) {
-    k_systolic_fast64<16, true, true><<<grid, 256, 0, st>>>(a, fl);
+    k_systolic_fast64<16, true, true, 2><<<grid, 512, 0, st>>>(a, fl);
     return;
   }
   switch (size) {
-    case 4: k_systolic_fast64<4, true, false><<<grid, 256, 0, st>>>(a, fl); break;
-    case 8: k_systolic_fast64<8, true, false><<<grid, 256, 0, st>>>(a, fl); break;
-    case 16: k_systolic_fast64<16, true, false><<<grid, 256, 0, st>>>(a, fl); break;
-    default: k_systolic_fast64<32, true, false><<<grid, 256, 0, st>>>(a, fl); break;
+    case 4: k_systolic_fast64<4, true, false, 2><<<grid, 512, 0, st>>>(a, fl); break;
+    case 8: k_systolic_fast64<8, true, false, 2><<<grid, 512, 0, st>>>(a, fl); break;
+    case 16: k_systolic_fast64<16, true, false, 2><<<grid, 512, 0, st>>>(a, fl); break;
+    default: k_systolic_fast64<32, true, false, 2><<<grid, 512, 0, st>>>(a, fl); break;
   }
 }
 
