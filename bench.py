@@ -434,8 +434,9 @@ def lut_line(torch, steps, inp):
     pick_bytes = elems + elems * 4                                    # codes read, entries written
     mm = lambda: matmul.systolic(PA, XA, PB, XB, matmul.MXGEMMINI(), matmul.HW_FINAL)        # noqa: E731
     Y = mm()
-    ms_mm = _events_ms(mm, steps, s)
-    kms, _ = _kernel_ms(mm, steps, "systolic_fast")
+    _warm(mm, 3)
+    ms_mm = _events_ms(mm, max(steps, 5), s)
+    kms, _ = _kernel_ms(mm, max(steps, 5), "systolic_fast")
     macs = 4096 ** 3
     line = {"workload": "block.lut MXFP6_E3M2 4096x4096 (quantize and count, k-means, pick) + systolic 4096^3",
             "lut_quantize_ms": round(ms_q, 3),

@@ -9,7 +9,7 @@
 //
 // Operands are strided and batched: element (r, c) of problem z of an operand sits at base + z*batch + r*ld + c.
 //
-// Two kernels, both launched:
+// A fast kernel, then the general one:
 //   k_systolic_fast MXGEMMINI with size in {4, 8, 16, 32}, lanes (4, m <= 9) of non-decreasing m, optionally a
 //                   last (8, 7) lane, prod_m <= every e4 lane's m (checked on the host).  A's rows are staged
 //                   into LDS times 2^(6 + m) of their lane, so an e4 lane works in units of its subnormal step
@@ -28,8 +28,12 @@
 //                   While it computes, each workgroup keeps the largest |a|, |b| and scale it has read.  Its
 //                   results are exact when those are finite, max|a| < 2^100 and max|a| * max|b| stays under
 //                   the ladder's overflow bound; then it writes its tile and a 0 flag, otherwise only a 1 flag.
+//   k_systolic_fast64  the same check and results for ladders ending in a bf16 lane on 64 x 64 tiles, when the
+//                   operands need no bounds checks and the call has no hints or epilogue: 64-row stages loaded
+//                   straight into LDS, the lanes in value units (a product rounded to its lane's step by adding
+//                   and subtracting a constant, full rate, no staging scale or rescale), eight waves.
 //   k_systolic_gen  the full per-step rule for any codes, any lanes (e <= 8), MXGEMMINI or MXQUANT, NaN, Inf,
-//                   saturation and overflow included.  After the fast kernel it computes only the tiles whose
+//                   saturation and overflow included.  After a fast kernel it computes only the tiles whose
 //                   flag is 1; alone (no fast case, or forced) it computes everything.
 #include <algorithm>
 #include <cmath>
@@ -783,9 +787,9 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
 }
 
-// ------------------------------------------------------------------------- fast datapath, small grids
-// k_systolic_fast64: k_systolic_fast's datapath for grids too small to give every CU 4 workgroups of 64 x 64
-// outputs (e.g. 512 x 4096 outputs: 512 workgroups), where a workgroup must carry more work per staged byte.
+// ------------------------------------------------------------------------- fast datapath, 64-row stages
+// k_systolic_fast64: k_systolic_fast's datapath on 64 x 64 tiles for operands that need no bounds checks and
+// calls with no hints or epilogue, eight waves a workgroup (4 x 2 outputs a thread).
 // Its operands lie whole inside the matrices (M, N and K multiples of 64, rows 16-byte aligned, blocks of 32),
 // so every stage of 64 rows moves straight from global memory into LDS (global_load_lds_dwordx4: no registers,
 // no LDS stores, 1 KB per instruction per wave) while the previous stage is reduced; one barrier per two
@@ -1267,10 +1271,11 @@ void launch_fast64(int size, bool hwf, dim3 grid, hipStream_t st, const SysArgs&
   }
 }
 
-// Whether k_systolic_fast64 takes the launch: a ladder ending in a bf16 lane, a grid of 64 x 64 tiles that
-// gives every CU at least 2 but fewer than 4 workgroups, every 64-row stage inside the operands and 16-byte
-// aligned, blocks of 32, no hints and no epilogue (on 512 x 4096 outputs, K = 4096: 1.06 ms against 1.16 for
-// k_systolic_fast on 32 x 64 tiles).
+// Whether k_systolic_fast64 takes the launch: a ladder ending in a bf16 lane, at least one 64 x 64 tile per CU
+// (256), every 64-row stage inside the operands and 16-byte aligned, blocks of 32, no hints and no epilogue.
+// Measured against k_systolic_fast on MXGEMMINI HW_FINAL, the same bits: 512 x 4096 outputs, K = 4096: 1.06 ms
+// against 1.16 (32 x 64 tiles); 4096 x 4096 x 4096: 7.86 against 8.18; 1024 x 4096 x 4096: 2.04 against 2.45;
+// 256 x 4096 x 4096: 0.59 against 0.66; with 128 tiles (256 x 2048) half the CUs idle: 0.59 against 0.43.
 bool takes_fast64(const SysArgs& a, int64_t count) {
   const int64_t tiles = mxq::ceil_div(a.M, 64) * mxq::ceil_div(a.N, 64) * count;
   auto aligned = [](const Operand& o) {
@@ -1278,7 +1283,7 @@ bool takes_fast64(const SysArgs& a, int64_t count) {
   };
   return a.lane_e[a.size - 1] == 8 && !a.skip && !a.k_end && !a.epi_on && a.block_size == KT && a.K > 0 &&
          a.M % 64 == 0 && a.N % 64 == 0 &&
-         a.K % KS64 == 0 && tiles >= 2 * 256 && tiles < 4 * 256 && aligned(a.A) && aligned(a.B);
+         a.K % KS64 == 0 && tiles >= 256 && aligned(a.A) && aligned(a.B);
 }
 
 bool lanes_valid(const int32_t* e, const int32_t* m, int size) {
