@@ -40,8 +40,9 @@ HBM_PEAK_GBS = 8000.0
 # and v_and_b32 at that rate and v_rndne_f32, v_bfe_u32, v_add3_u32 at half of it (`--valu-rates`).
 VALU_LANE_OPS = 157.3e12 / 2
 # The emulated MAC's VALU issue on gfx950 in full-rate slots: an e4 lane step multiplies, masks the product,
-# rounds it to the lane grid (v_rndne_f32, half rate: 2 slots), adds exactly and rounds to nearest even at m
-# bits (three full-rate operations) = 8.  The roof prices every MAC at that step.
+# rounds it to the lane grid (adding and subtracting a constant, two full-rate operations, or v_rndne_f32 at half
+# rate: 2 slots either way), adds exactly and rounds to nearest even at m bits (three full-rate operations) = 8.
+# The roof prices every MAC at that step.
 SLOTS_PER_MAC_MODEL = 8
 VALU_ROOF_TOPS = VALU_LANE_OPS / SLOTS_PER_MAC_MODEL * 2 / 1e12   # 19.66 TOP/s emulated
 # The survey's algorithmic model: 10 lane-operations per emulated MAC (multiply, truncate, flush, saturate, the
@@ -778,9 +779,9 @@ def main():
                      "note": "VALU-bound emulation (neither HBM nor MFMA): achieved = 2 x 8,589,934,592 emulated "
                              "MACs / the fast kernel's average duration; peak = MI355X vector FP32 157.3 TFLOP/s = "
                              "78.6 T full-rate lane-slots/s, / 8 slots per emulated MAC (an e4 lane step on gfx950: "
-                             "multiply, mask, add and a 3-op nearest-even split at one slot each, round-to-integer "
-                             "at two as it issues at half rate) x 2 ops per MAC; frac_survey_model prices every "
-                             "MAC at 10 lane-operations (15.73 TOP/s), a model the kernel's 7-operation step beats; "
+                             "multiply, mask, the add and subtract that round to the lane's step, the exact add and "
+                             "a 3-op nearest-even split, one slot each) x 2 ops per MAC; frac_survey_model prices every "
+                             "MAC at 10 lane-operations (15.73 TOP/s), a model the kernel's 8-operation step beats; "
                              "`executed.frac` holds the counted instructions (full- and half-rate alike) against "
                              "the 78.6 T lane rate"},
     }

@@ -31,8 +31,9 @@ typedef void* mxq_stream_t;
  *   1  the first release.
  *   2  mxq_lut_tables takes the code format (fmt_e, fmt_m) before the grid; mxq_systolic_hints gained a_live
  *      and c_end; mxq_softmax_quantize_t takes a tail; mxq_mask_minabs and mxq_attend_hints give the largest
- *      mask values; mxq_systolic_fast_lanes; the dither entry points. */
-#define MXQ_ABI_VERSION 2
+ *      mask values; mxq_systolic_fast_lanes; the dither entry points.
+ *   3  mxq_mx_pack_bytes; the MXQ_EBUSY status of mxq_systolic_noalloc. */
+#define MXQ_ABI_VERSION 3
 
 enum { MXQ_OK = 0, MXQ_EINVAL = 1, MXQ_EHIP = 2, MXQ_EBUSY = 3 };
 
