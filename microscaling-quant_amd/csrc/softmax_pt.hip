@@ -35,6 +35,7 @@ namespace {
 constexpr int H = 2;          // 64-row groups per workgroup
 constexpr int RB = 64 * H;    // rows per workgroup
 constexpr int NT = 256 * H;   // threads per workgroup: 4 waves per row group
+static_assert(H == 2, "a workgroup pairs a front and a back row group");
 
 // torch's statistics of one row: lane l's elements l + 64 it, keys at and past `stored` taken from `tail`
 // (a mask row, through the score step) when it is not NULL, else -Inf (no part in the maximum, +0 in the sum)
@@ -79,7 +80,16 @@ __global__ void __launch_bounds__(NT) k_softmax_pt(const float* __restrict__ S, 
   __shared__ float mx_s[RB], sum_s[RB];
   __shared__ uint8_t full_s[RB];     // the row took the full-row path (its scores past k_end from the mask)
   __shared__ int group_full[H];      // some row of the 64-row group did
-  const int64_t r0 = (int64_t)blockIdx.x * RB;
+  // The workgroup's two 64-row groups: the x-th from the front and the x-th from the back of S's G groups.
+  // Under a causal mask a group's work grows with its query rows, and every workgroup is resident at once,
+  // so pairing a late group with an early one gives each workgroup (and CU) about the same work.
+  const int64_t G = (R + 63) / 64;
+  int64_t gbase[H];
+  bool gvalid[H];
+  gbase[0] = (int64_t)blockIdx.x * 64;
+  gbase[1] = (G - 1 - (int64_t)blockIdx.x) * 64;
+  gvalid[0] = true;
+  gvalid[1] = G - 1 - (int64_t)blockIdx.x > (int64_t)blockIdx.x;   // the middle group of an odd G once
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   // k_end and tail_max of each 64-row group (rows of one group share a problem: cols % 64 == 0)
   int ke[H];
@@ -88,8 +98,8 @@ __global__ void __launch_bounds__(NT) k_softmax_pt(const float* __restrict__ S, 
   for (int g = 0; g < H; ++g) {
     ke[g] = T;
     tmax[g] = -INFINITY;
-    if (has_tail && r0 + 64 * g < R) {
-      const int64_t rg = r0 + 64 * g, z = rg / cols, t = (rg - z * cols) / 64;
+    if (has_tail && gvalid[g]) {
+      const int64_t rg = gbase[g], z = rg / cols, t = (rg - z * cols) / 64;
       const int k = tl.k_end[z * (cols / 64) + t];
       ke[g] = k < 0 ? 0 : (k < T ? k : T);
       tmax[g] = tl.tail_max[z * (cols / 64) + t];
@@ -99,15 +109,16 @@ __global__ void __launch_bounds__(NT) k_softmax_pt(const float* __restrict__ S, 
   __syncthreads();
   // pass 1: each wave takes every (4 H)th row
   for (int j = w; j < RB; j += 4 * H) {
-    if (r0 + j >= R) break;
     const int g = j / 64;
-    const float* row = S + (r0 + j) * T;
+    const int64_t rr = gbase[g] + (j % 64);
+    if (!gvalid[g] || rr >= R) continue;
+    const float* row = S + rr * T;
     float mx, sm;
     row_stats<IT>(row, T, ke[g], nullptr, 0.0f, lane, mx, sm);
     bool full = false;
     if (ke[g] < T && !(mx < INFINITY && tmax[g] - mx <= -128.0f)) {       // the same in every lane
       full = true;
-      row_stats<IT>(row, T, ke[g], tail_row(tl, cols, r0 + j), tl.score.scale, lane, mx, sm);
+      row_stats<IT>(row, T, ke[g], tail_row(tl, cols, rr), tl.score.scale, lane, mx, sm);
     }
     if (lane == 0) {
       mx_s[j] = mx;
@@ -117,16 +128,16 @@ __global__ void __launch_bounds__(NT) k_softmax_pt(const float* __restrict__ S, 
     }
   }
   __syncthreads();
-  // pass 2: lane m of wave w takes row r0 + 64 (w % H) + m and the key blocks w / H, w / H + 4, ...: the
+  // pass 2: lane m of wave w takes row gbase[w % H] + m and the key blocks w / H, w / H + 4, ...: the
   // block's 32 probabilities recomputed, its maximum, scale and codes in the lane, and each code stored as
   // P^T[key][row], a run of 64 rows per store across the wave and of 64 H rows across the H waves that take
   // the same blocks (128 rows: 382.5 us against 387.5 with 64 on 32 heads x 2048 causal queries x 2048 keys;
   // no gain at 256)
   const int hg = w % H, wb = w / H;                 // row group, and first key block, of the wave
-  const int64_t r = r0 + 64 * hg + lane;
-  const bool live = r < R;
+  const int64_t r = gbase[hg] + lane;
+  const bool live = gvalid[hg] && r < R;
   const float mx = mx_s[64 * hg + lane], sm = sum_s[64 * hg + lane];
-  const float* src = S + (live ? r : r0) * T;
+  const float* src = S + (live ? r : gbase[0]) * T;
   const float* tail = live && full_s[64 * hg + lane] ? tail_row(tl, cols, r) : nullptr;
   const int nb = (T + 31) / 32;
   const int kg = ke[hg];                            // keys stored in S for this group
@@ -172,8 +183,8 @@ __global__ void __launch_bounds__(NT) k_softmax_pt(const float* __restrict__ S, 
       // per 32 rows (a half wave, inside one problem: cols % 32 == 0): any nonzero code or non-finite scale
       const uint64_t bal = __ballot(live && (nz != 0u || !(fabsf(xs) < INFINITY)));
       const int half = lane & 32;
-      const int64_t rh = r0 + 64 * hg + half;
-      if ((lane & 31) == 0 && rh < R) {
+      const int64_t rh = gbase[hg] + half;
+      if ((lane & 31) == 0 && gvalid[hg] && rh < R) {
         const int64_t z = rh / cols, g = (rh - z * cols) / 32;
         stage_live[(z * nb + b) * (cols / 32) + g] = ((bal >> half) & 0xFFFFFFFFull) != 0ull ? 1u : 0u;
       }
@@ -182,8 +193,8 @@ __global__ void __launch_bounds__(NT) k_softmax_pt(const float* __restrict__ S, 
   // the blocks past the written keys: codes +0, a zero block's scale, so their stage bytes are 0
   if (stage_live && nbw < nb) {
     const int half = lane & 32;
-    const int64_t rh = r0 + 64 * hg + half;
-    if ((lane & 31) == 0 && rh < R) {
+    const int64_t rh = gbase[hg] + half;
+    if ((lane & 31) == 0 && gvalid[hg] && rh < R) {
       const int64_t z = rh / cols, g = (rh - z * cols) / 32;
       for (int b = nbw + wb; b < nb; b += 4) stage_live[(z * nb + b) * (cols / 32) + g] = 0u;
     }
@@ -230,7 +241,7 @@ extern "C" int mxq_softmax_quantize_t(const float* S, int64_t R, int64_t T, floa
   if (!S || !PT_P || !PT_X) return mxq::invalid("mxq_softmax_quantize_t: NULL pointer");
   int it = 1;
   while (64 * it < T) it <<= 1;                        // next_pow2(T) / 64
-  const dim3 grid((unsigned)mxq::ceil_div(R, RB));
+  const dim3 grid((unsigned)mxq::ceil_div(mxq::ceil_div(R, 64), H));   // a front and a back 64-row group each
   hipStream_t st = mxq::as_stream(stream);
   const int ht = tail ? 1 : 0;
   switch (spec->rounding) {
