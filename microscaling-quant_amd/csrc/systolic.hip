@@ -29,7 +29,7 @@
 //                   results are exact when those are finite, max|a| < 2^100 and max|a| * max|b| stays under
 //                   the ladder's overflow bound; then it writes its tile and a 0 flag, otherwise only a 1 flag.
 //   k_systolic_fast64  the same check and results for ladders ending in a bf16 lane on 64 x 64 tiles, when the
-//                   operands need no bounds checks and the call has no hints or epilogue: 64-row stages loaded
+//                   operands need no bounds checks (hints and the epilogue as above): 64-row stages loaded
 //                   straight into LDS, the lanes in value units (a product rounded to its lane's step by adding
 //                   and subtracting a constant, full rate, no staging scale or rescale), eight waves.
 //   k_systolic_gen  the full per-step rule for any codes, any lanes (e <= 8), MXGEMMINI or MXQUANT, NaN, Inf,
@@ -788,8 +788,8 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 }
 
 // ------------------------------------------------------------------------- fast datapath, 64-row stages
-// k_systolic_fast64: k_systolic_fast's datapath on 64 x 64 tiles for operands that need no bounds checks and
-// calls with no hints or epilogue, eight waves a workgroup (4 x 2 outputs a thread).
+// k_systolic_fast64: k_systolic_fast's datapath on 64 x 64 tiles for operands that need no bounds checks,
+// eight waves a workgroup (4 x 2 outputs a thread).
 // Its operands lie whole inside the matrices (M, N and K multiples of 64, rows 16-byte aligned, blocks of 32),
 // so every stage of 64 rows moves straight from global memory into LDS (global_load_lds_dwordx4: no registers,
 // no LDS stores, 1 KB per instruction per wave) while the previous stage is reduced; one barrier per two
@@ -797,7 +797,9 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
 // and subtracting 1.5 * 2^(17-m) (exact: |p| stays far below 2^(16-m) whenever the tile's results are kept),
 // so A is staged as it is, no sum is rescaled between lanes, and every operation issues at full rate.  The
 // sums, roundings and tile adds are k_systolic_fast's, value for value.  The workgroup's operand maxima are
-// read back from LDS once per stage; its verdict and flag are k_systolic_fast's.  No hints, no epilogue.
+// read back from LDS once per stage; its verdict and flag are k_systolic_fast's, and so are the caller's hints
+// (dispatch order, skipped tiles, the reduction's stop under k_end and the check of the rows past it) and the
+// epilogue.
 constexpr int KS64 = 64;                            // rows per stage
 
 template <int SIZE, bool BF16_LAST, bool HWF, int TN>
@@ -817,10 +819,22 @@ __global__ void __launch_bounds__(64 * 64 / (4 * TN)) k_systolic_fast64(const Sy
   __shared__ __align__(16) float xs_a[2][NBS][BM];
   __shared__ __align__(16) float xs_b[2][NBS][BN];
   __shared__ uint32_t inexact_w[2][NBS][NWV];       // per buffer, block and wave: a scale denies the short add
-  __shared__ uint32_t red[3][NWV];
+  __shared__ uint32_t red[4][NWV];
   const int tn = threadIdx.x % (BN / TN), tm = threadIdx.x / (BN / TN);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t z = blockIdx.z, ty = blockIdx.y, tx = blockIdx.x;
+  // the tile: from the caller's dispatch order (k_tile_order: heaviest first) when there is one, else the grid's
+  int64_t z, ty, tx;
+  if (args.order) {
+    const uint32_t t = args.order[blockIdx.x + args.tiles_x * (blockIdx.y + args.tiles_y * (int64_t)blockIdx.z)];
+    const uint32_t zy = t / (uint32_t)args.tiles_x;
+    tx = t - zy * (uint32_t)args.tiles_x;
+    z = zy / (uint32_t)args.tiles_y;
+    ty = zy - (uint32_t)z * (uint32_t)args.tiles_y;
+  } else {
+    z = blockIdx.z;
+    ty = blockIdx.y;
+    tx = blockIdx.x;
+  }
   const int64_t m0 = ty * BM, n0 = tx * BN;
   const float* A = args.A.p + z * args.A.batch + m0;
   const float* B = args.B.p + z * args.B.batch + n0;
@@ -966,42 +980,82 @@ __global__ void __launch_bounds__(64 * 64 / (4 * TN)) k_systolic_fast64(const Sy
     }
   };
 
-  load_stage(0, sa0, sb0);
-  finish_stage(0);
-  for (int64_t k0 = 0; k0 < K; k0 += 2 * KS64) {
+  // a tile made only of groups the caller does not need is written as +0 (through the epilogue), uncomputed
+  if (args.skip && tile_skipped(args, z, m0, n0, BM, BN)) {
+    if (threadIdx.x == 0) args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = 0u;
+    if (!args.c_end || n0 < args.c_end[z * args.kend_groups + m0 / 64])
+      write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
+    return;
+  }
+  // the reduction stops past the caller's k_end for these columns of A: at ks32 (a multiple of 32, as
+  // k_systolic_fast and the general kernel's pieces take it), rounded up here to a whole 64-row stage; the rows
+  // read past ks32 join the operand maxima, and every row from ks32 on is checked below
+  const int64_t ks32 = tile_kstop(args, z, m0);
+  const int64_t kst = (ks32 + KS64 - 1) / KS64 * KS64 < K ? (ks32 + KS64 - 1) / KS64 * KS64 : K;
+  if (kst > 0) {
+    load_stage(0, sa0, sb0);
+    finish_stage(0);
+  }
+  for (int64_t k0 = 0; k0 < kst; k0 += 2 * KS64) {
     // even stage: buffer 0 reduced while stage k0 + 64 lands in buffer 1; odd stage: the other way round
-    const bool more1 = k0 + KS64 < K;
+    const bool more1 = k0 + KS64 < kst;
     if (more1) load_stage(k0 + KS64, sa1, sb1);
     reduce_stage(sa0, sb0, 0);
     if (!more1) break;
     finish_stage(1);
-    const bool more2 = k0 + 2 * KS64 < K;
+    const bool more2 = k0 + 2 * KS64 < kst;
     if (more2) load_stage(k0 + 2 * KS64, sa0, sb0);
     reduce_stage(sa1, sb1, 1);
     if (more2) finish_stage(0);
+  }
+
+  // rows from ks32 on: exact only if A holds +-0 there and B and every remaining block scale are finite
+  // (k_suffix_flags' bytes, as k_systolic_fast reads them); bit j for the tile's 32-column group j of A, then B
+  constexpr int GT = BM / 32 + BN / 32;
+  uint32_t bad = 0u;
+  if (ks32 < K) {
+    const int64_t s0 = ks32 / KT, ga = (args.M + 31) / 32, gb = (args.N + 31) / 32;
+    for (int64_t i = threadIdx.x; i < (args.stages - s0) * GT; i += NT) {
+      const int64_t st = s0 + i / GT;
+      const int j = (int)(i % GT);
+      bool b;
+      if (j < BM / 32) {
+        const int64_t g = m0 / 32 + j;
+        b = g < ga && args.suf_a[(z * args.stages + st) * ga + g];
+      } else {
+        const int64_t g = n0 / 32 + (j - BM / 32);
+        b = g < gb && args.suf_b[(z * args.stages + st) * gb + g];
+      }
+      bad |= b ? 1u << j : 0u;
+    }
   }
 
   for (int off = 32; off > 0; off >>= 1) {
     max_a = umax(max_a, (uint32_t)__shfl_xor((int)max_a, off, 64));
     max_b = umax(max_b, (uint32_t)__shfl_xor((int)max_b, off, 64));
     max_x = umax(max_x, (uint32_t)__shfl_xor((int)max_x, off, 64));
+    bad |= (uint32_t)__shfl_xor((int)bad, off, 64);
   }
   if (lane == 0) {
     red[0][wave] = max_a;
     red[1][wave] = max_b;
     red[2][wave] = max_x;
+    red[3][wave] = bad;
   }
   __syncthreads();
-  uint32_t wa = 0u, wb = 0u, wx = 0u;
+  uint32_t wa = 0u, wb = 0u, wx = 0u, wbad = 0u;
 #pragma unroll
   for (int v = 0; v < NWV; ++v) {
     wa = umax(wa, red[0][v]);
     wb = umax(wb, red[1][v]);
     wx = umax(wx, red[2][v]);
+    wbad |= red[3][v];
   }
-  const bool ok = wa < kFastAMaxBits && wb < 0x7F800000u && wx < 0x7F800000u &&
+  const bool ok = wbad == 0u && wa < kFastAMaxBits && wb < 0x7F800000u && wx < 0x7F800000u &&
                   u2f(wa) * u2f(wb) <= args.fast_prod_max;
-  if (threadIdx.x == 0) args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = ok ? 0u : 1u;
+  // the flag: bit 0, the general kernel computes the tile; bits 1..GT, which groups' left-out rows failed their
+  // check (piece_kstop)
+  if (threadIdx.x == 0) args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = ok ? 0u : 1u | (wbad << 1);
   if (!ok) return;
   write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
 }
@@ -1272,7 +1326,8 @@ void launch_fast64(int size, bool hwf, dim3 grid, hipStream_t st, const SysArgs&
 }
 
 // Whether k_systolic_fast64 takes the launch: a ladder ending in a bf16 lane, at least one 64 x 64 tile per CU
-// (256), every 64-row stage inside the operands and 16-byte aligned, blocks of 32, no hints and no epilogue.
+// (256), every 64-row stage inside the operands and 16-byte aligned, blocks of 32; hints and the epilogue as
+// k_systolic_fast takes them.
 // Measured against k_systolic_fast on MXGEMMINI HW_FINAL, the same bits: 512 x 4096 outputs, K = 4096: 1.06 ms
 // against 1.16 (32 x 64 tiles); 4096 x 4096 x 4096: 7.86 against 8.18; 1024 x 4096 x 4096: 2.04 against 2.45;
 // 256 x 4096 x 4096: 0.59 against 0.66; with 128 tiles (256 x 2048) half the CUs idle: 0.59 against 0.43.
@@ -1281,7 +1336,7 @@ bool takes_fast64(const SysArgs& a, int64_t count) {
   auto aligned = [](const Operand& o) {
     return o.ld % 4 == 0 && o.batch % 4 == 0 && reinterpret_cast<uintptr_t>(o.p) % 16 == 0;
   };
-  return a.lane_e[a.size - 1] == 8 && !a.skip && !a.k_end && !a.epi_on && a.block_size == KT && a.K > 0 &&
+  return a.lane_e[a.size - 1] == 8 && a.block_size == KT && a.K > 0 &&
          a.M % 64 == 0 && a.N % 64 == 0 &&
          a.K % KS64 == 0 && tiles >= 256 && aligned(a.A) && aligned(a.B);
 }

@@ -340,17 +340,18 @@ def test_zero_stages_skip_exactly(cuda):
         assert_bits_equal(got, osys.systolic(P_A, X_A, P_B, X_B, orc, sched), "fast vs oracle")
 
 
-@pytest.mark.parametrize("count,M,N", [(32, 512, 512), (3, 200, 300)], ids=["tiles64", "tiles32"])
-def test_batched_hints(cuda, count, M, N):
+@pytest.mark.parametrize("count,M,N,K", [(32, 512, 512, 160), (32, 512, 512, 192), (3, 200, 300, 160)],
+                         ids=["tiles64", "stages64", "tiles32"])
+def test_batched_hints(cuda, count, M, N, K):
     """mxq_systolic_batched's hints change no needed bit.  Skip maps (a causal triangle, random 32 x 32 groups,
     random whole 64 x 64 tiles, everything): each group the map leaves is bit-equal to the hint-free result, each
     it marks is that result or +0, and a fully marked map gives +0 everywhere.  k_end: the true bound of A's
     nonzero rows, and a bound too small for some groups (those tiles fall back to the general kernel), both
-    equal to the hint-free result."""
+    equal to the hint-free result.  K = 192 runs the 64-row-stage kernel (2048 tiles of 64 x 64), whose
+    stop under k_end rounds up to a whole stage."""
     from mxq import _lib, matmul
     from mxq.matmul._systolic import systolic_batched
-    rng = np.random.default_rng(M)
-    K = 160
+    rng = np.random.default_rng(M + K)
     P_A, X_A = _codes(rng, K, count * M)
     P_B, X_B = _codes(rng, K, count * N, scale=0.1)
     gm, gn, g64 = -(-M // 32), -(-N // 32), -(-M // 64)
@@ -394,13 +395,14 @@ def test_batched_hints(cuda, count, M, N):
     assert_bits_equal(got[keep], want[keep], "skip and k_end together")
 
 
-def test_k_end_nonfinite_past_the_end(cuda):
+@pytest.mark.parametrize("count,K,M,N", [(3, 200, 96, 70), (8, 256, 512, 256)], ids=["stages32", "stages64"])
+def test_k_end_nonfinite_past_the_end(cuda, count, K, M, N):
     """Rows past k_end where A is +-0 but B holds an Inf, or a scale of A's is NaN, or one of B's is Inf: 0 * Inf
-    makes NaN there, so those tiles must not stop early.  Every output equals the hint-free run (NaN included)."""
+    makes NaN there, so those tiles must not stop early.  Every output equals the hint-free run (NaN included).
+    The second shape runs the 64-row-stage kernel, whose stop rounds k_end = 40 up to 64 rows."""
     from mxq import _lib, matmul
     from mxq.matmul._systolic import systolic_batched
     rng = np.random.default_rng(5)
-    count, K, M, N = 3, 200, 96, 70
     P_A, X_A = _codes(rng, K, count * M)
     P_B, X_B = _codes(rng, K, count * N, scale=0.1)
     P_A[40:, :] = 0.0
@@ -412,7 +414,7 @@ def test_k_end_nonfinite_past_the_end(cuda):
     lay = _lib.SystolicLayout(ld_a=count * M, batch_a=M, ld_xa=count * M, batch_xa=M,
                               ld_b=count * N, batch_b=N, ld_xb=count * N, batch_xb=N, ld_c=N, batch_c=M * N)
     outs = []
-    for ke in (None, torch.full((count, 2), 40, dtype=torch.int32, device="cuda")):
+    for ke in (None, torch.full((count, -(-M // 64)), 40, dtype=torch.int32, device="cuda")):
         C = torch.full((count, M, N), float("nan"), device="cuda")
         systolic_batched(ops, lay, count, K, M, N, C, matmul.MXGEMMINI(), HW_FINAL, k_end=ke)
         outs.append(C.cpu().numpy())
