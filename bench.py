@@ -37,7 +37,8 @@ METRIC = "emulated MX GEMM GOP/s (systolic, bit-exact) + quantize GB/s vs HBM ro
 HBM_PEAK_GBS = 8000.0
 # MI355X's published vector FP32 peak, 157.3 TFLOP/s, is 78.6 T lane-operations per second: its 1024 SIMDs each
 # retiring one full-rate wave64 VALU instruction every 2 clocks at 2.4 GHz.  gfx950 issues v_add_f32, v_mul_f32
-# and v_and_b32 at that rate and v_rndne_f32, v_bfe_u32, v_add3_u32 at half of it (`--valu-rates`).
+# and v_and_b32 at that rate and v_rndne_f32, v_bfe_u32, v_add3_u32, the packed float16 operations, the mixed
+# fma and the float16 and bf16 pack conversions at half of it (`--valu-rates`).
 VALU_LANE_OPS = 157.3e12 / 2
 # The emulated MAC's VALU issue on gfx950 in full-rate slots: an e4 lane step multiplies, masks the product,
 # rounds it to the lane grid (adding and subtracting a constant, two full-rate operations, or v_rndne_f32 at half
@@ -50,7 +51,9 @@ VALU_ROOF_TOPS = VALU_LANE_OPS / SLOTS_PER_MAC_MODEL * 2 / 1e12   # 19.66 TOP/s 
 # 78.6 T lane-operations per second; the fast kernel does the step in fewer, so this fraction can pass 1.
 OPS_PER_MAC_SURVEY = 10
 SURVEY_ROOF_TOPS = VALU_LANE_OPS / OPS_PER_MAC_SURVEY * 2 / 1e12    # 15.73 TOP/s emulated
-VALU_PROBE_KINDS = ("v_add_f32", "v_mul_f32", "v_and_b32", "v_rndne_f32", "v_bfe_u32", "v_add3_u32")
+VALU_PROBE_KINDS = ("v_add_f32", "v_mul_f32", "v_and_b32", "v_rndne_f32", "v_bfe_u32", "v_add3_u32", "v_pk_mul_f16",
+                    "v_pk_add_f16", "v_fma_mix_f32", "v_cvt_pkrtz_f16_f32", "v_cvt_pk_bf16_f32")
+VALU_CHAIN_KINDS = ("v_mul_f32", "v_pk_mul_f16")     # probe kinds 11 and 12: one dependent chain each
 FP8_PEAK_TFLOPS = 5000.0                    # MI355X dense FP8 matrix-core peak
 FP6_FP4_PEAK_TFLOPS = 10100.0               # MI355X dense FP6 and FP4 matrix-core peak
 MAX_POOL = 16                               # host processes for the CPU baselines (one GPU's CPU share)
@@ -630,7 +633,8 @@ def mfma_line(torch, steps, P_A, X_A, P_B, X_B, inp):
 def valu_rates():
     """gfx950's VALU issue rate per instruction kind (mxq_valu_probe: 8192 workgroups x 256 threads, 64 x 2000
     independent instructions each): lane-operations per second over the chip against the 78.6 T of the vector
-    FP32 peak."""
+    FP32 peak; then, with one wave per SIMD (256 workgroups), the time from one instruction to the next that
+    depends on it."""
     import torch
 
     from mxq import _lib
@@ -646,7 +650,15 @@ def valu_rates():
         rate = wg * 256 * 64 * iters / (ms / 1e3)
         res[name] = {"ms": round(ms, 4), "lane_ops_per_s_T": round(rate / 1e12, 1),
                      "frac_of_78.6T": round(rate / VALU_LANE_OPS, 3)}
-    print(json.dumps({"valu_rates": res}), flush=True)
+    chains = {}
+    for j, name in enumerate(VALU_CHAIN_KINDS):
+        kind = len(VALU_PROBE_KINDS) + j
+        def f():
+            _lib.run("mxq_valu_probe", kind, iters, 256, _lib.ptr(out), _lib.stream(out.device))
+        f()
+        ns = _events_ms(f, 3, st) * 1e6 / (64 * iters)
+        chains[name] = {"ns_per_dependent_instruction": round(ns, 3), "clocks_at_2.4GHz": round(ns * 2.4, 2)}
+    print(json.dumps({"valu_rates": res, "dependent_chains": chains}), flush=True)
 
 
 def copy_calibration():

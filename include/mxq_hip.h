@@ -87,7 +87,9 @@ int mxq_timer_read(const char* kernel, double* total_ms, int64_t* launches);
 /* VALU issue-rate probe for measurement tools; no counterpart in the reference (the VALU roofline of the
  * emulation kernels prices each instruction by its issue rate).  Launches `workgroups` x 256 threads, each
  * issuing 64 * iters independent instructions of one kind: 0 v_add_f32, 1 v_mul_f32, 2 v_and_b32,
- * 3 v_rndne_f32, 4 v_bfe_u32, 5 v_add3_u32.  out: workgroups * 256 floats (a sink for the results). */
+ * 3 v_rndne_f32, 4 v_bfe_u32, 5 v_add3_u32, 6 v_pk_mul_f16, 7 v_pk_add_f16, 8 v_fma_mix_f32,
+ * 9 v_cvt_pkrtz_f16_f32, 10 v_cvt_pk_bf16_f32; or one dependent chain of 64 * iters: 11 v_mul_f32,
+ * 12 v_pk_mul_f16.  out: workgroups * 256 floats (a sink for the results). */
 int mxq_valu_probe(int32_t kind, int32_t iters, int64_t workgroups, float* out, mxq_stream_t stream);
 
 /* Fused block quantization: per block, amax -> scale X (step 1) -> z = block / X -> P = element rule (step 2).
