@@ -162,7 +162,8 @@ typedef struct mxq_systolic_layout {
   int64_t ld_xa, batch_xa;  /* scales X_A, nb x M */
   int64_t ld_b, batch_b;    /* codes B, K x N   */
   int64_t ld_xb, batch_xb;  /* scales X_B, nb x N */
-  int64_t ld_c, batch_c;    /* C, M x N (problems may not overlap) */
+  int64_t ld_c, batch_c;    /* C, M x N: problems one after another (batch_c >= (M - 1) * ld_c + N) or side
+                             * by side within each row (batch_c >= N, (count - 1) * batch_c + N <= ld_c) */
 } mxq_systolic_layout;
 
 /* Optional hints to mxq_systolic_batched (no counterpart in the reference; they let attention skip the work its

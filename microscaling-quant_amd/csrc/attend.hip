@@ -171,14 +171,26 @@ __global__ void __launch_bounds__(256) k_attend_windows(const double* __restrict
   const int last0 = (Tk - 1) / block * block, j0 = chunk * WROWS;
   const int nrows = min(WROWS, m - j0);
   int live = 0;
-  for (int i = threadIdx.x; i < nrows * block; i += 256) {
-    const int j = i / block, key = i - j * block;
-    const float* r = rows + (int64_t)(j0 + j) * mask_row_stride;
-    const float c = r[key];                                   // key < block < Tk
-    if (!((c + bnd) == c && (c - bnd) == c)) live |= 1;
-    if (last0 + key < Tk) {
-      const float e = r[last0 + key];
-      if (!((e + bnd) == e && (e - bnd) == e)) live |= 2;
+  // eight elements of each of the two blocks a thread per round, every load issued before any is tested
+  constexpr int PER = 8;
+  const int total = nrows * block;
+  for (int i0 = threadIdx.x; i0 < total; i0 += 256 * PER) {
+    float c[PER], e[PER];
+    bool in[PER], in_last[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = i0 + 256 * u;
+      in[u] = i < total;
+      const int j = in[u] ? i / block : 0, key = in[u] ? i - j * block : 0;
+      const float* r = rows + (int64_t)(j0 + j) * mask_row_stride;
+      c[u] = in[u] ? r[key] : 0.0f;                           // key < block < Tk
+      in_last[u] = in[u] && last0 + key < Tk;
+      e[u] = in_last[u] ? r[last0 + key] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      if (in[u] && !((c[u] + bnd) == c[u] && (c[u] - bnd) == c[u])) live |= 1;
+      if (in_last[u] && !((e[u] + bnd) == e[u] && (e[u] - bnd) == e[u])) live |= 2;
     }
   }
   const int first = __syncthreads_or(live & 1), last = __syncthreads_or(live & 2);
@@ -192,12 +204,26 @@ __global__ void __launch_bounds__(256) k_mask_minabs(const float* __restrict__ m
   const int64_t bb = blockIdx.z, rg = blockIdx.y, key = (int64_t)blockIdx.x * 256 + threadIdx.x;
   float mn = f_inf(), mx = -f_inf();                           // keys past Tk take no part
   if (key < Tk) {
-    for (int i = 0; i < 32; ++i) {
-      const int64_t r = rg * 32 + i;
-      if (r >= rows) break;
-      const float c = mask[bb * mask_b_stride + (r % m) * mask_row_stride + key];
-      mn = fminf(mn, c != c ? 0.0f : fabsf(c));
-      mx = fmaxf(mx, c);                                       // a NaN takes no part
+    const int64_t r0 = rg * 32, q0 = r0 % m;
+    if (r0 + 32 <= rows && q0 + 32 <= m) {
+      // 32 consecutive mask rows: every load issued before the first is used
+      const float* col = mask + bb * mask_b_stride + q0 * mask_row_stride + key;
+      float c[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) c[i] = col[i * mask_row_stride];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        mn = fminf(mn, c[i] != c[i] ? 0.0f : fabsf(c[i]));
+        mx = fmaxf(mx, c[i]);                                  // a NaN takes no part
+      }
+    } else {
+      for (int i = 0; i < 32; ++i) {
+        const int64_t r = r0 + i;
+        if (r >= rows) break;
+        const float c = mask[bb * mask_b_stride + (r % m) * mask_row_stride + key];
+        mn = fminf(mn, c != c ? 0.0f : fabsf(c));
+        mx = fmaxf(mx, c);                                     // a NaN takes no part
+      }
     }
   }
   for (int off = 16; off > 0; off >>= 1) {
@@ -223,6 +249,21 @@ __global__ void __launch_bounds__(256) k_attend_hints(const double* __restrict__
   __shared__ int last;
   __shared__ float tmax[4];
   const int64_t t = blockIdx.x, z = blockIdx.y;
+  const int64_t bb = batched ? (z0 + z) / z_per_b - z0 / z_per_b : 0;
+  // with at most 256 key groups a thread tests one of each of the two row groups: its minimum (and largest
+  // value) loaded before the bound is formed, so their latency and the bound's overlap
+  const bool one = kgroups <= 256;
+  float pre_c[2] = {0.0f, 0.0f}, pre_v[2] = {-f_inf(), -f_inf()};
+  bool pre_in[2] = {false, false};
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int64_t rg = 2 * t + g;
+    pre_in[g] = one && rg < rgroups && threadIdx.x < kgroups;
+    if (pre_in[g]) {
+      pre_c[g] = minabs[(bb * rgroups + rg) * kgroups + threadIdx.x];
+      if (maxval) pre_v[g] = maxval[(bb * rgroups + rg) * kgroups + threadIdx.x];
+    }
+  }
   __shared__ double terms[256];
   const double bound = call_bound(amax_a, lda, amax_k, ldk, D, z, slack_scale, terms);
   if (threadIdx.x == 0) {
@@ -232,16 +273,26 @@ __global__ void __launch_bounds__(256) k_attend_hints(const double* __restrict__
   __syncthreads();
   const float b = b2;
   const bool usable = is_finite_f(b);
-  const int64_t bb = batched ? (z0 + z) / z_per_b - z0 / z_per_b : 0;
   int mine = -1;
-  for (int64_t rg = 2 * t; rg < 2 * t + 2 && rg < rgroups; ++rg) {
-    const float* mrow = minabs + (bb * rgroups + rg) * kgroups;
-    uint8_t* srow = skip + (z * rgroups + rg) * kgroups;
-    for (int64_t kg = threadIdx.x; kg < kgroups; kg += 256) {
-      const float c = mrow[kg];
+  if (one) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      if (!pre_in[g]) continue;
+      const float c = pre_c[g];
       const bool sk = usable && (c + b) == c && (c - b) == c;
-      srow[kg] = sk ? 1 : 0;
-      if (!sk && kg > mine) mine = (int)kg;
+      skip[(z * rgroups + 2 * t + g) * kgroups + threadIdx.x] = sk ? 1 : 0;
+      if (!sk) mine = (int)threadIdx.x;
+    }
+  } else {
+    for (int64_t rg = 2 * t; rg < 2 * t + 2 && rg < rgroups; ++rg) {
+      const float* mrow = minabs + (bb * rgroups + rg) * kgroups;
+      uint8_t* srow = skip + (z * rgroups + rg) * kgroups;
+      for (int64_t kg = threadIdx.x; kg < kgroups; kg += 256) {
+        const float c = mrow[kg];
+        const bool sk = usable && (c + b) == c && (c - b) == c;
+        srow[kg] = sk ? 1 : 0;
+        if (!sk && kg > mine) mine = (int)kg;
+      }
     }
   }
   atomicMax(&last, mine);
@@ -250,9 +301,16 @@ __global__ void __launch_bounds__(256) k_attend_hints(const double* __restrict__
   if (!tail_max) return;
   // the largest mask value of the groups past k_end (every one of them skipped): the largest score there
   float tm = -f_inf();
-  for (int64_t rg = 2 * t; rg < 2 * t + 2 && rg < rgroups; ++rg) {
-    const float* vrow = maxval + (bb * rgroups + rg) * kgroups;
-    for (int64_t kg = last + 1 + threadIdx.x; kg < kgroups; kg += 256) tm = fmaxf(tm, vrow[kg]);
+  if (one) {
+    const int lst = last;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+      if (pre_in[g] && (int)threadIdx.x > lst) tm = fmaxf(tm, pre_v[g]);
+  } else {
+    for (int64_t rg = 2 * t; rg < 2 * t + 2 && rg < rgroups; ++rg) {
+      const float* vrow = maxval + (bb * rgroups + rg) * kgroups;
+      for (int64_t kg = last + 1 + threadIdx.x; kg < kgroups; kg += 256) tm = fmaxf(tm, vrow[kg]);
+    }
   }
   for (int off = 32; off > 0; off >>= 1) tm = fmaxf(tm, __shfl_xor(tm, off, 64));
   if ((threadIdx.x & 63) == 0) tmax[threadIdx.x >> 6] = tm;

@@ -33,8 +33,9 @@
 //                   straight into LDS, the lanes in value units (a product rounded to its lane's step by adding
 //                   and subtracting a constant, full rate, no staging scale or rescale), eight waves.
 //   k_systolic_gen  the full per-step rule for any codes, any lanes (e <= 8), MXGEMMINI or MXQUANT, NaN, Inf,
-//                   saturation and overflow included.  After a fast kernel it computes only the tiles whose
-//                   flag is 1; alone (no fast case, or forced) it computes everything.
+//                   saturation and overflow included.  After a fast kernel its flagged form
+//                   (k_systolic_gen_flagged) computes only the tiles whose flag is 1; alone (no fast case, or
+//                   forced) it computes everything.
 #include <algorithm>
 #include <cmath>
 #include <mutex>
@@ -360,29 +361,6 @@ __device__ __forceinline__ uint32_t grid_tile(const SysArgs& a, uint32_t p, uint
 }
 
 
-// atomicAdd(&cur[b], 1) for every active lane; returns the lane's old value.  The buckets of up to two lanes'
-// (the wave's first active lanes') take one atomic each for every lane holding them: under a skip map most of
-// a wave shares one or two buckets, whose returning atomics would otherwise serialize.  The rest (k_end gives
-// a wave many buckets, each held by few lanes) go one lane at a time.
-__device__ __forceinline__ uint32_t wave_bucket_add(uint32_t* cur, int b, bool active) {
-  const int lane = threadIdx.x & 63;
-  uint64_t todo = __ballot(active);
-  uint32_t pos = 0u;
-  for (int round = 0; round < 2 && todo; ++round) {
-    const int leader = __ffsll((unsigned long long)todo) - 1;
-    const int lb = __shfl(b, leader, 64);
-    const bool mine = ((todo >> lane) & 1ull) && b == lb;
-    const uint64_t same = __ballot(mine);
-    uint32_t base = 0u;
-    if (lane == leader) base = atomicAdd(&cur[lb], (uint32_t)__popcll(same));
-    base = (uint32_t)__shfl((int)base, leader, 64);
-    if (mine) pos = base + (uint32_t)__popcll(same & ((1ull << lane) - 1ull));
-    todo &= ~same;
-  }
-  if ((todo >> lane) & 1ull) pos = atomicAdd(&cur[b], 1u);
-  return pos;
-}
-
 // Each dispatch position's work bucket (0: skipped; else 1 + stages to reduce, the last bucket holding
 // everything longer) into `bucket`, one thread per position over the whole grid.
 __global__ void __launch_bounds__(256) k_tile_bucket(const SysArgs a, uint32_t total, uint16_t* bucket) {
@@ -400,8 +378,38 @@ __global__ void __launch_bounds__(256) k_tile_bucket(const SysArgs a, uint32_t t
 }
 
 // The counting sort of the positions by bucket, heaviest first, in one workgroup: sixteen adjacent positions'
-// buckets per thread per pass (two 16-byte loads), counted, then placed.
+// buckets per thread per pass (two 16-byte loads).  Adjacent positions mostly share a bucket (a row of tiles has
+// one, skipped tiles aside), so a thread takes its sixteen as runs of equal buckets and makes one LDS atomic
+// per run, all issued before any result is used: the pass waits on one atomic's latency, where an atomic per
+// position, each waiting on the one before, kept the single workgroup waiting for tens of microseconds.
 constexpr int kOrderRun = 16;
+constexpr uint32_t kNoBucket = 0xFFFFu;           // a position past the grid
+
+// Each run of equal buckets among b (run starts at u when u == 0 or b[u] != b[u - 1]) adds its length to
+// cur[bucket]; with `place`, pos[u] gets the position's place in its bucket (the run's base from the atomic,
+// plus its index in the run).  Positions of bucket kNoBucket take no part.
+template <bool PLACE>
+__device__ __forceinline__ void count_runs(uint32_t* cur, const uint16_t (&b)[kOrderRun], uint32_t (&pos)[kOrderRun]) {
+  uint32_t len[kOrderRun];
+  len[kOrderRun - 1] = 1u;
+#pragma unroll
+  for (int u = kOrderRun - 2; u >= 0; --u) len[u] = b[u] == b[u + 1] ? len[u + 1] + 1u : 1u;
+  uint32_t base[kOrderRun];
+#pragma unroll
+  for (int u = 0; u < kOrderRun; ++u) {
+    const bool start = (u == 0 || b[u] != b[u - 1]) && b[u] != kNoBucket;
+    base[u] = 0u;
+    if (start) {
+      if constexpr (PLACE) base[u] = atomicAdd(&cur[b[u]], len[u]);
+      else atomicAdd(&cur[b[u]], len[u]);
+    }
+  }
+  if constexpr (PLACE) {
+#pragma unroll
+    for (int u = 0; u < kOrderRun; ++u) pos[u] = (u == 0 || b[u] != b[u - 1]) ? base[u] : pos[u - 1] + 1u;
+  }
+}
+
 __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, uint32_t total,
                                                               const uint16_t* __restrict__ bucket, uint32_t* order) {
   constexpr int PB = kOrderBuckets / kOrderThreads;
@@ -424,15 +432,15 @@ __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, u
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < kOrderRun; ++u) b[u] = p0 + u < total ? bucket[p0 + u] : 0;
+      for (int u = 0; u < kOrderRun; ++u) b[u] = p0 + u < total ? bucket[p0 + u] : (uint16_t)kNoBucket;
     }
   };
   for (uint32_t c0 = 0; c0 < total; c0 += stride) {
     const uint32_t p0 = c0 + (uint32_t)threadIdx.x * kOrderRun;
     uint16_t b[kOrderRun];
+    uint32_t pos[kOrderRun];
     load_run(p0, b);
-#pragma unroll
-    for (int u = 0; u < kOrderRun; ++u) wave_bucket_add(cur, b[u], p0 + u < total);
+    count_runs<false>(cur, b, pos);
   }
   __syncthreads();
   // cur[b] <- the first position of bucket b: the count of every bucket above it (heavier work first)
@@ -461,12 +469,13 @@ __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, u
   for (uint32_t c0 = 0; c0 < total; c0 += stride) {
     const uint32_t p0 = c0 + (uint32_t)threadIdx.x * kOrderRun;
     uint16_t b[kOrderRun];
+    uint32_t pos[kOrderRun];
     load_run(p0, b);
+    count_runs<true>(cur, b, pos);
 #pragma unroll
     for (int u = 0; u < kOrderRun; ++u) {
-      const uint32_t pos = wave_bucket_add(cur, b[u], p0 + u < total);
       uint32_t z, ty, tx;
-      if (p0 + u < total) order[pos] = grid_tile(a, p0 + u, z, ty, tx);
+      if (p0 + u < total) order[pos[u]] = grid_tile(a, p0 + u, z, ty, tx);
     }
   }
 }
@@ -1185,22 +1194,45 @@ __device__ __forceinline__ int64_t piece_kstop(const SysArgs& a, uint32_t flag, 
 // only_flagged: the grid is the fast kernel's tiles (it ran first); a workgroup whose tile has its flag set
 // computes that tile's BM x BN pieces in turn, the others return at once.  Otherwise one piece per workgroup.
 template <int BM, int BN, int TM, int TN>
-__global__ void __launch_bounds__((BM / TM) * (BN / TN), 4) k_systolic_gen(const SysArgs args, int only_flagged) {
-  static_assert(32 % BM == 0 && 32 % BN == 0, "a general tile lies inside one fast tile");
+__global__ void __launch_bounds__((BM / TM) * (BN / TN), 4) k_systolic_gen(const SysArgs args) {
   __shared__ Smem<BM, BN> sm;
-  const int64_t z = blockIdx.z;
-  if (!only_flagged) {
-    gen_tile_at<BM, BN, TM, TN>(args, z, (int64_t)blockIdx.y * BM, (int64_t)blockIdx.x * BN, args.K, sm);
-    return;
-  }
-  const uint32_t flag = args.flags[(z * args.tiles_y + blockIdx.y) * args.tiles_x + blockIdx.x];
-  if (flag == 0u) return;
-  const int64_t tm0 = (int64_t)blockIdx.y * args.fbm, tn0 = (int64_t)blockIdx.x * args.fbn;
-  for (int64_t m0 = tm0; m0 < tm0 + args.fbm && m0 < args.M; m0 += BM)
-    for (int64_t n0 = tn0; n0 < tn0 + args.fbn && n0 < args.N; n0 += BN) {
-      gen_tile_at<BM, BN, TM, TN>(args, z, m0, n0, piece_kstop(args, flag, z, m0, n0, tm0, tn0), sm);
-      __syncthreads();   // the next piece restages sm
+  gen_tile_at<BM, BN, TM, TN>(args, blockIdx.z, (int64_t)blockIdx.y * BM, (int64_t)blockIdx.x * BN, args.K, sm);
+}
+
+// After a fast kernel, the tiles it flagged: workgroup g reads the flags of tiles [g * per, (g + 1) * per) of
+// the `total` (in the flags' order), 256 at a time, lists the set ones in LDS and recomputes each in BM x BN
+// pieces.  At most 1024 workgroups, so a launch whose tiles are all exact (the usual case) costs the loads of
+// the flags, not a workgroup per tile that exits at once (9 us for the 32768 tiles of one attention product).
+template <int BM, int BN, int TM, int TN>
+__global__ void __launch_bounds__((BM / TM) * (BN / TN), 4) k_systolic_gen_flagged(const SysArgs args, int64_t total,
+                                                                                  int64_t per) {
+  static_assert(32 % BM == 0 && 32 % BN == 0, "a general tile lies inside one fast tile");
+  static_assert((BM / TM) * (BN / TN) == 256, "a flag per thread");
+  __shared__ Smem<BM, BN> sm;
+  __shared__ uint32_t list[256];
+  __shared__ uint32_t nl;
+  const int64_t t0 = (int64_t)blockIdx.x * per, t1 = t0 + per < total ? t0 + per : total;
+  for (int64_t c0 = t0; c0 < t1; c0 += 256) {
+    if (threadIdx.x == 0) nl = 0u;
+    __syncthreads();
+    const int64_t t = c0 + threadIdx.x;
+    if (t < t1 && args.flags[t] != 0u) list[atomicAdd(&nl, 1u)] = threadIdx.x;
+    __syncthreads();
+    const uint32_t n = nl;
+    for (uint32_t j = 0; j < n; ++j) {
+      const int64_t tt = c0 + list[j];
+      const uint32_t flag = args.flags[tt];
+      const int64_t zy = tt / args.tiles_x, tx = tt - zy * args.tiles_x;
+      const int64_t z = zy / args.tiles_y, ty = zy - z * args.tiles_y;
+      const int64_t tm0 = ty * args.fbm, tn0 = tx * args.fbn;
+      for (int64_t m0 = tm0; m0 < tm0 + args.fbm && m0 < args.M; m0 += BM)
+        for (int64_t n0 = tn0; n0 < tn0 + args.fbn && n0 < args.N; n0 += BN) {
+          gen_tile_at<BM, BN, TM, TN>(args, z, m0, n0, piece_kstop(args, flag, z, m0, n0, tm0, tn0), sm);
+          __syncthreads();   // the next piece restages sm
+        }
     }
+    __syncthreads();         // list and nl are rewritten for the next 256 flags
+  }
 }
 
 // ------------------------------------------------------------------------------------------- host side
@@ -1367,7 +1399,6 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
   a.fast_prod_max = 0.0f;
   const dim3 grid_f((unsigned)a.tiles_x, (unsigned)a.tiles_y, (unsigned)count);
   const dim3 grid_g((unsigned)mxq::ceil_div(a.N, 32), (unsigned)mxq::ceil_div(a.M, 32), (unsigned)count);
-  const dim3 grid_gf((unsigned)a.tiles_x, (unsigned)a.tiles_y, (unsigned)count);   // after the fast kernel
   if (fast_lanes) {
     a.fast_prod_max = fast_prod_bound(lane_e, lane_m, a.size);
     // workspace: a flag per 32 x 32 tile (W), the dispatch order (W), the suffix bytes of A's and B's groups
@@ -1406,10 +1437,13 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
     }
     if (int rc = mxq::check_launch("mxq_systolic fast")) return rc;
     mxq::KernelTimer timer("systolic_general", st);
-    k_systolic_gen<32, 32, 2, 2><<<grid_gf, 256, 0, st>>>(a, 1);
+    const int64_t tiles = a.tiles_x * a.tiles_y * count;
+    const int64_t wgs = tiles < 1024 ? tiles : 1024;
+    if (wgs > 0)
+      k_systolic_gen_flagged<32, 32, 2, 2><<<(unsigned)wgs, 256, 0, st>>>(a, tiles, mxq::ceil_div(tiles, wgs));
   } else {
     mxq::KernelTimer timer("systolic_general", st);
-    k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a, 0);
+    k_systolic_gen<32, 32, 2, 2><<<grid_g, 256, 0, st>>>(a);
   }
   return mxq::check_launch("mxq_systolic");
 }
@@ -1463,7 +1497,10 @@ extern "C" int mxq_systolic_batched(const float* P_A, const float* X_A, const fl
     return mxq::invalid("mxq_systolic_batched: a row stride is shorter than its row");
   if (L.batch_a < 0 || L.batch_b < 0 || L.batch_xa < 0 || L.batch_xb < 0 || L.batch_c < 0)
     return mxq::invalid("mxq_systolic_batched: negative batch stride");
-  if (count > 1 && M > 0 && N > 0 && L.batch_c < (M - 1) * L.ld_c + N)
+  // the problems' outputs one after another, or side by side within each row (problem z's row r at
+  // z * batch_c + r * ld_c, the rows of all problems together no longer than ld_c); any other layout is refused
+  if (count > 1 && M > 0 && N > 0 && L.batch_c < (M - 1) * L.ld_c + N &&
+      !(L.batch_c >= N && (count - 1) * L.batch_c + N <= L.ld_c))
     return mxq::invalid("mxq_systolic_batched: outputs of two problems overlap");
   if (epilogue && (epilogue->m < 1 || epilogue->m > 0x7FFFFFFF || epilogue->z_per_b < 1 ||
                    epilogue->z_per_b > 0x7FFFFFFF || epilogue->z0 < 0 || epilogue->z0 + count > 0x7FFFFFFF))

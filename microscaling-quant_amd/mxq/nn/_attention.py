@@ -450,12 +450,23 @@ class _Batched:
         else:
             PT_P, PT_X, a_live = PT
         arith, sched, size = self.pv_red
-        O = torch.empty(Zc, cols, D, dtype=torch.float32, device=qg.device)
+        # one query head per KV head, float32 out, the chunk's pairs in one batch row: the products go straight
+        # into out (query j of pair z at out[b, s0 + j, z - b * Hkv]), no copy; else into O, copied below
+        b0 = z0 // Hkv
+        direct = n == 1 and out.dtype == torch.float32 and out.is_contiguous() and (z1 - 1) // Hkv == b0
+        if direct:
+            O = out[b0, s0:e0, z0 - b0 * Hkv:z1 - b0 * Hkv]
+            ld_c, batch_c = out.stride(1), out.stride(2)
+        else:
+            O = torch.empty(Zc, cols, D, dtype=torch.float32, device=qg.device)
+            ld_c, batch_c = D, cols * D
         systolic_batched((PT_P, PT_X, V_P[z0:], V_X[z0:]),
                          _lib.SystolicLayout(ld_a=Zc * cols, batch_a=cols, ld_xa=Zc * cols, batch_xa=cols,
                                              ld_b=D, batch_b=Tk * D, ld_xb=D, batch_xb=V_X.shape[1] * D,
-                                             ld_c=D, batch_c=cols * D),
+                                             ld_c=ld_c, batch_c=batch_c),
                          Zc, Tk, cols, D, O, arith, sched, size, pv.block_size, k_end=k_end, a_live=a_live)
+        if direct:
+            return
         O = O.view(Zc, n, m, D)
         for b in range(z0 // Hkv, (z1 - 1) // Hkv + 1):                          # pairs into B x Tq x H x D
             h0, h1 = max(z0, b * Hkv) - b * Hkv, min(z1, (b + 1) * Hkv) - b * Hkv

@@ -259,6 +259,35 @@ def test_batched_matches_single(cuda, sched_name):
         assert torch.isnan(C[z, :, N:]).all(), "columns past N are left alone"
 
 
+def test_batched_side_by_side_outputs(cuda):
+    """Outputs side by side within each row (problem z's row r at z * batch_c + r * ld_c, as attention writes
+    one head per KV head into its B x Tq x H x D output) equal the stacked layout's, on the 64-row-stage kernel
+    (M, N, K multiples of 64) and on a ragged shape; a layout whose problems' rows would overlap is refused."""
+    from mxq import _lib, matmul
+    from mxq.matmul._systolic import systolic_batched
+    rng = np.random.default_rng(11)
+    ar = matmul.MXGEMMINI()
+    for count, K, M, N in ((8, 128, 1024, 128), (3, 70, 40, 72)):
+        P_A, X_A = _codes(rng, K, count * M)
+        P_B, X_B = _codes(rng, K, count * N)
+        t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()      # noqa: E731
+        ops = (t(P_A), t(X_A), t(P_B), t(X_B))
+        base = dict(ld_a=count * M, batch_a=M, ld_xa=count * M, batch_xa=M, ld_b=count * N, batch_b=N,
+                    ld_xb=count * N, batch_xb=N)
+        stacked = torch.empty(count, M, N, device="cuda")
+        systolic_batched(ops, _lib.SystolicLayout(**base, ld_c=N, batch_c=M * N), count, K, M, N, stacked, ar,
+                         HW_FINAL)
+        side = torch.full((M, count + 1, N), float("nan"), device="cuda")
+        systolic_batched(ops, _lib.SystolicLayout(**base, ld_c=(count + 1) * N, batch_c=N), count, K, M, N, side,
+                         ar, HW_FINAL)
+        assert_bits_equal(side[:, :count].permute(1, 0, 2).cpu().numpy(), stacked.cpu().numpy(),
+                          f"side by side {count}x{M}x{N}x{K}")
+        assert torch.isnan(side[:, count]).all(), "the row's last N elements are left alone"
+        with pytest.raises(RuntimeError, match="overlap"):
+            systolic_batched(ops, _lib.SystolicLayout(**base, ld_c=count * N - 1, batch_c=N), count, K, M, N, side,
+                             ar, HW_FINAL)
+
+
 def test_all_fast_tile_shapes(cuda):
     """The fast kernel's three tiles: 2048 x 4096 outputs run on 64 x 64 tiles, 1024 x 4096 on 32 x 64 and
     500 x 4000 on 32 x 32 (too few larger tiles to give every CU 8 workgroups), with HW_FINAL's instance and a
