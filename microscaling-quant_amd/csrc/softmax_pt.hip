@@ -128,22 +128,37 @@ __global__ void __launch_bounds__(NT) k_softmax_pt(const float* __restrict__ S, 
     }
   }
   __syncthreads();
-  // pass 2: lane m of wave w takes row gbase[w % H] + m and the key blocks w / H, w / H + 4, ...: the
-  // block's 32 probabilities recomputed, its maximum, scale and codes in the lane, and each code stored as
-  // P^T[key][row], a run of 64 rows per store across the wave and of 64 H rows across the H waves that take
-  // the same blocks (128 rows: 382.5 us against 387.5 with 64 on 32 heads x 2048 causal queries x 2048 keys;
-  // no gain at 256)
-  const int hg = w % H, wb = w / H;                 // row group, and first key block, of the wave
-  const int64_t r = gbase[hg] + lane;
-  const bool live = gvalid[hg] && r < R;
-  const float mx = mx_s[64 * hg + lane], sm = sum_s[64 * hg + lane];
-  const float* src = S + (live ? r : gbase[0]) * T;
-  const float* tail = live && full_s[64 * hg + lane] ? tail_row(tl, cols, r) : nullptr;
+  // pass 2: lane m takes row gbase[g] + m of row group g, one 32-key block at a time: the block's 32
+  // probabilities recomputed, its maximum, scale and codes in the lane, and each code stored as P^T[key][row],
+  // a run of 64 rows per store across the wave.  The two groups' blocks, the first group's first, are dealt to
+  // the workgroup's 4 H waves in turn: under a causal mask one group of the pair is short and the other long,
+  // and four waves on each left half the waves idle while the others worked through the long group.
   const int nb = (T + 31) / 32;
-  const int kg = ke[hg];                            // keys stored in S for this group
-  const int kw = group_full[hg] ? T : kg;           // keys of P^T written
-  const int nbw = (kw + 31) / 32;
-  for (int b = wb; b < nbw; b += 4) {
+  int nbw[H];                                       // blocks of P^T written per group
+  const float* srcv[H];
+  const float* tailv[H];
+  float mxv[H], smv[H];
+  bool livev[H];
+#pragma unroll
+  for (int g = 0; g < H; ++g) {
+    const int kw = group_full[g] ? T : ke[g];      // keys of P^T written
+    nbw[g] = gvalid[g] ? (kw + 31) / 32 : 0;
+    const int64_t r = gbase[g] + lane;
+    livev[g] = gvalid[g] && r < R;
+    mxv[g] = mx_s[64 * g + lane];
+    smv[g] = sum_s[64 * g + lane];
+    srcv[g] = S + (livev[g] ? r : gbase[0]) * T;
+    tailv[g] = livev[g] && full_s[64 * g + lane] ? tail_row(tl, cols, r) : nullptr;
+  }
+  for (int i = w; i < nbw[0] + nbw[1]; i += 4 * H) {
+    const int hg = i < nbw[0] ? 0 : 1;              // the same in every lane
+    const int b = hg == 0 ? i : i - nbw[0];
+    const int64_t r = gbase[hg] + lane;
+    const bool live = livev[hg];
+    const float mx = mxv[hg], sm = smv[hg];
+    const float* src = srcv[hg];
+    const float* tail = tailv[hg];
+    const int kg = ke[hg];                          // keys stored in S for this group
     const int k0 = b * 32;
     float v[32];
     if ((T & 3) == 0 && k0 + 32 <= kg) {              // rows 16-byte aligned: 16-byte loads
@@ -191,12 +206,15 @@ __global__ void __launch_bounds__(NT) k_softmax_pt(const float* __restrict__ S, 
     }
   }
   // the blocks past the written keys: codes +0, a zero block's scale, so their stage bytes are 0
-  if (stage_live && nbw < nb) {
+  if (stage_live) {
     const int half = lane & 32;
-    const int64_t rh = gbase[hg] + half;
-    if ((lane & 31) == 0 && gvalid[hg] && rh < R) {
-      const int64_t z = rh / cols, g = (rh - z * cols) / 32;
-      for (int b = nbw + wb; b < nb; b += 4) stage_live[(z * nb + b) * (cols / 32) + g] = 0u;
+#pragma unroll
+    for (int hg = 0; hg < H; ++hg) {
+      const int64_t rh = gbase[hg] + half;
+      if ((lane & 31) == 0 && gvalid[hg] && rh < R && nbw[hg] < nb) {
+        const int64_t z = rh / cols, g = (rh - z * cols) / 32;
+        for (int b = nbw[hg] + w; b < nb; b += 4 * H) stage_live[(z * nb + b) * (cols / 32) + g] = 0u;
+      }
     }
   }
 }
