@@ -113,7 +113,19 @@ __global__ void __launch_bounds__(256) k_group_amax(const float* __restrict__ P,
   const float* p = P + k * cols + g * per;
   const float* x = X + (k / bs) * cols + g * per;
   uint32_t am = 0u;
-  for (int64_t c = threadIdx.x; c < per; c += 256) am = max(am, f2u(fabsf(p[c]) * x[c]) & 0x7FFFFFFFu);
+  // eight columns a thread per round, every load issued before the first product
+  constexpr int PER = 8;
+  for (int64_t c0 = threadIdx.x; c0 < per; c0 += 256 * PER) {
+    float pv[PER], xv[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int64_t c = c0 + 256 * u;
+      pv[u] = c < per ? p[c] : 0.0f;
+      xv[u] = c < per ? x[c] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) am = max(am, f2u(fabsf(pv[u]) * xv[u]) & 0x7FFFFFFFu);
+  }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) am = max(am, (uint32_t)__shfl_xor((int)am, off, 64));
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = am;
