@@ -32,8 +32,10 @@ typedef void* mxq_stream_t;
  *   2  mxq_lut_tables takes the code format (fmt_e, fmt_m) before the grid; mxq_systolic_hints gained a_live
  *      and c_end; mxq_softmax_quantize_t takes a tail; mxq_mask_minabs and mxq_attend_hints give the largest
  *      mask values; mxq_systolic_fast_lanes; the dither entry points.
- *   3  mxq_mx_pack_bytes; the MXQ_EBUSY status of mxq_systolic_noalloc. */
-#define MXQ_ABI_VERSION 3
+ *   3  mxq_mx_pack_bytes; the MXQ_EBUSY status of mxq_systolic_noalloc.
+ *   4  mxq_attend_windows writes one flag word per call and 64 query rows, each whole (was one per call, zeroed
+ *      by the caller). */
+#define MXQ_ABI_VERSION 4
 
 enum { MXQ_OK = 0, MXQ_EINVAL = 1, MXQ_EHIP = 2, MXQ_EBUSY = 3 };
 
@@ -257,10 +259,11 @@ int mxq_group_amax(const float* P, const float* X, int64_t K, int64_t cols, int6
 
 /* For each of Z attention calls, whether it keeps every key: bound = max(slack_scale * sum over d < D of
  * amax_a[d * lda + z] * amax_k[d * ldk + z], FLT_MIN) (float64), b32 = float(bound); a mask value c absorbs
- * the call's scores when c + b32 == c and c - b32 == c in float32.  flags (Z int32, zero on entry) gain bit 0
- * when the first key block (`block` keys) holds a key that some of the call's m query rows does not absorb, bit
- * 1 for the last block; Tk <= block sets both.  A call keeps every key iff its flag is 3.  Mask rows are
- * addressed as in mxq_scores_scale_mask.  Replaces the bound and `_live_span` == (0, Tk) test of
+ * the call's scores when c + b32 == c and c - b32 == c in float32.  flags (Z x ceil(m/64) int32, each written
+ * whole: nothing to clear first): word z * ceil(m/64) + c gets bit 0 when the first key block (`block` keys)
+ * holds a key that some of the call's query rows [64 c, 64 c + 64) does not absorb, bit 1 for the last block;
+ * Tk <= block sets both.  A call keeps every key iff the OR of its words is 3.  Mask rows are addressed as in
+ * mxq_scores_scale_mask.  Replaces the bound and `_live_span` == (0, Tk) test of
  * mxq/nn/_attention.py:117-127 for a batch of calls. */
 int mxq_attend_windows(const double* amax_a, int64_t lda, const double* amax_k, int64_t ldk, int64_t D, int64_t Z,
                        double slack_scale, const float* mask, int64_t mask_b_stride, int64_t mask_row_stride,

@@ -135,9 +135,10 @@ __global__ void __launch_bounds__(256) k_group_amax(const float* __restrict__ P,
 
 // Workgroup (z, chunk) of the Z x chunks grid checks query rows [chunk * WROWS, +WROWS) of call z.  Its bound:
 // max(slack_scale * sum over d of amax_a[d, z] * amax_k[d, z], FLT_MIN) in float64, b32 = float(bound); a mask
-// value c absorbs the call's scores when c + b32 == c and c - b32 == c (float32).  flags[z] (zero on entry)
-// gains bit 0 when some checked row leaves a key of the first key block unabsorbed, bit 1 for the last block;
-// Tk <= block sets both.  The mask row of query j of call z as in k_scores_scale_mask.
+// value c absorbs the call's scores when c + b32 == c and c - b32 == c (float32).  Its word of flags
+// (z * chunks + chunk, written whole: nothing to clear first) holds bit 0 when some checked row leaves a key of
+// the first key block unabsorbed, bit 1 for the last block; Tk <= block sets both.  The mask row of query j of
+// call z as in k_scores_scale_mask.
 constexpr int WROWS = 64;
 
 // Thread 0 gets the masked-key bound of call z: slack_scale * the float64 sum over d, in d order, of
@@ -171,7 +172,7 @@ __global__ void __launch_bounds__(256) k_attend_windows(const double* __restrict
   __shared__ float b32;
   const int z = blockIdx.x / chunks, chunk = blockIdx.x - z * chunks;
   if (Tk <= block) {
-    if (threadIdx.x == 0 && chunk == 0) atomicOr(flags + z, 3);
+    if (threadIdx.x == 0) flags[blockIdx.x] = 3;
     return;
   }
   __shared__ double terms[256];
@@ -206,7 +207,7 @@ __global__ void __launch_bounds__(256) k_attend_windows(const double* __restrict
     }
   }
   const int first = __syncthreads_or(live & 1), last = __syncthreads_or(live & 2);
-  if (threadIdx.x == 0 && (first || last)) atomicOr(flags + z, (first ? 1 : 0) | (last ? 2 : 0));
+  if (threadIdx.x == 0) flags[blockIdx.x] = (first ? 1 : 0) | (last ? 2 : 0);
 }
 
 __global__ void __launch_bounds__(256) k_mask_minabs(const float* __restrict__ mask, int64_t mask_b_stride,

@@ -81,6 +81,9 @@ struct SysArgs {
   // (z * tiles_y + ty) * tiles_x + tx, by descending work (k_tile_order); NULL: the grid's own tile, rows last
   // first
   const uint32_t* order;
+  // with an order and skip: bit 31 of an order entry set when its tile is skipped (tile_skipped at the fast tile
+  // size, as k_tile_bucket found it), so the fast kernels read no skip bytes; the tile is the low 31 bits
+  int order_skip;
   // with k_end: per problem, 32-row stage and 32-column group of A (suf_a) and of B (suf_b), nonzero when rows
   // of that stage may not be skipped (k_suffix_flags)
   const uint8_t* suf_a;
@@ -410,16 +413,24 @@ __device__ __forceinline__ void count_runs(uint32_t* cur, const uint16_t (&b)[kO
   }
 }
 
+// With STAGE (total <= kOrderStage), the positions' buckets stay in registers between the two passes (one read
+// of them), and the order is placed in LDS and then written out in runs of consecutive positions (placed straight
+// into global memory, one store instruction's lanes land 16 places apart).  Each thread's 16 adjacent positions
+// step their tile coordinates along the row instead of dividing for each.
+constexpr uint32_t kOrderStage = 36864;            // 144 KiB of LDS beside the 8 KiB of bucket counters
+
+template <bool STAGE>
 __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, uint32_t total,
                                                               const uint16_t* __restrict__ bucket, uint32_t* order) {
   constexpr int PB = kOrderBuckets / kOrderThreads;
   static_assert(PB * kOrderThreads == kOrderBuckets, "whole buckets per thread");
+  constexpr uint32_t stride = (uint32_t)kOrderThreads * kOrderRun;
+  constexpr int SI = STAGE ? (int)((kOrderStage + stride - 1) / stride) : 1;   // passes held in registers
   __shared__ uint32_t cur[kOrderBuckets];
   __shared__ uint32_t wsum[kOrderThreads / 64];
+  __shared__ uint32_t stage[STAGE ? kOrderStage : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderThreads) cur[b] = 0u;
-  __syncthreads();
-  const uint32_t stride = (uint32_t)kOrderThreads * kOrderRun;
   auto load_run = [&](uint32_t p0, uint16_t (&b)[kOrderRun]) {
     if (p0 + kOrderRun <= total) {
       const uint4* q = reinterpret_cast<const uint4*>(bucket + p0);   // p0 is a multiple of 16: 32-byte aligned
@@ -435,12 +446,56 @@ __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, u
       for (int u = 0; u < kOrderRun; ++u) b[u] = p0 + u < total ? bucket[p0 + u] : (uint16_t)kNoBucket;
     }
   };
-  for (uint32_t c0 = 0; c0 < total; c0 += stride) {
-    const uint32_t p0 = c0 + (uint32_t)threadIdx.x * kOrderRun;
-    uint16_t b[kOrderRun];
+  // pass 2's placement of positions p0 .. p0 + 15: tiles from one division, then stepped
+  const uint32_t nx = (uint32_t)a.tiles_x, ny = (uint32_t)a.tiles_y;
+  auto place = [&](uint32_t p0, const uint16_t (&b)[kOrderRun]) __attribute__((always_inline)) {
     uint32_t pos[kOrderRun];
-    load_run(p0, b);
-    count_runs<false>(cur, b, pos);
+    count_runs<true>(cur, b, pos);
+    uint32_t z, ty, tx;
+    uint32_t t = grid_tile(a, p0, z, ty, tx);
+#pragma unroll
+    for (int u = 0; u < kOrderRun; ++u) {
+      if (p0 + u < total) {
+        const uint32_t e = t | (a.order_skip && b[u] == 0 ? 0x80000000u : 0u);
+        if constexpr (STAGE) stage[pos[u]] = e;
+        else order[pos[u]] = e;
+      }
+      if (tx + 1u < nx) {                           // the next position: the next tile of the row, or of the
+        ++tx;                                       // row above (rows run last first), or of the next problem
+        ++t;
+      } else {
+        tx = 0u;
+        if (ty > 0u) {
+          --ty;
+        } else {
+          ++z;
+          ty = ny - 1u;
+        }
+        t = (z * ny + ty) * nx;
+      }
+    }
+  };
+  uint16_t held[SI][kOrderRun];
+  if constexpr (STAGE) {
+#pragma unroll
+    for (int i = 0; i < SI; ++i) load_run((uint32_t)i * stride + (uint32_t)threadIdx.x * kOrderRun, held[i]);
+  }
+  __syncthreads();
+  // (a thread's runs past the grid take no part: skipped, not counted as empty)
+  if constexpr (STAGE) {
+#pragma unroll
+    for (int i = 0; i < SI; ++i) {
+      uint32_t pos[kOrderRun];
+      if ((uint32_t)i * stride + (uint32_t)threadIdx.x * kOrderRun < total) count_runs<false>(cur, held[i], pos);
+    }
+  } else {
+    for (uint32_t c0 = 0; c0 < total; c0 += stride) {
+      uint16_t b[kOrderRun];
+      uint32_t pos[kOrderRun];
+      if (c0 + (uint32_t)threadIdx.x * kOrderRun >= total) break;
+      load_run(c0 + (uint32_t)threadIdx.x * kOrderRun, b);
+      count_runs<false>(cur, b, pos);
+    }
   }
   __syncthreads();
   // cur[b] <- the first position of bucket b: the count of every bucket above it (heavier work first)
@@ -466,16 +521,20 @@ __global__ void __launch_bounds__(kOrderThreads) k_tile_order(const SysArgs a, u
     at += cnt[u];
   }
   __syncthreads();
-  for (uint32_t c0 = 0; c0 < total; c0 += stride) {
-    const uint32_t p0 = c0 + (uint32_t)threadIdx.x * kOrderRun;
-    uint16_t b[kOrderRun];
-    uint32_t pos[kOrderRun];
-    load_run(p0, b);
-    count_runs<true>(cur, b, pos);
+  if constexpr (STAGE) {
 #pragma unroll
-    for (int u = 0; u < kOrderRun; ++u) {
-      uint32_t z, ty, tx;
-      if (p0 + u < total) order[pos[u]] = grid_tile(a, p0 + u, z, ty, tx);
+    for (int i = 0; i < SI; ++i) {
+      const uint32_t p0 = (uint32_t)i * stride + (uint32_t)threadIdx.x * kOrderRun;
+      if (p0 < total) place(p0, held[i]);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < total; i += kOrderThreads) order[i] = stage[i];
+  } else {
+    for (uint32_t c0 = 0; c0 < total; c0 += stride) {
+      uint16_t b[kOrderRun];
+      if (c0 + (uint32_t)threadIdx.x * kOrderRun >= total) break;
+      load_run(c0 + (uint32_t)threadIdx.x * kOrderRun, b);
+      place(c0 + (uint32_t)threadIdx.x * kOrderRun, b);
     }
   }
 }
@@ -503,8 +562,13 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   // Row tiles are dispatched last row first.  Where A is zero above a diagonal (attention's P^T under a causal
   // mask) the late rows carry the most nonzero stages: starting them first keeps them out of the tail.
   int64_t z, ty, tx;
+  bool marked = false;                              // skipped, as the order entry says (order_skip)
   if (args.order) {
-    const uint32_t t = args.order[blockIdx.x + args.tiles_x * (blockIdx.y + args.tiles_y * (int64_t)blockIdx.z)];
+    uint32_t t = args.order[blockIdx.x + args.tiles_x * (blockIdx.y + args.tiles_y * (int64_t)blockIdx.z)];
+    if (args.order_skip) {
+      marked = (t >> 31) != 0u;
+      t &= 0x7FFFFFFFu;
+    }
     const uint32_t zy = t / (uint32_t)args.tiles_x;
     tx = t - zy * (uint32_t)args.tiles_x;
     z = zy / (uint32_t)args.tiles_y;
@@ -532,7 +596,7 @@ __global__ void __launch_bounds__(256) k_systolic_fast(const SysArgs args, const
   // a tile made only of groups the caller does not need is written as +0, uncomputed (the same decision in
   // every thread)
   if (args.skip) {
-    if (tile_skipped(args, z, m0, n0, BM, BN)) {
+    if (args.order_skip ? marked : tile_skipped(args, z, m0, n0, BM, BN)) {
       if (threadIdx.x == 0) args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = 0u;
       if (!args.c_end || n0 < args.c_end[z * args.kend_groups + m0 / 64])
         write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
@@ -833,8 +897,13 @@ __global__ void __launch_bounds__(64 * 64 / (4 * TN)) k_systolic_fast64(const Sy
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // the tile: from the caller's dispatch order (k_tile_order: heaviest first) when there is one, else the grid's
   int64_t z, ty, tx;
+  bool marked = false;                              // skipped, as the order entry says (order_skip)
   if (args.order) {
-    const uint32_t t = args.order[blockIdx.x + args.tiles_x * (blockIdx.y + args.tiles_y * (int64_t)blockIdx.z)];
+    uint32_t t = args.order[blockIdx.x + args.tiles_x * (blockIdx.y + args.tiles_y * (int64_t)blockIdx.z)];
+    if (args.order_skip) {
+      marked = (t >> 31) != 0u;
+      t &= 0x7FFFFFFFu;
+    }
     const uint32_t zy = t / (uint32_t)args.tiles_x;
     tx = t - zy * (uint32_t)args.tiles_x;
     z = zy / (uint32_t)args.tiles_y;
@@ -990,7 +1059,7 @@ __global__ void __launch_bounds__(64 * 64 / (4 * TN)) k_systolic_fast64(const Sy
   };
 
   // a tile made only of groups the caller does not need is written as +0 (through the epilogue), uncomputed
-  if (args.skip && tile_skipped(args, z, m0, n0, BM, BN)) {
+  if (args.skip && (args.order_skip ? marked : tile_skipped(args, z, m0, n0, BM, BN))) {
     if (threadIdx.x == 0) args.flags[(z * args.tiles_y + ty) * args.tiles_x + tx] = 0u;
     if (!args.c_end || n0 < args.c_end[z * args.kend_groups + m0 / 64])
       write_tile<TM, TN>(args, z, m0 + tm * TM, n0 + tn * TN, C);
@@ -1422,8 +1491,10 @@ int run_systolic(const SysArgs& base, const int32_t* lane_e, const int32_t* lane
       // the buckets live in the flag area until the fast kernel rewrites it
       uint32_t* order = a.flags + W;
       uint16_t* bucket = reinterpret_cast<uint16_t*>(a.flags);
+      a.order_skip = a.skip && total <= (int64_t)0x80000000u ? 1 : 0;
       k_tile_bucket<<<(unsigned)mxq::ceil_div(total, 256), 256, 0, st>>>(a, (uint32_t)total, bucket);
-      k_tile_order<<<1, kOrderThreads, 0, st>>>(a, (uint32_t)total, bucket, order);
+      if (total <= kOrderStage) k_tile_order<true><<<1, kOrderThreads, 0, st>>>(a, (uint32_t)total, bucket, order);
+      else k_tile_order<false><<<1, kOrderThreads, 0, st>>>(a, (uint32_t)total, bucket, order);
       a.order = order;
     }
     {

@@ -26,7 +26,7 @@ _lib: Optional[ctypes.CDLL] = None
 _FN = {}            # entry point name -> its ctypes function, filled by load()
 
 #: the MXQ_ABI_VERSION of include/mxq_hip.h these signatures follow; a library reporting another is refused
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 c_i32, c_i64, c_f32, c_f64, c_ptr = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
 

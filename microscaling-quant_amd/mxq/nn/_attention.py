@@ -27,6 +27,7 @@ from dataclasses import dataclass
 from functools import partial
 from typing import Iterator, Optional, Tuple
 
+import numpy as np
 import torch
 
 from ..scheme import Scheme
@@ -251,12 +252,13 @@ def _mask_rows(bias: torch.Tensor, z0: int, Hkv: int, s0: int):
 
 def _windows(a_amax: torch.Tensor, k_amax: torch.Tensor, z0: int, Zc: int, scale: float, bias: torch.Tensor,
              Hkv: int, s0: int, m: int, block: int) -> torch.Tensor:
-    """Per pair z0..z0+Zc, 3 when its call keeps every key: the reference's bound (SLACK * |scale| * sum over
-    D of the two amax factors, at least FLT_MIN) and its live-key span == (0, Tk) (mxq/nn/_attention.py:117-127),
-    as int32 flags on the device (no host synchronisation)."""
+    """Per pair z0..z0+Zc, words whose OR is 3 when its call keeps every key: the reference's bound (SLACK *
+    |scale| * sum over D of the two amax factors, at least FLT_MIN) and its live-key span == (0, Tk)
+    (mxq/nn/_attention.py:117-127), as Zc x ceil(m/64) int32 words on the device (one per 64 query rows, each
+    written whole; no host synchronisation)."""
     from .. import _lib
     D, Tk = a_amax.shape[0], bias.shape[2]
-    flags = torch.zeros(Zc, dtype=torch.int32, device=a_amax.device)
+    flags = torch.empty(Zc, -(-m // 64), dtype=torch.int32, device=a_amax.device)
     mask, b_stride, r_stride = _mask_rows(bias, z0, Hkv, s0)
     with _lib.on(a_amax.device):
         _lib.run("mxq_attend_windows", _lib.ptr(a_amax), a_amax.shape[1], _lib.ptr(k_amax[:, z0:]), k_amax.shape[1],
@@ -369,25 +371,26 @@ class _Batched:
         the matmuls with an event behind it, so the host queues the matmuls while the GPU works, then waits for
         the copy alone and returns without waiting for the matmuls."""
         if bias is not None:
-            flags = torch.cat([c.flags for c in chunks])
+            flags = chunks[0].flags.view(-1) if len(chunks) == 1 else torch.cat([c.flags.view(-1) for c in chunks])
             host = torch.empty(flags.shape, dtype=flags.dtype, pin_memory=True)
             host.copy_(flags, non_blocking=True)
             copied = torch.cuda.Event()
             copied.record(torch.cuda.current_stream(flags.device))
         for c in chunks:
             self._chunk(c, qg, bias, kv, scale, vector, dims, out)
-        if bias is not None:
-            copied.synchronize()
-            every = host.tolist()
-        else:
-            every = []
+        if bias is None:
+            return
+        copied.synchronize()
+        words = host.numpy()
         # a pair that would skip masked keys gets the reference's own call, on the same codes, over its outputs
         at = 0
         for c in chunks:
-            for z in range(c.z1 - c.z0 if bias is not None else 0):
-                if every[at + z] != 3:
+            zc, w = c.flags.shape
+            every = np.bitwise_or.reduce(words[at:at + zc * w].reshape(zc, w), axis=1)
+            for z in range(zc):
+                if every[z] != 3:
                     self._per_pair(q, bias, kv, scale, vector, rnd, dims, c.z0 + z, c.z0 + z + 1, c.s0, c.e0, out)
-            at += c.z1 - c.z0 if bias is not None else 0
+            at += zc * w
 
     def _prepare(self, qg, bias, kv, k_amax, scale, vector, dims: _Dims, z0, z1, s0, e0) -> "_Prepared":
         """Pairs z0..z1, queries s0..e0: Q^T's codes and, with a mask, each pair's flag (int32 on the device: 3

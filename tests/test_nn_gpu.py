@@ -271,6 +271,33 @@ def test_attend_batched_pairwise_fallback(cuda):
     assert_bits_equal(got, want, "pairwise fallback")
 
 
+@pytest.mark.parametrize("K,cols,groups,bs,aligned", [(128, 65536, 32, 32, True), (70, 108, 3, 32, True),
+                                                       (9, 80, 4, 5, True), (9, 80, 4, 5, False),
+                                                       (13, 30, 3, 3, True)])
+def test_group_amax_against_torch(cuda, K, cols, groups, bs, aligned):
+    """mxq_group_amax against _code_amax of each column group (the reference's |code| * scale maximum per
+    contraction row): C5's Q^T shape, row counts that leave a partial group of four rows, block sizes that split
+    one, codes at a 4-byte offset and groups of 10 columns (4-byte loads), with NaN, Inf and zero scales."""
+    from mxq.nn import _attention
+    g = torch.Generator().manual_seed(K * 7 + cols)
+    nb = -(-K // bs)
+    flat = torch.randn(K * cols + 1, generator=g)
+    codes = (flat[:K * cols] if aligned else flat[1:]).view(K, cols)
+    scales = torch.ldexp(torch.ones(nb, cols), torch.randint(-6, 6, (nb, cols), generator=g).float())
+    codes[1, 5], codes[2, cols - 1], codes[K - 1, 0] = float("nan"), float("inf"), float("inf")
+    scales[0, 3], scales[(K - 1) // bs, 0] = 0.0, 0.0                 # 0 * Inf = NaN in the last row
+    dflat = flat.cuda()                                               # the offset kept on the device
+    dc, ds = (dflat[:K * cols] if aligned else dflat[1:]).view(K, cols), scales.cuda()
+    assert (dc.data_ptr() % 16 == 0) == aligned
+    got = _attention._group_amax(dc, ds, bs, groups).cpu()
+    per = cols // groups
+    want = torch.stack([_attention._code_amax(codes[:, j * per:(j + 1) * per], scales[:, j * per:(j + 1) * per], bs)
+                        for j in range(groups)], dim=1)
+    assert got.shape == want.shape == (K, groups)
+    assert torch.equal(got.isnan(), want.isnan()), "NaN positions differ"
+    assert torch.equal(torch.nan_to_num(got), torch.nan_to_num(want)), "group maxima differ"
+
+
 @pytest.mark.parametrize("kind", ["causal_min", "causal_weak", "window"])
 def test_attend_skip_hints(cuda, monkeypatch, kind):
     """The batched path's skip hints (32 x 32 score groups whose mask absorbs every score the call can make):
