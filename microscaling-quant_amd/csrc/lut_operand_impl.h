@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(1024) k_lut_quant(const T* __restrict__ V, Lut
     } else if (s.scale_rule) {
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
-        const float inv = 1.0f / xs[j];
+        const float inv = make_div(xs[j]).inv;        // every scale here is a normal power of two: exact
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i][j] = v[i][j] * inv;
       }

@@ -516,10 +516,14 @@ MXQ_HD float block_scale(float amax, const mxq_block_spec& s) {
 struct Div {
   float X, inv;
 };
+// inv: the reciprocal of a positive normal power of two 2^(be - 127), exact, from its bits: 2^(127 - be), normal
+// for be <= 253 and the subnormal 2^-127 for be = 254 (what 1.0f / X gives, without the division's sequence);
+// 0 for any other X.
 MXQ_HD Div make_div(float X) {
   const uint32_t u = f2u(X), be = (u >> 23) & 0xFFu;
   const bool p2 = (u & 0x807FFFFFu) == 0u && be >= 1u && be <= 254u;
-  return Div{X, p2 ? 1.0f / X : 0.0f};
+  const uint32_t ib = be <= 253u ? (254u - be) << 23 : 0x00400000u;
+  return Div{X, p2 ? u2f(ib) : 0.0f};
 }
 MXQ_HD float apply_div(float v, const Div& d) { return d.inv != 0.0f ? v * d.inv : v / d.X; }
 

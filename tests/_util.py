@@ -91,6 +91,9 @@ class HostNumerics:
     def bf16(self, x):
         return self._un("h_bf16", x)
 
+    def div_inv(self, x):
+        return self._un("h_div_inv", x)
+
     def floor_log2(self, x):
         return self._un("h_floor_log2", x, out_dtype=np.int32)
 

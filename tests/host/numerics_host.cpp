@@ -40,6 +40,9 @@ void h_truncate(const float* x, float* out, int64_t n, int m) {
 void h_flush(const float* x, float* out, int64_t n, float thr) {
   for (int64_t i = 0; i < n; ++i) out[i] = flush_product(x[i], thr);
 }
+void h_div_inv(const float* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = make_div(x[i]).inv;
+}
 void h_saturate(const float* x, float* out, int64_t n, float limit, float value) {
   for (int64_t i = 0; i < n; ++i) out[i] = saturate(x[i], limit, value);
 }

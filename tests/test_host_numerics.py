@@ -44,6 +44,20 @@ def test_bf16_and_round_bits(H, corpus):
             assert_bits_equal(H.round_bits(b, keep, MODE[mode]), nx.round_bits(b, keep, mode), f"round_bits {keep} {mode}")
 
 
+def test_div_reciprocal(H, corpus):
+    """make_div's reciprocal, read off the exponent bits, against numpy's IEEE float32 division 1 / x for every
+    positive normal power of two 2^-126 .. 2^127 (2^127's reciprocal is the subnormal 2^-127), and 0 for
+    everything else: negative powers, the subnormal 2^-127 itself, non-powers, zeros, infinities and NaNs."""
+    p2 = np.ldexp(np.float32(1.0), np.arange(-126, 128)).astype(np.float32)
+    with np.errstate(over="ignore", under="ignore"):
+        want = (np.float32(1.0) / p2).astype(np.float32)
+    assert_bits_equal(H.div_inv(p2), want, "power-of-two reciprocals")
+    assert H.div_inv(np.float32([2.0 ** 127]))[0] == np.float32(2.0 ** -127), "2^-127 is kept as a subnormal"
+    others = np.concatenate([corpus, -p2, np.float32([0.0, -0.0, np.inf, -np.inf, np.nan, 2.0 ** -127, 3.0, 0.75])])
+    others = others[~np.isin(others.view(np.uint32), p2.view(np.uint32))].astype(np.float32)
+    assert not H.div_inv(others).any(), "only positive normal powers of two have a reciprocal"
+
+
 @pytest.mark.parametrize("grid", ["qtorch", "ieee"])
 @pytest.mark.parametrize("mode", MODES)
 def test_float_em_f32(H, corpus, grid, mode):
