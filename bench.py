@@ -46,11 +46,12 @@ VALU_LANE_OPS = 157.3e12 / 2
 # The roof prices every MAC at that step.
 SLOTS_PER_MAC_MODEL = 8
 VALU_ROOF_TOPS = VALU_LANE_OPS / SLOTS_PER_MAC_MODEL * 2 / 1e12   # 19.66 TOP/s emulated
-# The survey's algorithmic model: 10 lane-operations per emulated MAC (multiply, truncate, flush, saturate, the
-# two lane roundings, the +0 fix-up, the exact add, its rounding, the zero short-circuit), priced at the same
-# 78.6 T lane-operations per second; the fast kernel does the step in fewer, so this fraction can pass 1.
-OPS_PER_MAC_SURVEY = 10
-SURVEY_ROOF_TOPS = VALU_LANE_OPS / OPS_PER_MAC_SURVEY * 2 / 1e12    # 15.73 TOP/s emulated
+# The algorithmic model of the reference's MAC (roofline.frac_survey_model): 10 lane-operations per emulated MAC
+# (multiply, truncate, flush, saturate, the two lane roundings, the +0 fix-up, the exact add, its rounding, the
+# zero short-circuit), priced at the same 78.6 T lane-operations per second; the fast kernel does the step in
+# fewer, so this fraction can pass 1.
+OPS_PER_MAC_MODEL10 = 10
+MODEL10_ROOF_TOPS = VALU_LANE_OPS / OPS_PER_MAC_MODEL10 * 2 / 1e12    # 15.73 TOP/s emulated
 VALU_PROBE_KINDS = ("v_add_f32", "v_mul_f32", "v_and_b32", "v_rndne_f32", "v_bfe_u32", "v_add3_u32", "v_pk_mul_f16",
                     "v_pk_add_f16", "v_fma_mix_f32", "v_cvt_pkrtz_f16_f32", "v_cvt_pk_bf16_f32")
 VALU_CHAIN_KINDS = ("v_mul_f32", "v_pk_mul_f16")     # probe kinds 11 and 12: one dependent chain each
@@ -780,7 +781,7 @@ def main():
         "roofline": {"bound": "valu", "achieved": round(k_tops, 4) if k_tops else None,
                      "peak": round(VALU_ROOF_TOPS, 3), "unit": "TOP/s",
                      "frac": round(k_tops / VALU_ROOF_TOPS, 4) if k_tops else None,
-                     "frac_survey_model": round(k_tops / SURVEY_ROOF_TOPS, 4) if k_tops else None,
+                     "frac_survey_model": round(k_tops / MODEL10_ROOF_TOPS, 4) if k_tops else None,
                      "traffic": _profile_value("systolic_fast_c2_traffic", "bytes_per_launch"),
                      "kernel": "k_systolic_fast64<16, true, true, 2>", "kernel_ms": round(kms, 4) if kms else None,
                      "kernel_launches_timed": launches,
