@@ -424,6 +424,47 @@ def test_batched_hints(cuda, count, M, N, K):
     assert_bits_equal(got[keep], want[keep], "skip and k_end together")
 
 
+@pytest.mark.parametrize("count", [136, 160], ids=["order_34816_tiles", "order_40960_tiles"])
+def test_batched_hints_large_orders(cuda, count):
+    """The dispatch order over 34,816 and 40,960 tiles of 64 x 64 (1024 x 1024 problems): the order kernel holds
+    three runs of positions a thread, and past 36,864 positions it writes the order without staging it in LDS.
+    A causal skip map (the skipped tiles marked in the order) leaves every unmarked group equal to the hint-free
+    result and every marked one that result or +0; a k_end bound (tiles ordered by their stages) gives the
+    hint-free result everywhere.  Compared on the device."""
+    from mxq import _lib, block, matmul
+    from mxq.matmul._systolic import systolic_batched
+    M = N = 1024
+    K = 64
+    g = torch.Generator().manual_seed(count)
+    A = torch.randn(K, count * M, generator=g)
+    ends = (torch.randint(0, 3, (count, M // 64), generator=g) * 32).to(torch.int32)
+    for z in range(count):
+        for t in range(M // 64):
+            A[int(ends[z, t]):, z * M + 64 * t:z * M + 64 * t + 64] = 0.0
+    P_A, X_A = block.mxgemmini.quantize(A.cuda(), "MXFP8_E4M3", axis=0)
+    P_B, X_B = block.mxgemmini.quantize((torch.randn(K, count * N, generator=g) * 0.1).cuda(), "MXFP8_E4M3", axis=0)
+    lay = _lib.SystolicLayout(ld_a=count * M, batch_a=M, ld_xa=count * M, batch_xa=M,
+                              ld_b=count * N, batch_b=N, ld_xb=count * N, batch_xb=N, ld_c=N, batch_c=M * N)
+    ar = matmul.MXGEMMINI()
+
+    def run(**hints):
+        C = torch.full((count, M, N), float("nan"), device="cuda")
+        systolic_batched((P_A, X_A, P_B, X_B), lay, count, K, M, N, C, ar, HW_FINAL, **hints)
+        return C.view(torch.int32)
+
+    want = run()
+    gm = M // 32
+    tri = (torch.arange(gm)[None, :] > torch.arange(gm)[:, None]).to(torch.uint8)
+    skip = tri[None].expand(count, gm, gm).contiguous().cuda()
+    got = run(skip=skip)
+    full = skip.bool().repeat_interleave(32, 1).repeat_interleave(32, 2)
+    assert torch.equal(got[~full], want[~full]), "groups left differ from the hint-free result"
+    assert ((got == want) | (got == 0))[full].all(), "marked groups are neither the result nor +0"
+    del got, full
+    got = run(k_end=ends.cuda())
+    assert torch.equal(got, want), "k_end changed a result"
+
+
 @pytest.mark.parametrize("count,K,M,N", [(3, 200, 96, 70), (8, 256, 512, 256)], ids=["stages32", "stages64"])
 def test_k_end_nonfinite_past_the_end(cuda, count, K, M, N):
     """Rows past k_end where A is +-0 but B holds an Inf, or a scale of A's is NaN, or one of B's is Inf: 0 * Inf
